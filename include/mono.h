@@ -1,0 +1,128 @@
+/* C-ABI of the MI355X (gfx950) decoder-layer monokernel path.
+ *
+ * One shared library, libmono_gfx950.so, exports the entry points below. Every
+ * argument is a plain pointer, integer or float: device pointers to tensors the
+ * caller owns (SGLang's weights and caches, read in place), sizes, and a HIP stream
+ * passed as `void*` (a hipStream_t; NULL is the null stream). Every call is
+ * stream-ordered and performs no host synchronisation, so a caller may capture it
+ * in a HIP graph.
+ *
+ * Errors: every int-returning call returns MONO_OK (0) or a MONO_E* code and leaves
+ * a message for `mono_last_error()` (per host thread) naming the argument and what
+ * was expected, in the manner of the reference's ValueError / RuntimeError
+ * (sgl_amd_mono/glm53/gfx950/runner.py:218-273).
+ *
+ * Reference interfaces replaced (yuychang/sgl-amd-mono):
+ *   - Glm53Runtime(key, rank, group, device)            glm53/gfx950/runner.py:133-215
+ *       -> mono_moe_create / mono_attn_create (scratch, counters, guard words)
+ *   - Glm53Runtime.set_deadline / advance_step          glm53/gfx950/runner.py:197-210
+ *       -> mono_set_deadline / mono_advance_step
+ *   - Glm53LayerOp.launch(h, caches, cos, sin, step)    glm53/gfx950/runner.py:240-321
+ *       (rt.dispatch of 42 raw data_ptr() ints + stream)
+ *       -> mono_moe_fp8_forward  (its MoE half, stages 8-10, kernel.py:4199-5187)
+ *       -> mono_attn_forward     (its sparse-attention half, kernel.py:2684-4123)
+ *   - minimax_m31 FFN launch, A16W4 experts              minimax_m31/ffn.py:1182-1378
+ *       -> mono_moe_mxfp4_forward
+ *   - guard error words read back by tests              common/guard.py:16-30,100-241
+ *       -> mono_read_error_words
+ */
+#ifndef MONO_GFX950_H
+#define MONO_GFX950_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MONO_ABI_VERSION 1
+
+enum {
+  MONO_OK = 0,
+  MONO_EINVAL = 1, /* an argument is out of range / the wrong shape */
+  MONO_EHIP = 2,   /* a HIP runtime call failed */
+  MONO_ESTATE = 3, /* wrong device current, destroyed handle, ... */
+  MONO_ENOMEM = 4,
+};
+
+enum { MONO_ROUTER_SIGMOID_BIAS = 0, MONO_ROUTER_SOFTMAX = 1 };
+enum { MONO_WEIGHT_FP8_BLOCK128 = 0, MONO_WEIGHT_MXFP4 = 1 };
+
+/* Version of this ABI (MONO_ABI_VERSION of the library). */
+int mono_abi_version(void);
+
+/* Message of the last failing call on this host thread ("" if none). */
+const char* mono_last_error(void);
+
+/* ------------------------------------------------------------------ MoE phase */
+
+typedef struct mono_moe mono_moe;
+
+typedef struct {
+  int32_t device;        /* HIP device ordinal the runtime lives on */
+  int32_t max_rows;      /* widest decode step served, 1..16 */
+  int32_t hidden;        /* H */
+  int32_t n_experts;     /* routed experts E; the shared expert is id E */
+  int32_t top_k;         /* routed picks a row (8) */
+  int32_t inter;         /* expert intermediate I of this GPU's share */
+  int32_t weight_format; /* MONO_WEIGHT_* */
+  int32_t router;        /* MONO_ROUTER_* */
+  float route_scale;     /* routed_scaling_factor (2.5 sigmoid router, 1 softmax) */
+  float eps;             /* RMSNorm epsilon of the post-attention norm */
+} mono_moe_config;
+
+/* Replaces Glm53Runtime's MoE scratch (runner.py:133-195). Allocates the runtime's
+ * device scratch on `cfg->device` (which must be current). */
+int mono_moe_create(const mono_moe_config* cfg, mono_moe** out);
+/* Frees the scratch. NULL is a no-op; idempotent like PeerBuffer.close
+ * (common/peer.py:157-165). */
+int mono_moe_destroy(mono_moe* moe);
+
+/* FP8 MoE block of one decode step (kernel.py:4199-5187):
+ * out = a + sum_slots w * down_e(silu(gate_e(xq)) * up_e(xq)),
+ * xq = FP8(RMSNorm(a) * g_post), sigmoid + bias top-k router, shared expert id E
+ * with weight 1. Optional outputs (NULL skips) expose the routing for tests. */
+typedef struct {
+  const void* a;        /* bf16 [rows, H] residual stream after attention */
+  const void* g_post;   /* bf16 [H] post-attention RMSNorm weight */
+  const void* w_router; /* bf16 [E, H] gate weight */
+  const float* bias;    /* f32 [E] e_score_correction_bias */
+  const void* w13;      /* e4m3 [E+1, 2I, H] gate rows then up rows */
+  const float* s13;     /* f32 [E+1, 2I/128, H/128] */
+  const void* w2;       /* e4m3 [E+1, H, I] */
+  const float* s2;      /* f32 [E+1, H/128, I/128] */
+  void* out;            /* bf16 [rows, H] */
+  int32_t rows;         /* 1..max_rows */
+  float* y;             /* optional f32 [rows, H]: the MoE sum before the residual */
+  float* scores;        /* optional f32 [rows, E]: sigmoid scores */
+  int32_t* topk_ids;    /* optional i32 [rows, top_k] in pick order */
+  float* topk_w;        /* optional f32 [rows, top_k] */
+} mono_moe_fp8_args;
+
+int mono_moe_fp8_forward(mono_moe* moe, const mono_moe_fp8_args* args, void* stream);
+
+/* MXFP4 (E2M1 + E8M0 per 32) A16W4 MoE of one decode step:
+ * out = bf16(sum_slots w * down_e(bf16(silu(gate_e(x)) * up_e(x)))), softmax top-k
+ * router on the given f32 logits, shared expert id E with weight 1. */
+typedef struct {
+  const void* x;        /* bf16 [rows, H] */
+  const float* logits;  /* f32 [rows, E] gate logits */
+  const void* w13;      /* u8 [E+1, 2I, H/2] packed E2M1 (even k in the low nibble) */
+  const void* s13;      /* u8 [E+1, 2I, H/32] E8M0 */
+  const void* w2;       /* u8 [E+1, H, I/2] */
+  const void* s2;       /* u8 [E+1, H, I/32] */
+  void* out;            /* bf16 [rows, H] */
+  int32_t rows;
+  float* y;             /* optional f32 [rows, H] */
+  int32_t* topk_ids;    /* optional i32 [rows, top_k] */
+  float* topk_w;        /* optional f32 [rows, top_k] */
+} mono_moe_mxfp4_args;
+
+int mono_moe_mxfp4_forward(mono_moe* moe, const mono_moe_mxfp4_args* args, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MONO_GFX950_H */

@@ -1,0 +1,99 @@
+"""ctypes binding of libmono_gfx950.so (the C-ABI declared in include/mono.h).
+
+The library is built in-tree by ``sgl_amd_mono_amd.build``. There is no fallback:
+if the library is missing or fails to load, every entry point raises.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import threading
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libmono_gfx950.so"
+ABI_VERSION = 1
+
+MONO_OK, MONO_EINVAL, MONO_EHIP, MONO_ESTATE, MONO_ENOMEM = 0, 1, 2, 3, 4
+ROUTER_SIGMOID_BIAS, ROUTER_SOFTMAX = 0, 1
+WEIGHT_FP8_BLOCK128, WEIGHT_MXFP4 = 0, 1
+
+_VP, _I32, _F32 = C.c_void_p, C.c_int32, C.c_float
+
+
+class MoeConfig(C.Structure):
+    _fields_ = [
+        ("device", _I32), ("max_rows", _I32), ("hidden", _I32), ("n_experts", _I32),
+        ("top_k", _I32), ("inter", _I32), ("weight_format", _I32), ("router", _I32),
+        ("route_scale", _F32), ("eps", _F32),
+    ]
+
+
+class MoeFp8Args(C.Structure):
+    _fields_ = [
+        ("a", _VP), ("g_post", _VP), ("w_router", _VP), ("bias", _VP),
+        ("w13", _VP), ("s13", _VP), ("w2", _VP), ("s2", _VP), ("out", _VP),
+        ("rows", _I32), ("y", _VP), ("scores", _VP), ("topk_ids", _VP), ("topk_w", _VP),
+    ]
+
+
+class MoeMxfp4Args(C.Structure):
+    _fields_ = [
+        ("x", _VP), ("logits", _VP), ("w13", _VP), ("s13", _VP), ("w2", _VP), ("s2", _VP),
+        ("out", _VP), ("rows", _I32), ("y", _VP), ("topk_ids", _VP), ("topk_w", _VP),
+    ]
+
+
+# entry point -> (restype, argtypes); every name include/mono.h declares
+SIGNATURES = {
+    "mono_abi_version": (C.c_int, []),
+    "mono_last_error": (C.c_char_p, []),
+    "mono_moe_create": (C.c_int, [C.POINTER(MoeConfig), C.POINTER(_VP)]),
+    "mono_moe_destroy": (C.c_int, [_VP]),
+    "mono_moe_fp8_forward": (C.c_int, [_VP, C.POINTER(MoeFp8Args), _VP]),
+    "mono_moe_mxfp4_forward": (C.c_int, [_VP, C.POINTER(MoeMxfp4Args), _VP]),
+}
+
+_lock = threading.Lock()
+_lib = None
+
+
+class MonoError(RuntimeError):
+    """A C-ABI call returned an error code."""
+
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"[mono error {code}] {msg}")
+        self.code = code
+
+
+def lib() -> C.CDLL:
+    """The loaded library (loads on first use; raises if it is not built)."""
+    global _lib
+    with _lock:
+        if _lib is None:
+            if not LIB_PATH.exists():
+                raise RuntimeError(
+                    f"{LIB_PATH} is not built: run `python -m sgl_amd_mono_amd.build` "
+                    "(the HIP path has no CPU fallback)"
+                )
+            h = C.CDLL(str(LIB_PATH))
+            for name, (res, args) in SIGNATURES.items():
+                fn = getattr(h, name)
+                fn.restype, fn.argtypes = res, args
+            got = h.mono_abi_version()
+            if got != ABI_VERSION:
+                raise RuntimeError(f"{LIB_PATH}: ABI version {got}, this binding expects {ABI_VERSION}")
+            _lib = h
+        return _lib
+
+
+def check(rc: int) -> None:
+    if rc != MONO_OK:
+        msg = lib().mono_last_error().decode(errors="replace")
+        if rc == MONO_EINVAL:
+            raise ValueError(msg)
+        raise MonoError(rc, msg)
+
+
+def ptr(t) -> int | None:
+    """Device pointer of a tensor (None -> NULL)."""
+    return None if t is None else t.data_ptr()

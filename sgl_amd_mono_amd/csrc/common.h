@@ -1,0 +1,158 @@
+// Device helpers shared by the gfx950 kernels of the decoder-layer path.
+//
+// Wave64 reductions, the FP8 / FP4 / bf16 converts of CDNA4, the 16x16 MFMA tiles
+// the GEMVs use, nontemporal weight loads, and the "last workgroup to arrive"
+// hand-off that lets a stage finish a reduction without any workgroup waiting on
+// another (no spin, so no deadlock whatever the residency).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define MONO_DEV __device__ __forceinline__
+
+typedef int32_t i32x8 __attribute__((ext_vector_type(8)));
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+namespace mono {
+
+constexpr int WAVE = 64;
+constexpr float FP8_MAX = 448.0f;
+
+// ------------------------------------------------------------------ lanes
+MONO_DEV int lane_id() { return __lane_id(); }
+
+MONO_DEV float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
+  return v;
+}
+
+MONO_DEV float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, WAVE));
+  return v;
+}
+
+MONO_DEV uint32_t wave_umax(uint32_t v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    uint32_t p = __shfl_xor(v, o, WAVE);
+    v = v > p ? v : p;
+  }
+  return v;
+}
+
+// max over groups of `width` consecutive lanes (width a power of two <= 64)
+template <int WIDTH>
+MONO_DEV float group_max(float v) {
+#pragma unroll
+  for (int o = WIDTH / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, WAVE));
+  return v;
+}
+
+// ------------------------------------------------------------------ math
+MONO_DEV float hw_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
+MONO_DEV float hw_rsq(float x) { return __builtin_amdgcn_rsqf(x); }
+MONO_DEV float hw_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.4426950408889634f); }
+MONO_DEV float sigmoid(float x) { return hw_rcp(1.0f + hw_exp(-x)); }
+MONO_DEV float silu(float x) { return x * sigmoid(x); }
+
+// ------------------------------------------------------------------ bf16
+MONO_DEV float bf16_bits_to_f32(uint32_t b16) { return __uint_as_float(b16 << 16); }
+MONO_DEV float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+MONO_DEV float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+MONO_DEV uint16_t f32_to_bf16_bits(float f) {
+  __bf16 b = (__bf16)f;  // round to nearest even
+  return __builtin_bit_cast(uint16_t, b);
+}
+MONO_DEV uint32_t pack_bf16x2(float lo, float hi) {
+  return (uint32_t)f32_to_bf16_bits(lo) | ((uint32_t)f32_to_bf16_bits(hi) << 16);
+}
+MONO_DEV float bf16_round(float f) { return (float)(__bf16)f; }
+
+// ------------------------------------------------------------------ FP8 (OCP E4M3)
+// two f32 (already clamped to +-448) -> two E4M3 bytes in the low 16 bits, RNE
+MONO_DEV uint32_t fp8x2_pack(float a, float b) {
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false) & 0xffffu;
+}
+// four f32 -> one dword of four E4M3 bytes
+MONO_DEV uint32_t fp8x4_pack(float a, float b, float c, float d) {
+  int lo = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c, d, lo, true);
+}
+// bytes 0,1 (HI=false) or 2,3 (HI=true) of a dword -> two f32
+template <bool HI>
+MONO_DEV f32x2 fp8x2_unpack(uint32_t w) {
+  return __builtin_amdgcn_cvt_pk_f32_fp8((int)w, HI);
+}
+
+// ------------------------------------------------------------------ FP4 (E2M1) + E8M0
+// byte `sel` (0..3) of `w` (two E2M1 codes, low nibble first) times `scale` -> two bf16
+MONO_DEV bf16x2 fp4x2_to_bf16(uint32_t w, float scale, int sel) {
+  switch (sel) {
+    case 0: return __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 0);
+    case 1: return __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 1);
+    case 2: return __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 2);
+    default: return __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 3);
+  }
+}
+// E8M0 code -> f32 2^(code-127) (code 0 -> 2^-127 is denormal: built from bits)
+MONO_DEV float e8m0_to_f32(uint32_t code) {
+  return code == 0 ? __uint_as_float(0x00400000u) : __uint_as_float(code << 23);
+}
+
+// ------------------------------------------------------------------ MFMA tiles
+// C[16x16] += A[16x128] * B[128x16], E4M3 x E4M3, unit block scales.
+// Lane l supplies row / column (l % 16) and one 32-element k group (l / 16).
+MONO_DEV f32x4 mfma_fp8(const i32x8& a, const i32x8& b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 127, 0, 127);
+}
+// E2M1 x E2M1 with per-lane E8M0 scales (lane l: its row / column's scale of k group l / 16)
+MONO_DEV f32x4 mfma_fp4(const i32x8& a, const i32x8& b, const f32x4& c, int sa, int sb) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 4, 4, 0, sa, 0, sb);
+}
+// C[16x16] += A[16x32] * B[32x16] in bf16; lane l: row / column l % 16, k 8*(l/16)..+7
+MONO_DEV f32x4 mfma_bf16(const bf16x8& a, const bf16x8& b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// ------------------------------------------------------------------ memory
+MONO_DEV u32x4 ld_nt_u32x4(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+MONO_DEV u32x4 ld_u32x4(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+// 32 bytes (two dwordx4) straight into one MFMA operand tuple
+MONO_DEV i32x8 ld_nt_i32x8(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const i32x8*>(p));
+}
+MONO_DEV i32x8 ld_i32x8(const void* p) { return *reinterpret_cast<const i32x8*>(p); }
+
+// Release this workgroup's global writes, then count it in; true for exactly one
+// workgroup, the last of `total` to arrive, which then sees every other's writes
+// and resets the counter for the next launch. Call from the whole workgroup.
+MONO_DEV bool last_arrival(uint32_t* counter, uint32_t total, uint32_t* lds_flag) {
+  __threadfence();  // every wave releases its own stores at device scope
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t prev = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    uint32_t last = prev + 1 == total;
+    if (last) {
+      __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __threadfence();
+    }
+    *lds_flag = last;
+  }
+  __syncthreads();
+  bool last = *lds_flag != 0;
+  if (last) __threadfence();  // acquire for every thread of the last workgroup
+  return last;
+}
+
+}  // namespace mono

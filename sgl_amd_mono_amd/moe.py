@@ -1,0 +1,184 @@
+"""Host side of the MoE phase: a runtime per (width, geometry) and its forward calls.
+
+Mirrors the reference's runtime / launch split (sgl_amd_mono/glm53/gfx950/runner.py:
+``Glm53Runtime`` :133-215 owns the scratch; ``Glm53LayerOp.launch`` :240-321 checks
+every tensor's shape, dtype and stride and dispatches raw pointers). Here the
+scratch lives in the C library's handle; this module checks the tensors, passes
+their ``data_ptr()`` through the C-ABI and enqueues on the current stream.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+
+
+@dataclass(frozen=True)
+class MoeGeometry:
+    """One GPU's share of a MoE layer."""
+
+    hidden: int
+    n_experts: int
+    top_k: int
+    inter: int
+    route_scale: float
+    eps: float
+    router: str  # "sigmoid_bias" | "softmax"
+    weights: str  # "fp8_block128" | "mxfp4"
+
+
+# DeepSeek-V3.2-shaped MoE at TP=4 (intermediate 2048 / 4)
+FP8_MOE = MoeGeometry(7168, 256, 8, 512, 2.5, 1e-6, "sigmoid_bias", "fp8_block128")
+# MXFP4 experts at TP=4 (intermediate 1536 / 4), softmax router
+MXFP4_MOE = MoeGeometry(3072, 256, 8, 384, 1.0, 0.0, "softmax", "mxfp4")
+
+
+@dataclass
+class Fp8MoeWeights:
+    """One layer's MoE tensors as SGLang loads them (read in place, never copied)."""
+
+    g_post: torch.Tensor  # bf16 [H]
+    w_router: torch.Tensor  # bf16 [E, H]
+    bias: torch.Tensor  # f32 [E]
+    w13: torch.Tensor  # float8_e4m3fn / uint8 [E+1, 2I, H]
+    s13: torch.Tensor  # f32 [E+1, 2I/128, H/128]
+    w2: torch.Tensor  # float8_e4m3fn / uint8 [E+1, H, I]
+    s2: torch.Tensor  # f32 [E+1, H/128, I/128]
+
+
+@dataclass
+class Mxfp4MoeWeights:
+    w13: torch.Tensor  # uint8 [E+1, 2I, H/2] packed E2M1
+    s13: torch.Tensor  # uint8 [E+1, 2I, H/32] E8M0
+    w2: torch.Tensor  # uint8 [E+1, H, I/2]
+    s2: torch.Tensor  # uint8 [E+1, H, I/32]
+
+
+def need(t: torch.Tensor, name: str, shape: tuple, dtypes, device: torch.device) -> None:
+    """Raise ValueError naming the tensor unless it has this shape / dtype and is a
+    contiguous tensor on ``device`` (the checks of glm53/gfx950/runner.py:250-273)."""
+    if not isinstance(t, torch.Tensor):
+        raise ValueError(f"{name}: expected a tensor, got {type(t).__name__}")
+    dtypes = dtypes if isinstance(dtypes, tuple) else (dtypes,)
+    if tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{name}: expected shape {tuple(shape)}, got {tuple(t.shape)}")
+    if t.dtype not in dtypes:
+        raise ValueError(f"{name}: expected dtype {' or '.join(map(str, dtypes))}, got {t.dtype}")
+    if t.device != device:
+        raise ValueError(f"{name}: expected device {device}, got {t.device}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name}: expected a contiguous tensor (strides {t.stride()})")
+
+
+FP8_TYPES = (torch.float8_e4m3fn, torch.uint8)
+
+
+class MoeRuntime:
+    """The C library's MoE handle for one geometry and a widest step ``max_rows``."""
+
+    def __init__(self, geo: MoeGeometry, max_rows: int, device=None):
+        self.geo = geo
+        self.device = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
+        if self.device.type != "cuda":
+            raise ValueError(f"MoeRuntime needs a GPU device, got {self.device}")
+        cfg = _lib.MoeConfig(
+            device=self.device.index, max_rows=max_rows, hidden=geo.hidden, n_experts=geo.n_experts,
+            top_k=geo.top_k, inter=geo.inter,
+            weight_format=_lib.WEIGHT_FP8_BLOCK128 if geo.weights == "fp8_block128" else _lib.WEIGHT_MXFP4,
+            router=_lib.ROUTER_SIGMOID_BIAS if geo.router == "sigmoid_bias" else _lib.ROUTER_SOFTMAX,
+            route_scale=geo.route_scale, eps=geo.eps,
+        )  # fmt: skip
+        self.max_rows = max_rows
+        h = C.c_void_p()
+        with torch.cuda.device(self.device):
+            _lib.check(_lib.lib().mono_moe_create(C.byref(cfg), C.byref(h)))
+        self._h = h
+
+    def close(self) -> None:
+        if getattr(self, "_h", None) is not None and self._h.value:
+            _lib.check(_lib.lib().mono_moe_destroy(self._h))
+            self._h = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _stream(self) -> int:
+        return torch.cuda.current_stream(self.device).cuda_stream
+
+    def forward_fp8(self, a: torch.Tensor, w: Fp8MoeWeights, out: torch.Tensor | None = None,
+                    debug: bool = False):
+        """``a + MoE(a)`` for one decode step. ``debug`` also
+        returns the routing (scores, top-k ids / weights) and the f32 MoE sum."""
+        g, dev = self.geo, self.device
+        H, E, I, K = g.hidden, g.n_experts, g.inter, g.top_k
+        if a.dim() != 2 or not 1 <= a.shape[0] <= self.max_rows:
+            raise ValueError(f"a: expected [rows <= {self.max_rows}, {H}], got {tuple(a.shape)}")
+        S = a.shape[0]
+        need(a, "a", (S, H), torch.bfloat16, dev)
+        need(w.g_post, "g_post", (H,), torch.bfloat16, dev)
+        need(w.w_router, "w_router", (E, H), torch.bfloat16, dev)
+        need(w.bias, "bias", (E,), torch.float32, dev)
+        need(w.w13, "w13", (E + 1, 2 * I, H), FP8_TYPES, dev)
+        need(w.s13, "s13", (E + 1, 2 * I // 128, H // 128), torch.float32, dev)
+        need(w.w2, "w2", (E + 1, H, I), FP8_TYPES, dev)
+        need(w.s2, "s2", (E + 1, H // 128, I // 128), torch.float32, dev)
+        if out is None:
+            out = torch.empty_like(a)
+        need(out, "out", (S, H), torch.bfloat16, dev)
+        dbg = {}
+        if debug:
+            dbg = dict(
+                y=torch.empty(S, H, dtype=torch.float32, device=dev),
+                scores=torch.empty(S, E, dtype=torch.float32, device=dev),
+                topk_ids=torch.empty(S, K, dtype=torch.int32, device=dev),
+                topk_w=torch.empty(S, K, dtype=torch.float32, device=dev),
+            )
+        P = _lib.ptr
+        args = _lib.MoeFp8Args(
+            a=P(a), g_post=P(w.g_post), w_router=P(w.w_router), bias=P(w.bias),
+            w13=P(w.w13), s13=P(w.s13), w2=P(w.w2), s2=P(w.s2), out=P(out), rows=S,
+            y=P(dbg.get("y")), scores=P(dbg.get("scores")),
+            topk_ids=P(dbg.get("topk_ids")), topk_w=P(dbg.get("topk_w")),
+        )  # fmt: skip
+        _lib.check(_lib.lib().mono_moe_fp8_forward(self._h, C.byref(args), self._stream()))
+        return (out, dbg) if debug else out
+
+    def forward_mxfp4(self, x: torch.Tensor, logits: torch.Tensor, w: Mxfp4MoeWeights,
+                      out: torch.Tensor | None = None, debug: bool = False):
+        """``MoE(x)`` with MXFP4 experts behind a softmax router."""
+        g, dev = self.geo, self.device
+        H, E, I, K = g.hidden, g.n_experts, g.inter, g.top_k
+        if x.dim() != 2 or not 1 <= x.shape[0] <= self.max_rows:
+            raise ValueError(f"x: expected [rows <= {self.max_rows}, {H}], got {tuple(x.shape)}")
+        S = x.shape[0]
+        need(x, "x", (S, H), torch.bfloat16, dev)
+        need(logits, "logits", (S, E), torch.float32, dev)
+        need(w.w13, "w13", (E + 1, 2 * I, H // 2), torch.uint8, dev)
+        need(w.s13, "s13", (E + 1, 2 * I, H // 32), torch.uint8, dev)
+        need(w.w2, "w2", (E + 1, H, I // 2), torch.uint8, dev)
+        need(w.s2, "s2", (E + 1, H, I // 32), torch.uint8, dev)
+        if out is None:
+            out = torch.empty_like(x)
+        need(out, "out", (S, H), torch.bfloat16, dev)
+        dbg = {}
+        if debug:
+            dbg = dict(
+                y=torch.empty(S, H, dtype=torch.float32, device=dev),
+                topk_ids=torch.empty(S, K, dtype=torch.int32, device=dev),
+                topk_w=torch.empty(S, K, dtype=torch.float32, device=dev),
+            )
+        P = _lib.ptr
+        args = _lib.MoeMxfp4Args(
+            x=P(x), logits=P(logits), w13=P(w.w13), s13=P(w.s13), w2=P(w.w2), s2=P(w.s2),
+            out=P(out), rows=S, y=P(dbg.get("y")), topk_ids=P(dbg.get("topk_ids")),
+            topk_w=P(dbg.get("topk_w")),
+        )  # fmt: skip
+        _lib.check(_lib.lib().mono_moe_mxfp4_forward(self._h, C.byref(args), self._stream()))
+        return (out, dbg) if debug else out

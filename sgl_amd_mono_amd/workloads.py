@@ -1,0 +1,83 @@
+"""Seeded synthetic inputs of the BASELINE configs (random-init weights of the real
+shapes; there is no checkpoint or dataset offline).
+
+Distributions follow the reference's own test generators where they exist
+(test/kernels/glm53/check_layer.py:52-146 for the FP8 layer,
+test/kernels/test_minimax_m31_ffn.py:40-60 for MXFP4 codes and scales,
+test/kernels/test_deepseek_v41_k2i.py:103-130 for FP4 index keys). Generators run
+on whatever device they are given; the GPU's and the CPU's random streams differ,
+so a parity test generates once and copies.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from .moe import Fp8MoeWeights, MoeGeometry, Mxfp4MoeWeights
+
+
+def _gen(device, seed: int) -> torch.Generator:
+    return torch.Generator(device=device).manual_seed(seed)
+
+
+def fp8_codes(shape, g: torch.Generator, device) -> torch.Tensor:
+    """E4M3 codes of N(0, 1) samples rounded through bf16 (check_layer.py:56-59)."""
+    x = torch.randn(*shape, generator=g, device=device, dtype=torch.float32)
+    return x.to(torch.bfloat16).to(torch.float8_e4m3fn).view(torch.uint8)
+
+
+def fp8_moe_weights(geo: MoeGeometry, device, seed: int = 0) -> Fp8MoeWeights:
+    """One layer's FP8 MoE weights: router ~N(0,1)*2/sqrt(H) bf16 (check_layer.py:96-98),
+    bias ~N(0, 0.1) f32 (:99), post-norm weight 1 + 0.1*N(0,1) bf16, experts E4M3 from
+    N(0,1) with 128x128 f32 block scales ~U(0.5, 2)/448. Expert E is the shared one."""
+    H, E, I = geo.hidden, geo.n_experts, geo.inter
+    g = _gen(device, seed)
+    w_router = (torch.randn(E, H, generator=g, device=device) * (2.0 / H**0.5)).to(torch.bfloat16)
+    bias = torch.randn(E, generator=g, device=device) * 0.1
+    g_post = (1.0 + 0.1 * torch.randn(H, generator=g, device=device)).to(torch.bfloat16)
+    w13 = torch.empty(E + 1, 2 * I, H, dtype=torch.uint8, device=device)
+    w2 = torch.empty(E + 1, H, I, dtype=torch.uint8, device=device)
+    for e in range(E + 1):  # one expert at a time keeps the f32 temporaries small
+        w13[e] = fp8_codes((2 * I, H), g, device)
+        w2[e] = fp8_codes((H, I), g, device)
+    s13 = (torch.rand(E + 1, 2 * I // 128, H // 128, generator=g, device=device) * 1.5 + 0.5) / 448.0
+    s2 = (torch.rand(E + 1, H // 128, I // 128, generator=g, device=device) * 1.5 + 0.5) / 448.0
+    return Fp8MoeWeights(g_post=g_post, w_router=w_router, bias=bias, w13=w13, s13=s13, w2=w2, s2=s2)
+
+
+def rows_bf16(rows: int, hidden: int, device, seed: int) -> torch.Tensor:
+    """Activation rows ~N(0, 1) in bf16."""
+    g = _gen(device, seed)
+    return torch.randn(rows, hidden, generator=g, device=device).to(torch.bfloat16)
+
+
+def mxfp4_moe_weights(geo: MoeGeometry, device, seed: int = 0) -> Mxfp4MoeWeights:
+    """MXFP4 experts: uniform random E2M1 code bytes, E8M0 scales uniform in [119, 123)
+    (test_minimax_m31_ffn.py:47-51: 'e8m0 codes around 2^-7')."""
+    H, E, I = geo.hidden, geo.n_experts, geo.inter
+    g = _gen(device, seed)
+    u8 = dict(generator=g, device=device, dtype=torch.uint8)
+    return Mxfp4MoeWeights(
+        w13=torch.randint(0, 256, (E + 1, 2 * I, H // 2), **u8),
+        s13=torch.randint(119, 123, (E + 1, 2 * I, H // 32), **u8),
+        w2=torch.randint(0, 256, (E + 1, H, I // 2), **u8),
+        s2=torch.randint(119, 123, (E + 1, H, I // 32), **u8),
+    )
+
+
+def gate_logits(rows: int, n_experts: int, device, seed: int) -> torch.Tensor:
+    """f32 gate logits ~N(0, 1)."""
+    return torch.randn(rows, n_experts, generator=_gen(device, seed), device=device)
+
+
+def toy_moe(seed: int = 0, rows: int = 4, hidden: int = 1024, n_experts: int = 8, inter: int = 512):
+    """BASELINE config 1 on the CPU: bf16 weights ~N(0, 0.02), rows ~N(0, 1),
+    ``torch.manual_seed(seed)``."""
+    torch.manual_seed(seed)
+    return dict(
+        x=torch.randn(rows, hidden).to(torch.bfloat16),
+        w_router=(torch.randn(n_experts, hidden) * 0.02).to(torch.bfloat16),
+        w_gate=(torch.randn(n_experts, inter, hidden) * 0.02).to(torch.bfloat16),
+        w_up=(torch.randn(n_experts, inter, hidden) * 0.02).to(torch.bfloat16),
+        w_down=(torch.randn(n_experts, hidden, inter) * 0.02).to(torch.bfloat16),
+    )

@@ -1,0 +1,126 @@
+"""FP8 routed MoE on the GPU against the CPU oracle.
+
+Routing is checked bit-exact on identical inputs: the oracle's top-8 rule applied to
+the device's own sigmoid scores must give the device's ids in the same order. The
+expert outputs are then compared on that routing: the f32 MoE sum within 1e-2
+relative (norm) and the bf16 output within 2e-2 max-abs / 1e-2 relative.
+"""
+
+import pytest
+import torch
+
+from oracle import moe as omoe
+from oracle import topk as otopk
+from sgl_amd_mono_amd import workloads
+from sgl_amd_mono_amd.moe import FP8_MOE, MoeRuntime
+
+pytestmark = pytest.mark.gpu
+
+G = FP8_MOE
+OUT_MAX_ABS, OUT_REL = 2e-2, 1e-2  # the north star's bf16 output bound
+Y_REL = 1e-2  # the MoE sum itself (f32), relative to its norm
+SCORE_ABS = 1e-4  # sigmoid scores: f32 GEMV order differences only
+
+
+class CpuExperts:
+    """Expert tensors fetched to the CPU on first use (the oracle reads a few)."""
+
+    def __init__(self, t):
+        self.t, self.cache = t, {}
+
+    def __getitem__(self, e):
+        if e not in self.cache:
+            self.cache[e] = self.t[e].cpu()
+        return self.cache[e]
+
+
+@pytest.fixture(scope="module")
+def setup(gpu_device):
+    print(f"[setup] generating FP8 MoE weights {G}", flush=True)
+    w = workloads.fp8_moe_weights(G, gpu_device, seed=0)
+    rt = MoeRuntime(G, 16, gpu_device)
+    torch.cuda.synchronize()
+    cpu = dict(
+        g_post=w.g_post.cpu(), w_router=w.w_router.cpu(), bias=w.bias.cpu(),
+        w13=CpuExperts(w.w13), s13=CpuExperts(w.s13), w2=CpuExperts(w.w2), s2=CpuExperts(w.s2),
+    )  # fmt: skip
+    yield w, rt, cpu
+    rt.close()
+
+
+def _rel(a, b):
+    return ((a.float() - b.float()).norm() / b.float().norm().clamp_min(1e-30)).item()
+
+
+def _run(rt, w, a):
+    out, dbg = rt.forward_fp8(a, w, debug=True)
+    torch.cuda.synchronize()
+    return out.cpu(), {k: v.cpu() for k, v in dbg.items()}
+
+
+@pytest.mark.parametrize("rows", [1, 4, 8, 16])
+def test_fp8_moe_matches_oracle(setup, gpu_device, rows):
+    w, rt, cpu = setup
+    print(f"[fp8 moe] rows={rows}", flush=True)
+    a = workloads.rows_bf16(rows, G.hidden, gpu_device, seed=100 + rows)
+    out, dbg = _run(rt, w, a)
+    a_cpu = a.cpu()
+
+    _, scores_ref = omoe.fp8_router(a_cpu, cpu["g_post"], cpu["w_router"], G.eps)
+    assert (dbg["scores"] - scores_ref).abs().max().item() < SCORE_ABS
+
+    ids_ref, w_ref = otopk.router_top8(dbg["scores"], cpu["bias"], G.top_k, G.route_scale)
+    assert torch.equal(dbg["topk_ids"].long(), ids_ref), (dbg["topk_ids"], ids_ref)
+    torch.testing.assert_close(dbg["topk_w"], w_ref, rtol=1e-5, atol=1e-6)
+
+    ref = omoe.fp8_moe_block(
+        a_cpu, cpu["g_post"], cpu["w_router"], cpu["bias"], cpu["w13"], cpu["s13"], cpu["w2"],
+        cpu["s2"], eps=G.eps, top_k=G.top_k, inter=G.inter, ids=ids_ref, weights=w_ref,
+    )  # fmt: skip
+    y_rel = _rel(dbg["y"], ref["y"])
+    print(f"[fp8 moe] rows={rows} y rel={y_rel:.3e}", flush=True)
+    assert y_rel < Y_REL
+    assert (out.float() - ref["out"].float()).abs().max().item() <= OUT_MAX_ABS
+    assert _rel(out, ref["out"]) <= OUT_REL
+
+
+def test_fp8_moe_repeat_is_bitwise_and_resets_counters(setup, gpu_device):
+    """Two launches in a row give identical bits (the last-arrival counters return to
+    zero and the plan order is deterministic); a narrower step after a wider one too."""
+    w, rt, _ = setup
+    a16 = workloads.rows_bf16(16, G.hidden, gpu_device, seed=7)
+    first, d1 = _run(rt, w, a16)
+    second, d2 = _run(rt, w, a16)
+    assert torch.equal(first, second) and torch.equal(d1["y"], d2["y"])
+    small, ds = _run(rt, w, a16[:3].contiguous())
+    again, da = _run(rt, w, a16[:3].contiguous())
+    assert torch.equal(small, again) and torch.equal(ds["topk_ids"], da["topk_ids"])
+    # rows are independent: the 3-row step's routing equals the 16-row step's first rows
+    assert torch.equal(ds["topk_ids"], d1["topk_ids"][:3])
+
+
+def test_fp8_router_ties_take_lowest_ids(setup, gpu_device):
+    """Ten experts with identical router rows and bias tie for the top; the eight lowest
+    ids win (glm53/gfx950/kernel.py:1575-1629)."""
+    w, rt, cpu = setup
+    w_r = w.w_router.clone()
+    bias = w.bias.clone()
+    tied = list(range(40, 50))
+    w_r[tied] = w_r[40].clone()
+    bias[tied] = 5.0
+    wt = type(w)(g_post=w.g_post, w_router=w_r, bias=bias, w13=w.w13, s13=w.s13, w2=w.w2, s2=w.s2)
+    a = workloads.rows_bf16(4, G.hidden, gpu_device, seed=11)
+    _, dbg = _run(rt, wt, a)
+    assert dbg["topk_ids"].tolist() == [tied[:8]] * 4
+    ids_ref, _ = otopk.router_top8(dbg["scores"], bias.cpu(), G.top_k, G.route_scale)
+    assert torch.equal(dbg["topk_ids"].long(), ids_ref)
+
+
+def test_fp8_moe_rejects_bad_shapes(setup, gpu_device):
+    w, rt, _ = setup
+    a = workloads.rows_bf16(17, G.hidden, gpu_device, seed=1)
+    with pytest.raises(ValueError, match="rows"):
+        rt.forward_fp8(a, w)
+    a = workloads.rows_bf16(2, G.hidden, gpu_device, seed=1).float()
+    with pytest.raises(ValueError, match="dtype"):
+        rt.forward_fp8(a, w)
