@@ -47,6 +47,18 @@ enum {
 };
 
 enum { MONO_ROUTER_SIGMOID_BIAS = 0, MONO_ROUTER_SOFTMAX = 1 };
+
+/* Guard words a runtime exposes (mono_*_read_errors), after the reference's guard
+ * block (sgl_amd_mono/common/guard.py:16-30):
+ *   [0] launch tickets (workgroups x launches so far)
+ *   [1] 0, or 1 + the id of the first inter-workgroup wait that passed its deadline;
+ *       sticky: every later launch of the runtime exits at once (fail-stop) until
+ *       mono_*_clear_errors
+ *   [2] tag of the launch that failed
+ *   [3] the workgroup that failed first
+ * Wait sites of the MoE launch: 0 router logits, 1 route picks, 2 expert mid
+ * activations, 3 expert outputs. */
+#define MONO_GUARD_WORDS 4
 enum { MONO_WEIGHT_FP8_BLOCK128 = 0, MONO_WEIGHT_MXFP4 = 1 };
 
 /* Version of this ABI (MONO_ABI_VERSION of the library). */
@@ -72,25 +84,30 @@ typedef struct {
   float eps;             /* RMSNorm epsilon of the post-attention norm */
 } mono_moe_config;
 
-/* Replaces Glm53Runtime's MoE scratch (runner.py:133-195). Allocates the runtime's
- * device scratch on `cfg->device` (which must be current). */
+/* Replaces Glm53Runtime's MoE scratch (runner.py:133-195): allocates the runtime's
+ * mailboxes and guard words on `cfg->device` (which must be current) and checks that
+ * the persistent kernel fits one workgroup on every CU. A runtime's launches must be
+ * stream-ordered (one stream at a time), like the reference's single caller thread. */
 int mono_moe_create(const mono_moe_config* cfg, mono_moe** out);
 /* Frees the scratch. NULL is a no-op; idempotent like PeerBuffer.close
  * (common/peer.py:157-165). */
 int mono_moe_destroy(mono_moe* moe);
 
-/* FP8 MoE block of one decode step (kernel.py:4199-5187):
- * out = a + sum_slots w * down_e(silu(gate_e(xq)) * up_e(xq)),
- * xq = FP8(RMSNorm(a) * g_post), sigmoid + bias top-k router, shared expert id E
- * with weight 1. Optional outputs (NULL skips) expose the routing for tests. */
+/* FP8 MoE block of one decode step, one persistent launch (
+ * glm53/gfx950/kernel.py:4199-5187, called through Glm53LayerOp.launch,
+ * runner.py:240-321): out = a + sum_slots w * down_e(silu(gate_e(xq)) * up_e(xq)),
+ * xq = FP8(RMSNorm(a) * g_post), sigmoid + bias top-k router, shared expert id E with
+ * weight 1. Expert weights are read in place in AITER's (16, 16) shuffled layout
+ * (glm53/gfx950/kernel.py:787-808): the [N, K] E4M3 matrix of an expert stored as
+ * [N/16, K/32, 2, 16, 16] bytes. Optional outputs (NULL skips) expose the routing. */
 typedef struct {
   const void* a;        /* bf16 [rows, H] residual stream after attention */
   const void* g_post;   /* bf16 [H] post-attention RMSNorm weight */
   const void* w_router; /* bf16 [E, H] gate weight */
   const float* bias;    /* f32 [E] e_score_correction_bias */
-  const void* w13;      /* e4m3 [E+1, 2I, H] gate rows then up rows */
+  const void* w13;      /* e4m3 [E+1, 2I, H] gate rows then up rows, (16,16)-shuffled */
   const float* s13;     /* f32 [E+1, 2I/128, H/128] */
-  const void* w2;       /* e4m3 [E+1, H, I] */
+  const void* w2;       /* e4m3 [E+1, H, I], (16,16)-shuffled */
   const float* s2;      /* f32 [E+1, H/128, I/128] */
   void* out;            /* bf16 [rows, H] */
   int32_t rows;         /* 1..max_rows */
@@ -101,6 +118,18 @@ typedef struct {
 } mono_moe_fp8_args;
 
 int mono_moe_fp8_forward(mono_moe* moe, const mono_moe_fp8_args* args, void* stream);
+
+/* Deadline of every inter-workgroup wait of the runtime's launches, in seconds (default
+ * 2). Replaces Glm53Runtime.set_deadline (runner.py:197-204, guard.py:69-76). */
+int mono_moe_set_deadline(mono_moe* moe, double seconds);
+/* Synchronise the device and copy the MONO_GUARD_WORDS guard words to `words`. */
+int mono_moe_read_errors(mono_moe* moe, int32_t* words);
+/* Synchronise, then clear guard words 1.. so the runtime launches again. */
+int mono_moe_clear_errors(mono_moe* moe);
+/* Tests of the fail-stop path: every wait at site `site` of later launches fails at
+ * once, as if its deadline had passed (the host-forced fault of guard.py:79-88); -1
+ * turns it off. */
+int mono_moe_set_fault(mono_moe* moe, int32_t site);
 
 /* MXFP4 (E2M1 + E8M0 per 32) A16W4 MoE of one decode step:
  * out = bf16(sum_slots w * down_e(bf16(silu(gate_e(x)) * up_e(x)))), softmax top-k

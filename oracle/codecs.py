@@ -148,3 +148,20 @@ def bf16_round(x: torch.Tensor) -> torch.Tensor:
 def f32_bits(x: torch.Tensor) -> np.ndarray:
     """float32 tensor -> its IEEE bits as uint32 numpy."""
     return x.float().contiguous().numpy().view(np.uint32)
+
+
+def aiter_unshuffle(ws: torch.Tensor) -> torch.Tensor:
+    """AITER (16, 16)-shuffled ``[..., N, K]`` bytes -> row-major ``[..., N, K]`` uint8.
+
+    Byte (n, k) of the row-major matrix sits at flat offset
+    ``((n // 16 * K / 32 + k // 32) * 2 + (k % 32) // 16) * 256 + (n % 16) * 16 + k % 16``
+    of the shuffled one: the ``[N/16, K/32, 2, 16 rows, 16 B]`` order that
+    glm53/gfx950/kernel.py:787-808 (``ld_fp8_chunk``) reads and
+    test/kernels/glm53_flash/check_layer.py:932-939 (``_dequant``) undoes. Computed as
+    a gather from that formula."""
+    *lead, n, k = ws.shape
+    flat = ws.contiguous().view(torch.uint8).reshape(*lead, n * k)
+    ni = torch.arange(n)[:, None]
+    ki = torch.arange(k)[None, :]
+    src = ((ni // 16 * (k // 32) + ki // 32) * 2 + (ki % 32) // 16) * 256 + (ni % 16) * 16 + ki % 16
+    return flat[..., src.reshape(-1)].reshape(*lead, n, k)

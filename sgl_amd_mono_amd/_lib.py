@@ -51,7 +51,14 @@ SIGNATURES = {
     "mono_moe_destroy": (C.c_int, [_VP]),
     "mono_moe_fp8_forward": (C.c_int, [_VP, C.POINTER(MoeFp8Args), _VP]),
     "mono_moe_mxfp4_forward": (C.c_int, [_VP, C.POINTER(MoeMxfp4Args), _VP]),
+    "mono_moe_set_deadline": (C.c_int, [_VP, C.c_double]),
+    "mono_moe_read_errors": (C.c_int, [_VP, C.POINTER(C.c_int32)]),
+    "mono_moe_clear_errors": (C.c_int, [_VP]),
+    "mono_moe_set_fault": (C.c_int, [_VP, C.c_int32]),
 }
+GUARD_WORDS = 4
+# wait sites of the MoE launch (guard word 1 = site + 1)
+MOE_SITES = {0: "router logits", 1: "route picks", 2: "expert mid activations", 3: "expert outputs"}
 
 _lock = threading.Lock()
 _lib = None

@@ -8,6 +8,7 @@
 
 #include <cstdarg>
 #include <cstdio>
+#include <algorithm>
 #include <cstring>
 #include <string>
 
@@ -52,14 +53,18 @@ int check_device(int device) {
 
 struct mono_moe {
   mono_moe_config cfg;
-  int n_cu;
+  int grid;  // workgroups of the persistent launch: one a CU
   void* blob;
   size_t blob_bytes;
-  mono::moe::Scratch sc;
+  mono::moe::Mail mail;
+  mono::GuardArgs guard;
   uint32_t magic;
 };
 
 static const uint32_t MOE_MAGIC = 0x6d6f6531u;
+static const double TICKS_PER_S = 100e6;  // s_memrealtime runs at 100 MHz
+static const double DEFAULT_DEADLINE_S = 2.0;
+static const double MAX_DEADLINE_S = 3600.0;
 
 extern "C" int mono_abi_version(void) { return MONO_ABI_VERSION; }
 
@@ -87,60 +92,53 @@ extern "C" int mono_moe_create(const mono_moe_config* cfg, mono_moe** out) {
                 "FP8 MoE geometry H=%d E=%d top_k=%d I=%d has no compiled kernel (built: H=7168 E=256 top_k=8 I=512)",
                 c.hidden, c.n_experts, c.top_k, c.inter);
   if (int rc = check_device(c.device)) return rc;
-
   const size_t H = c.hidden, E = c.n_experts, I = c.inter;
+  const size_t max_act = (size_t)std::min(c.max_rows * c.top_k, c.n_experts) + 1;
   size_t off = 0;
   auto take = [&](size_t bytes) {
     size_t at = off;
     off += align256(bytes);
     return at;
   };
-  const size_t o_plan = take(sizeof(Plan));
-  const size_t o_rstd = take(MAX_ROWS * 4);
-  const size_t o_xq = take(MAX_ROWS * H);
-  const size_t o_xs = take(MAX_ROWS * (H / 128) * 4);
-  const size_t o_rpart = take((size_t)ROUTER_SLICES * MAX_ROWS * E * 4);
-  const size_t o_rcount = take(4);
-  const size_t o_mid = take((size_t)MAX_ACT * MAX_ROWS * I * 4);
-  const size_t o_mcount = take((size_t)MAX_ACT * (I / 128) * 4);
-  const size_t o_mq = take((size_t)MAX_ACT * MAX_ROWS * I * 2);
-  const size_t o_mcoef = take((size_t)MAX_ACT * MAX_ROWS * (I / 128) * 4);
+  const size_t o_guard = take(mono::G_WORDS * 4);
+  const size_t o_rlog = take((size_t)moe_fp8_router_slices() * MAX_ROWS * E * 8);
+  const size_t o_rsel = take((size_t)MAX_ROWS * 2 * MAX_TOPK * 8);
+  const size_t o_mid = take(max_act * MAX_ROWS * I * 8);
+  const size_t o_ypart = take(max_act * MAX_ROWS * H * 8);
 
+  hipDeviceProp_t prop;
+  HIP_TRY(hipGetDeviceProperties(&prop, c.device));
+  int per_cu = 0;
+  HIP_TRY(moe_fp8_occupancy(&per_cu));
+  if (per_cu < 1)
+    return fail(MONO_ESTATE, "the persistent MoE kernel does not fit on a CU (occupancy %d)", per_cu);
   mono_moe* m = new mono_moe();
   m->cfg = c;
   m->magic = MOE_MAGIC;
   m->blob_bytes = off;
-  hipDeviceProp_t prop;
-  hipError_t e = hipGetDeviceProperties(&prop, c.device);
+  m->grid = prop.multiProcessorCount;
+  hipError_t e = hipMalloc(&m->blob, off);
   if (e != hipSuccess) {
     delete m;
-    return fail(MONO_EHIP, "hipGetDeviceProperties: %s", hipGetErrorString(e));
+    return fail(MONO_ENOMEM, "hipMalloc(%zu) for the MoE mailboxes: %s", off, hipGetErrorString(e));
   }
-  m->n_cu = prop.multiProcessorCount;
-  e = hipMalloc(&m->blob, off);
-  if (e != hipSuccess) {
-    delete m;
-    return fail(MONO_ENOMEM, "hipMalloc(%zu) for the MoE scratch: %s", off, hipGetErrorString(e));
-  }
-  // counters start at zero; every later launch leaves them at zero
+  // tag 0 is never a launch's tag, so zeroed mailboxes read as empty
   e = hipMemset(m->blob, 0, off);
   if (e == hipSuccess) e = hipDeviceSynchronize();
   if (e != hipSuccess) {
     (void)hipFree(m->blob);
     delete m;
-    return fail(MONO_EHIP, "clearing the MoE scratch: %s", hipGetErrorString(e));
+    return fail(MONO_EHIP, "clearing the MoE mailboxes: %s", hipGetErrorString(e));
   }
   char* b = static_cast<char*>(m->blob);
-  m->sc.plan = reinterpret_cast<Plan*>(b + o_plan);
-  m->sc.rstd = reinterpret_cast<float*>(b + o_rstd);
-  m->sc.xq = reinterpret_cast<uint8_t*>(b + o_xq);
-  m->sc.xs = reinterpret_cast<float*>(b + o_xs);
-  m->sc.rpart = reinterpret_cast<float*>(b + o_rpart);
-  m->sc.rcount = reinterpret_cast<uint32_t*>(b + o_rcount);
-  m->sc.mid = reinterpret_cast<float*>(b + o_mid);
-  m->sc.mcount = reinterpret_cast<uint32_t*>(b + o_mcount);
-  m->sc.mq = reinterpret_cast<uint8_t*>(b + o_mq);
-  m->sc.mcoef = reinterpret_cast<float*>(b + o_mcoef);
+  m->mail.guard = reinterpret_cast<uint32_t*>(b + o_guard);
+  m->mail.rlog = reinterpret_cast<uint64_t*>(b + o_rlog);
+  m->mail.rsel = reinterpret_cast<uint64_t*>(b + o_rsel);
+  m->mail.mid = reinterpret_cast<uint64_t*>(b + o_mid);
+  m->mail.ypart = reinterpret_cast<uint64_t*>(b + o_ypart);
+  m->guard.words = m->mail.guard;
+  m->guard.deadline_ticks = (uint64_t)(DEFAULT_DEADLINE_S * TICKS_PER_S);
+  m->guard.fault_site = -1;
   *out = m;
   return ok();
 }
@@ -186,10 +184,43 @@ extern "C" int mono_moe_fp8_forward(mono_moe* m, const mono_moe_fp8_args* args, 
   REQUIRE_PTR(args->w2);
   REQUIRE_PTR(args->s2);
   REQUIRE_PTR(args->out);
-  const MoeGeom geo{m->cfg.hidden, m->cfg.n_experts, m->cfg.top_k, m->cfg.inter};
   MoeFp8Args g(*args, m->cfg.route_scale, m->cfg.eps);
-  hipError_t e = moe_fp8_forward(g, geo, m->n_cu, m->sc, static_cast<hipStream_t>(stream));
+  hipError_t e = moe_fp8_forward(g, m->grid, m->mail, m->guard, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return fail(MONO_EHIP, "launching the FP8 MoE: %s", hipGetErrorString(e));
+  return ok();
+}
+
+extern "C" int mono_moe_set_deadline(mono_moe* m, double seconds) {
+  if (!m || m->magic != MOE_MAGIC) return fail(MONO_ESTATE, "not a live MoE runtime");
+  if (!(seconds > 0.0) || seconds > MAX_DEADLINE_S)
+    return fail(MONO_EINVAL, "deadline must be in (0, %.0f] seconds, got %g", MAX_DEADLINE_S, seconds);
+  const double ticks = seconds * TICKS_PER_S;
+  m->guard.deadline_ticks = ticks < 1.0 ? 1u : (uint64_t)ticks;
+  return ok();
+}
+
+extern "C" int mono_moe_set_fault(mono_moe* m, int32_t site) {
+  if (!m || m->magic != MOE_MAGIC) return fail(MONO_ESTATE, "not a live MoE runtime");
+  if (site < -1 || site > 15) return fail(MONO_EINVAL, "fault site must be -1 (none) or a wait site 0..15, got %d", site);
+  m->guard.fault_site = site;
+  return ok();
+}
+
+extern "C" int mono_moe_read_errors(mono_moe* m, int32_t* words) {
+  if (!m || m->magic != MOE_MAGIC) return fail(MONO_ESTATE, "not a live MoE runtime");
+  if (!words) return fail(MONO_EINVAL, "mono_moe_read_errors: words is NULL");
+  if (int rc = check_device(m->cfg.device)) return rc;
+  HIP_TRY(hipDeviceSynchronize());
+  HIP_TRY(hipMemcpy(words, m->mail.guard, MONO_GUARD_WORDS * sizeof(int32_t), hipMemcpyDeviceToHost));
+  return ok();
+}
+
+extern "C" int mono_moe_clear_errors(mono_moe* m) {
+  if (!m || m->magic != MOE_MAGIC) return fail(MONO_ESTATE, "not a live MoE runtime");
+  if (int rc = check_device(m->cfg.device)) return rc;
+  HIP_TRY(hipDeviceSynchronize());
+  HIP_TRY(hipMemset(m->mail.guard + mono::G_ERROR, 0, (MONO_GUARD_WORDS - 1) * sizeof(int32_t)));
+  HIP_TRY(hipDeviceSynchronize());
   return ok();
 }
 

@@ -1,9 +1,7 @@
 // Device helpers shared by the gfx950 kernels of the decoder-layer path.
 //
 // Wave64 reductions, the FP8 / FP4 / bf16 converts of CDNA4, the 16x16 MFMA tiles
-// the GEMVs use, nontemporal weight loads, and the "last workgroup to arrive"
-// hand-off that lets a stage finish a reduction without any workgroup waiting on
-// another (no spin, so no deadlock whatever the residency).
+// the GEMVs use, and nontemporal weight loads.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -133,26 +131,5 @@ MONO_DEV i32x8 ld_nt_i32x8(const void* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const i32x8*>(p));
 }
 MONO_DEV i32x8 ld_i32x8(const void* p) { return *reinterpret_cast<const i32x8*>(p); }
-
-// Release this workgroup's global writes, then count it in; true for exactly one
-// workgroup, the last of `total` to arrive, which then sees every other's writes
-// and resets the counter for the next launch. Call from the whole workgroup.
-MONO_DEV bool last_arrival(uint32_t* counter, uint32_t total, uint32_t* lds_flag) {
-  __threadfence();  // every wave releases its own stores at device scope
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    uint32_t prev = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-    uint32_t last = prev + 1 == total;
-    if (last) {
-      __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __threadfence();
-    }
-    *lds_flag = last;
-  }
-  __syncthreads();
-  bool last = *lds_flag != 0;
-  if (last) __threadfence();  // acquire for every thread of the last workgroup
-  return last;
-}
 
 }  // namespace mono

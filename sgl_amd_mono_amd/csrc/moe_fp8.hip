@@ -1,78 +1,120 @@
-// FP8 (128 x 128 block-scaled) routed + shared MoE of one decode step on gfx950.
+// FP8 (128 x 128 block-scaled) routed + shared MoE of one decode step on gfx950, as ONE
+// persistent launch: one 512-thread workgroup per CU, every workgroup resident at once.
 //
-// The post-attention half of the decoder layer (reference: glm53/gfx950/kernel.py
-// stages 8-10, :4199-5187, W8A8 mode) as four stream-ordered kernels:
+// This is the post-attention half of the reference's decoder-layer launch
+// (sgl_amd_mono/glm53/gfx950/kernel.py stages router / ug / down, :4199-5187, W8A8 MoE
+// mode) with the tensor-parallel reduce replaced by a local residual add. Stages hand
+// data to each other through tagged mailbox words (sync.h); nothing waits at a grid
+// barrier and every wait is bounded by the guard's deadline.
 //
-//   prep    one workgroup a row: RMSNorm statistics, FP8 quantisation of the normed
-//           row in 128-blocks (amax / 448, hardware rcp, kernel.py:1440-1450)
-//   router  bf16 MFMA GEMV split over 16-expert x 896-k tiles; the last workgroup to
-//           arrive sums the K slices, applies the sigmoid, picks each row's top-8 by
-//           f32(score + bias) with lowest-id ties (kernel.py:1575-1629) and writes the
-//           step's plan: the distinct experts (shared expert last), their row masks
-//           and route weights
-//   up      persistent loop over (expert, 16-channel tile): FP8 x FP8 MFMA
-//           (v_mfma_scale_f32_16x16x128_f8f6f4, unit E8M0 scales) with the f32 block
-//           scales applied per 128-k, SiLU(gate) * up; the last tile of a 128-channel
-//           block to arrive quantises that block of mid to FP8 (kernel.py:5118-5125)
-//   down    one workgroup per 16 output rows, looping over the plan's experts: FP8
-//           MFMA, x weight block scale x (mid scale x route weight), summed in plan
-//           order, + the residual, bf16 out (kernel.py:5001-5187, TP reduce dropped)
+// Work, in the order each workgroup walks it:
+//   ticket   one atomic add a workgroup -> the launch's tag (sync.h)
+//   norm     every workgroup: the RMSNorm statistics of all rows (kernel.py:1367-1415)
+//   router   task t < 16 * RK on workgroup t: 16 experts x a 512-wide K slice of the
+//            bf16 router GEMV on the bf16-rounded normed rows (MFMA 16x16x32 bf16)
+//            -> partial logits (mailbox rlog)
+//   route    row s on workgroup G-1-s: the K slices summed in order, sigmoid, top-8 by
+//            the f32 bits of (score + bias) with lowest-id ties, weights = score / sum
+//            x route_scale (kernel.py:1575-1629) -> the row's picks (mailbox rsel)
+//   xq       every workgroup: per-128 FP8 quantisation of the normed rows into LDS
+//            (amax / 448 with a hardware reciprocal, kernel.py:1440-1450)
+//   plan     every workgroup, before its first routed tile: the distinct experts of
+//            the step; slot 0 is the shared expert (weight 1), slots 1.. the picked
+//            experts by ascending id
+//   tasks    one round-robin list over the workgroups:
+//            up     (slot, 16-channel tile): FP8 x FP8 MFMA 16x16x128 with the 128x128
+//                   weight block scale x the activation block scale per 128-k, the 8
+//                   waves splitting K, SiLU(gate) * up -> mailbox mid
+//            down   (slot, 256 output rows): the slot's mid quantised per 128 to FP8 in
+//                   LDS (kernel.py:5118-5125), FP8 MFMA, x weight block scale x mid
+//                   block scale x route weight -> mailbox ypart
+//            final  (32 output rows): the row's slots summed in plan order + the
+//                   residual -> bf16 out (kernel.py:5176-5185 without the peer reduce)
 //
-// Weights stream once with nontemporal dwordx4 loads issued in batches before the
-// MFMAs that consume them. Activation columns of rows that do not route to an expert
-// load nothing and contribute zero.
+// Expert weights are read in place in AITER's (16, 16) shuffled layout
+// ([N/16, K/32, 2, 16 rows, 16 B], glm53/gfx950/kernel.py:787-808): a lane's two
+// 16-byte loads are exactly its MFMA operand, and a wave's pair covers 2 KB of
+// contiguous HBM. Each workgroup issues a task's weight loads before it waits on or
+// reduces the previous task, so weights stream while mailboxes are polled.
 #include "common.h"
-#include "moe_plan.h"
 #include "moe_ops.h"
+#include "moe_plan.h"
+#include "sync.h"
 
 namespace mono {
 namespace moe {
 
-constexpr int THREADS = 256;
-constexpr int WAVES = THREADS / WAVE;
+namespace {
 
-// ------------------------------------------------------------------ prep
-template <int H>
-__global__ __launch_bounds__(THREADS) void k_prep_w8a8(const uint16_t* __restrict__ a,
-                                                       const uint16_t* __restrict__ gamma,
-                                                       float eps, Scratch sc) {
-  const int s = blockIdx.x;
-  const int lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
-  const uint16_t* row = a + (size_t)s * H;
-  __shared__ float red[WAVES];
-  float ss = 0.f;
-  for (int v = threadIdx.x; v < H / 8; v += THREADS) {
-    u32x4 w = ld_u32x4(row + v * 8);
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      float lo = bf16_lo(w[q]), hi = bf16_hi(w[q]);
-      ss += lo * lo + hi * hi;
-    }
-  }
-  ss = wave_sum(ss);
-  if (lane == 0) red[wave] = ss;
-  __syncthreads();
-  const float rstd = hw_rsq((red[0] + red[1] + red[2] + red[3]) * (1.0f / H) + eps);
-  if (threadIdx.x == 0) sc.rstd[s] = rstd;
-  uint16_t* xq = reinterpret_cast<uint16_t*>(sc.xq + (size_t)s * H);
-  for (int b = wave; b < H / 128; b += WAVES) {
-    const int k = b * 128 + lane * 2;
-    const uint32_t av = *reinterpret_cast<const uint32_t*>(row + k);
-    const uint32_t gv = *reinterpret_cast<const uint32_t*>(gamma + k);
-    const float x0 = bf16_lo(av) * rstd * bf16_lo(gv);
-    const float x1 = bf16_hi(av) * rstd * bf16_hi(gv);
-    const float amax = wave_max(fmaxf(fabsf(x0), fabsf(x1)));
-    const bool nz = amax > 0.f;
-    const float qs = nz ? amax * (1.0f / FP8_MAX) : 1.0f;
-    const float inv = nz ? hw_rcp(amax) * FP8_MAX : 1.0f;
-    const float q0 = fminf(fmaxf(x0 * inv, -FP8_MAX), FP8_MAX);
-    const float q1 = fminf(fmaxf(x1 * inv, -FP8_MAX), FP8_MAX);
-    xq[k / 2] = (uint16_t)fp8x2_pack(q0, q1);
-    if (lane == 0) sc.xs[s * (H / 128) + b] = qs;
-  }
-}
+constexpr int FT = 512;
+constexpr int FW = FT / WAVE;  // 8 waves
 
-// ------------------------------------------------------------------ router
+// BASELINE config 2 geometry
+constexpr int H = 7168, E = 256, I = 512, TOPK = 8;
+constexpr int KB = H / 128;          // 128-k blocks of a hidden row
+constexpr int IB = I / 128;          // 128-k blocks of a mid row
+constexpr int NT = I / 16;           // up tiles a slot
+constexpr int UP_KBW = KB / FW;      // k blocks a wave of an up tile
+constexpr int RK = 14;               // router K slices
+constexpr int RKW = H / RK / FW;     // k a wave of a router task
+constexpr int RSTEP = RKW / 32;      // bf16 MFMA steps a wave of a router task
+constexpr int ROUTER_TASKS = (E / 16) * RK;
+constexpr int DN_ROWS = 256;         // output rows of a down task (8 waves x 2 tiles)
+constexpr int DN_GROUPS = H / DN_ROWS;
+constexpr int FIN_ROWS = 32;
+constexpr int FIN_TASKS = H / FIN_ROWS;
+constexpr int NSLOT = TOPK + 1;      // slots a row uses: the shared expert and its picks
+static_assert(KB % FW == 0 && RKW % 32 == 0 && H % (RK * FW) == 0, "tiling");
+static_assert(UP_KBW * 2 <= 14 && 2 * IB <= 14, "weight registers");
+static_assert(FT == MAX_ROWS * (I / 16), "a down task's thread owns 16 mid channels of one row");
+static_assert(MAX_ROWS * FIN_ROWS <= FT, "a final task's thread owns one (row, output)");
+
+// wait sites (guard error word = site + 1)
+enum { W_LOGITS = 0, W_PICKS = 1, W_MID = 2, W_YPART = 3 };
+
+struct Lds {
+  uint8_t xq[MAX_ROWS][H];          // FP8 normed rows
+  float xs[MAX_ROWS][KB];           // their block scales
+  float rstd[MAX_ROWS];
+  f32x4 red[2][FW][WAVE];           // cross-wave sums
+  uint8_t bq[MAX_ROWS][I];          // a down task's FP8 mid
+  float coef[MAX_ROWS][IB];         // its block scale x route weight
+  int32_t expert[MAX_ACT];          // the plan: expert id of each slot
+  uint32_t rowmask[MAX_ACT];        // rows each slot serves
+  int32_t dmap[E];                  // slot of a picked expert
+  int32_t pick_id[MAX_ROWS][TOPK];
+  float pick_w[MAX_ROWS][TOPK];
+  int32_t rowslot[MAX_ROWS][NSLOT]; // a row's slots in plan order
+  uint32_t used[E];
+  uint32_t rkey[E];
+  float rraw[E];
+  int32_t wcount[FW];
+  int32_t n_act;
+  uint32_t tag;
+  uint32_t err;
+};
+
+struct Args {
+  const uint16_t* a;
+  const uint16_t* g_post;
+  const uint16_t* w_router;
+  const float* bias;
+  const uint8_t* w13;
+  const float* s13;
+  const uint8_t* w2;
+  const float* s2;
+  uint16_t* out;
+  float* y_out;
+  float* scores;
+  int32_t* topk_ids;
+  float* topk_w;
+  int rows;
+  float route_scale;
+  float eps;
+  Mail mail;
+  GuardArgs guard;
+};
+
 MONO_DEV uint32_t radix_key(float f) {
   const uint32_t b = __float_as_uint(f);
   return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
@@ -93,116 +135,29 @@ MONO_DEV void sort4(uint32_t (&k)[4], int (&id)[4], float (&raw)[4]) {
   }
 }
 
-// Every row's top-k of the finished logits and the step's plan (one workgroup).
-// logit(s, e) = sum over the K slices in slice order; the candidates of lane l are
-// experts l + 64 i.
-template <int E, int TOPK>
-MONO_DEV void finish_route_sigmoid(const MoeRouteOut& ro, const float* __restrict__ bias,
-                                   int rows, float route_scale, Scratch sc) {
-  static_assert(E == 256, "the lane layout holds 4 candidates a lane");
-  const int lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
-  __shared__ uint32_t used[E + 1];
-  __shared__ int pick_id[MAX_ROWS][TOPK];
-  __shared__ float pick_w[MAX_ROWS][TOPK];
-  for (int x = threadIdx.x; x <= E; x += THREADS) used[x] = 0;
-  __syncthreads();
-  for (int s = wave; s < rows; s += WAVES) {
-    uint32_t key[4];
-    int id[4];
-    float raw[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int e = lane + 64 * i;
-      float lg = 0.f;
-#pragma unroll
-      for (int ks = 0; ks < ROUTER_SLICES; ++ks) lg += sc.rpart[(ks * MAX_ROWS + s) * E + e];
-      raw[i] = sigmoid(lg);
-      if (ro.scores) ro.scores[s * E + e] = raw[i];
-      key[i] = radix_key(raw[i] + bias[e]);
-      id[i] = e;
-    }
-    sort4(key, id, raw);
-    float my_raw = 0.f;  // lane k < TOPK: the raw score and id of pick k
-    int my_id = 0;
-    for (int k = 0; k < TOPK; ++k) {
-      const uint32_t m = wave_umax(key[0]);
-      const uint32_t cand = key[0] == m ? 0xffffu - (uint32_t)id[0] : 0u;
-      const int expert = (int)(0xffffu - wave_umax(cand));
-      const bool hit = key[0] == m && id[0] == expert;
-      const uint64_t bal = __ballot(hit);
-      const int src = __ffsll((long long)bal) - 1;
-      const float r = __shfl(raw[0], src, WAVE);
-      if (lane == k) {
-        my_raw = r;
-        my_id = expert;
-      }
-      if (hit) {
-        key[0] = key[1]; key[1] = key[2]; key[2] = key[3]; key[3] = 0u;
-        id[0] = id[1]; id[1] = id[2]; id[2] = id[3]; id[3] = 0xffff;
-        raw[0] = raw[1]; raw[1] = raw[2]; raw[2] = raw[3]; raw[3] = 0.f;
-      }
-    }
-    // sum of the picks' raw scores in the butterfly order of lanes 0..7
-    float tot = lane < TOPK ? my_raw : 0.f;
-#pragma unroll
-    for (int o = 1; o < TOPK; o <<= 1) tot += __shfl_xor(tot, o, WAVE);
-    const float w = my_raw * (hw_rcp(tot) * route_scale);
-    if (lane < TOPK) {
-      pick_id[s][lane] = my_id;
-      pick_w[s][lane] = w;
-      atomicOr(&used[my_id], 1u << s);
-      if (ro.topk_ids) ro.topk_ids[s * TOPK + lane] = my_id;
-      if (ro.topk_w) ro.topk_w[s * TOPK + lane] = w;
-    }
-  }
-  __syncthreads();
-  if (threadIdx.x == 0) used[E] = rows >= 32 ? 0xffffffffu : ((1u << rows) - 1u);
-  __syncthreads();
-  // compact the used experts in ascending id order
-  __shared__ int wcount[WAVES];
-  __shared__ int dmap[E + 1];
-  int base = 0;
-  for (int c0 = 0; c0 <= E; c0 += THREADS) {
-    const int e = c0 + threadIdx.x;
-    const bool f = e <= E && used[e] != 0u;
-    const uint64_t bal = __ballot(f);
-    const int before = __popcll(bal & ((1ull << lane) - 1ull));
-    if (lane == 0) wcount[wave] = __popcll(bal);
-    __syncthreads();
-    int off = base;
-    for (int w = 0; w < wave; ++w) off += wcount[w];
-    if (f) {
-      const int d = off + before;
-      dmap[e] = d;
-      sc.plan->expert[d] = e;
-      sc.plan->rowmask[d] = used[e];
-    }
-    base += wcount[0] + wcount[1] + wcount[2] + wcount[3];
-    __syncthreads();
-  }
-  const int n_act = base;
-  for (int idx = threadIdx.x; idx < n_act * MAX_ROWS; idx += THREADS) {
-    const int d = idx / MAX_ROWS, s = idx % MAX_ROWS;
-    float w = 0.f;
-    if (s < rows) {
-      // the shared expert is the last slot
-      if (d == n_act - 1) {
-        w = 1.0f;
-      } else {
-        for (int k = 0; k < TOPK; ++k)
-          if (dmap[pick_id[s][k]] == d) w = pick_w[s][k];
-      }
-    }
-    sc.plan->weight[idx] = w;
-  }
-  if (threadIdx.x == 0) {
-    sc.plan->n_act = n_act;
-    sc.plan->rows = rows;
-  }
+// The 32 bytes lane (g, r) holds of 128-k block kb of 16-row group rg of a shuffled
+// [N, K] E4M3 matrix at wb (kdiv32 = K / 32): k = 128 kb + 32 g + [0, 32) of row
+// 16 rg + r, as two nontemporal dwordx4 loads 256 bytes apart.
+MONO_DEV i32x8 ld_shuf(const uint8_t* wb, int kdiv32, int rg, int kb, int g, int r) {
+  const uint8_t* p = wb + (size_t)(rg * kdiv32 + kb * 4 + g) * 512 + r * 16;
+  const u32x4 lo = ld_nt_u32x4(p), hi = ld_nt_u32x4(p + 256);
+  i32x8 v;
+  v[0] = lo[0]; v[1] = lo[1]; v[2] = lo[2]; v[3] = lo[3];
+  v[4] = hi[0]; v[5] = hi[1]; v[6] = hi[2]; v[7] = hi[3];
+  return v;
 }
 
-// bf16(a * rstd * gamma) of 8 consecutive k, as one MFMA operand (stage_x_rmsnorm,
-// kernel.py:1367-1400)
+// 32 bytes of an LDS row as one MFMA operand
+MONO_DEV i32x8 lds32(const uint8_t* p) {
+  const u32x4 lo = *reinterpret_cast<const u32x4*>(p), hi = *reinterpret_cast<const u32x4*>(p + 16);
+  i32x8 v;
+  v[0] = lo[0]; v[1] = lo[1]; v[2] = lo[2]; v[3] = lo[3];
+  v[4] = hi[0]; v[5] = hi[1]; v[6] = hi[2]; v[7] = hi[3];
+  return v;
+}
+
+// bf16(a * rstd * gamma) of 8 consecutive k as one bf16 MFMA operand
+// (stage_x_rmsnorm, kernel.py:1367-1400)
 MONO_DEV bf16x8 normed8(const uint16_t* a, const uint16_t* g, float rstd) {
   const u32x4 av = ld_u32x4(a), gv = ld_u32x4(g);
   u32x4 o;
@@ -212,223 +167,539 @@ MONO_DEV bf16x8 normed8(const uint16_t* a, const uint16_t* g, float rstd) {
   return __builtin_bit_cast(bf16x8, o);
 }
 
-template <int H, int E, int TOPK>
-__global__ __launch_bounds__(THREADS) void k_router_sigmoid(
-    const uint16_t* __restrict__ a, const uint16_t* __restrict__ gamma,
-    const uint16_t* __restrict__ w_router, const float* __restrict__ bias, int rows,
-    float route_scale, MoeRouteOut ro, Scratch sc) {
-  constexpr int ET = E / 16;
-  constexpr int KSL = H / ROUTER_SLICES;
-  constexpr int STEPS = KSL / 32 / WAVES;
-  static_assert(KSL % (32 * WAVES) == 0, "router K slice");
-  const int lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
-  const int et = blockIdx.x % ET, ks = blockIdx.x / ET;
-  const int r = lane % 16, grp = lane / 16;
-  const bool live = r < rows;
-  const float rj = live ? sc.rstd[r] : 0.f;
-  const uint16_t* wrow = w_router + (size_t)(et * 16 + r) * H;
-  const uint16_t* arow = a + (size_t)r * H;
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  u32x4 wa[STEPS];
-#pragma unroll
-  for (int st = 0; st < STEPS; ++st)
-    wa[st] = ld_nt_u32x4(wrow + ks * KSL + (wave * STEPS + st) * 32 + grp * 8);
-#pragma unroll
-  for (int st = 0; st < STEPS; ++st) {
-    const int k = ks * KSL + (wave * STEPS + st) * 32 + grp * 8;
-    bf16x8 b = {};
-    if (live) b = normed8(arow + k, gamma + k, rj);
-    acc = mfma_bf16(__builtin_bit_cast(bf16x8, wa[st]), b, acc);
-  }
-  __shared__ f32x4 red[WAVES][WAVE];
-  __shared__ uint32_t flag;
-  red[wave][lane] = acc;
-  __syncthreads();
-  {
-    const int l = threadIdx.x % WAVE, i = threadIdx.x / WAVE;
-    const float v = red[0][l][i] + red[1][l][i] + red[2][l][i] + red[3][l][i];
-    const int col = l % 16, rowi = 4 * (l / 16) + i;
-    if (col < rows) sc.rpart[(ks * MAX_ROWS + col) * E + et * 16 + rowi] = v;
-  }
-  if (!last_arrival(sc.rcount, gridDim.x, &flag)) return;
-  finish_route_sigmoid<E, TOPK>(ro, bias, rows, route_scale, sc);
-}
+// Task kinds of the round-robin list
+enum { K_NONE = 0, K_UP = 1, K_DOWN = 2, K_FINAL = 3 };
 
-// ------------------------------------------------------------------ up / gate
-
-// FP8 quantisation of one 128-block of mid for every row of expert slot d (one wave a
-// row), folding the route weight into the block's coefficient (kernel.py:5118-5125).
-template <int I>
-MONO_DEV void quant_mid_block(int d, int b, uint32_t mask, Scratch sc) {
-  const int lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
-  for (int s = wave; s < MAX_ROWS; s += WAVES) {
-    if (!((mask >> s) & 1u)) continue;
-    const size_t base = ((size_t)d * MAX_ROWS + s) * I + b * 128;
-    const f32x2 m = *reinterpret_cast<const f32x2*>(sc.mid + base + lane * 2);
-    const float amax = wave_max(fmaxf(fabsf(m[0]), fabsf(m[1])));
-    const bool nz = amax > 0.f;
-    const float qs = nz ? amax * (1.0f / FP8_MAX) : 1.0f;
-    const float inv = nz ? hw_rcp(amax) * FP8_MAX : 1.0f;
-    const float q0 = fminf(fmaxf(m[0] * inv, -FP8_MAX), FP8_MAX);
-    const float q1 = fminf(fmaxf(m[1] * inv, -FP8_MAX), FP8_MAX);
-    reinterpret_cast<uint16_t*>(sc.mq + base)[lane] = (uint16_t)fp8x2_pack(q0, q1);
-    if (lane == 0) sc.mcoef[((size_t)d * MAX_ROWS + s) * (I / 128) + b] = qs * sc.plan->weight[d * MAX_ROWS + s];
+class Step {
+ public:
+  MONO_DEV Step(const Args& a, Lds& l) : A(a), L(l) {
+    tid = threadIdx.x;
+    lane = tid % WAVE;
+    wave = tid / WAVE;
+    g = lane / 16;
+    r = lane % 16;
+    G = gridDim.x;
+    S = a.rows;
+    plan_ready = false;
   }
-}
 
-template <int H, int I>
-__global__ __launch_bounds__(THREADS) void k_up_w8a8(const uint8_t* __restrict__ w13,
-                                                     const float* __restrict__ s13, Scratch sc) {
-  constexpr int NT = I / 16;    // 16-channel tiles an expert
-  constexpr int KB = H / 128;   // 128-k blocks
-  constexpr int KBW = KB / WAVES;
-  constexpr int BATCH = KBW % 7 == 0 ? 7 : (KBW % 4 == 0 ? 4 : (KBW % 2 == 0 ? 2 : 1));
-  static_assert(KB % WAVES == 0, "K blocks split evenly over the waves");
-  const int lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
-  const int r = lane % 16, grp = lane / 16;
-  __shared__ f32x4 redg[WAVES][WAVE], redu[WAVES][WAVE];
-  __shared__ uint32_t flag;
-  const int n_items = sc.plan->n_act * NT;
-  for (int t = blockIdx.x; t < n_items; t += gridDim.x) {
-    const int d = t / NT, c = t % NT;
-    const int e = sc.plan->expert[d];
-    const uint32_t mask = sc.plan->rowmask[d];
-    const uint8_t* wg = w13 + ((size_t)e * 2 * I + c * 16 + r) * H;
-    const uint8_t* wu = wg + (size_t)I * H;
-    const float* sg = s13 + ((size_t)e * (2 * I / 128) + (c * 16) / 128) * KB;
-    const float* su = s13 + ((size_t)e * (2 * I / 128) + (I + c * 16) / 128) * KB;
-    const uint8_t* xrow = sc.xq + (size_t)r * H;
-    const float* xsr = sc.xs + r * KB;
-    f32x4 accg = {0.f, 0.f, 0.f, 0.f}, accu = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 1
-    for (int b0 = 0; b0 < KBW; b0 += BATCH) {
-      // columns of rows this expert does not serve load their (finite) row anyway and
-      // are never stored
-      i32x8 ag[BATCH], au[BATCH], bx[BATCH];
+  MONO_DEV void run() {
+    if (tid == 0) {
+      const uint32_t ticket = __hip_atomic_fetch_add(&A.guard.words[G_TICKET], 1u, __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT);
+      L.tag = ticket / (uint32_t)G + 1u;
+      L.err = ld_agent_u32(&A.guard.words[G_ERROR]);
+    }
+    // the router task's weights go out before anything waits
+    const int rt = blockIdx.x;
+    u32x4 wr[RSTEP];
+    if (rt < ROUTER_TASKS) router_load(rt, wr);
+    __syncthreads();
+    if (L.err != 0) return;  // a failed launch stops the runtime until the host clears it
+    gd.a = A.guard;
+    gd.tag = L.tag;
+    gd.deadline = now_ticks() + A.guard.deadline_ticks;
+
+    norm_stats();
+    __syncthreads();
+    if (rt < ROUTER_TASKS) router(rt, wr);
+    if ((int)blockIdx.x >= G - S) {
+      if (!route(G - 1 - (int)blockIdx.x)) return;
+    }
+    quant_rows();
+    __syncthreads();
+    tasks();
+  }
+
+ private:
+  const Args& A;
+  Lds& L;
+  Guard gd;
+  int tid, lane, wave, g, r, G, S;
+  bool plan_ready;
+  i32x8 W[14];  // weights of the next task: an up tile (14) or a down task (8)
+
+  // ---------------------------------------------------------------- norm
+  MONO_DEV void norm_stats() {
+    for (int s = wave; s < S; s += FW) {
+      const uint16_t* row = A.a + (size_t)s * H;
+      float ss = 0.f;
 #pragma unroll
-      for (int q = 0; q < BATCH; ++q) {
-        const int k = (wave * KBW + b0 + q) * 128 + grp * 32;
-        ag[q] = ld_nt_i32x8(wg + k);
-        au[q] = ld_nt_i32x8(wu + k);
-        bx[q] = ld_i32x8(xrow + k);
+      for (int j = 0; j < H / 8 / WAVE; ++j) {
+        const u32x4 w = ld_u32x4(row + (j * WAVE + lane) * 8);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float lo = bf16_lo(w[q]), hi = bf16_hi(w[q]);
+          ss += lo * lo + hi * hi;
+        }
+      }
+      ss = wave_sum(ss);
+      if (lane == 0) L.rstd[s] = hw_rsq(ss * (1.0f / H) + A.eps);
+    }
+  }
+
+  // ---------------------------------------------------------------- router
+  MONO_DEV void router_load(int t, u32x4 (&wr)[RSTEP]) {
+    const int et = t % (E / 16), ks = t / (E / 16);
+    const uint16_t* wrow = A.w_router + (size_t)(et * 16 + r) * H + ks * (H / RK) + wave * RKW + g * 8;
+#pragma unroll
+    for (int st = 0; st < RSTEP; ++st) wr[st] = ld_nt_u32x4(wrow + st * 32);
+  }
+
+  MONO_DEV void router(int t, const u32x4 (&wr)[RSTEP]) {
+    const int et = t % (E / 16), ks = t / (E / 16);
+    const bool live = r < S;
+    const float rj = live ? L.rstd[r] : 0.f;
+    const uint16_t* arow = A.a + (size_t)(live ? r : 0) * H;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int st = 0; st < RSTEP; ++st) {
+      const int k = ks * (H / RK) + wave * RKW + st * 32 + g * 8;
+      bf16x8 b = {};
+      if (live) b = normed8(arow + k, A.g_post + k, rj);
+      acc = mfma_bf16(__builtin_bit_cast(bf16x8, wr[st]), b, acc);
+    }
+    L.red[0][wave][lane] = acc;
+    __syncthreads();
+    if (tid < 256) {
+      const int l = tid % WAVE, i = tid / WAVE;
+      float v = 0.f;
+#pragma unroll
+      for (int w = 0; w < FW; ++w) v += L.red[0][w][l][i];
+      const int s = l % 16, e = et * 16 + 4 * (l / 16) + i;
+      if (s < S) mb_putf(&A.mail.rlog[((size_t)ks * MAX_ROWS + s) * E + e], v, gd.tag);
+    }
+    __syncthreads();
+  }
+
+  // ---------------------------------------------------------------- route
+  MONO_DEV bool route(int s) {
+    bool ok = true;
+    if (tid < E) {
+      const uint64_t* base = &A.mail.rlog[(size_t)s * E + tid];
+      uint32_t v[RK];
+      ok = poll_words<RK>([base](int ks) { return base + (size_t)ks * MAX_ROWS * E; }, v, (1u << RK) - 1u,
+                          W_LOGITS, gd);
+      float lg = 0.f;
+#pragma unroll
+      for (int ks = 0; ks < RK; ++ks) lg += __uint_as_float(v[ks]);
+      const float raw = sigmoid(lg);
+      L.rraw[tid] = raw;
+      L.rkey[tid] = radix_key(raw + A.bias[tid]);
+      if (A.scores && ok) A.scores[s * E + tid] = raw;
+    }
+    if (!block_all(ok)) return false;
+    if (wave == 0) {
+      uint32_t key[4];
+      int id[4];
+      float raw[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        id[i] = lane + 64 * i;
+        key[i] = L.rkey[id[i]];
+        raw[i] = L.rraw[id[i]];
+      }
+      sort4(key, id, raw);
+      float my_raw = 0.f;  // lane k < TOPK: the raw score and id of pick k
+      int my_id = 0;
+      for (int k = 0; k < TOPK; ++k) {
+        const uint32_t m = wave_umax(key[0]);
+        const uint32_t cand = key[0] == m ? 0xffffu - (uint32_t)id[0] : 0u;
+        const int expert = min((int)(0xffffu - wave_umax(cand)), E - 1);
+        const bool hit = key[0] == m && id[0] == expert;
+        const uint64_t bal = __ballot(hit);
+        const int src = __ffsll((long long)bal) - 1;
+        const float rv = __shfl(raw[0], src, WAVE);
+        if (lane == k) {
+          my_raw = rv;
+          my_id = expert;
+        }
+        if (hit) {
+          key[0] = key[1]; key[1] = key[2]; key[2] = key[3]; key[3] = 0u;
+          id[0] = id[1]; id[1] = id[2]; id[2] = id[3]; id[3] = 0xffff;
+          raw[0] = raw[1]; raw[1] = raw[2]; raw[2] = raw[3]; raw[3] = 0.f;
+        }
+      }
+      // sum of the picks' raw scores in the butterfly order of lanes 0..7
+      float tot = lane < TOPK ? my_raw : 0.f;
+#pragma unroll
+      for (int o = 1; o < TOPK; o <<= 1) tot += __shfl_xor(tot, o, WAVE);
+      const float w = my_raw * (hw_rcp(tot) * A.route_scale);
+      if (lane < TOPK) {
+        mb_put(&A.mail.rsel[s * 2 * MAX_TOPK + lane], (uint32_t)my_id, gd.tag);
+        mb_putf(&A.mail.rsel[s * 2 * MAX_TOPK + MAX_TOPK + lane], w, gd.tag);
+        if (A.topk_ids) A.topk_ids[s * TOPK + lane] = my_id;
+        if (A.topk_w) A.topk_w[s * TOPK + lane] = w;
+      }
+    }
+    return true;
+  }
+
+  // ---------------------------------------------------------------- xq
+  // Lane quantises 8 consecutive k of a row; 16 lanes make a 128-block.
+  MONO_DEV void quant_rows() {
+    constexpr int PER_ROW = H / (8 * WAVE);  // wave passes a row
+    const int npass = S * PER_ROW;
+    for (int p0 = wave; p0 < npass; p0 += FW * 2) {
+      u32x4 av[2], gv[2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int p = p0 + u * FW;
+        if (p < npass) {
+          const int s = p / PER_ROW, k = ((p % PER_ROW) * WAVE + lane) * 8;
+          av[u] = ld_u32x4(A.a + (size_t)s * H + k);
+          gv[u] = ld_u32x4(A.g_post + k);
+        }
       }
 #pragma unroll
-      for (int q = 0; q < BATCH; ++q) {
-        const int kb = wave * KBW + b0 + q;
-        const float xsj = xsr[kb];
+      for (int u = 0; u < 2; ++u) {
+        const int p = p0 + u * FW;
+        if (p >= npass) continue;  // wave-uniform
+        const int s = p / PER_ROW, k = ((p % PER_ROW) * WAVE + lane) * 8;
+        const float rj = L.rstd[s];
+        float x[8];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          x[2 * q] = bf16_lo(av[u][q]) * rj * bf16_lo(gv[u][q]);
+          x[2 * q + 1] = bf16_hi(av[u][q]) * rj * bf16_hi(gv[u][q]);
+        }
+        float m = 0.f;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) m = fmaxf(m, fabsf(x[q]));
+        const float amax = group_max<16>(m);
+        const bool nz = amax > 0.f;
+        const float inv = nz ? hw_rcp(amax) * FP8_MAX : 1.0f;
+        u32x2 packed;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          float q4[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) q4[q] = fminf(fmaxf(x[4 * h + q] * inv, -FP8_MAX), FP8_MAX);
+          packed[h] = fp8x4_pack(q4[0], q4[1], q4[2], q4[3]);
+        }
+        *reinterpret_cast<u32x2*>(&L.xq[s][k]) = packed;
+        if ((lane % 16) == 0) L.xs[s][k / 128] = nz ? amax * (1.0f / FP8_MAX) : 1.0f;
+      }
+    }
+  }
+
+  // ---------------------------------------------------------------- plan
+  MONO_DEV bool load_plan() {
+    bool ok = true;
+    for (int e = tid; e < E; e += FT) L.used[e] = 0u;
+    if (tid < S * 2 * MAX_TOPK) {
+      const int s = tid / (2 * MAX_TOPK), k = tid % (2 * MAX_TOPK);
+      if (k % MAX_TOPK < TOPK) {
+        uint32_t v = 0;
+        ok = poll_word(&A.mail.rsel[s * 2 * MAX_TOPK + k], v, W_PICKS, gd);
+        if (k < MAX_TOPK) L.pick_id[s][k] = (int)v;
+        else L.pick_w[s][k - MAX_TOPK] = __uint_as_float(v);
+      }
+    }
+    if (!block_all(ok)) return false;
+    if (tid < S * TOPK) {
+      const int s = tid / TOPK, k = tid % TOPK;
+      atomicOr(&L.used[L.pick_id[s][k]], 1u << s);
+    }
+    __syncthreads();
+    // slot 0: the shared expert (id E) over every row; slots 1..: used experts ascending
+    const bool f = tid < E && L.used[tid] != 0u;
+    const uint64_t bal = __ballot(f);
+    const int before = __popcll(bal & ((1ull << lane) - 1ull));
+    if (lane == 0) L.wcount[wave] = __popcll(bal);
+    __syncthreads();
+    int off = 1;
+    for (int w = 0; w < wave; ++w) off += L.wcount[w];
+    if (f) {
+      const int d = off + before;
+      L.expert[d] = tid;
+      L.rowmask[d] = L.used[tid];
+      L.dmap[tid] = d;
+    }
+    if (tid == 0) {
+      L.expert[0] = E;
+      L.rowmask[0] = (1u << S) - 1u;
+      int n = 1;
+      for (int w = 0; w < FW; ++w) n += L.wcount[w];
+      L.n_act = n;
+    }
+    __syncthreads();
+    if (tid < S) {
+      int sl[NSLOT];
+      sl[0] = 0;
+      for (int k = 0; k < TOPK; ++k) {
+        const int d = L.dmap[L.pick_id[tid][k]];
+        int j = k + 1;
+        while (j > 1 && sl[j - 1] > d) {
+          sl[j] = sl[j - 1];
+          --j;
+        }
+        sl[j] = d;
+      }
+      for (int k = 0; k < NSLOT; ++k) L.rowslot[tid][k] = sl[k];
+    }
+    __syncthreads();
+    plan_ready = true;
+    return true;
+  }
+
+  MONO_DEV float route_weight(int d, int s) const {
+    if (d == 0) return 1.0f;
+    const int e = L.expert[d];
+    float w = 0.f;
+#pragma unroll
+    for (int k = 0; k < TOPK; ++k)
+      if (L.pick_id[s][k] == e) w = L.pick_w[s][k];
+    return w;
+  }
+
+  // ---------------------------------------------------------------- task list
+  // kind of task T (loads the plan first when T needs it); K_NONE past the list
+  MONO_DEV int classify(int T, bool& ok) {
+    ok = true;
+    if (T < NT) return K_UP;  // the shared expert's tiles need no plan
+    if (!plan_ready && !(ok = load_plan())) return K_NONE;
+    const int n_up = L.n_act * NT, n_dn = L.n_act * DN_GROUPS;
+    if (T < n_up) return K_UP;
+    if (T < n_up + n_dn) return K_DOWN;
+    if (T < n_up + n_dn + FIN_TASKS) return K_FINAL;
+    return K_NONE;
+  }
+
+  // Issue task T's weight loads into W. Every entry of W is written on every path
+  // (zero where the task has no weights), so none stays live into the next task.
+  MONO_DEV void load_task(int kind, int T) {
+    const i32x8 zero = {};
+    if (kind == K_UP) {
+      const int d = T / NT, c = T % NT;
+      const int e = d == 0 ? E : L.expert[d];
+      const uint8_t* wb = A.w13 + (size_t)e * (2 * I) * H;
+#pragma unroll
+      for (int j = 0; j < UP_KBW; ++j) {
+        const int kb = wave * UP_KBW + j;
+        W[2 * j] = ld_shuf(wb, H / 32, c, kb, g, r);            // gate rows 16c..
+        W[2 * j + 1] = ld_shuf(wb, H / 32, NT + c, kb, g, r);   // up rows I + 16c..
+      }
+    } else if (kind == K_DOWN) {
+      const int j = T - L.n_act * NT;
+      const int d = j / DN_GROUPS, grp = j % DN_GROUPS;
+      const uint8_t* wb = A.w2 + (size_t)L.expert[d] * H * I;
+      const int rg0 = (grp * DN_ROWS + wave * 32) / 16;
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int kb = 0; kb < IB; ++kb) W[t * IB + kb] = ld_shuf(wb, I / 32, rg0 + t, kb, g, r);
+#pragma unroll
+      for (int q = 2 * IB; q < 14; ++q) W[q] = zero;
+    } else {
+#pragma unroll
+      for (int q = 0; q < 14; ++q) W[q] = zero;
+    }
+  }
+
+  // Each turn: consume the task's weights (waiting on its inputs), issue the next
+  // task's weight loads, then publish the task's results while those loads fly.
+  MONO_DEV void tasks() {
+    int T = blockIdx.x;
+    bool ok;
+    int kind = classify(T, ok);
+    if (!ok) return;
+    load_task(kind, T);
+    while (kind != K_NONE) {
+      f32x4 acc[2];
+      if (kind == K_UP) {
+        up_compute(T, acc[0], acc[1]);
+      } else if (kind == K_DOWN) {
+        if (!down_compute(T, acc)) return;
+      }
+      const int T2 = T + G;
+      const int kind2 = classify(T2, ok);
+      if (!ok) return;
+      load_task(kind2, T2);
+      if (kind == K_UP) {
+        up_publish(T, acc[0], acc[1]);
+      } else if (kind == K_DOWN) {
+        down_publish(T, acc);
+      } else {
+        if (!final_task(T)) return;
+      }
+      T = T2;
+      kind = kind2;
+    }
+  }
+
+  // ---------------------------------------------------------------- up
+  MONO_DEV void up_compute(int T, f32x4& ag, f32x4& au) {
+    const int d = T / NT, c = T % NT;
+    const int e = d == 0 ? E : L.expert[d];
+    const float* sg = A.s13 + ((size_t)e * (2 * I / 128) + c / 8) * KB;
+    const float* su = A.s13 + ((size_t)e * (2 * I / 128) + I / 128 + c / 8) * KB;
+    ag = f32x4{0.f, 0.f, 0.f, 0.f};
+    au = ag;
+#pragma unroll
+    for (int j = 0; j < UP_KBW; ++j) {
+      const int kb = wave * UP_KBW + j;
+      const i32x8 b = lds32(&L.xq[r][kb * 128 + g * 32]);
+      const float xsj = L.xs[r][kb];
+      const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+      const f32x4 cg = mfma_fp8(W[2 * j], b, zero);
+      const f32x4 cu = mfma_fp8(W[2 * j + 1], b, zero);
+      ag += cg * (sg[kb] * xsj);
+      au += cu * (su[kb] * xsj);
+    }
+  }
+
+  MONO_DEV void up_publish(int T, const f32x4& ag, const f32x4& au) {
+    const int d = T / NT, c = T % NT;
+    const uint32_t mask = d == 0 ? (1u << S) - 1u : L.rowmask[d];
+    L.red[0][wave][lane] = ag;
+    L.red[1][wave][lane] = au;
+    __syncthreads();
+    if (tid < 256) {
+      const int l = tid % WAVE, i = tid / WAVE;
+      float gs = 0.f, us = 0.f;
+#pragma unroll
+      for (int w = 0; w < FW; ++w) {
+        gs += L.red[0][w][l][i];
+        us += L.red[1][w][l][i];
+      }
+      const int s = l % 16, ch = c * 16 + 4 * (l / 16) + i;
+      if ((mask >> s) & 1u) mb_putf(&A.mail.mid[((size_t)d * MAX_ROWS + s) * I + ch], silu(gs) * us, gd.tag);
+    }
+    __syncthreads();
+  }
+
+  // ---------------------------------------------------------------- down
+  MONO_DEV bool down_compute(int T, f32x4 (&acc)[2]) {
+    const int j = T - L.n_act * NT;
+    const int d = j / DN_GROUPS, grp = j % DN_GROUPS;
+    const int e = L.expert[d];
+    const uint32_t mask = L.rowmask[d];
+    // thread (row s, 16-channel group cg) polls its 16 contiguous mid words; 8 groups
+    // (8 consecutive lanes) make a 128-channel quantisation block
+    constexpr int CG = 16;
+    const int s = tid / (I / CG), cg = tid % (I / CG);
+    const bool in = s < MAX_ROWS && ((mask >> s) & 1u);
+    const uint64_t* base = &A.mail.mid[((size_t)d * MAX_ROWS + (in ? s : 0)) * I + cg * CG];
+    uint32_t v[CG];
+    const bool ok = poll_words<CG>([base](int q) { return base + q; }, v, in ? 0xffffu : 0u, W_MID, gd);
+    if (!block_all(ok)) return false;
+    float m = 0.f;
+#pragma unroll
+    for (int q = 0; q < CG; ++q) m = fmaxf(m, in ? fabsf(__uint_as_float(v[q])) : 0.f);
+    const float am = group_max<128 / CG>(m);
+    const bool nz = am > 0.f;
+    const float inv = nz ? hw_rcp(am) * FP8_MAX : 1.0f;
+    if (s < MAX_ROWS) {
+      u32x4 packed;
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        float q4[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) q4[q] = in ? fminf(fmaxf(__uint_as_float(v[4 * h + q]) * inv, -FP8_MAX), FP8_MAX) : 0.f;
+        packed[h] = fp8x4_pack(q4[0], q4[1], q4[2], q4[3]);
+      }
+      *reinterpret_cast<u32x4*>(&L.bq[s][cg * CG]) = packed;
+      if ((cg % (128 / CG)) == 0)
+        L.coef[s][cg / (128 / CG)] = in ? (nz ? am * (1.0f / FP8_MAX) : 1.0f) * route_weight(d, s) : 0.f;
+    }
+    __syncthreads();
+    const float* ws = A.s2 + ((size_t)e * (H / 128) + (grp * DN_ROWS + wave * 32) / 128) * IB;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kb = 0; kb < IB; ++kb) {
+        const i32x8 bb = lds32(&L.bq[r][kb * 128 + g * 32]);
         const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-        const f32x4 cg = mfma_fp8(ag[q], bx[q], zero);
-        const f32x4 cu = mfma_fp8(au[q], bx[q], zero);
-        accg += cg * (sg[kb] * xsj);
-        accu += cu * (su[kb] * xsj);
+        const f32x4 c = mfma_fp8(W[t * IB + kb], bb, zero);
+        acc[t] += c * (ws[kb] * L.coef[r][kb]);
       }
     }
-    redg[wave][lane] = accg;
-    redu[wave][lane] = accu;
-    __syncthreads();
-    {
-      const int l = threadIdx.x % WAVE, i = threadIdx.x / WAVE;
-      const float g = redg[0][l][i] + redg[1][l][i] + redg[2][l][i] + redg[3][l][i];
-      const float u = redu[0][l][i] + redu[1][l][i] + redu[2][l][i] + redu[3][l][i];
-      const int col = l % 16, ch = 4 * (l / 16) + i;
-      if ((mask >> col) & 1u) sc.mid[((size_t)d * MAX_ROWS + col) * I + c * 16 + ch] = silu(g) * u;
-    }
-    if (last_arrival(&sc.mcount[d * (I / 128) + c / 8], 8, &flag)) quant_mid_block<I>(d, c / 8, mask, sc);
-    __syncthreads();
+    return true;
   }
-}
 
-// ------------------------------------------------------------------ down
-template <int H, int I>
-__global__ __launch_bounds__(THREADS) void k_down_w8a8(const uint8_t* __restrict__ w2,
-                                                       const float* __restrict__ s2,
-                                                       const uint16_t* __restrict__ a,
-                                                       uint16_t* __restrict__ out,
-                                                       float* __restrict__ y_out, int rows,
-                                                       Scratch sc) {
-  constexpr int NB = I / 128;
-  const int lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
-  const int r = lane % 16, grp = lane / 16;
-  const int h0 = blockIdx.x * 16;
-  const int n_act = sc.plan->n_act;
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 1
-  for (int d0 = wave; d0 < n_act; d0 += 2 * WAVES) {
-    // two experts' tiles in flight a wave; the second is skipped past the plan (uniform)
-    i32x8 A[2][NB], B[2][NB];
+  MONO_DEV void down_publish(int T, const f32x4 (&acc)[2]) {
+    const int j = T - L.n_act * NT;
+    const int d = j / DN_GROUPS, grp = j % DN_GROUPS;
+    const uint32_t mask = L.rowmask[d];
+    if ((mask >> r) & 1u) {
 #pragma unroll
-    for (int p = 0; p < 2; ++p) {
-      const int d = d0 + p * WAVES;
-      if (d < n_act) {
-        const int e = sc.plan->expert[d];
-        const uint8_t* wrow = w2 + ((size_t)e * H + h0 + r) * I;
-        const uint8_t* mrow = sc.mq + ((size_t)d * MAX_ROWS + r) * I;
+      for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int b = 0; b < NB; ++b) {
-          A[p][b] = ld_nt_i32x8(wrow + b * 128 + grp * 32);
-          B[p][b] = ld_i32x8(mrow + b * 128 + grp * 32);
+        for (int i = 0; i < 4; ++i) {
+          const int h = grp * DN_ROWS + wave * 32 + t * 16 + 4 * g + i;
+          mb_putf(&A.mail.ypart[((size_t)d * MAX_ROWS + r) * H + h], acc[t][i], gd.tag);
         }
+    }
+    __syncthreads();  // the next down task rewrites bq / coef / amax
+  }
+
+  // ---------------------------------------------------------------- final
+  MONO_DEV bool final_task(int T) {
+    const int f = T - L.n_act * (NT + DN_GROUPS);
+    bool ok = true;
+    if (tid < S * FIN_ROWS) {
+      const int s = tid / FIN_ROWS, h = f * FIN_ROWS + tid % FIN_ROWS;
+      const uint64_t* base = &A.mail.ypart[(size_t)s * H + h];
+      const int32_t* slots = L.rowslot[s];
+      uint32_t v[NSLOT];
+      ok = poll_words<NSLOT>([base, slots](int k) { return base + (size_t)slots[k] * MAX_ROWS * H; }, v,
+                             (1u << NSLOT) - 1u, W_YPART, gd);
+      if (ok) {
+        float y = 0.f;
+#pragma unroll
+        for (int k = 0; k < NSLOT; ++k) y += __uint_as_float(v[k]);
+        const float res = bf16_bits_to_f32(A.a[(size_t)s * H + h]);
+        A.out[(size_t)s * H + h] = f32_to_bf16_bits(res + y);
+        if (A.y_out) A.y_out[(size_t)s * H + h] = y;
       }
     }
-#pragma unroll
-    for (int p = 0; p < 2; ++p) {
-      const int d = d0 + p * WAVES;
-      if (d < n_act) {
-        const int e = sc.plan->expert[d];
-        // a row the expert does not serve adds nothing (a select, so stale mid bytes
-        // of that row cannot reach the sum)
-        const bool lv = (sc.plan->rowmask[d] >> r) & 1u;
-        const float* ws = s2 + ((size_t)e * (H / 128) + h0 / 128) * NB;
-#pragma unroll
-        for (int b = 0; b < NB; ++b) {
-          const float coef = sc.mcoef[((size_t)d * MAX_ROWS + r) * NB + b];
-          const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-          const f32x4 c = mfma_fp8(A[p][b], B[p][b], zero);
-          const f32x4 t = acc + c * (ws[b] * coef);
-          acc = lv ? t : acc;
-        }
-      }
-    }
+    return block_all(ok);
   }
-  __shared__ f32x4 red[WAVES][WAVE];
-  red[wave][lane] = acc;
-  __syncthreads();
-  const int l = threadIdx.x % WAVE, i = threadIdx.x / WAVE;
-  const float y = red[0][l][i] + red[1][l][i] + red[2][l][i] + red[3][l][i];
-  const int col = l % 16, h = h0 + 4 * (l / 16) + i;
-  if (col < rows) {
-    const float res = bf16_bits_to_f32(a[(size_t)col * H + h]);
-    out[(size_t)col * H + h] = f32_to_bf16_bits(res + y);
-    if (y_out) y_out[(size_t)col * H + h] = y;
-  }
+};
+
+__global__ __launch_bounds__(FT, 1) void k_moe_fp8(Args args) {
+  __shared__ Lds lds;
+  Step st(args, lds);
+  st.run();
 }
 
-// ------------------------------------------------------------------ host
-template <int H, int E, int I, int TOPK>
-static hipError_t launch_w8a8(const MoeFp8Args& g, int n_cu, Scratch sc, hipStream_t st) {
-  const uint16_t* a = static_cast<const uint16_t*>(g.a);
-  const uint16_t* gp = static_cast<const uint16_t*>(g.g_post);
-  k_prep_w8a8<H><<<g.rows, THREADS, 0, st>>>(a, gp, g.eps, sc);
-  MoeRouteOut ro{g.scores, g.topk_ids, g.topk_w};
-  k_router_sigmoid<H, E, TOPK><<<(E / 16) * ROUTER_SLICES, THREADS, 0, st>>>(
-      a, gp, static_cast<const uint16_t*>(g.w_router), g.bias, g.rows, g.route_scale, ro, sc);
-  const int max_act = (g.rows * TOPK < E ? g.rows * TOPK : E) + 1;
-  int grid_up = max_act * (I / 16);
-  if (grid_up > 2 * n_cu) grid_up = 2 * n_cu;
-  k_up_w8a8<H, I><<<grid_up, THREADS, 0, st>>>(static_cast<const uint8_t*>(g.w13), g.s13, sc);
-  k_down_w8a8<H, I><<<H / 16, THREADS, 0, st>>>(static_cast<const uint8_t*>(g.w2), g.s2, a,
-                                                static_cast<uint16_t*>(g.out), g.y, g.rows, sc);
-  return hipGetLastError();
-}
-
-hipError_t moe_fp8_forward(const MoeFp8Args& g, const MoeGeom& geo, int n_cu, Scratch sc, hipStream_t st) {
-  if (geo.hidden == 7168 && geo.n_experts == 256 && geo.inter == 512 && geo.top_k == 8)
-    return launch_w8a8<7168, 256, 512, 8>(g, n_cu, sc, st);
-  return hipErrorInvalidValue;
-}
+}  // namespace
 
 bool moe_fp8_supported(const MoeGeom& geo) {
-  return geo.hidden == 7168 && geo.n_experts == 256 && geo.inter == 512 && geo.top_k == 8;
+  return geo.hidden == H && geo.n_experts == E && geo.inter == I && geo.top_k == TOPK;
+}
+
+int moe_fp8_router_slices() { return RK; }
+
+hipError_t moe_fp8_occupancy(int* blocks_per_cu) {
+  return hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, k_moe_fp8, FT, 0);
+}
+
+hipError_t moe_fp8_forward(const MoeFp8Args& g, int grid, const Mail& mail, const GuardArgs& guard, hipStream_t st) {
+  if (grid < ROUTER_TASKS || grid < MAX_ROWS || g.rows < 1 || g.rows > MAX_ROWS) return hipErrorInvalidConfiguration;
+  Args a;
+  a.a = static_cast<const uint16_t*>(g.a);
+  a.g_post = static_cast<const uint16_t*>(g.g_post);
+  a.w_router = static_cast<const uint16_t*>(g.w_router);
+  a.bias = g.bias;
+  a.w13 = static_cast<const uint8_t*>(g.w13);
+  a.s13 = g.s13;
+  a.w2 = static_cast<const uint8_t*>(g.w2);
+  a.s2 = g.s2;
+  a.out = static_cast<uint16_t*>(g.out);
+  a.y_out = g.y;
+  a.scores = g.scores;
+  a.topk_ids = g.topk_ids;
+  a.topk_w = g.topk_w;
+  a.rows = g.rows;
+  a.route_scale = g.route_scale;
+  a.eps = g.eps;
+  a.mail = mail;
+  a.guard = guard;
+  k_moe_fp8<<<grid, FT, 0, st>>>(a);
+  return hipGetLastError();
 }
 
 }  // namespace moe

@@ -5,6 +5,7 @@
 
 #include "mono.h"
 #include "moe_plan.h"
+#include "sync.h"
 
 namespace mono {
 namespace moe {
@@ -13,23 +14,20 @@ struct MoeGeom {
   int hidden, n_experts, top_k, inter;
 };
 
-// The C-ABI argument blocks, with the runtime's scalars folded in.
+// The C-ABI argument block with the runtime's scalars folded in.
 struct MoeFp8Args : mono_moe_fp8_args {
   float route_scale;
   float eps;
   MoeFp8Args(const mono_moe_fp8_args& a, float rs, float e) : mono_moe_fp8_args(a), route_scale(rs), eps(e) {}
-  const uint16_t* a16() const { return static_cast<const uint16_t*>(a); }
-};
-
-// Optional routing outputs of the router's last workgroup.
-struct MoeRouteOut {
-  float* scores;
-  int32_t* topk_ids;
-  float* topk_w;
 };
 
 bool moe_fp8_supported(const MoeGeom& geo);
-hipError_t moe_fp8_forward(const MoeFp8Args& g, const MoeGeom& geo, int n_cu, Scratch sc, hipStream_t st);
+// Router K slices of the FP8 kernel (rows of the rlog mailbox).
+int moe_fp8_router_slices();
+// Workgroups of the persistent launch that fit on one CU (must be >= 1).
+hipError_t moe_fp8_occupancy(int* blocks_per_cu);
+// Enqueue the one persistent launch on `st` with `grid` workgroups (one a CU).
+hipError_t moe_fp8_forward(const MoeFp8Args& g, int grid, const Mail& mail, const GuardArgs& guard, hipStream_t st);
 
 }  // namespace moe
 }  // namespace mono

@@ -1,0 +1,120 @@
+// Inter-workgroup hand-off inside one persistent launch: tagged mailbox words and the
+// guard that bounds every wait.
+//
+// A mailbox word is 64 bits: the payload (an f32 or i32's bits) in the low half and
+// the launch's tag in the high half, written by one agent-scope relaxed atomic store
+// (global_store_dwordx2 sc1) and read by agent-scope relaxed atomic loads
+// (global_load_dwordx2 sc1). The tag makes every word self-validating, so a producer
+// needs no release fence and a consumer no acquire fence: on gfx950 those are an L2
+// writeback / invalidate of the XCD, which costs far more than the hand-off. This is
+// the reference's tagged (value, tag) pair (sgl_amd_mono/common/sync.py:30-207,
+// glm53/gfx950/kernel.py:29-35,636-647), restated for HIP.
+//
+// Tags: every workgroup of a launch takes a ticket from guard word 0 with one atomic
+// add; ticket / gridDim.x is the launch's ordinal (launches of one runtime are
+// stream-ordered, so their tickets never interleave) and the tag is ordinal + 1. A
+// HIP-graph replay takes fresh tickets, so it never sees a stale word as ready.
+//
+// Guard words (int32 [8] in device memory, common/guard.py:16-30 in the reference):
+//   0  launch tickets
+//   1  error: 1 + the id of the first wait site that ran out of time (sticky: every
+//      later launch of the runtime exits at once until the host clears it)
+//   2  tag of the failing launch (waits of that launch give up when they see it)
+//   3  workgroup that failed first
+// Every wait polls its words until their tags match, checking the deadline
+// (s_memrealtime, 100 MHz) every POLL_CHECK polls. On expiry it records the error,
+// raises word 2 and returns false; the caller makes the failure workgroup-uniform and
+// the workgroup exits. No wait ever blocks past the deadline and nothing faults: the
+// launch drains and the host reads the error words (fail-stop without a GPU fault).
+#pragma once
+
+#include "common.h"
+
+namespace mono {
+
+enum GuardWord { G_TICKET = 0, G_ERROR = 1, G_FAIL_TAG = 2, G_FAIL_BLOCK = 3, G_WORDS = 8 };
+constexpr int POLL_CHECK = 32;
+
+// Kernel-argument part of the guard: the words, the deadline and the host-forced
+// fault (a wait site whose waits the host makes fail at once, for tests of the error
+// path; -1 = none).
+struct GuardArgs {
+  uint32_t* words;
+  uint64_t deadline_ticks;
+  int32_t fault_site;
+};
+
+MONO_DEV uint64_t now_ticks() { return __builtin_amdgcn_s_memrealtime(); }
+
+MONO_DEV void mb_put(uint64_t* p, uint32_t bits, uint32_t tag) {
+  __hip_atomic_store(p, ((uint64_t)tag << 32) | bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+MONO_DEV void mb_putf(uint64_t* p, float v, uint32_t tag) { mb_put(p, __float_as_uint(v), tag); }
+MONO_DEV uint64_t mb_load(const uint64_t* p) {
+  return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+MONO_DEV uint32_t ld_agent_u32(const uint32_t* p) {
+  return __hip_atomic_load(const_cast<uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+struct Guard {
+  GuardArgs a;
+  uint64_t deadline;  // absolute s_memrealtime tick
+  uint32_t tag;
+
+  // Record a failure at `site` (first one wins) and raise the launch's fail tag.
+  MONO_DEV void fail(int site) const {
+    uint32_t expect = 0;
+    if (__hip_atomic_compare_exchange_strong(&a.words[G_ERROR], &expect, (uint32_t)site + 1u, __ATOMIC_RELAXED,
+                                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+      __hip_atomic_store(&a.words[G_FAIL_BLOCK], (uint32_t)blockIdx.x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(&a.words[G_FAIL_TAG], tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  // True (and the failure recorded) once the deadline has passed or another
+  // workgroup of this launch has failed.
+  MONO_DEV bool expired(int site) const {
+    if (now_ticks() > deadline) {
+      fail(site);
+      return true;
+    }
+    return ld_agent_u32(&a.words[G_FAIL_TAG]) == tag;
+  }
+};
+
+// Poll the mailbox words at(j) of this lane whose bit j is set in `pending` until each
+// carries `tag`; their payloads go to v[j]. `at` computes an address from its index,
+// so callers hold no arrays of pointers. False if the guard expired first.
+template <int N, class At>
+MONO_DEV bool poll_words(At at, uint32_t (&v)[N], uint32_t pending, int site, const Guard& g) {
+  if (pending && site == g.a.fault_site) {  // host-forced fault: the wait fails at once
+    g.fail(site);
+    return false;
+  }
+  for (uint32_t spin = 1;; ++spin) {
+    uint64_t w[N];
+#pragma unroll
+    for (int j = 0; j < N; ++j)
+      if ((pending >> j) & 1u) w[j] = mb_load(at(j));
+#pragma unroll
+    for (int j = 0; j < N; ++j)
+      if (((pending >> j) & 1u) && (uint32_t)(w[j] >> 32) == g.tag) {
+        v[j] = (uint32_t)w[j];
+        pending &= ~(1u << j);
+      }
+    if (!pending) return true;
+    if (spin % POLL_CHECK == 1 && g.expired(site)) return false;  // after the 1st, 33rd, ... poll
+    __builtin_amdgcn_s_sleep(1);
+  }
+}
+
+MONO_DEV bool poll_word(const uint64_t* p, uint32_t& v, int site, const Guard& g) {
+  uint32_t vs[1];
+  const bool ok = poll_words<1>([p](int) { return p; }, vs, 1u, site, g);
+  v = vs[0];
+  return ok;
+}
+
+// Workgroup-uniform AND of a per-thread flag (a full barrier).
+MONO_DEV bool block_all(bool ok) { return __syncthreads_and(ok ? 1 : 0) != 0; }
+
+}  // namespace mono

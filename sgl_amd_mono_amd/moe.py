@@ -44,9 +44,9 @@ class Fp8MoeWeights:
     g_post: torch.Tensor  # bf16 [H]
     w_router: torch.Tensor  # bf16 [E, H]
     bias: torch.Tensor  # f32 [E]
-    w13: torch.Tensor  # float8_e4m3fn / uint8 [E+1, 2I, H]
+    w13: torch.Tensor  # float8_e4m3fn / uint8 [E+1, 2I, H], AITER (16, 16) layout
     s13: torch.Tensor  # f32 [E+1, 2I/128, H/128]
-    w2: torch.Tensor  # float8_e4m3fn / uint8 [E+1, H, I]
+    w2: torch.Tensor  # float8_e4m3fn / uint8 [E+1, H, I], AITER (16, 16) layout
     s2: torch.Tensor  # f32 [E+1, H/128, I/128]
 
 
@@ -111,6 +111,39 @@ class MoeRuntime:
 
     def _stream(self) -> int:
         return torch.cuda.current_stream(self.device).cuda_stream
+
+    # ---------------------------------------------------------------- guard
+    def set_deadline(self, seconds: float) -> None:
+        """Deadline of every inter-workgroup wait (Glm53Runtime.set_deadline,
+        glm53/gfx950/runner.py:197-204)."""
+        _lib.check(_lib.lib().mono_moe_set_deadline(self._h, float(seconds)))
+
+    def set_fault(self, site: int) -> None:
+        """Tests of the fail-stop path: wait ``site`` never sees its data (-1: off)."""
+        _lib.check(_lib.lib().mono_moe_set_fault(self._h, int(site)))
+
+    def error_words(self) -> list[int]:
+        """The guard words (synchronises): [tickets, 1 + failed wait site or 0, failing
+        launch tag, failing workgroup]."""
+        words = (C.c_int32 * _lib.GUARD_WORDS)()
+        with torch.cuda.device(self.device):
+            _lib.check(_lib.lib().mono_moe_read_errors(self._h, words))
+        return list(words)
+
+    def check_errors(self) -> None:
+        """Raise MonoError if a launch of this runtime failed a wait (fail-stop)."""
+        w = self.error_words()
+        if w[1]:
+            site = w[1] - 1
+            raise _lib.MonoError(
+                _lib.MONO_ESTATE,
+                f"MoE launch (tag {w[2]}) stopped: wait '{_lib.MOE_SITES.get(site, site)}' passed its "
+                f"deadline in workgroup {w[3]}; the runtime refuses launches until clear_errors()",
+            )
+
+    def clear_errors(self) -> None:
+        with torch.cuda.device(self.device):
+            _lib.check(_lib.lib().mono_moe_clear_errors(self._h))
 
     def forward_fp8(self, a: torch.Tensor, w: Fp8MoeWeights, out: torch.Tensor | None = None,
                     debug: bool = False):

@@ -13,6 +13,7 @@ from __future__ import annotations
 
 import torch
 
+from .layouts import shuffle_16x16
 from .moe import Fp8MoeWeights, MoeGeometry, Mxfp4MoeWeights
 
 
@@ -29,7 +30,8 @@ def fp8_codes(shape, g: torch.Generator, device) -> torch.Tensor:
 def fp8_moe_weights(geo: MoeGeometry, device, seed: int = 0) -> Fp8MoeWeights:
     """One layer's FP8 MoE weights: router ~N(0,1)*2/sqrt(H) bf16 (check_layer.py:96-98),
     bias ~N(0, 0.1) f32 (:99), post-norm weight 1 + 0.1*N(0,1) bf16, experts E4M3 from
-    N(0,1) with 128x128 f32 block scales ~U(0.5, 2)/448. Expert E is the shared one."""
+    N(0,1) with 128x128 f32 block scales ~U(0.5, 2)/448, stored in AITER's (16, 16)
+    shuffled layout as SGLang's ROCm MoE leaves them. Expert E is the shared one."""
     H, E, I = geo.hidden, geo.n_experts, geo.inter
     g = _gen(device, seed)
     w_router = (torch.randn(E, H, generator=g, device=device) * (2.0 / H**0.5)).to(torch.bfloat16)
@@ -38,8 +40,8 @@ def fp8_moe_weights(geo: MoeGeometry, device, seed: int = 0) -> Fp8MoeWeights:
     w13 = torch.empty(E + 1, 2 * I, H, dtype=torch.uint8, device=device)
     w2 = torch.empty(E + 1, H, I, dtype=torch.uint8, device=device)
     for e in range(E + 1):  # one expert at a time keeps the f32 temporaries small
-        w13[e] = fp8_codes((2 * I, H), g, device)
-        w2[e] = fp8_codes((H, I), g, device)
+        w13[e] = shuffle_16x16(fp8_codes((2 * I, H), g, device))
+        w2[e] = shuffle_16x16(fp8_codes((H, I), g, device))
     s13 = (torch.rand(E + 1, 2 * I // 128, H // 128, generator=g, device=device) * 1.5 + 0.5) / 448.0
     s2 = (torch.rand(E + 1, H // 128, I // 128, generator=g, device=device) * 1.5 + 0.5) / 448.0
     return Fp8MoeWeights(g_post=g_post, w_router=w_router, bias=bias, w13=w13, s13=s13, w2=w2, s2=s2)

@@ -9,6 +9,7 @@ relative (norm) and the bf16 output within 2e-2 max-abs / 1e-2 relative.
 import pytest
 import torch
 
+from oracle import codecs as ocodecs
 from oracle import moe as omoe
 from oracle import topk as otopk
 from sgl_amd_mono_amd import workloads
@@ -23,14 +24,16 @@ SCORE_ABS = 1e-4  # sigmoid scores: f32 GEMV order differences only
 
 
 class CpuExperts:
-    """Expert tensors fetched to the CPU on first use (the oracle reads a few)."""
+    """Expert tensors fetched to the CPU on first use (the oracle reads a few); the
+    (16, 16)-shuffled FP8 matrices are unshuffled by the oracle's own gather."""
 
-    def __init__(self, t):
-        self.t, self.cache = t, {}
+    def __init__(self, t, shuffled=False):
+        self.t, self.shuffled, self.cache = t, shuffled, {}
 
     def __getitem__(self, e):
         if e not in self.cache:
-            self.cache[e] = self.t[e].cpu()
+            x = self.t[e].cpu()
+            self.cache[e] = ocodecs.aiter_unshuffle(x) if self.shuffled else x
         return self.cache[e]
 
 
@@ -42,7 +45,7 @@ def setup(gpu_device):
     torch.cuda.synchronize()
     cpu = dict(
         g_post=w.g_post.cpu(), w_router=w.w_router.cpu(), bias=w.bias.cpu(),
-        w13=CpuExperts(w.w13), s13=CpuExperts(w.s13), w2=CpuExperts(w.w2), s2=CpuExperts(w.s2),
+        w13=CpuExperts(w.w13, True), s13=CpuExperts(w.s13), w2=CpuExperts(w.w2, True), s2=CpuExperts(w.s2),
     )  # fmt: skip
     yield w, rt, cpu
     rt.close()
@@ -124,3 +127,49 @@ def test_fp8_moe_rejects_bad_shapes(setup, gpu_device):
     a = workloads.rows_bf16(2, G.hidden, gpu_device, seed=1).float()
     with pytest.raises(ValueError, match="dtype"):
         rt.forward_fp8(a, w)
+
+
+def test_fp8_moe_fail_stop_on_forced_wait(setup, gpu_device):
+    """A wait the host forces to fail (guard.py:79-88) ends the launch with its site
+    recorded; later launches refuse to run until the error is cleared, then the
+    runtime computes the same bits as before."""
+    w, rt, _ = setup
+    a = workloads.rows_bf16(8, G.hidden, gpu_device, seed=21)
+    good, _ = _run(rt, w, a)
+    rt.check_errors()
+    for site in (2, 3, 0):
+        print(f"[fault] forcing wait site {site}", flush=True)
+        rt.set_deadline(0.02)
+        rt.set_fault(site)
+        _run(rt, w, a)
+        words = rt.error_words()
+        assert words[1] == site + 1, words
+        with pytest.raises(Exception, match="stopped"):
+            rt.check_errors()
+        rt.set_fault(-1)
+        rt.set_deadline(2.0)
+        _run(rt, w, a)  # sticky: exits at once, the error stays
+        assert rt.error_words()[1] == site + 1
+        rt.clear_errors()
+        again, _ = _run(rt, w, a)
+        rt.check_errors()
+        assert torch.equal(again, good)
+
+
+def test_fp8_moe_deadline_expiry_stops_the_launch(setup, gpu_device):
+    """With a deadline of one 10 ns tick, a wait that has to spin passes its deadline:
+    the launch stops with a valid site recorded instead of hanging, and the runtime
+    recovers once the error is cleared and the deadline restored."""
+    w, rt, _ = setup
+    a = workloads.rows_bf16(8, G.hidden, gpu_device, seed=22)
+    good, _ = _run(rt, w, a)
+    rt.set_deadline(1e-8)
+    _run(rt, w, a)
+    words = rt.error_words()
+    print(f"[deadline] guard words {words}", flush=True)
+    assert 1 <= words[1] <= 4, words
+    rt.set_deadline(2.0)
+    rt.clear_errors()
+    again, _ = _run(rt, w, a)
+    rt.check_errors()
+    assert torch.equal(again, good)
