@@ -150,6 +150,57 @@ typedef struct {
 
 int mono_moe_mxfp4_forward(mono_moe* moe, const mono_moe_mxfp4_args* args, void* stream);
 
+/* --------------------------------------------------- sparse-attention phase */
+
+typedef struct mono_attn mono_attn;
+
+typedef struct {
+  int32_t device;
+  int32_t max_rows;      /* widest decode step, 1..64 */
+  int32_t max_ctx;       /* keys a row may hold, a multiple of 1024, <= 32768 */
+  float softmax_scale;   /* (qk_nope + qk_rope)^-1/2 = 192^-1/2 for this path */
+} mono_attn_config;
+
+/* Replaces the sparse-attention scratch of Glm53Runtime (runner.py:133-195): the
+ * runtime's mailboxes (scores, selections, split partials) and guard words. */
+int mono_attn_create(const mono_attn_config* cfg, mono_attn** out);
+int mono_attn_destroy(mono_attn* attn);
+
+/* Sparse-attention phase of one decode step, one persistent launch (
+ * glm53/gfx950/kernel.py:2684-4123 index score / top-k / split / merge, with the FP4
+ * indexer of deepseek_v4/gfx950/kernels/stages/indexer.py:460-802):
+ *   score[t] = sum_h w_h relu(q_h . k_t) over the row's FP4 index keys,
+ *   sel = exact top-2048 positions by (score desc, position asc) -> cache slots,
+ *   out = softmax((q . kv_j) * scale) . kv_j[:512] over the selected slots.
+ * Caches are SGLang's, read in place: 64-token pages, a slot is page * 64 + offset. */
+typedef struct {
+  const void* iq;            /* u8 [rows, 64, 64] E2M1 index query (dim 2i in the low nibble) */
+  const void* iqs;           /* u8 [rows, 64, 4] E8M0, one per 32 dims */
+  const void* iw;            /* bf16 [rows, 64] index head weights */
+  const void* ikv;           /* u8 [pages, 4, 64, 16] FP4 index keys: chunk, key, 16 B */
+  const void* iks;           /* u8 [pages, 4, 64] E8M0; key t at byte (t % 16) * 4 + t / 16 */
+  const void* q;             /* bf16 [rows, 32, 576] absorbed latent query then RoPE query */
+  const void* kv;            /* u8 [pages * 64, 576] E4M3 latent then RoPE key */
+  const float* kv_scale;     /* f32 [pages * 64] per-token dequantisation scale */
+  const int32_t* page_table; /* i32 [rows, pt_stride] logical page -> cache page */
+  const int32_t* seq_lens;   /* i32 [rows] keys of each row (clamped to [0, max_ctx]) */
+  int32_t pt_stride;
+  int32_t n_pages;           /* pages of the caches; page ids are clamped below it */
+  void* out;                 /* bf16 [rows, 32, 512] */
+  int32_t rows;
+  float* scores;             /* optional f32 [rows, max_ctx] index scores */
+  int32_t* topk;             /* optional i32 [rows, 2048] selected slots, -1 past the count */
+} mono_attn_args;
+
+int mono_attn_forward(mono_attn* attn, const mono_attn_args* args, void* stream);
+
+/* Guard controls of an attention runtime (as the MoE runtime's). Wait sites: 0 index
+ * scores, 1 selected slots, 2 split partials. */
+int mono_attn_set_deadline(mono_attn* attn, double seconds);
+int mono_attn_read_errors(mono_attn* attn, int32_t* words);
+int mono_attn_clear_errors(mono_attn* attn);
+int mono_attn_set_fault(mono_attn* attn, int32_t site);
+
 #ifdef __cplusplus
 }
 #endif

@@ -43,6 +43,18 @@ class MoeMxfp4Args(C.Structure):
     ]
 
 
+class AttnConfig(C.Structure):
+    _fields_ = [("device", _I32), ("max_rows", _I32), ("max_ctx", _I32), ("softmax_scale", _F32)]
+
+
+class AttnArgs(C.Structure):
+    _fields_ = [
+        ("iq", _VP), ("iqs", _VP), ("iw", _VP), ("ikv", _VP), ("iks", _VP), ("q", _VP), ("kv", _VP),
+        ("kv_scale", _VP), ("page_table", _VP), ("seq_lens", _VP), ("pt_stride", _I32),
+        ("n_pages", _I32), ("out", _VP), ("rows", _I32), ("scores", _VP), ("topk", _VP),
+    ]
+
+
 # entry point -> (restype, argtypes); every name include/mono.h declares
 SIGNATURES = {
     "mono_abi_version": (C.c_int, []),
@@ -55,10 +67,18 @@ SIGNATURES = {
     "mono_moe_read_errors": (C.c_int, [_VP, C.POINTER(C.c_int32)]),
     "mono_moe_clear_errors": (C.c_int, [_VP]),
     "mono_moe_set_fault": (C.c_int, [_VP, C.c_int32]),
+    "mono_attn_create": (C.c_int, [C.POINTER(AttnConfig), C.POINTER(_VP)]),
+    "mono_attn_destroy": (C.c_int, [_VP]),
+    "mono_attn_forward": (C.c_int, [_VP, C.POINTER(AttnArgs), _VP]),
+    "mono_attn_set_deadline": (C.c_int, [_VP, C.c_double]),
+    "mono_attn_read_errors": (C.c_int, [_VP, C.POINTER(C.c_int32)]),
+    "mono_attn_clear_errors": (C.c_int, [_VP]),
+    "mono_attn_set_fault": (C.c_int, [_VP, C.c_int32]),
 }
 GUARD_WORDS = 4
-# wait sites of the MoE launch (guard word 1 = site + 1)
+# wait sites of the launches (guard word 1 = site + 1)
 MOE_SITES = {0: "router logits", 1: "route picks", 2: "expert mid activations", 3: "expert outputs"}
+ATTN_SITES = {0: "index scores", 1: "selected slots", 2: "split partials"}
 
 _lock = threading.Lock()
 _lib = None

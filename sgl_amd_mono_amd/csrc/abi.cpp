@@ -1,17 +1,19 @@
 // The C-ABI of libmono_gfx950.so: runtime handles, argument checks, error strings.
 //
-// A handle owns its device scratch (one hipMalloc at create, freed at destroy), the
-// way the reference's Glm53Runtime owns its scratch mailboxes and guard words
+// A handle owns its device scratch (one hipMalloc at create, freed at destroy): the
+// mailboxes and guard words of its persistent launch, the way the reference's
+// Glm53Runtime owns its scratch mailboxes and guard words
 // (glm53/gfx950/runner.py:133-215). Forward calls validate their arguments on the
-// host, then enqueue the phase's kernels on the caller's stream and return.
+// host, then enqueue one launch on the caller's stream and return.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
-#include <algorithm>
 #include <cstring>
 #include <string>
 
+#include "attn_ops.h"
 #include "mono.h"
 #include "moe_ops.h"
 
@@ -40,6 +42,9 @@ int ok() {
     if (e_ != hipSuccess) return fail(MONO_EHIP, "%s: %s", #call, hipGetErrorString(e_)); \
   } while (0)
 
+#define REQUIRE_PTR(p) \
+  if (!(p)) return fail(MONO_EINVAL, "argument %s must be a device pointer, got NULL", #p)
+
 size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
 
 int check_device(int device) {
@@ -49,26 +54,132 @@ int check_device(int device) {
   return MONO_OK;
 }
 
+const double TICKS_PER_S = 100e6;  // s_memrealtime runs at 100 MHz
+const double DEFAULT_DEADLINE_S = 2.0;
+const double MAX_DEADLINE_S = 3600.0;
+
+// Carves one device allocation into 256-byte aligned pieces.
+struct Carve {
+  size_t off = 0;
+  size_t take(size_t bytes) {
+    const size_t at = off;
+    off += align256(bytes);
+    return at;
+  }
+};
+
 }  // namespace
 
-struct mono_moe {
+// What every runtime handle has: its device, the persistent grid, the scratch blob
+// and the guard (common/guard.py:100-241 in the reference).
+struct RuntimeBase {
+  uint32_t magic = 0;
+  int device = 0;
+  int grid = 0;  // workgroups of the persistent launch: one a CU
+  void* blob = nullptr;
+  size_t blob_bytes = 0;
+  mono::GuardArgs guard{};
+
+  // Allocate and zero `bytes` of scratch with the guard words at `guard_off`. Tag 0
+  // is never a launch's tag, so zeroed mailboxes read as empty.
+  int init(int dev, size_t bytes, size_t guard_off, int (*occupancy)(int*), const char* what) {
+    device = dev;
+    hipDeviceProp_t prop;
+    HIP_TRY(hipGetDeviceProperties(&prop, dev));
+    int per_cu = 0;
+    if (int rc = occupancy(&per_cu)) return rc;
+    if (per_cu < 1) return fail(MONO_ESTATE, "the persistent %s kernel does not fit on a CU (occupancy %d)", what, per_cu);
+    grid = prop.multiProcessorCount;
+    hipError_t e = hipMalloc(&blob, bytes);
+    if (e != hipSuccess) {
+      blob = nullptr;
+      return fail(MONO_ENOMEM, "hipMalloc(%zu) for the %s mailboxes: %s", bytes, what, hipGetErrorString(e));
+    }
+    blob_bytes = bytes;
+    e = hipMemset(blob, 0, bytes);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) return fail(MONO_EHIP, "clearing the %s mailboxes: %s", what, hipGetErrorString(e));
+    guard.words = reinterpret_cast<uint32_t*>(at(guard_off));
+    guard.deadline_ticks = (uint64_t)(DEFAULT_DEADLINE_S * TICKS_PER_S);
+    guard.fault_site = -1;
+    return MONO_OK;
+  }
+  char* at(size_t off) const { return static_cast<char*>(blob) + off; }
+  // Free the scratch; the handle is dead afterwards (idempotent like PeerBuffer.close,
+  // common/peer.py:157-165).
+  int release() {
+    magic = 0;
+    if (!blob) return MONO_OK;
+    hipError_t e = hipFree(blob);
+    blob = nullptr;
+    if (e != hipSuccess) return fail(MONO_EHIP, "hipFree: %s", hipGetErrorString(e));
+    return MONO_OK;
+  }
+};
+
+struct mono_moe : RuntimeBase {
   mono_moe_config cfg;
-  int grid;  // workgroups of the persistent launch: one a CU
-  void* blob;
-  size_t blob_bytes;
   mono::moe::Mail mail;
-  mono::GuardArgs guard;
-  uint32_t magic;
+};
+
+struct mono_attn : RuntimeBase {
+  mono_attn_config cfg;
+  mono::attn::Mail mail;
 };
 
 static const uint32_t MOE_MAGIC = 0x6d6f6531u;
-static const double TICKS_PER_S = 100e6;  // s_memrealtime runs at 100 MHz
-static const double DEFAULT_DEADLINE_S = 2.0;
-static const double MAX_DEADLINE_S = 3600.0;
+static const uint32_t ATTN_MAGIC = 0x6174746eu;
+
+namespace {
+
+int moe_occupancy(int* n) {
+  HIP_TRY(mono::moe::moe_fp8_occupancy(n));
+  return MONO_OK;
+}
+int attn_occupancy(int* n) {
+  HIP_TRY(mono::attn::attn_occupancy(n));
+  return MONO_OK;
+}
+
+bool live(const RuntimeBase* r, uint32_t magic) { return r && r->magic == magic; }
+
+int guard_set_deadline(RuntimeBase* r, double seconds) {
+  if (!(seconds > 0.0) || seconds > MAX_DEADLINE_S)
+    return fail(MONO_EINVAL, "deadline must be in (0, %.0f] seconds, got %g", MAX_DEADLINE_S, seconds);
+  const double ticks = seconds * TICKS_PER_S;
+  r->guard.deadline_ticks = ticks < 1.0 ? 1u : (uint64_t)ticks;
+  return ok();
+}
+
+int guard_set_fault(RuntimeBase* r, int32_t site) {
+  if (site < -1 || site > 15) return fail(MONO_EINVAL, "fault site must be -1 (none) or a wait site 0..15, got %d", site);
+  r->guard.fault_site = site;
+  return ok();
+}
+
+int guard_read(RuntimeBase* r, int32_t* words) {
+  if (!words) return fail(MONO_EINVAL, "read_errors: words is NULL");
+  if (int rc = check_device(r->device)) return rc;
+  HIP_TRY(hipDeviceSynchronize());
+  HIP_TRY(hipMemcpy(words, r->guard.words, MONO_GUARD_WORDS * sizeof(int32_t), hipMemcpyDeviceToHost));
+  return ok();
+}
+
+int guard_clear(RuntimeBase* r) {
+  if (int rc = check_device(r->device)) return rc;
+  HIP_TRY(hipDeviceSynchronize());
+  HIP_TRY(hipMemset(r->guard.words + mono::G_ERROR, 0, (MONO_GUARD_WORDS - 1) * sizeof(int32_t)));
+  HIP_TRY(hipDeviceSynchronize());
+  return ok();
+}
+
+}  // namespace
 
 extern "C" int mono_abi_version(void) { return MONO_ABI_VERSION; }
 
 extern "C" const char* mono_last_error(void) { return g_error.c_str(); }
+
+// ------------------------------------------------------------------ MoE runtime
 
 extern "C" int mono_moe_create(const mono_moe_config* cfg, mono_moe** out) {
   using namespace mono::moe;
@@ -94,80 +205,43 @@ extern "C" int mono_moe_create(const mono_moe_config* cfg, mono_moe** out) {
   if (int rc = check_device(c.device)) return rc;
   const size_t H = c.hidden, E = c.n_experts, I = c.inter;
   const size_t max_act = (size_t)std::min(c.max_rows * c.top_k, c.n_experts) + 1;
-  size_t off = 0;
-  auto take = [&](size_t bytes) {
-    size_t at = off;
-    off += align256(bytes);
-    return at;
-  };
-  const size_t o_guard = take(mono::G_WORDS * 4);
-  const size_t o_rlog = take((size_t)moe_fp8_router_slices() * MAX_ROWS * E * 8);
-  const size_t o_rsel = take((size_t)MAX_ROWS * 2 * MAX_TOPK * 8);
-  const size_t o_mid = take(max_act * MAX_ROWS * I * 8);
-  const size_t o_ypart = take(max_act * MAX_ROWS * H * 8);
-
-  hipDeviceProp_t prop;
-  HIP_TRY(hipGetDeviceProperties(&prop, c.device));
-  int per_cu = 0;
-  HIP_TRY(moe_fp8_occupancy(&per_cu));
-  if (per_cu < 1)
-    return fail(MONO_ESTATE, "the persistent MoE kernel does not fit on a CU (occupancy %d)", per_cu);
+  Carve cv;
+  const size_t o_guard = cv.take(mono::G_WORDS * 4);
+  const size_t o_rlog = cv.take((size_t)moe_fp8_router_slices() * MAX_ROWS * E * 8);
+  const size_t o_rsel = cv.take((size_t)MAX_ROWS * 2 * MAX_TOPK * 8);
+  const size_t o_mid = cv.take(max_act * MAX_ROWS * I * 8);
+  const size_t o_ypart = cv.take(max_act * MAX_ROWS * H * 8);
   mono_moe* m = new mono_moe();
-  m->cfg = c;
   m->magic = MOE_MAGIC;
-  m->blob_bytes = off;
-  m->grid = prop.multiProcessorCount;
-  hipError_t e = hipMalloc(&m->blob, off);
-  if (e != hipSuccess) {
+  m->cfg = c;
+  if (int rc = m->init(c.device, cv.off, o_guard, moe_occupancy, "MoE")) {
+    (void)m->release();
     delete m;
-    return fail(MONO_ENOMEM, "hipMalloc(%zu) for the MoE mailboxes: %s", off, hipGetErrorString(e));
+    return rc;
   }
-  // tag 0 is never a launch's tag, so zeroed mailboxes read as empty
-  e = hipMemset(m->blob, 0, off);
-  if (e == hipSuccess) e = hipDeviceSynchronize();
-  if (e != hipSuccess) {
-    (void)hipFree(m->blob);
-    delete m;
-    return fail(MONO_EHIP, "clearing the MoE mailboxes: %s", hipGetErrorString(e));
-  }
-  char* b = static_cast<char*>(m->blob);
-  m->mail.guard = reinterpret_cast<uint32_t*>(b + o_guard);
-  m->mail.rlog = reinterpret_cast<uint64_t*>(b + o_rlog);
-  m->mail.rsel = reinterpret_cast<uint64_t*>(b + o_rsel);
-  m->mail.mid = reinterpret_cast<uint64_t*>(b + o_mid);
-  m->mail.ypart = reinterpret_cast<uint64_t*>(b + o_ypart);
-  m->guard.words = m->mail.guard;
-  m->guard.deadline_ticks = (uint64_t)(DEFAULT_DEADLINE_S * TICKS_PER_S);
-  m->guard.fault_site = -1;
+  m->mail.guard = m->guard.words;
+  m->mail.rlog = reinterpret_cast<uint64_t*>(m->at(o_rlog));
+  m->mail.rsel = reinterpret_cast<uint64_t*>(m->at(o_rsel));
+  m->mail.mid = reinterpret_cast<uint64_t*>(m->at(o_mid));
+  m->mail.ypart = reinterpret_cast<uint64_t*>(m->at(o_ypart));
   *out = m;
   return ok();
 }
 
 extern "C" int mono_moe_destroy(mono_moe* m) {
   if (!m) return ok();
-  if (m->magic != MOE_MAGIC) return fail(MONO_ESTATE, "mono_moe_destroy: not a live MoE runtime");
-  m->magic = 0;
-  if (m->blob) {
-    hipError_t e = hipFree(m->blob);
-    m->blob = nullptr;
-    if (e != hipSuccess) {
-      delete m;
-      return fail(MONO_EHIP, "hipFree: %s", hipGetErrorString(e));
-    }
-  }
+  if (!live(m, MOE_MAGIC)) return fail(MONO_ESTATE, "mono_moe_destroy: not a live MoE runtime");
+  const int rc = m->release();
   delete m;
-  return ok();
+  return rc ? rc : ok();
 }
 
 static int check_moe(const mono_moe* m, int rows) {
-  if (!m || m->magic != MOE_MAGIC) return fail(MONO_ESTATE, "not a live MoE runtime");
+  if (!live(m, MOE_MAGIC)) return fail(MONO_ESTATE, "not a live MoE runtime");
   if (rows < 1 || rows > m->cfg.max_rows)
     return fail(MONO_EINVAL, "rows must be in [1, %d] (the runtime's max_rows), got %d", m->cfg.max_rows, rows);
-  return check_device(m->cfg.device);
+  return check_device(m->device);
 }
-
-#define REQUIRE_PTR(p) \
-  if (!(p)) return fail(MONO_EINVAL, "argument %s must be a device pointer, got NULL", #p)
 
 extern "C" int mono_moe_fp8_forward(mono_moe* m, const mono_moe_fp8_args* args, void* stream) {
   using namespace mono::moe;
@@ -190,43 +264,123 @@ extern "C" int mono_moe_fp8_forward(mono_moe* m, const mono_moe_fp8_args* args, 
   return ok();
 }
 
-extern "C" int mono_moe_set_deadline(mono_moe* m, double seconds) {
-  if (!m || m->magic != MOE_MAGIC) return fail(MONO_ESTATE, "not a live MoE runtime");
-  if (!(seconds > 0.0) || seconds > MAX_DEADLINE_S)
-    return fail(MONO_EINVAL, "deadline must be in (0, %.0f] seconds, got %g", MAX_DEADLINE_S, seconds);
-  const double ticks = seconds * TICKS_PER_S;
-  m->guard.deadline_ticks = ticks < 1.0 ? 1u : (uint64_t)ticks;
-  return ok();
-}
-
-extern "C" int mono_moe_set_fault(mono_moe* m, int32_t site) {
-  if (!m || m->magic != MOE_MAGIC) return fail(MONO_ESTATE, "not a live MoE runtime");
-  if (site < -1 || site > 15) return fail(MONO_EINVAL, "fault site must be -1 (none) or a wait site 0..15, got %d", site);
-  m->guard.fault_site = site;
-  return ok();
-}
-
-extern "C" int mono_moe_read_errors(mono_moe* m, int32_t* words) {
-  if (!m || m->magic != MOE_MAGIC) return fail(MONO_ESTATE, "not a live MoE runtime");
-  if (!words) return fail(MONO_EINVAL, "mono_moe_read_errors: words is NULL");
-  if (int rc = check_device(m->cfg.device)) return rc;
-  HIP_TRY(hipDeviceSynchronize());
-  HIP_TRY(hipMemcpy(words, m->mail.guard, MONO_GUARD_WORDS * sizeof(int32_t), hipMemcpyDeviceToHost));
-  return ok();
-}
-
-extern "C" int mono_moe_clear_errors(mono_moe* m) {
-  if (!m || m->magic != MOE_MAGIC) return fail(MONO_ESTATE, "not a live MoE runtime");
-  if (int rc = check_device(m->cfg.device)) return rc;
-  HIP_TRY(hipDeviceSynchronize());
-  HIP_TRY(hipMemset(m->mail.guard + mono::G_ERROR, 0, (MONO_GUARD_WORDS - 1) * sizeof(int32_t)));
-  HIP_TRY(hipDeviceSynchronize());
-  return ok();
-}
-
 extern "C" int mono_moe_mxfp4_forward(mono_moe* m, const mono_moe_mxfp4_args* args, void* stream) {
   (void)m;
   (void)args;
   (void)stream;
   return fail(MONO_EINVAL, "mono_moe_mxfp4_forward: not built yet");
+}
+
+extern "C" int mono_moe_set_deadline(mono_moe* m, double seconds) {
+  if (!live(m, MOE_MAGIC)) return fail(MONO_ESTATE, "not a live MoE runtime");
+  return guard_set_deadline(m, seconds);
+}
+
+extern "C" int mono_moe_set_fault(mono_moe* m, int32_t site) {
+  if (!live(m, MOE_MAGIC)) return fail(MONO_ESTATE, "not a live MoE runtime");
+  return guard_set_fault(m, site);
+}
+
+extern "C" int mono_moe_read_errors(mono_moe* m, int32_t* words) {
+  if (!live(m, MOE_MAGIC)) return fail(MONO_ESTATE, "not a live MoE runtime");
+  return guard_read(m, words);
+}
+
+extern "C" int mono_moe_clear_errors(mono_moe* m) {
+  if (!live(m, MOE_MAGIC)) return fail(MONO_ESTATE, "not a live MoE runtime");
+  return guard_clear(m);
+}
+
+// ------------------------------------------------------------------ attention runtime
+
+extern "C" int mono_attn_create(const mono_attn_config* cfg, mono_attn** out) {
+  using namespace mono::attn;
+  if (!cfg || !out) return fail(MONO_EINVAL, "mono_attn_create: cfg and out must be non-NULL");
+  *out = nullptr;
+  const mono_attn_config& c = *cfg;
+  if (c.max_rows < 1 || c.max_rows > MAX_ROWS)
+    return fail(MONO_EINVAL, "max_rows must be in [1, %d], got %d", MAX_ROWS, c.max_rows);
+  if (c.max_ctx < CHUNK || c.max_ctx > MAX_CTX || c.max_ctx % CHUNK)
+    return fail(MONO_EINVAL, "max_ctx must be a multiple of %d in [%d, %d], got %d", CHUNK, CHUNK, MAX_CTX, c.max_ctx);
+  if (!(c.softmax_scale > 0.f)) return fail(MONO_EINVAL, "softmax_scale must be positive, got %g", c.softmax_scale);
+  if (int rc = check_device(c.device)) return rc;
+  const size_t R = c.max_rows;
+  Carve cv;
+  const size_t o_guard = cv.take(mono::G_WORDS * 4);
+  const size_t o_score = cv.take(R * c.max_ctx * 8);
+  const size_t o_sel = cv.take(R * TOPK * 8);
+  const size_t o_part = cv.take(R * SPLITS * NH * DV * 8);
+  const size_t o_ml = cv.take(R * SPLITS * NH * 2 * 8);
+  mono_attn* a = new mono_attn();
+  a->magic = ATTN_MAGIC;
+  a->cfg = c;
+  if (int rc = a->init(c.device, cv.off, o_guard, attn_occupancy, "attention")) {
+    (void)a->release();
+    delete a;
+    return rc;
+  }
+  a->mail.guard = a->guard.words;
+  a->mail.score = reinterpret_cast<uint64_t*>(a->at(o_score));
+  a->mail.sel = reinterpret_cast<uint64_t*>(a->at(o_sel));
+  a->mail.part = reinterpret_cast<uint64_t*>(a->at(o_part));
+  a->mail.ml = reinterpret_cast<uint64_t*>(a->at(o_ml));
+  a->mail.max_ctx = c.max_ctx;
+  *out = a;
+  return ok();
+}
+
+extern "C" int mono_attn_destroy(mono_attn* a) {
+  if (!a) return ok();
+  if (!live(a, ATTN_MAGIC)) return fail(MONO_ESTATE, "mono_attn_destroy: not a live attention runtime");
+  const int rc = a->release();
+  delete a;
+  return rc ? rc : ok();
+}
+
+extern "C" int mono_attn_forward(mono_attn* a, const mono_attn_args* args, void* stream) {
+  using namespace mono::attn;
+  if (!args) return fail(MONO_EINVAL, "mono_attn_forward: args is NULL");
+  if (!live(a, ATTN_MAGIC)) return fail(MONO_ESTATE, "not a live attention runtime");
+  if (args->rows < 1 || args->rows > a->cfg.max_rows)
+    return fail(MONO_EINVAL, "rows must be in [1, %d] (the runtime's max_rows), got %d", a->cfg.max_rows, args->rows);
+  if (args->pt_stride < a->cfg.max_ctx / PAGE)
+    return fail(MONO_EINVAL, "pt_stride must cover max_ctx / 64 = %d pages, got %d", a->cfg.max_ctx / PAGE,
+                args->pt_stride);
+  if (args->n_pages < 1) return fail(MONO_EINVAL, "n_pages must be positive, got %d", args->n_pages);
+  if (int rc = check_device(a->device)) return rc;
+  REQUIRE_PTR(args->iq);
+  REQUIRE_PTR(args->iqs);
+  REQUIRE_PTR(args->iw);
+  REQUIRE_PTR(args->ikv);
+  REQUIRE_PTR(args->iks);
+  REQUIRE_PTR(args->q);
+  REQUIRE_PTR(args->kv);
+  REQUIRE_PTR(args->kv_scale);
+  REQUIRE_PTR(args->page_table);
+  REQUIRE_PTR(args->seq_lens);
+  REQUIRE_PTR(args->out);
+  AttnArgs g(*args, a->cfg.softmax_scale);
+  hipError_t e = attn_forward(g, a->grid, a->mail, a->guard, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(MONO_EHIP, "launching the sparse attention: %s", hipGetErrorString(e));
+  return ok();
+}
+
+extern "C" int mono_attn_set_deadline(mono_attn* a, double seconds) {
+  if (!live(a, ATTN_MAGIC)) return fail(MONO_ESTATE, "not a live attention runtime");
+  return guard_set_deadline(a, seconds);
+}
+
+extern "C" int mono_attn_set_fault(mono_attn* a, int32_t site) {
+  if (!live(a, ATTN_MAGIC)) return fail(MONO_ESTATE, "not a live attention runtime");
+  return guard_set_fault(a, site);
+}
+
+extern "C" int mono_attn_read_errors(mono_attn* a, int32_t* words) {
+  if (!live(a, ATTN_MAGIC)) return fail(MONO_ESTATE, "not a live attention runtime");
+  return guard_read(a, words);
+}
+
+extern "C" int mono_attn_clear_errors(mono_attn* a) {
+  if (!live(a, ATTN_MAGIC)) return fail(MONO_ESTATE, "not a live attention runtime");
+  return guard_clear(a);
 }

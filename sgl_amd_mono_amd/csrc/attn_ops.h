@@ -1,0 +1,44 @@
+// Host-side declarations of the sparse-attention phase (internal to the library).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "mono.h"
+#include "sync.h"
+
+namespace mono {
+namespace attn {
+
+constexpr int IH = 64;          // index heads
+constexpr int ID = 128;         // index head dim (4 E2M1 chunks of 32)
+constexpr int NH = 32;          // attention heads of this GPU's share
+constexpr int DQK = 576;        // latent 512 + RoPE 64
+constexpr int DV = 512;         // latent dims attended as values
+constexpr int PAGE = 64;        // tokens a cache page
+constexpr int TOPK = 2048;      // tokens a row attends
+constexpr int MAX_ROWS = 64;
+constexpr int MAX_CTX = 32768;  // keys a row the one-workgroup top-k holds in LDS
+constexpr int CHUNK = 1024;     // keys a score task
+constexpr int SPLITS = 8;       // attention splits a row
+constexpr int SPLIT = TOPK / SPLITS;
+
+// Mailboxes of one attention runtime (tagged 64-bit words, see sync.h).
+struct Mail {
+  uint64_t* score;  // [max_rows][max_ctx]           index scores, f32
+  uint64_t* sel;    // [max_rows][TOPK]               selected slots, i32
+  uint64_t* part;   // [max_rows][SPLITS][NH][DV]     a split's unnormalised output, f32
+  uint64_t* ml;     // [max_rows][SPLITS][NH][2]      a split's max logit and sum
+  uint32_t* guard;  // [G_WORDS]
+  int max_ctx;
+};
+
+struct AttnArgs : mono_attn_args {
+  float softmax_scale;
+  AttnArgs(const mono_attn_args& a, float sc) : mono_attn_args(a), softmax_scale(sc) {}
+};
+
+hipError_t attn_occupancy(int* blocks_per_cu);
+hipError_t attn_forward(const AttnArgs& a, int grid, const Mail& mail, const GuardArgs& guard, hipStream_t st);
+
+}  // namespace attn
+}  // namespace mono

@@ -15,6 +15,7 @@ from dataclasses import dataclass
 import torch
 
 from . import _lib
+from .runtime import Runtime, need
 
 
 @dataclass(frozen=True)
@@ -58,33 +59,20 @@ class Mxfp4MoeWeights:
     s2: torch.Tensor  # uint8 [E+1, H, I/32]
 
 
-def need(t: torch.Tensor, name: str, shape: tuple, dtypes, device: torch.device) -> None:
-    """Raise ValueError naming the tensor unless it has this shape / dtype and is a
-    contiguous tensor on ``device`` (the checks of glm53/gfx950/runner.py:250-273)."""
-    if not isinstance(t, torch.Tensor):
-        raise ValueError(f"{name}: expected a tensor, got {type(t).__name__}")
-    dtypes = dtypes if isinstance(dtypes, tuple) else (dtypes,)
-    if tuple(t.shape) != tuple(shape):
-        raise ValueError(f"{name}: expected shape {tuple(shape)}, got {tuple(t.shape)}")
-    if t.dtype not in dtypes:
-        raise ValueError(f"{name}: expected dtype {' or '.join(map(str, dtypes))}, got {t.dtype}")
-    if t.device != device:
-        raise ValueError(f"{name}: expected device {device}, got {t.device}")
-    if not t.is_contiguous():
-        raise ValueError(f"{name}: expected a contiguous tensor (strides {t.stride()})")
-
-
 FP8_TYPES = (torch.float8_e4m3fn, torch.uint8)
 
 
-class MoeRuntime:
+class MoeRuntime(Runtime):
     """The C library's MoE handle for one geometry and a widest step ``max_rows``."""
 
+    PREFIX = "mono_moe"
+    SITES = _lib.MOE_SITES
+    KIND = "MoE"
+
     def __init__(self, geo: MoeGeometry, max_rows: int, device=None):
+        super().__init__(device)
         self.geo = geo
-        self.device = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
-        if self.device.type != "cuda":
-            raise ValueError(f"MoeRuntime needs a GPU device, got {self.device}")
+        self.max_rows = max_rows
         cfg = _lib.MoeConfig(
             device=self.device.index, max_rows=max_rows, hidden=geo.hidden, n_experts=geo.n_experts,
             top_k=geo.top_k, inter=geo.inter,
@@ -92,58 +80,7 @@ class MoeRuntime:
             router=_lib.ROUTER_SIGMOID_BIAS if geo.router == "sigmoid_bias" else _lib.ROUTER_SOFTMAX,
             route_scale=geo.route_scale, eps=geo.eps,
         )  # fmt: skip
-        self.max_rows = max_rows
-        h = C.c_void_p()
-        with torch.cuda.device(self.device):
-            _lib.check(_lib.lib().mono_moe_create(C.byref(cfg), C.byref(h)))
-        self._h = h
-
-    def close(self) -> None:
-        if getattr(self, "_h", None) is not None and self._h.value:
-            _lib.check(_lib.lib().mono_moe_destroy(self._h))
-            self._h = C.c_void_p()
-
-    def __del__(self):
-        try:
-            self.close()
-        except Exception:
-            pass
-
-    def _stream(self) -> int:
-        return torch.cuda.current_stream(self.device).cuda_stream
-
-    # ---------------------------------------------------------------- guard
-    def set_deadline(self, seconds: float) -> None:
-        """Deadline of every inter-workgroup wait (Glm53Runtime.set_deadline,
-        glm53/gfx950/runner.py:197-204)."""
-        _lib.check(_lib.lib().mono_moe_set_deadline(self._h, float(seconds)))
-
-    def set_fault(self, site: int) -> None:
-        """Tests of the fail-stop path: wait ``site`` never sees its data (-1: off)."""
-        _lib.check(_lib.lib().mono_moe_set_fault(self._h, int(site)))
-
-    def error_words(self) -> list[int]:
-        """The guard words (synchronises): [tickets, 1 + failed wait site or 0, failing
-        launch tag, failing workgroup]."""
-        words = (C.c_int32 * _lib.GUARD_WORDS)()
-        with torch.cuda.device(self.device):
-            _lib.check(_lib.lib().mono_moe_read_errors(self._h, words))
-        return list(words)
-
-    def check_errors(self) -> None:
-        """Raise MonoError if a launch of this runtime failed a wait (fail-stop)."""
-        w = self.error_words()
-        if w[1]:
-            site = w[1] - 1
-            raise _lib.MonoError(
-                _lib.MONO_ESTATE,
-                f"MoE launch (tag {w[2]}) stopped: wait '{_lib.MOE_SITES.get(site, site)}' passed its "
-                f"deadline in workgroup {w[3]}; the runtime refuses launches until clear_errors()",
-            )
-
-    def clear_errors(self) -> None:
-        with torch.cuda.device(self.device):
-            _lib.check(_lib.lib().mono_moe_clear_errors(self._h))
+        self._create(cfg)
 
     def forward_fp8(self, a: torch.Tensor, w: Fp8MoeWeights, out: torch.Tensor | None = None,
                     debug: bool = False):

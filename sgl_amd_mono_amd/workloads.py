@@ -83,3 +83,39 @@ def toy_moe(seed: int = 0, rows: int = 4, hidden: int = 1024, n_experts: int = 8
         w_up=(torch.randn(n_experts, inter, hidden) * 0.02).to(torch.bfloat16),
         w_down=(torch.randn(n_experts, hidden, inter) * 0.02).to(torch.bfloat16),
     )
+
+
+def attn_case(ctx_lens, device, seed: int = 0, max_ctx: int = 32768, spare_pages: int = 3):
+    """BASELINE config 3 inputs: ``len(ctx_lens)`` rows, each an independent request of
+    ``ctx_lens[s]`` keys whose pages are scattered over SGLang-layout caches
+    (test/kernels/test_deepseek_v41_k2i.py:103-130 ``fp4_case``): index keys are uniform
+    random E2M1 bytes with E8M0 scales in [123, 130), index queries likewise, head
+    weights ~N(0, 0.05) bf16, the MLA cache E4M3 of N(0, 1) samples with per-token
+    scales ~U(0.5, 2), q ~N(0, 1) bf16. Returns (AttnStep, AttnCaches)."""
+    from .attn import DQK, IH, ID, NH, PAGE, AttnCaches, AttnStep
+
+    g = _gen(device, seed)
+    S = len(ctx_lens)
+    ppr = max_ctx // PAGE
+    used = [-(-int(n) // PAGE) for n in ctx_lens]
+    pages = sum(used) + spare_pages
+    u8 = dict(generator=g, device=device, dtype=torch.uint8)
+    ikv = torch.randint(0, 256, (pages, 4, PAGE, 16), **u8)
+    iks = torch.randint(123, 130, (pages, 4, PAGE), **u8)
+    kv = fp8_codes((pages * PAGE, DQK), g, device)
+    kv_scale = torch.rand(pages * PAGE, generator=g, device=device) * 1.5 + 0.5
+    perm = torch.randperm(pages, generator=g, device=device).to(torch.int32)
+    table = torch.zeros(S, ppr, dtype=torch.int32, device=device)
+    at = 0
+    for s, u in enumerate(used):
+        table[s, :u] = perm[at:at + u]
+        at += u
+    step = AttnStep(
+        iq=torch.randint(0, 256, (S, IH, ID // 2), **u8),
+        iqs=torch.randint(123, 130, (S, IH, ID // 32), **u8),
+        iw=(torch.randn(S, IH, generator=g, device=device) * 0.05).to(torch.bfloat16),
+        q=torch.randn(S, NH, DQK, generator=g, device=device).to(torch.bfloat16),
+        page_table=table,
+        seq_lens=torch.tensor([int(n) for n in ctx_lens], dtype=torch.int32, device=device),
+    )
+    return step, AttnCaches(ikv=ikv, iks=iks, kv=kv, kv_scale=kv_scale)

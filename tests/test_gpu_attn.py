@@ -1,0 +1,123 @@
+"""Sparse-attention phase on the GPU against the CPU oracle.
+
+* Index scores against the oracle's f32 restatement of the FP4 indexer (within f32
+  summation-order error).
+* The exact top-2048 bit-exact: the oracle's rule (score desc, position asc, mapped
+  through the page table) applied to the device's own scores must give exactly the
+  device's slots, in order.
+* The attention output against the oracle's sparse MLA over the device's selection:
+  bf16 within the (atol 2e-2, rtol 1e-2) pair elementwise and 1e-2 relative in norm.
+Rows mirror the reference's decode positions (test/kernels/glm53/check_layer.py:45-47)
+below and above 2048 keys, plus a full 32768-key context.
+"""
+
+import pytest
+import torch
+
+from oracle import attention as oatt
+from sgl_amd_mono_amd import workloads
+from sgl_amd_mono_amd.attn import AttnRuntime
+
+pytestmark = pytest.mark.gpu
+
+OUT_MAX_ABS, OUT_REL = 2e-2, 1e-2
+SCORE_REL = 1e-4  # of the row's largest score magnitude: f32 summation order only
+
+CTX_8 = [8447, 1500, 5000, 300, 32768, 2047, 2048, 9000]
+
+
+@pytest.fixture(scope="module")
+def rt(gpu_device):
+    r = AttnRuntime(64, 32768, device=gpu_device)
+    yield r
+    r.close()
+
+
+def _check(rt, ctx, seed, gpu_device):
+    print(f"[attn] rows={len(ctx)} seed={seed} ctx={ctx[:8]}...", flush=True)
+    step, caches = workloads.attn_case(ctx, gpu_device, seed=seed)
+    out, dbg = rt.forward(step, caches, debug=True)
+    torch.cuda.synchronize()
+    rt.check_errors()
+    c = {k: v.cpu() for k, v in vars(caches).items()}
+    st = {k: v.cpu() for k, v in vars(step).items()}
+    scores, sel = dbg["scores"].cpu(), dbg["topk"].cpu()
+    ref_scores = oatt.index_scores(st["iq"], st["iqs"], st["iw"], c["ikv"], c["iks"], st["page_table"],
+                                   st["seq_lens"], rt.max_ctx)
+    for s, n in enumerate(ctx):
+        d = (scores[s, :n] - ref_scores[s, :n]).abs().max().item()
+        scale = ref_scores[s, :n].abs().max().item()
+        assert d <= SCORE_REL * scale + 1e-6, (s, d, scale)
+    want_sel = oatt.select_topk(scores, st["seq_lens"], st["page_table"])
+    assert torch.equal(sel, want_sel), [s for s in range(len(ctx)) if not torch.equal(sel[s], want_sel[s])]
+    ref = oatt.sparse_mla(st["q"], c["kv"], c["kv_scale"], sel)
+    got = out.cpu().float()
+    err = (got - ref).abs()
+    rel = ((got - ref).norm() / ref.norm()).item()
+    print(f"[attn] out max-abs {err.max().item():.3e} (|ref| max {ref.abs().max().item():.2f}) "
+          f"norm-rel {rel:.3e}", flush=True)
+    # the bound as an (atol, rtol) pair, elementwise: |a - b| <= 2e-2 + 1e-2 |b|
+    assert bool((err <= OUT_MAX_ABS + OUT_REL * ref.abs()).all()) and rel <= OUT_REL
+    return out, sel
+
+
+def test_attn_8_rows_matches_oracle(rt, gpu_device):
+    _check(rt, CTX_8, 0, gpu_device)
+
+
+def test_attn_1_row_full_context(rt, gpu_device):
+    _check(rt, [32768], 1, gpu_device)
+
+
+def test_attn_48_rows_mixed_contexts(rt, gpu_device):
+    g = torch.Generator().manual_seed(2)
+    ctx = torch.randint(1, 12000, (48,), generator=g).tolist()
+    ctx[0], ctx[1], ctx[2] = 32768, 2048, 2049
+    _check(rt, ctx, 2, gpu_device)
+
+
+def test_attn_ties_take_lowest_positions(rt, gpu_device):
+    """An index query of all-zero codes makes every score 0: the selection must be the
+    first 2048 positions of the row (lowest-position ties, glm53/check.py:100-117)."""
+    step, caches = workloads.attn_case([5000, 3000], gpu_device, seed=3)
+    step.iq.zero_()
+    out, dbg = rt.forward(step, caches, debug=True)
+    torch.cuda.synchronize()
+    rt.check_errors()
+    pt = step.page_table.cpu()
+    pos = torch.arange(2048)
+    for s in range(2):
+        want = (pt[s, pos // 64].long() * 64 + pos % 64).to(torch.int32)
+        assert torch.equal(dbg["topk"][s].cpu(), want)
+
+
+def test_attn_repeat_is_bitwise(rt, gpu_device):
+    step, caches = workloads.attn_case(CTX_8, gpu_device, seed=4)
+    a, da = rt.forward(step, caches, debug=True)
+    b, db = rt.forward(step, caches, debug=True)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b) and torch.equal(da["topk"], db["topk"]) and torch.equal(da["scores"], db["scores"])
+
+
+def test_attn_fail_stop_each_site(rt, gpu_device):
+    step, caches = workloads.attn_case([5000, 1000, 3000], gpu_device, seed=5)
+    good = rt.forward(step, caches)
+    torch.cuda.synchronize()
+    for site in (0, 1, 2):
+        print(f"[attn fault] site {site}", flush=True)
+        rt.set_fault(site)
+        rt.forward(step, caches)
+        assert rt.error_words()[1] == site + 1
+        rt.set_fault(-1)
+        rt.clear_errors()
+        again = rt.forward(step, caches)
+        torch.cuda.synchronize()
+        rt.check_errors()
+        assert torch.equal(again, good)
+
+
+def test_attn_rejects_bad_arguments(rt, gpu_device):
+    step, caches = workloads.attn_case([100], gpu_device, seed=6)
+    step.q = step.q.float()
+    with pytest.raises(ValueError, match="q"):
+        rt.forward(step, caches)
