@@ -7,6 +7,8 @@ whose inputs and weights are already resident in HBM:
 * ``moe_fp8`` (default; BASELINE config 2 at 8 rows): the FP8 routed + shared MoE half
   of the decoder layer (RMSNorm, router, top-8, W8A8 experts, residual) through
   ``mono_moe_fp8_forward``.
+* ``attn``: FP4 index scores over ``--ctx`` keys a row, the exact
+  top-2048 and sparse MLA decode, through ``mono_attn_forward``.
 
 Weight sets and activation batches rotate from step to step so every step streams its
 experts from HBM rather than from the 256 MB Infinity Cache. The timed region is K
@@ -197,7 +199,101 @@ def cpu_baseline_moe_fp8(args, w, acts, G):
     )
 
 
-WORKLOADS = {"moe_fp8": bench_moe_fp8}
+# ------------------------------------------------------------------ sparse attention (config 3)
+def attn_step_bytes(ctx_lens) -> int:
+    """Algorithmic bytes of one attention step: every index key of every row (16 B of
+    E2M1 + 1 E8M0 byte per 32 dims = 68 B a key), the selected cache rows (576 B of E4M3 +
+    a 4-byte scale), the row's queries (FP4 index query + scales + weights, bf16 q), its
+    page-table entries, and the bf16 output."""
+    total = 0
+    for n in ctx_lens:
+        sel = min(n, 2048)
+        total += n * 68 + sel * 580 + (64 * 64 + 64 * 4 + 64 * 2) + 32 * 576 * 2 + (-(-n // 64)) * 4 + 32 * 512 * 2
+    return total
+
+
+def bench_attn(args, dev):
+    import torch
+
+    from sgl_amd_mono_amd import workloads
+    from sgl_amd_mono_amd.attn import AttnRuntime
+
+    S, ctx = args.rows, args.ctx
+    lens = [ctx] * S
+    step_b = attn_step_bytes(lens)
+    sets = max(args.sets, -(-1_500_000_000 // step_b))  # > 1.5 GB streamed before a set repeats
+    log(f"generating {sets} attention cases of {S} rows x {ctx} keys ({step_b / 1e6:.1f} MB a step)")
+    cases = [workloads.attn_case(lens, dev, seed=3000 + i) for i in range(sets)]
+    rt = AttnRuntime(S, max(ctx, 1024), device=dev)
+    out = torch.empty(S, 32, 512, dtype=torch.bfloat16, device=dev)
+    for i in range(args.warmup):
+        st, ca = cases[i % sets]
+        rt.forward(st, ca, out=out)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
+    ev[0].record(stream)
+    for i in range(args.steps):
+        st, ca = cases[(args.warmup + i) % sets]
+        rt.forward(st, ca, out=out)
+        ev[i + 1].record(stream)
+    torch.cuda.synchronize()
+    rt.check_errors()
+    per = [ev[i].elapsed_time(ev[i + 1]) * 1e3 for i in range(args.steps)]
+    us = ev[0].elapsed_time(ev[-1]) * 1e3 / args.steps
+    achieved = step_b / (statistics.fmean(per) * 1e-6) / 1e9
+    log(f"{us:.2f} us/step (median {statistics.median(per):.2f}), {achieved:.0f} GB/s")
+    cpu = None
+    if args.cpu_seconds > 0:
+        cpu = cpu_baseline_attn(args, cases[0])
+    rt.close()
+    return dict(
+        value=us, unit="us", ms_per_step=us / 1e3, dtype="fp4_e2m1 scores, fp8_e4m3 kv (bf16 MFMA, f32 accumulate)",
+        config=dict(workload="BASELINE config 3: sparse MLA decode with FP4 indexer top-2048", rows=S,
+                    context=ctx, heads=32, index_heads=64, topk=2048, cache_sets=sets),
+        extra=dict(us_median=statistics.median(per), us_min=min(per), us_max=max(per),
+                   rows_per_s=S / (us * 1e-6), algorithmic_bytes=step_b),
+        roofline=dict(bound="hbm", achieved=achieved, peak=HBM_PEAK_GBS, unit="GB/s", frac=achieved / HBM_PEAK_GBS,
+                      traffic=None, kernel="k_attn (one persistent launch: score, top-k, split, merge)",
+                      bytes_per_launch=step_b, avg_launch_us=statistics.fmean(per)),
+        cpu_baseline=cpu,
+    )
+
+
+def cpu_baseline_attn(args, case):
+    """The CPU oracle's attention step (index scores, exact top-2048, sparse MLA)."""
+    import torch
+
+    from oracle import attention as oatt
+
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    st, ca = case
+    c = {k: v.cpu() for k, v in vars(ca).items()}
+    s = {k: v.cpu() for k, v in vars(st).items()}
+
+    def one():
+        sc = oatt.index_scores(s["iq"], s["iqs"], s["iw"], c["ikv"], c["iks"], s["page_table"], s["seq_lens"],
+                               args.ctx)
+        sel = oatt.select_topk(sc, s["seq_lens"], s["page_table"])
+        return oatt.sparse_mla(s["q"], c["kv"], c["kv_scale"], sel)
+
+    one()
+    times = []
+    t_end = time.perf_counter() + args.cpu_seconds
+    while (len(times) < 3 or time.perf_counter() < t_end) and len(times) < 20:
+        t = time.perf_counter()
+        one()
+        times.append((time.perf_counter() - t) * 1e6)
+    med = statistics.median(times)
+    log(f"cpu oracle: {med:.0f} us/step median of {len(times)} on {threads} threads")
+    return dict(value=med, unit="us", cores=torch.get_num_threads(), kind="port",
+                sample=(f"oracle.attention index_scores + select_topk + sparse_mla (f32 torch restatement) on "
+                        f"{len(times)} steps of {args.rows} rows x {args.ctx} keys, one cache set; median; "
+                        f"host '{cpu_model()}', os.cpu_count()={os.cpu_count()}"))
+
+
+WORKLOADS = {"moe_fp8": bench_moe_fp8, "attn": bench_attn}
 
 
 def main() -> int:
@@ -209,6 +305,7 @@ def main() -> int:
     ap.add_argument("--workload", choices=sorted(WORKLOADS), default="moe_fp8")
     ap.add_argument("--sets", type=int, default=2, help="weight sets rotated over the steps")
     ap.add_argument("--batches", type=int, default=16, help="activation batches rotated")
+    ap.add_argument("--ctx", type=int, default=32768, help="keys a row (attn workload)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="wall budget of the CPU baseline sample (0 skips it)")
     args = ap.parse_args()

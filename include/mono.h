@@ -190,12 +190,16 @@ typedef struct {
   int32_t rows;
   float* scores;             /* optional f32 [rows, max_ctx] index scores */
   int32_t* topk;             /* optional i32 [rows, 2048] selected slots, -1 past the count */
+  int64_t* timeline;         /* optional i64 [tasks, 4] per task of the launch: start,
+                                inputs-ready and end s_memrealtime ticks (100 MHz), and
+                                workgroup << 8 | kind (the reference's timeline stamps,
+                                common/stamps.py:24-33) */
 } mono_attn_args;
 
 int mono_attn_forward(mono_attn* attn, const mono_attn_args* args, void* stream);
 
 /* Guard controls of an attention runtime (as the MoE runtime's). Wait sites: 0 index
- * scores, 1 selected slots, 2 split partials. */
+ * scores, 1 selected slots, 2 split partials, 3 top-k team histograms and counts. */
 int mono_attn_set_deadline(mono_attn* attn, double seconds);
 int mono_attn_read_errors(mono_attn* attn, int32_t* words);
 int mono_attn_clear_errors(mono_attn* attn);

@@ -52,6 +52,7 @@ class AttnArgs(C.Structure):
         ("iq", _VP), ("iqs", _VP), ("iw", _VP), ("ikv", _VP), ("iks", _VP), ("q", _VP), ("kv", _VP),
         ("kv_scale", _VP), ("page_table", _VP), ("seq_lens", _VP), ("pt_stride", _I32),
         ("n_pages", _I32), ("out", _VP), ("rows", _I32), ("scores", _VP), ("topk", _VP),
+        ("timeline", _VP),
     ]
 
 
@@ -78,7 +79,7 @@ SIGNATURES = {
 GUARD_WORDS = 4
 # wait sites of the launches (guard word 1 = site + 1)
 MOE_SITES = {0: "router logits", 1: "route picks", 2: "expert mid activations", 3: "expert outputs"}
-ATTN_SITES = {0: "index scores", 1: "selected slots", 2: "split partials"}
+ATTN_SITES = {0: "index scores", 1: "selected slots", 2: "split partials", 3: "top-k team"}
 
 _lock = threading.Lock()
 _lib = None

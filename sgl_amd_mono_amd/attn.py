@@ -61,10 +61,18 @@ class AttnRuntime(Runtime):
         self._create(_lib.AttnConfig(device=self.device.index, max_rows=max_rows, max_ctx=max_ctx,
                                      softmax_scale=softmax_scale))
 
+    def n_tasks(self, rows: int) -> int:
+        """Tasks of one launch over ``rows`` rows (the timeline's length)."""
+        n_score = -(-rows * (self.max_ctx // 1024) // 16) * 16  # padded to whole top-k teams
+        return n_score + rows * 16 + rows * 16 + rows * (NH // 2)
+
     def forward(self, step: AttnStep, caches: AttnCaches, out: torch.Tensor | None = None,
-                debug: bool = False):
+                debug: bool = False, timeline: torch.Tensor | None = None):
         """o_lat [rows, 32, 512] bf16 for one decode step. ``debug`` also returns the
-        index scores [rows, max_ctx] and the selected slots [rows, 2048]."""
+        index scores [rows, max_ctx] and the selected slots [rows, 2048]. ``timeline``
+        (int64 [n_tasks(rows), 4]) receives each task's start, inputs-ready and end
+        s_memrealtime ticks (100 MHz) and workgroup << 8 | kind (0 score, 1 top-k,
+        2 split, 3 merge)."""
         dev = self.device
         S = step.q.shape[0] if step.q.dim() == 3 else -1
         if not 1 <= S <= self.max_rows:
@@ -94,7 +102,9 @@ class AttnRuntime(Runtime):
             iq=P(step.iq), iqs=P(step.iqs), iw=P(step.iw), ikv=P(caches.ikv), iks=P(caches.iks),
             q=P(step.q), kv=P(caches.kv), kv_scale=P(caches.kv_scale), page_table=P(step.page_table),
             seq_lens=P(step.seq_lens), pt_stride=step.page_table.shape[1], n_pages=pages, out=P(out),
-            rows=S, scores=P(dbg.get("scores")), topk=P(dbg.get("topk")),
+            rows=S, scores=P(dbg.get("scores")), topk=P(dbg.get("topk")), timeline=P(timeline),
         )  # fmt: skip
+        if timeline is not None:
+            need(timeline, "timeline", (self.n_tasks(S), 4), torch.int64, dev)
         _lib.check(_lib.lib().mono_attn_forward(self._h, C.byref(args), self._stream()))
         return (out, dbg) if debug else out

@@ -309,6 +309,8 @@ extern "C" int mono_attn_create(const mono_attn_config* cfg, mono_attn** out) {
   const size_t o_guard = cv.take(mono::G_WORDS * 4);
   const size_t o_score = cv.take(R * c.max_ctx * 8);
   const size_t o_sel = cv.take(R * TOPK * 8);
+  const size_t o_hist = cv.take(R * PASSES * TEAM * 256 * 8);
+  const size_t o_cnt = cv.take(R * TEAM * 2 * 8);
   const size_t o_part = cv.take(R * SPLITS * NH * DV * 8);
   const size_t o_ml = cv.take(R * SPLITS * NH * 2 * 8);
   mono_attn* a = new mono_attn();
@@ -319,9 +321,16 @@ extern "C" int mono_attn_create(const mono_attn_config* cfg, mono_attn** out) {
     delete a;
     return rc;
   }
+  if (a->grid % TEAM) {  // top-k teams must not straddle a round of the task list
+    (void)a->release();
+    delete a;
+    return fail(MONO_ESTATE, "the attention launch needs a CU count divisible by %d, got %d", TEAM, a->grid);
+  }
   a->mail.guard = a->guard.words;
   a->mail.score = reinterpret_cast<uint64_t*>(a->at(o_score));
   a->mail.sel = reinterpret_cast<uint64_t*>(a->at(o_sel));
+  a->mail.hist = reinterpret_cast<uint64_t*>(a->at(o_hist));
+  a->mail.cnt = reinterpret_cast<uint64_t*>(a->at(o_cnt));
   a->mail.part = reinterpret_cast<uint64_t*>(a->at(o_part));
   a->mail.ml = reinterpret_cast<uint64_t*>(a->at(o_ml));
   a->mail.max_ctx = c.max_ctx;

@@ -5,24 +5,28 @@
 // top-2048 (indexer.py:604-802, glm53/gfx950/kernel.py:3000-3636), the sparse MLA
 // split (kernel.py:3638-3973) and the split merge (kernel.py:3975-4123).
 //
-// Tasks, dealt round-robin over the workgroups in this order (a workgroup only ever
-// waits on tasks that come earlier in every workgroup's list, so the launch cannot
-// deadlock while all workgroups are resident; every wait is guarded, sync.h):
+// Tasks, dealt round-robin over the workgroups in this order. A workgroup waits only on
+// tasks earlier in the list or on its own top-k team, whose members share one round
+// of the deal (teams never straddle a round), so the launch cannot deadlock while all
+// workgroups are resident; every wait is guarded (sync.h):
 //   score  (row, 1024 keys): 8 waves x 128 keys. The row's FP4 query (64 heads x 128
 //          dims, E2M1 + E8M0 per 32) is the A operand and 16 keys of SGLang's FP4 index
 //          plane the B operand of v_mfma_scale_f32_16x16x128_f8f6f4 with FP4 formats:
 //          the plane's E8M0 bytes are the MFMA's per-lane B scales as they lie (a
 //          lane's dword holds its key's scale for the page's four 16-key tiles).
 //          score = sum_h w_h relu(q_h . k) -> mailbox score
-//   topk   (row): the row's scores as order-preserving u32 keys in LDS, an MSB-first
-//          8-bit radix select of the 2048th key, then a stable compaction: every key
-//          above it and the lowest positions equal to it, ascending -> cache slots
+//   topk   (row, member of a team of 16): the row's scores as order-preserving u32
+//          keys, 2048 a member; an MSB-first 8-bit radix select of the 2048th largest
+//          key, each digit from the sum of the members' histograms (mailbox hist; a
+//          wave's most common digits go in as one atomic); then a stable compaction
+//          from the members' counts (mailbox cnt): every key above it and the lowest
+//          positions equal to it, ascending -> cache slots
 //          (page_table[p / 64] * 64 + p % 64) -> mailbox sel (glm53/check.py:100-117)
-//   split  (row, 256 selected tokens): 4 sub-tiles of 64 tokens gathered from the FP8
-//          cache into LDS (row-major for q.k, transposed latent for p.v), bf16 MFMA
-//          16x16x32 with the FP8 values widened exactly, the per-token scale folded
-//          into the logit and the probability, online softmax -> mailboxes part, ml
-//   merge  (row, 4 heads): out = sum_j e^(m_j - M) acc_j / sum_j e^(m_j - M) l_j, bf16
+//   split  (row, 128 selected tokens): 2 sub-tiles of 64 tokens gathered from the FP8
+//          cache and widened exactly to bf16 in LDS, bf16 MFMA 16x16x32 for q.k and
+//          p.v, the per-token scale folded into the logit and the probability, online
+//          softmax -> mailboxes part, ml
+//   merge  (row, 2 heads): out = sum_j e^(m_j - M) acc_j / sum_j e^(m_j - M) l_j, bf16
 #include "attn_ops.h"
 #include "common.h"
 #include "sync.h"
@@ -34,33 +38,35 @@ namespace {
 
 constexpr int AT = 512;
 constexpr int AW = AT / WAVE;
-constexpr int KPT = MAX_CTX / AT;            // keys a thread holds in the top-k
-constexpr int KL_WORDS = MAX_CTX + AT;       // one pad word a thread range: no bank conflicts
+constexpr int KPM = MAX_CTX / TEAM;          // keys a top-k team member owns
+constexpr int KPT = KPM / AT;                // keys a thread of a member holds
 constexpr int SUB = 64;                      // tokens a split sub-tile
 constexpr int NSUB = SPLIT / SUB;
 constexpr int Q_STRIDE = DQK + 8;            // bf16 a q row in LDS
-constexpr int KV_STRIDE = DQK + 16;          // bytes a cached row in LDS
-constexpr int VT_STRIDE = SUB + 8;           // bytes a transposed latent row in LDS
+// dwords a cached row in LDS, as bf16 pairs: 16-byte aligned rows; the swizzle below
+// spreads a p.v column (8 rows, 8 apart for the 4 lane groups) over the banks
+constexpr int KVW = DQK / 2 + 4;
 constexpr int PB_STRIDE = SUB + 8;           // bf16 a probability row in LDS
 constexpr int KEYS_WAVE = CHUNK / AW;        // 128 keys a wave of a score task
 constexpr int KTILES = KEYS_WAVE / 16;
 constexpr float NEG_INF = -__builtin_huge_valf();
-static_assert(KPT % 16 == 0 && KEYS_WAVE % PAGE == 0 && SPLIT % SUB == 0, "tiling");
-static_assert(AT == NH * DV / 32, "a merge thread owns 4 outputs of one head");
+static_assert(KPM % AT == 0 && PAGE % KPT == 0 && TEAM <= 16 && KEYS_WAVE % PAGE == 0 && SPLIT % SUB == 0, "tiling");
+static_assert(AT == NH * DV / 32, "a merge task covers 2 heads");
 
-enum { W_SCORE = 0, W_SEL = 1, W_PART = 2 };
+enum { W_SCORE = 0, W_SEL = 1, W_PART = 2, W_TEAM = 3 };
 
 struct TopkLds {
-  uint32_t kl[KL_WORDS];
-  uint32_t hist[256];
+  int32_t pt[TOPK / PAGE];  // a short row's page table
+  uint32_t hist[256];       // this member's digit histogram
+  uint32_t tot[256];        // the team's
+  int32_t cnt[TEAM][2];     // the team's keys above / at the threshold
   uint32_t digit;
   int32_t above;
 };
 
 struct SplitLds {
   uint16_t q[NH][Q_STRIDE];
-  uint8_t kv[SUB][KV_STRIDE];
-  uint8_t vt[DV][VT_STRIDE];
+  uint32_t kvb[SUB * KVW];  // the sub-tile's rows widened to bf16, swizzled (kv_at)
   float pf[NH][SUB];
   uint16_t pb[NH][PB_STRIDE];
   int32_t slot[SPLIT];
@@ -95,6 +101,7 @@ struct Args {
   int rows;
   float* scores;
   int32_t* topk;
+  int64_t* timeline;
   float scale;
   Mail mail;
   GuardArgs guard;
@@ -103,9 +110,6 @@ struct Args {
 MONO_DEV uint32_t radix_key(float f) {
   const uint32_t b = __float_as_uint(f);
   return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-}
-MONO_DEV float key_value(uint32_t k) {
-  return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
 }
 
 // FP4 x FP4 16x16x128 with per-lane E8M0 scales; the B scale byte is picked by OPB.
@@ -117,16 +121,18 @@ MONO_DEV f32x4 mfma_fp4_opb(const u32x4& a, const u32x4& b, int sa, int sb) {
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A, B, z, 4, 4, 0, sa, OPB, sb);
 }
 
-// 8 E4M3 bytes -> 8 bf16 (exact: every E4M3 value is a bf16 value)
-MONO_DEV bf16x8 fp8x8_bf16(u32x2 w) {
-  u32x4 o;
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const f32x2 lo = fp8x2_unpack<false>(w[h]), hi = fp8x2_unpack<true>(w[h]);
-    o[2 * h] = (__float_as_uint(lo[0]) >> 16) | (__float_as_uint(lo[1]) & 0xffff0000u);
-    o[2 * h + 1] = (__float_as_uint(hi[0]) >> 16) | (__float_as_uint(hi[1]) & 0xffff0000u);
-  }
-  return __builtin_bit_cast(bf16x8, o);
+// Dword of (token t, dims 2 w, 2 w + 1) in a sub-tile's bf16 rows: rows 8 apart XOR
+// their dword index by 8 so a p.v column's 4 lane groups hit different banks; 4-dword
+// groups stay contiguous and aligned for the q.k reads.
+MONO_DEV int kv_at(int t, int w) { return t * KVW + (w ^ (((t >> 3) & 3) << 3)); }
+
+// 4 E4M3 bytes -> 4 bf16 as 2 dwords (exact: every E4M3 value is a bf16 value)
+MONO_DEV u32x2 fp8x4_bf16(uint32_t w) {
+  const f32x2 lo = fp8x2_unpack<false>(w), hi = fp8x2_unpack<true>(w);
+  u32x2 o;
+  o[0] = (__float_as_uint(lo[0]) >> 16) | (__float_as_uint(lo[1]) & 0xffff0000u);
+  o[1] = (__float_as_uint(hi[0]) >> 16) | (__float_as_uint(hi[1]) & 0xffff0000u);
+  return o;
 }
 
 class Step {
@@ -153,22 +159,33 @@ class Step {
     gd.a = A.guard;
     gd.tag = L.tag;
     gd.deadline = now_ticks() + A.guard.deadline_ticks;
-    const int n_score = A.rows * CH, n_topk = A.rows, n_split = A.rows * SPLITS, n_merge = A.rows * (NH / 4);
+    // score tasks padded to a multiple of TEAM so no top-k team straddles a round
+    const int n_score = (A.rows * CH + TEAM - 1) / TEAM * TEAM, n_topk = A.rows * TEAM;
+    const int n_split = A.rows * SPLITS, n_merge = A.rows * (NH / 2);
     const int total = n_score + n_topk + n_split + n_merge;
-    for (int T = blockIdx.x; T < total; T += G) {
-      bool ok = true;
-      if (T < n_score) {
-        score_task(T / CH, T % CH);
-      } else if (T < n_score + n_topk) {
-        ok = topk_task(T - n_score);
-      } else if (T < n_score + n_topk + n_split) {
-        const int j = T - n_score - n_topk;
-        ok = split_task(j / SPLITS, j % SPLITS);
-      } else {
-        const int j = T - n_score - n_topk - n_split;
-        ok = merge_task(j / (NH / 4), j % (NH / 4));
-      }
+    score_stage(blockIdx.x, A.rows * CH);
+    // a workgroup's list is ordered by stage: one loop a stage keeps each loop body to
+    // one task kind (and its registers)
+    int T = first_at_or_after(n_score);
+    for (; T < n_score + n_topk; T += G) {
+      const uint64_t t0 = now_ticks();
+      const bool ok = topk_member((T - n_score) / TEAM, (T - n_score) % TEAM);
+      stamp(T, t0, 1);
       if (!ok) return;  // workgroup-uniform
+    }
+    for (T = first_at_or_after(n_score + n_topk); T < n_score + n_topk + n_split; T += G) {
+      const uint64_t t0 = now_ticks();
+      const int j = T - n_score - n_topk;
+      const bool ok = split_task(j / SPLITS, j % SPLITS);
+      stamp(T, t0, 2);
+      if (!ok) return;
+    }
+    for (T = first_at_or_after(n_score + n_topk + n_split); T < total; T += G) {
+      const uint64_t t0 = now_ticks();
+      const int j = T - n_score - n_topk - n_split;
+      const bool ok = merge_task(j / (NH / 2), j % (NH / 2));
+      stamp(T, t0, 3);
+      if (!ok) return;
     }
   }
 
@@ -177,6 +194,7 @@ class Step {
   Lds& L;
   Guard gd;
   int tid, lane, wave, g, r, G, CH;
+  uint64_t waited = 0;
 
   MONO_DEV int row_len(int s) const { return min(max(A.seq_lens[s], 0), A.mail.max_ctx); }
   MONO_DEV int page_of(int s, int p) const {
@@ -185,41 +203,73 @@ class Step {
   }
   MONO_DEV int slot_of(int s, int p) const { return page_of(s, p) * PAGE + p % PAGE; }
 
+  // this workgroup's first task at or after list index `at` (tasks are dealt round-robin)
+  MONO_DEV int first_at_or_after(int at) const {
+    const int b = blockIdx.x;
+    return at <= b ? b : b + ((at - b + G - 1) / G) * G;
+  }
+
+  // timeline row of task T: start, inputs-ready and end ticks, workgroup << 8 | kind
+  // (kind 0 score .. 3 merge); `waited` is 0 for a task that waits on nothing
+  MONO_DEV void stamp(int T, uint64_t t0, int kind) const {
+    if (A.timeline && tid == 0) {
+      int64_t* tl = A.timeline + (size_t)T * 4;
+      tl[0] = (int64_t)t0;
+      tl[1] = (int64_t)waited;
+      tl[2] = (int64_t)now_ticks();
+      tl[3] = ((int64_t)blockIdx.x << 8) | kind;
+    }
+  }
+  MONO_DEV void mark_waited() { waited = now_ticks(); }
+
   // ---------------------------------------------------------------- score
-  MONO_DEV void score_task(int s, int c) {
-    const int n = row_len(s);
-    const int k0 = c * CHUNK + wave * KEYS_WAVE;
-    if (k0 >= n) return;  // wave-uniform; the task has no barrier
-    // the row's query: head tile ht is rows 16 ht .. of the 64 heads
+  // A score task's operands for one wave: the row's FP4 query (head tile ht = heads
+  // 16 ht ..), its head weights, and 128 keys = 2 pages = 8 tiles of 16 keys (lane
+  // (g, r) holds chunk g of key 16 t + r) with their pages' E8M0 dwords.
+  struct ScoreOps {
+    int s, k0, n;
     u32x4 qa[IH / 16];
     int qsc[IH / 16];
+    uint32_t w2[IH / 16][2];
+    u32x4 kb[KTILES];
+    uint32_t ks[KEYS_WAVE / PAGE];
+  };
+
+  MONO_DEV void score_load(int T, ScoreOps& o) {
+    o.s = T / CH;
+    o.k0 = (T % CH) * CHUNK + wave * KEYS_WAVE;
+    o.n = row_len(o.s);
+    if (o.k0 >= o.n) return;
+#pragma unroll
+    for (int ht = 0; ht < IH / 16; ++ht) {
+      const size_t row = (size_t)o.s * IH + 16 * ht + r;
+      o.qa[ht] = ld_u32x4(A.iq + row * (ID / 2) + g * 16);
+      o.qsc[ht] = A.iqs[row * (ID / 32) + g];
+      const u32x2 w4 = *reinterpret_cast<const u32x2*>(A.iw + (size_t)o.s * IH + 16 * ht + 4 * g);
+      o.w2[ht][0] = w4[0];
+      o.w2[ht][1] = w4[1];
+    }
+    int pg[KEYS_WAVE / PAGE];
+#pragma unroll
+    for (int i = 0; i < KEYS_WAVE / PAGE; ++i) pg[i] = page_of(o.s, o.k0 + i * PAGE);
+#pragma unroll
+    for (int kt = 0; kt < KTILES; ++kt)
+      o.kb[kt] = ld_nt_u32x4(A.ikv + ((size_t)(pg[kt / 4] * 4 + g) * PAGE + (kt % 4) * 16 + r) * 16);
+#pragma unroll
+    for (int i = 0; i < KEYS_WAVE / PAGE; ++i)
+      o.ks[i] = *reinterpret_cast<const uint32_t*>(A.iks + (size_t)(pg[i] * 4 + g) * PAGE + r * 4);
+  }
+
+  MONO_DEV void score_compute(const ScoreOps& o) {
+    if (o.k0 >= o.n) return;  // wave-uniform; no barrier in the score stage
     float wv[IH / 16][4];
 #pragma unroll
     for (int ht = 0; ht < IH / 16; ++ht) {
-      const size_t row = (size_t)s * IH + 16 * ht + r;
-      qa[ht] = ld_u32x4(A.iq + row * (ID / 2) + g * 16);
-      qsc[ht] = A.iqs[row * (ID / 32) + g];
-      const u32x2 w4 = *reinterpret_cast<const u32x2*>(A.iw + (size_t)s * IH + 16 * ht + 4 * g);
-      wv[ht][0] = bf16_lo(w4[0]);
-      wv[ht][1] = bf16_hi(w4[0]);
-      wv[ht][2] = bf16_lo(w4[1]);
-      wv[ht][3] = bf16_hi(w4[1]);
+      wv[ht][0] = bf16_lo(o.w2[ht][0]);
+      wv[ht][1] = bf16_hi(o.w2[ht][0]);
+      wv[ht][2] = bf16_lo(o.w2[ht][1]);
+      wv[ht][3] = bf16_hi(o.w2[ht][1]);
     }
-    // 128 keys = 2 pages = 8 tiles of 16 keys: lane (g, r) holds chunk g of key 16 t + r
-    const int p0 = k0 / PAGE;
-    int pg[KEYS_WAVE / PAGE];
-    uint32_t ks[KEYS_WAVE / PAGE];
-#pragma unroll
-    for (int i = 0; i < KEYS_WAVE / PAGE; ++i) pg[i] = page_of(s, (p0 + i) * PAGE);
-    u32x4 kb[KTILES];
-#pragma unroll
-    for (int kt = 0; kt < KTILES; ++kt) {
-      const int page = pg[kt / 4];
-      kb[kt] = ld_nt_u32x4(A.ikv + ((size_t)(page * 4 + g) * PAGE + (kt % 4) * 16 + r) * 16);
-    }
-#pragma unroll
-    for (int i = 0; i < KEYS_WAVE / PAGE; ++i)
-      ks[i] = *reinterpret_cast<const uint32_t*>(A.iks + (size_t)(pg[i] * 4 + g) * PAGE + r * 4);
 #pragma unroll
     for (int kt = 0; kt < KTILES; ++kt) {
       float part = 0.f;
@@ -227,27 +277,43 @@ class Step {
       for (int ht = 0; ht < IH / 16; ++ht) {
         f32x4 d;
         switch (kt % 4) {
-          case 0: d = mfma_fp4_opb<0>(qa[ht], kb[kt], qsc[ht], (int)ks[kt / 4]); break;
-          case 1: d = mfma_fp4_opb<1>(qa[ht], kb[kt], qsc[ht], (int)ks[kt / 4]); break;
-          case 2: d = mfma_fp4_opb<2>(qa[ht], kb[kt], qsc[ht], (int)ks[kt / 4]); break;
-          default: d = mfma_fp4_opb<3>(qa[ht], kb[kt], qsc[ht], (int)ks[kt / 4]); break;
+          case 0: d = mfma_fp4_opb<0>(o.qa[ht], o.kb[kt], o.qsc[ht], (int)o.ks[kt / 4]); break;
+          case 1: d = mfma_fp4_opb<1>(o.qa[ht], o.kb[kt], o.qsc[ht], (int)o.ks[kt / 4]); break;
+          case 2: d = mfma_fp4_opb<2>(o.qa[ht], o.kb[kt], o.qsc[ht], (int)o.ks[kt / 4]); break;
+          default: d = mfma_fp4_opb<3>(o.qa[ht], o.kb[kt], o.qsc[ht], (int)o.ks[kt / 4]); break;
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) part += wv[ht][i] * fmaxf(d[i], 0.f);
       }
       part += __shfl_xor(part, 16, WAVE);
       part += __shfl_xor(part, 32, WAVE);
-      const int pos = k0 + kt * 16 + r;
-      if (g == 0 && pos < n) {
-        mb_putf(&A.mail.score[(size_t)s * A.mail.max_ctx + pos], part, gd.tag);
-        if (A.scores) A.scores[(size_t)s * A.mail.max_ctx + pos] = part;
+      const int pos = o.k0 + kt * 16 + r;
+      if (g == 0 && pos < o.n) {
+        mb_putf(&A.mail.score[(size_t)o.s * A.mail.max_ctx + pos], part, gd.tag);
+        if (A.scores) A.scores[(size_t)o.s * A.mail.max_ctx + pos] = part;
       }
     }
   }
 
+  // The workgroup's score tasks T0, T0 + G, ... < n_score, each task's loads issued
+  // before the previous task computes.
+  MONO_DEV void score_stage(int T0, int n_score) {
+    if (T0 >= n_score) return;
+    ScoreOps cur, nxt;
+    score_load(T0, cur);
+    for (int T = T0; T < n_score; T += G) {
+      const uint64_t t0 = now_ticks();
+      const bool more = T + G < n_score;
+      if (more) score_load(T + G, nxt);
+      score_compute(cur);
+      stamp(T, t0, 0);
+      if (more) cur = nxt;
+    }
+  }
+
   // ---------------------------------------------------------------- top-k
-  // exclusive prefix sum of v over the workgroup (a full barrier); total to *tot
-  MONO_DEV int block_excl_scan(int v, int* tot) {
+  // exclusive prefix sum of v over the workgroup (a full barrier)
+  MONO_DEV int block_excl_scan(int v) {
     int incl = v;
 #pragma unroll
     for (int o = 1; o < WAVE; o <<= 1) {
@@ -256,15 +322,10 @@ class Step {
     }
     if (lane == WAVE - 1) L.scan[wave] = incl;
     __syncthreads();
-    int before = 0, all = 0;
+    int before = 0;
 #pragma unroll
-    for (int w = 0; w < AW; ++w) {
-      const int t = L.scan[w];
-      before += w < wave ? t : 0;
-      all += t;
-    }
+    for (int w = 0; w < AW; ++w) before += w < wave ? L.scan[w] : 0;
     __syncthreads();
-    if (tot) *tot = all;
     return before + incl - v;
   }
 
@@ -273,100 +334,214 @@ class Step {
     if (A.topk) A.topk[(size_t)s * TOPK + j] = slot;
   }
 
-  MONO_DEV bool topk_task(int s) {
+  // Count a key digit into hist, aggregating heavy hitters: the wave's two most common
+  // leading digits go in as one atomic each (scores share sign and exponent bits, so
+  // the first digits pile onto few bins), the rest lane by lane.
+  MONO_DEV void hist_add(uint32_t* hist, bool live, uint32_t d) {
+    uint64_t act = __ballot(live);
+#pragma unroll
+    for (int it = 0; it < 2; ++it) {
+      if (act == 0) break;
+      const int leader = __ffsll((long long)act) - 1;
+      const uint32_t dl = __shfl(d, leader, WAVE);
+      const uint64_t m = __ballot(live && d == dl) & act;
+      if (lane == leader) atomicAdd(&hist[dl], (uint32_t)__popcll(m));
+      act &= ~m;
+    }
+    if ((act >> lane) & 1ull) atomicAdd(&hist[d], 1u);
+  }
+
+  // Pick the next digit from a 256-bin histogram (wave 0): the highest digit d with
+  // (keys above d) < need <= (keys above d) + hist[d]; writes K.digit and K.above.
+  MONO_DEV void pick_digit(TopkLds& K, const uint32_t* hist, int need) {
+    if (wave != 0) return;
+    int c[4], tot = 0;  // lane l holds bins 255 - 4l .. 252 - 4l, highest first
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      c[j] = (int)hist[255 - 4 * lane - j];
+      tot += c[j];
+    }
+    int incl = tot;
+#pragma unroll
+    for (int o = 1; o < WAVE; o <<= 1) {
+      const int y = __shfl_up(incl, o, WAVE);
+      if (lane >= o) incl += y;
+    }
+    const int excl = incl - tot;
+    if (excl < need && need <= incl) {
+      int run = excl;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (run + c[j] >= need) {
+          K.digit = (uint32_t)(255 - 4 * lane - j);
+          K.above = run;
+          break;
+        }
+        run += c[j];
+      }
+    }
+  }
+
+  // Member m of row s's top-k team. The team selects the exact top-TOPK of the row
+  // (score desc, position asc) -> cache slots, ascending. Member m owns positions
+  // [m KPM, (m + 1) KPM), KPT of them in each thread's registers. Per 8-bit digit,
+  // MSB first, each member publishes its histogram of the live keys and sums the
+  // team's (every member computes the same digit); then members publish their counts
+  // above / at the threshold T and each writes its selected slots at its offset: keys
+  // above T, and the lowest positions equal to T.
+  MONO_DEV bool topk_member(int s, int m) {
+    TopkLds& K = L.u.t;
     const int n = row_len(s);
     if (n <= TOPK) {  // every key is selected; no score is needed
-      for (int j = tid; j < TOPK; j += AT) publish_sel(s, j, j < n ? slot_of(s, j) : -1);
+      if (m == 0) {
+        for (int i = tid; i < TOPK / PAGE; i += AT) K.pt[i] = i * PAGE < n ? page_of(s, i * PAGE) : 0;
+        __syncthreads();
+        for (int j = tid; j < TOPK; j += AT) publish_sel(s, j, j < n ? K.pt[j / PAGE] * PAGE + j % PAGE : -1);
+      }
       return true;
     }
-    uint32_t* kl = L.u.t.kl;
-    const int p0 = tid * KPT;
+    const int p0 = m * KPM + tid * KPT;
     const int cnt = min(max(n - p0, 0), KPT);
-    const int kb = p0 + tid;  // padded LDS base of this thread's range
-    const uint64_t* sc = &A.mail.score[(size_t)s * A.mail.max_ctx + p0];
-    bool ok = true;
-#pragma unroll 1
-    for (int b = 0; b < KPT / 16; ++b) {
-      const int have = min(max(cnt - b * 16, 0), 16);
-      const uint32_t pending = have >= 16 ? 0xffffu : (1u << have) - 1u;
-      uint32_t v[16];
-      const uint64_t* base = sc + b * 16;
-      if (ok) ok = poll_words<16>([base](int q) { return base + q; }, v, pending, W_SCORE, gd);
+    const int page = cnt > 0 ? page_of(s, p0) : 0;  // a thread's keys share one page
+    uint32_t key[KPT];
+    bool ok;
+    {
+      uint32_t v[KPT];
+      const uint64_t* base = &A.mail.score[(size_t)s * A.mail.max_ctx + p0];
+      ok = poll_words<KPT>([base](int q) { return base + q; }, v, (1u << cnt) - 1u, W_SCORE, gd);
 #pragma unroll
-      for (int q = 0; q < 16; ++q)
-        if (q < have) kl[kb + b * 16 + q] = radix_key(__uint_as_float(v[q]));
+      for (int q = 0; q < KPT; ++q) key[q] = radix_key(__uint_as_float(v[q]));
     }
     if (!block_all(ok)) return false;
-    // MSB-first 8-bit radix select of the TOPK-th largest key
+    mark_waited();
     uint32_t prefix = 0, mask = 0;
     int need = TOPK;
 #pragma unroll 1
-    for (int shift = 24; shift >= 0; shift -= 8) {
-      if (tid < 256) L.u.t.hist[tid] = 0u;
+    for (int pass = 0; pass < PASSES; ++pass) {
+      const int shift = 24 - 8 * pass;
+      if (tid < 256) K.hist[tid] = 0u;
       __syncthreads();
-      for (int q = 0; q < cnt; ++q) {
-        const uint32_t k = kl[kb + q];
-        if ((k & mask) == prefix) atomicAdd(&L.u.t.hist[(k >> shift) & 0xffu], 1u);
+#pragma unroll
+      for (int q = 0; q < KPT; ++q) hist_add(K.hist, q < cnt && (key[q] & mask) == prefix, (key[q] >> shift) & 0xffu);
+      __syncthreads();
+      uint64_t* hb = &A.mail.hist[((size_t)s * PASSES + pass) * TEAM * 256];
+      if (tid < 256) {
+        mb_put(&hb[m * 256 + tid], K.hist[tid], gd.tag);
+        uint32_t v[TEAM];
+        const uint64_t* col = hb + tid;
+        ok = poll_words<TEAM>([col](int j) { return col + j * 256; }, v, (1u << TEAM) - 1u, W_TEAM, gd);
+        uint32_t t = 0;
+#pragma unroll
+        for (int j = 0; j < TEAM; ++j) t += v[j];
+        K.tot[tid] = t;
       }
+      if (!block_all(ok)) return false;
+      pick_digit(K, K.tot, need);
       __syncthreads();
-      if (wave == 0) {
-        int c[4], tot = 0;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          c[j] = (int)L.u.t.hist[255 - 4 * lane - j];
-          tot += c[j];
-        }
-        int incl = tot;
-#pragma unroll
-        for (int o = 1; o < WAVE; o <<= 1) {
-          const int y = __shfl_up(incl, o, WAVE);
-          if (lane >= o) incl += y;
-        }
-        const int excl = incl - tot;
-        if (excl < need && need <= incl) {
-          int run = excl;
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            if (run + c[j] >= need) {
-              L.u.t.digit = (uint32_t)(255 - 4 * lane - j);
-              L.u.t.above = run;
-              break;
-            }
-            run += c[j];
-          }
-        }
-      }
-      __syncthreads();
-      need -= L.u.t.above;
-      prefix |= L.u.t.digit << shift;
+      need -= K.above;
+      prefix |= K.digit << shift;
       mask |= 0xffu << shift;
       __syncthreads();
     }
-    // stable compaction: keys above the threshold, then the lowest positions equal to it
+    // the team's counts above / at T, then this member's offsets
     const uint32_t T = prefix;
     int c_gt = 0, c_eq = 0;
-    for (int q = 0; q < cnt; ++q) {
-      const uint32_t k = kl[kb + q];
-      c_gt += k > T;
-      c_eq += k == T;
+#pragma unroll
+    for (int q = 0; q < KPT; ++q) {
+      c_gt += (q < cnt && key[q] > T) ? 1 : 0;
+      c_eq += (q < cnt && key[q] == T) ? 1 : 0;
     }
-    const int eq_before = block_excl_scan(c_eq, nullptr);
-    const int take = min(max(need - eq_before, 0), c_eq);
-    int idx = block_excl_scan(c_gt + take, nullptr);
+    const int gt_in = block_excl_scan(c_gt), eq_in = block_excl_scan(c_eq);
+    if (tid == AT - 1) {  // the last thread's inclusive sums are the member's totals
+      mb_put(&A.mail.cnt[((size_t)s * TEAM + m) * 2], (uint32_t)(gt_in + c_gt), gd.tag);
+      mb_put(&A.mail.cnt[((size_t)s * TEAM + m) * 2 + 1], (uint32_t)(eq_in + c_eq), gd.tag);
+    }
+    if (tid < 2 * TEAM) {
+      uint32_t v = 0;
+      ok = poll_word(&A.mail.cnt[(size_t)s * TEAM * 2 + tid], v, W_TEAM, gd);
+      K.cnt[tid / 2][tid % 2] = (int)v;
+    }
+    if (!block_all(ok)) return false;
+    int sel_before = 0, eq_before = 0;  // over the members before m, in position order
+    for (int j = 0; j < m; ++j) {
+      const int take_j = min(max(need - eq_before, 0), K.cnt[j][1]);
+      sel_before += K.cnt[j][0] + take_j;
+      eq_before += K.cnt[j][1];
+    }
+    const int take = min(max(need - (eq_before + eq_in), 0), c_eq);
+    int idx = sel_before + block_excl_scan(c_gt + take);
     int te = 0;
-    for (int q = 0; q < cnt; ++q) {
-      const uint32_t k = kl[kb + q];
-      const bool eq = k == T;
-      if ((k > T || (eq && te < take)) && idx < TOPK) {
-        te += eq;
-        publish_sel(s, idx++, slot_of(s, p0 + q));
+#pragma unroll
+    for (int q = 0; q < KPT; ++q) {
+      const bool eq = key[q] == T;
+      if (q < cnt && (key[q] > T || (eq && te < take)) && idx < TOPK) {
+        te += eq ? 1 : 0;
+        publish_sel(s, idx++, page * PAGE + (p0 + q) % PAGE);
       }
     }
-    __syncthreads();  // the LDS keys are reused by the next task
     return true;
   }
 
   // ---------------------------------------------------------------- split
+  static constexpr int GATHER = (SUB * (DQK / 16) + AT - 1) / AT;  // 16-byte loads a thread a sub-tile
+
+  // Issue sub-tile st's cache-row loads: consecutive lanes read consecutive 16-byte
+  // chunks of a row.
+  MONO_DEV void gather_load(const SplitLds& P, int st, u32x4 (&gv)[GATHER], float& gs) {
+#pragma unroll
+    for (int i = 0; i < GATHER; ++i) {
+      const int f = tid + i * AT;
+      gv[i] = u32x4{0u, 0u, 0u, 0u};
+      if (f < SUB * (DQK / 16)) {
+        const int t = f / (DQK / 16), c = f % (DQK / 16);
+        const int slot = P.slot[st * SUB + t];
+        if (slot >= 0) gv[i] = ld_nt_u32x4(A.kv + (size_t)slot * DQK + c * 16);
+      }
+    }
+    gs = 0.f;
+    if (tid < SUB) {
+      const int slot = P.slot[st * SUB + tid];
+      if (slot >= 0) gs = A.kv_scale[slot];
+    }
+  }
+
+  // bf16 column d of 8 consecutive rows from t0: a p.v operand (8 tokens of one dim).
+  MONO_DEV static bf16x8 column8(const SplitLds& P, int t0, int d) {
+    const uint16_t* b = reinterpret_cast<const uint16_t*>(P.kvb);
+    u32x4 w;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t lo = b[2 * kv_at(t0 + 2 * j, d >> 1) + (d & 1)];
+      const uint32_t hi = b[2 * kv_at(t0 + 2 * j + 1, d >> 1) + (d & 1)];
+      w[j] = lo | (hi << 16);
+    }
+    return __builtin_bit_cast(bf16x8, w);
+  }
+
+  // Store the gathered rows widened to bf16, row-major (swizzled).
+  MONO_DEV void gather_store(SplitLds& P, const u32x4 (&gv)[GATHER], float gs) {
+#pragma unroll
+    for (int i = 0; i < GATHER; ++i) {
+      const int f = tid + i * AT;
+      if (f < SUB * (DQK / 16)) {
+        const int t = f / (DQK / 16), c = f % (DQK / 16);
+        u32x4 lo, hi;
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          const u32x2 a = fp8x4_bf16(gv[i][q]), b = fp8x4_bf16(gv[i][q + 2]);
+          lo[2 * q] = a[0];
+          lo[2 * q + 1] = a[1];
+          hi[2 * q] = b[0];
+          hi[2 * q + 1] = b[1];
+        }
+        // dims 16c .. 16c + 15 are dwords 8c .. 8c + 7: one swizzled 8-dword block
+        *reinterpret_cast<u32x4*>(&P.kvb[kv_at(t, 8 * c)]) = lo;
+        *reinterpret_cast<u32x4*>(&P.kvb[kv_at(t, 8 * c) + 4]) = hi;
+      }
+    }
+    if (tid < SUB) P.kvs[tid] = gs;
+  }
+
   MONO_DEV bool split_task(int s, int j) {
     SplitLds& P = L.u.sp;
     const int nsel = min(row_len(s), TOPK);
@@ -380,9 +555,19 @@ class Step {
       }
       return true;
     }
-    for (int f = tid; f < NH * DQK / 8; f += AT) {
-      const int h = f / (DQK / 8), c8 = f % (DQK / 8);
-      *reinterpret_cast<u32x4*>(&P.q[h][c8 * 8]) = ld_u32x4(A.q + ((size_t)s * NH + h) * DQK + c8 * 8);
+    {
+      constexpr int QL = (NH * DQK / 8 + AT - 1) / AT;
+      u32x4 qv[QL];
+#pragma unroll
+      for (int i = 0; i < QL; ++i) {
+        const int f = tid + i * AT;
+        if (f < NH * DQK / 8) qv[i] = ld_u32x4(A.q + (size_t)s * NH * DQK + (size_t)f * 8);
+      }
+#pragma unroll
+      for (int i = 0; i < QL; ++i) {
+        const int f = tid + i * AT;
+        if (f < NH * DQK / 8) *reinterpret_cast<u32x4*>(&P.q[f / (DQK / 8)][(f % (DQK / 8)) * 8]) = qv[i];
+      }
     }
     bool ok = true;
     if (tid < SPLIT) {
@@ -396,6 +581,7 @@ class Step {
       P.slot[tid] = slot;
     }
     if (!block_all(ok)) return false;
+    mark_waited();
 
     const int ht = wave / 4, tt = wave % 4;  // logit tile of this wave
     f32x4 acc[2][4];
@@ -404,33 +590,23 @@ class Step {
 #pragma unroll
       for (int b = 0; b < 4; ++b) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
     float m_run[4] = {NEG_INF, NEG_INF, NEG_INF, NEG_INF}, l_run[4] = {0.f, 0.f, 0.f, 0.f};
+    const int nsub = (cnt + SUB - 1) / SUB;
+    u32x4 gv[GATHER];
+    float gs;
+    gather_load(P, 0, gv, gs);
 
 #pragma unroll 1
-    for (int st = 0; st < NSUB && st * SUB < cnt; ++st) {
-      // gather 64 cached rows: consecutive lanes read consecutive 16-byte chunks of a row
-      for (int f = tid; f < SUB * (DQK / 16); f += AT) {
-        const int t = f / (DQK / 16), c = f % (DQK / 16);
-        const int slot = P.slot[st * SUB + t];
-        u32x4 v = {0u, 0u, 0u, 0u};
-        if (slot >= 0) v = ld_nt_u32x4(A.kv + (size_t)slot * DQK + c * 16);
-        *reinterpret_cast<u32x4*>(&P.kv[t][c * 16]) = v;
-        if (c < DV / 16) {
-#pragma unroll
-          for (int b = 0; b < 16; ++b) P.vt[c * 16 + b][t] = (uint8_t)(v[b / 4] >> (8 * (b % 4)));
-        }
-      }
-      if (tid < SUB) {
-        const int slot = P.slot[st * SUB + tid];
-        P.kvs[tid] = slot >= 0 ? A.kv_scale[slot] : 0.f;
-      }
+    for (int st = 0; st < nsub; ++st) {
+      gather_store(P, gv, gs);
       __syncthreads();
+      if (st + 1 < nsub) gather_load(P, st + 1, gv, gs);  // in flight while this sub-tile computes
       // logits of 16 heads x 16 tokens a wave: K = 576 in 18 bf16 steps
       {
         f32x4 d = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int ks = 0; ks < DQK / 32; ++ks) {
           const bf16x8 qa = *reinterpret_cast<const bf16x8*>(&P.q[16 * ht + r][32 * ks + 8 * g]);
-          const bf16x8 kb = fp8x8_bf16(*reinterpret_cast<const u32x2*>(&P.kv[16 * tt + r][32 * ks + 8 * g]));
+          const bf16x8 kb = *reinterpret_cast<const bf16x8*>(&P.kvb[kv_at(16 * tt + r, 16 * ks + 4 * g)]);
           d = mfma_bf16(qa, kb, d);
         }
         const int t = 16 * tt + r;
@@ -472,7 +648,7 @@ class Step {
         for (int a = 0; a < 2; ++a) pa[a] = *reinterpret_cast<const bf16x8*>(&P.pb[16 * a + r][32 * kt + 8 * g]);
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
-          const bf16x8 vb = fp8x8_bf16(*reinterpret_cast<const u32x2*>(&P.vt[16 * (4 * wave + b) + r][32 * kt + 8 * g]));
+          const bf16x8 vb = column8(P, 32 * kt + 8 * g, 16 * (4 * wave + b) + r);
 #pragma unroll
           for (int a = 0; a < 2; ++a) acc[a][b] = mfma_bf16(pa[a], vb, acc[a][b]);
         }
@@ -500,40 +676,37 @@ class Step {
   }
 
   // ---------------------------------------------------------------- merge
-  MONO_DEV bool merge_task(int s, int hg) {
-    const int h = 4 * hg + tid / 128, d0 = (tid % 128) * 4;
+  MONO_DEV bool merge_task(int s, int hp) {
+    const int h = 2 * hp + tid / 256, d0 = (tid % 256) * 2;
     const size_t rb = (size_t)s * SPLITS;
     uint32_t ml[2 * SPLITS];
     const uint64_t* mlp = &A.mail.ml[(rb * NH + h) * 2];
     bool ok = poll_words<2 * SPLITS>([mlp](int q) { return mlp + (size_t)(q / 2) * NH * 2 + q % 2; }, ml,
-                                     (1u << (2 * SPLITS)) - 1u, W_PART, gd);
+                                     0xffffffffu >> (32 - 2 * SPLITS), W_PART, gd);
     float M = NEG_INF;
     uint32_t live = 0;
 #pragma unroll
     for (int j = 0; j < SPLITS; ++j) {
       if (__uint_as_float(ml[2 * j + 1]) > 0.f) {
         M = fmaxf(M, __uint_as_float(ml[2 * j]));
-        live |= 0xfu << (4 * j);
+        live |= 0x3u << (2 * j);
       }
     }
-    uint32_t av[4 * SPLITS];
+    uint32_t av[2 * SPLITS];
     const uint64_t* ap = &A.mail.part[(rb * NH + h) * DV + d0];
-    if (ok) ok = poll_words<4 * SPLITS>([ap](int q) { return ap + (size_t)(q / 4) * NH * DV + q % 4; }, av, live, W_PART, gd);
-    float o[4] = {0.f, 0.f, 0.f, 0.f}, den = 0.f;
+    if (ok) ok = poll_words<2 * SPLITS>([ap](int q) { return ap + (size_t)(q / 2) * NH * DV + q % 2; }, av, live, W_PART, gd);
+    float o[2] = {0.f, 0.f}, den = 0.f;
 #pragma unroll
     for (int j = 0; j < SPLITS; ++j) {
-      if ((live >> (4 * j)) & 1u) {
+      if ((live >> (2 * j)) & 1u) {
         const float w = hw_exp(__uint_as_float(ml[2 * j]) - M);
         den += w * __uint_as_float(ml[2 * j + 1]);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) o[i] += w * __uint_as_float(av[4 * j + i]);
+        for (int i = 0; i < 2; ++i) o[i] += w * __uint_as_float(av[2 * j + i]);
       }
     }
     const float inv = den > 0.f ? 1.0f / den : 0.f;
-    u32x2 packed;
-    packed[0] = pack_bf16x2(o[0] * inv, o[1] * inv);
-    packed[1] = pack_bf16x2(o[2] * inv, o[3] * inv);
-    if (ok) *reinterpret_cast<u32x2*>(A.out + ((size_t)s * NH + h) * DV + d0) = packed;
+    if (ok) *reinterpret_cast<uint32_t*>(A.out + ((size_t)s * NH + h) * DV + d0) = pack_bf16x2(o[0] * inv, o[1] * inv);
     return block_all(ok);
   }
 };
@@ -570,6 +743,7 @@ hipError_t attn_forward(const AttnArgs& g, int grid, const Mail& mail, const Gua
   a.rows = g.rows;
   a.scores = g.scores;
   a.topk = g.topk;
+  a.timeline = g.timeline;
   a.scale = g.softmax_scale;
   a.mail = mail;
   a.guard = guard;

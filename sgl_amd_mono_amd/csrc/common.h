@@ -26,33 +26,72 @@ constexpr float FP8_MAX = 448.0f;
 // ------------------------------------------------------------------ lanes
 MONO_DEV int lane_id() { return __lane_id(); }
 
-MONO_DEV float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
+// Cross-lane reductions without LDS traffic: DPP steps inside each 16-lane row
+// (xor 1, xor 2, 8-lane half mirror, 16-lane mirror), then the four rows' results read
+// into scalars. __shfl_xor would compile to ds_bpermute, an LDS round trip a step.
+enum : int {
+  DPP_XOR1 = 0xB1,         // quad_perm [1, 0, 3, 2]
+  DPP_XOR2 = 0x4E,         // quad_perm [2, 3, 0, 1]
+  DPP_HALF_MIRROR = 0x141, // lane i <-> 7 - i in each 8 lanes
+  DPP_MIRROR = 0x140,      // lane i <-> 15 - i in each 16 lanes
+};
+
+template <int CTRL>
+MONO_DEV float dpp_f(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+template <int CTRL>
+MONO_DEV uint32_t dpp_u(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xf, 0xf, false);
+}
+
+// Reduce over each group of WIDTH consecutive lanes (WIDTH in 2, 4, 8, 16); every
+// lane of a group gets the group's result.
+template <int WIDTH, class Op>
+MONO_DEV float row_reduce(float v, Op op) {
+  static_assert(WIDTH == 2 || WIDTH == 4 || WIDTH == 8 || WIDTH == 16, "a DPP row is 16 lanes");
+  v = op(v, dpp_f<DPP_XOR1>(v));
+  if (WIDTH >= 4) v = op(v, dpp_f<DPP_XOR2>(v));
+  if (WIDTH >= 8) v = op(v, dpp_f<DPP_HALF_MIRROR>(v));
+  if (WIDTH >= 16) v = op(v, dpp_f<DPP_MIRROR>(v));
   return v;
 }
 
-MONO_DEV float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, WAVE));
-  return v;
+template <class Op>
+MONO_DEV float wave_reduce(float v, Op op) {
+  v = row_reduce<16>(v, op);
+  const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+  const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
+  const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+  const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
+  return op(op(r0, r1), op(r2, r3));
 }
+
+struct OpAdd {
+  MONO_DEV float operator()(float a, float b) const { return a + b; }
+};
+struct OpMax {
+  MONO_DEV float operator()(float a, float b) const { return fmaxf(a, b); }
+};
+
+// sum / max over the wave, the same value in every lane (wave-uniform)
+MONO_DEV float wave_sum(float v) { return wave_reduce(v, OpAdd()); }
+MONO_DEV float wave_max(float v) { return wave_reduce(v, OpMax()); }
 
 MONO_DEV uint32_t wave_umax(uint32_t v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    uint32_t p = __shfl_xor(v, o, WAVE);
-    v = v > p ? v : p;
-  }
-  return v;
+  v = max(v, dpp_u<DPP_XOR1>(v));
+  v = max(v, dpp_u<DPP_XOR2>(v));
+  v = max(v, dpp_u<DPP_HALF_MIRROR>(v));
+  v = max(v, dpp_u<DPP_MIRROR>(v));
+  const uint32_t a = max((uint32_t)__builtin_amdgcn_readlane((int)v, 0), (uint32_t)__builtin_amdgcn_readlane((int)v, 16));
+  const uint32_t b = max((uint32_t)__builtin_amdgcn_readlane((int)v, 32), (uint32_t)__builtin_amdgcn_readlane((int)v, 48));
+  return max(a, b);
 }
 
-// max over groups of `width` consecutive lanes (width a power of two <= 64)
+// max over groups of `WIDTH` consecutive lanes (WIDTH a power of two <= 16)
 template <int WIDTH>
 MONO_DEV float group_max(float v) {
-#pragma unroll
-  for (int o = WIDTH / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, WAVE));
-  return v;
+  return row_reduce<WIDTH>(v, OpMax());
 }
 
 // ------------------------------------------------------------------ math

@@ -22,7 +22,8 @@
 //   2  tag of the failing launch (waits of that launch give up when they see it)
 //   3  workgroup that failed first
 // Every wait polls its words until their tags match, checking the deadline
-// (s_memrealtime, 100 MHz) every POLL_CHECK polls. On expiry it records the error,
+// (s_memrealtime, 100 MHz) after its first poll and then every POLL_CHECK polls, and
+// the launch's fail tag every POLL_CHECK polls. On expiry it records the error,
 // raises word 2 and returns false; the caller makes the failure workgroup-uniform and
 // the workgroup exits. No wait ever blocks past the deadline and nothing faults: the
 // launch drains and the host reads the error words (fail-stop without a GPU fault).
@@ -70,14 +71,14 @@ struct Guard {
       __hip_atomic_store(&a.words[G_FAIL_BLOCK], (uint32_t)blockIdx.x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __hip_atomic_store(&a.words[G_FAIL_TAG], tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-  // True (and the failure recorded) once the deadline has passed or another
-  // workgroup of this launch has failed.
-  MONO_DEV bool expired(int site) const {
+  // True (and the failure recorded) once the deadline has passed; with `peers`, also
+  // once another workgroup of this launch has failed (one more memory round trip).
+  MONO_DEV bool expired(int site, bool peers) const {
     if (now_ticks() > deadline) {
       fail(site);
       return true;
     }
-    return ld_agent_u32(&a.words[G_FAIL_TAG]) == tag;
+    return peers && ld_agent_u32(&a.words[G_FAIL_TAG]) == tag;
   }
 };
 
@@ -102,7 +103,9 @@ MONO_DEV bool poll_words(At at, uint32_t (&v)[N], uint32_t pending, int site, co
         pending &= ~(1u << j);
       }
     if (!pending) return true;
-    if (spin % POLL_CHECK == 1 && g.expired(site)) return false;  // after the 1st, 33rd, ... poll
+    // the deadline after the 1st, 33rd, ... poll; other workgroups' failures after the
+    // 32nd, 64th, ... (that check is a memory round trip, kept off the first retry)
+    if (spin % POLL_CHECK <= 1 && g.expired(site, spin % POLL_CHECK == 0)) return false;
     __builtin_amdgcn_s_sleep(1);
   }
 }

@@ -103,7 +103,7 @@ def test_attn_fail_stop_each_site(rt, gpu_device):
     step, caches = workloads.attn_case([5000, 1000, 3000], gpu_device, seed=5)
     good = rt.forward(step, caches)
     torch.cuda.synchronize()
-    for site in (0, 1, 2):
+    for site in (0, 1, 2, 3):
         print(f"[attn fault] site {site}", flush=True)
         rt.set_fault(site)
         rt.forward(step, caches)
