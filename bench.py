@@ -7,6 +7,8 @@ whose inputs and weights are already resident in HBM:
 * ``moe_fp8`` (default; BASELINE config 2 at 8 rows): the FP8 routed + shared MoE half
   of the decoder layer (RMSNorm, router, top-8, W8A8 experts, residual) through
   ``mono_moe_fp8_forward``.
+* ``moe_mxfp4``: the MXFP4 A16W4 routed + shared MoE behind a
+  softmax router through ``mono_moe_mxfp4_forward``.
 * ``attn``: FP4 index scores over ``--ctx`` keys a row, the exact
   top-2048 and sparse MLA decode, through ``mono_attn_forward``.
 
@@ -53,6 +55,31 @@ def cpu_model() -> str:
     return platform.processor() or "unknown"
 
 
+def time_steps(args, dev, step):
+    """``args.warmup`` untimed calls of ``step(i)``, then ``args.steps`` timed ones
+    bracketed by synchronisations, a HIP event on the launch stream after each.
+    Returns (per-step us, mean us, wall s)."""
+    import torch
+
+    log(f"warmup {args.warmup} steps")
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
+    log(f"timing {args.steps} steps")
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ev[0].record(stream)
+    for i in range(args.steps):
+        step(args.warmup + i)
+        ev[i + 1].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    per = [ev[i].elapsed_time(ev[i + 1]) * 1e3 for i in range(args.steps)]
+    return per, ev[0].elapsed_time(ev[-1]) * 1e3 / args.steps, wall
+
+
 # ------------------------------------------------------------------ FP8 MoE (config 2)
 def fp8_expert_bytes(geo) -> int:
     """Bytes of one FP8 expert: w13 [2I, H] + w2 [H, I] E4M3 and their f32 block scales."""
@@ -87,28 +114,12 @@ def bench_moe_fp8(args, dev):
     def pair(i):
         return i % len(wsets), (i // len(wsets)) % len(acts)
 
-    log(f"warmup {args.warmup} steps")
-    for i in range(args.warmup):
+    def step(i):
         wi, ai = pair(i)
         rt.forward_fp8(acts[ai], wsets[wi], out=out)
-    torch.cuda.synchronize()
 
-    stream = torch.cuda.current_stream(dev)
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
-    log(f"timing {args.steps} steps")
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    ev[0].record(stream)
-    for i in range(args.steps):
-        wi, ai = pair(args.warmup + i)
-        rt.forward_fp8(acts[ai], wsets[wi], out=out)
-        ev[i + 1].record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
+    per, us, wall = time_steps(args, dev, step)
     rt.check_errors()
-    per = [ev[i].elapsed_time(ev[i + 1]) * 1e3 for i in range(args.steps)]  # us
-    total_us = ev[0].elapsed_time(ev[-1]) * 1e3
-    us = total_us / args.steps
 
     exp_b = fp8_expert_bytes(G)
     fixed = E * H * 2 + E * 4 + H * 2 + 2 * S * H * 2  # router, bias, norm weight, a in + out
@@ -195,6 +206,131 @@ def cpu_baseline_moe_fp8(args, w, acts, G):
         value=med, unit="us", cores=torch.get_num_threads(), kind="port",
         sample=(f"oracle.moe.fp8_moe_block (f32 torch restatement) on {len(times)} steps of "
                 f"{args.rows} rows, alternating 2 activation batches of weight set 0; median; "
+                f"host '{cpu_model()}', os.cpu_count()={os.cpu_count()}"),
+    )
+
+
+# ------------------------------------------------------------------ MXFP4 MoE (config 4)
+def mxfp4_expert_bytes(geo) -> int:
+    """Bytes of one MXFP4 expert: w13 [2I, H] + w2 [H, I] E2M1 (two a byte) and their
+    E8M0 scales (one a 32 values)."""
+    H, I = geo.hidden, geo.inter
+    return (3 * I * H) // 2 + (3 * I * H) // 32
+
+
+def bench_moe_mxfp4(args, dev):
+    import torch
+
+    from sgl_amd_mono_amd import workloads
+    from sgl_amd_mono_amd.moe import MXFP4_MOE, MoeRuntime
+
+    G = MXFP4_MOE
+    H, E = G.hidden, G.n_experts
+    S = args.rows
+    n_sets = max(args.sets, 8)  # 483 MB a set: 8 sets keep the experts out of the Infinity Cache
+    log(f"generating {n_sets} MXFP4 MoE weight sets (H={H} E={E}+1 I={G.inter}) on {dev}")
+    wsets = [workloads.mxfp4_moe_weights(G, dev, seed=1100 + i) for i in range(n_sets)]
+    acts = [workloads.rows_bf16(S, H, dev, seed=2100 + i) for i in range(args.batches)]
+    lgts = [workloads.gate_logits(S, E, dev, seed=2200 + i) for i in range(args.batches)]
+    rt = MoeRuntime(G, max(S, 1), dev)
+    out = torch.empty(S, H, dtype=torch.bfloat16, device=dev)
+
+    def pair(i):
+        return i % len(wsets), (i // len(wsets)) % len(acts)
+
+    distinct = {}
+    for ai in range(len(acts)):  # routing depends on the logits only
+        _, dbg = rt.forward_mxfp4(acts[ai], lgts[ai], wsets[0], debug=True)
+        distinct[ai] = len(set(dbg["topk_ids"].flatten().tolist())) + 1  # + shared
+    torch.cuda.synchronize()
+
+    def step(i):
+        wi, ai = pair(i)
+        rt.forward_mxfp4(acts[ai], lgts[ai], wsets[wi], out=out)
+
+    per, us, wall = time_steps(args, dev, step)
+    rt.check_errors()
+
+    exp_b = mxfp4_expert_bytes(G)
+    fixed = S * E * 4 + 2 * S * H * 2  # logits, x in + out
+    step_bytes = [distinct[pair(args.warmup + i)[1]] * exp_b + fixed for i in range(args.steps)]
+    mean_bytes = statistics.fmean(step_bytes)
+    achieved = statistics.fmean(b / (t * 1e-6) for b, t in zip(step_bytes, per)) / 1e9
+    d_mean = statistics.fmean(distinct[pair(args.warmup + i)[1]] for i in range(args.steps))
+    log(f"{us:.2f} us/step (median {statistics.median(per):.2f}), {achieved:.0f} GB/s, "
+        f"{d_mean:.1f} distinct experts, wall {wall:.3f} s")
+
+    cpu = None
+    if args.cpu_seconds > 0:
+        cpu = cpu_baseline_moe_mxfp4(args, wsets[0], acts, lgts, G)
+    rt.close()
+    return dict(
+        value=us,
+        unit="us",
+        ms_per_step=us / 1e3,
+        dtype="bf16 x mxfp4 (f32 accumulate)",
+        config=dict(
+            workload="BASELINE config 4: MXFP4 A16W4 routed MoE decode, one GPU's TP=4 share",
+            rows=S, hidden=H, experts=E, top_k=G.top_k, shared_experts=1, inter=G.inter,
+            weight_sets=len(wsets), activation_batches=len(acts),
+        ),
+        extra=dict(
+            us_median=statistics.median(per), us_min=min(per), us_max=max(per),
+            rows_per_s=S / (us * 1e-6), distinct_experts_mean=d_mean,
+            algorithmic_bytes_mean=mean_bytes,
+        ),
+        roofline=dict(
+            bound="hbm", achieved=achieved, peak=HBM_PEAK_GBS, unit="GB/s",
+            frac=achieved / HBM_PEAK_GBS, traffic=None,
+            kernel="k_moe_mxfp4 (one persistent launch: route, up, down, final)",
+            bytes_per_launch=mean_bytes, avg_launch_us=statistics.fmean(per),
+        ),
+        cpu_baseline=cpu,
+    )
+
+
+def cpu_baseline_moe_mxfp4(args, w, acts, lgts, G):
+    """The CPU oracle's MXFP4 MoE block (its own router and experts) on this host."""
+    import torch
+
+    from oracle import codecs as ocodecs
+    from oracle import moe as omoe
+
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+
+    class Lazy:
+        def __init__(self, t, shuffled=False):
+            self.t, self.shuffled, self.c = t, shuffled, {}
+
+        def __getitem__(self, e):
+            if e not in self.c:
+                x = self.t[e].cpu()
+                self.c[e] = ocodecs.aiter_unshuffle(x) if self.shuffled else x
+            return self.c[e]
+
+    cw = [Lazy(w.w13, True), Lazy(w.s13), Lazy(w.w2, True), Lazy(w.s2)]
+    batches = [(a.cpu(), lg.cpu()) for a, lg in zip(acts[:2], lgts[:2])]
+
+    def one(b):
+        return omoe.mxfp4_moe_block(b[0], b[1], *cw, top_k=G.top_k, inter=G.inter)
+
+    for b in batches:
+        one(b)
+    times = []
+    t_end = time.perf_counter() + args.cpu_seconds
+    i = 0
+    while (len(times) < 5 or time.perf_counter() < t_end) and len(times) < 50:
+        t = time.perf_counter()
+        one(batches[i % 2])
+        times.append((time.perf_counter() - t) * 1e6)
+        i += 1
+    med = statistics.median(times)
+    log(f"cpu oracle: {med:.0f} us/step median of {len(times)} on {threads} threads")
+    return dict(
+        value=med, unit="us", cores=torch.get_num_threads(), kind="port",
+        sample=(f"oracle.moe.mxfp4_moe_block (f32 torch restatement) on {len(times)} steps of "
+                f"{args.rows} rows, alternating 2 batches of weight set 0; median; "
                 f"host '{cpu_model()}', os.cpu_count()={os.cpu_count()}"),
     )
 
@@ -293,7 +429,7 @@ def cpu_baseline_attn(args, case):
                         f"host '{cpu_model()}', os.cpu_count()={os.cpu_count()}"))
 
 
-WORKLOADS = {"moe_fp8": bench_moe_fp8, "attn": bench_attn}
+WORKLOADS = {"moe_fp8": bench_moe_fp8, "moe_mxfp4": bench_moe_mxfp4, "attn": bench_attn}
 
 
 def main() -> int:

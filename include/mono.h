@@ -131,15 +131,20 @@ int mono_moe_clear_errors(mono_moe* moe);
  * turns it off. */
 int mono_moe_set_fault(mono_moe* moe, int32_t site);
 
-/* MXFP4 (E2M1 + E8M0 per 32) A16W4 MoE of one decode step:
+/* MXFP4 (E2M1 + E8M0 per 32) A16W4 MoE of one decode step, one persistent launch
+ * (minimax_m31/a16w4.py:1-92, glm53/gfx950/kernel.py:966-970):
  * out = bf16(sum_slots w * down_e(bf16(silu(gate_e(x)) * up_e(x)))), softmax top-k
- * router on the given f32 logits, shared expert id E with weight 1. */
+ * router on the given f32 logits (lowest id on ties, weights = softmax over the
+ * picks), shared expert id E with weight 1. The packed E2M1 byte matrices are read in
+ * place in AITER's (16, 16) layout ([N/16, K/64, 2, 16, 16] bytes, a wave's 128-k step
+ * 1 KB contiguous); the E8M0 scales are row-major. Runtime: weight_format
+ * MONO_WEIGHT_MXFP4, router MONO_ROUTER_SOFTMAX, H 3072, E 256, top_k 8, I 384. */
 typedef struct {
   const void* x;        /* bf16 [rows, H] */
   const float* logits;  /* f32 [rows, E] gate logits */
-  const void* w13;      /* u8 [E+1, 2I, H/2] packed E2M1 (even k in the low nibble) */
+  const void* w13;      /* u8 [E+1, 2I, H/2] E2M1 pairs (even k in the low nibble), (16,16)-shuffled */
   const void* s13;      /* u8 [E+1, 2I, H/32] E8M0 */
-  const void* w2;       /* u8 [E+1, H, I/2] */
+  const void* w2;       /* u8 [E+1, H, I/2], (16,16)-shuffled */
   const void* s2;       /* u8 [E+1, H, I/32] */
   void* out;            /* bf16 [rows, H] */
   int32_t rows;

@@ -140,7 +140,7 @@ def mxfp4_moe_block(x, logits, w13, s13, w2, s2, *, top_k=8, inter=384, shared=N
     r_ids, r_w = topk.softmax_topk(logits, top_k)
     if ids is None:
         ids, weights = r_ids, r_w
-    y = torch.zeros(S, w2.shape[1])
+    y = torch.zeros(S, x.shape[1])
     experts = sorted(set(ids.flatten().tolist()) | {shared})
     for e in experts:
         if e == shared:

@@ -132,11 +132,15 @@ static const uint32_t ATTN_MAGIC = 0x6174746eu;
 
 namespace {
 
-int moe_occupancy(int* n) {
+int occ_moe_fp8(int* n) {
   HIP_TRY(mono::moe::moe_fp8_occupancy(n));
   return MONO_OK;
 }
-int attn_occupancy(int* n) {
+int occ_moe_mxfp4(int* n) {
+  HIP_TRY(mono::moe::moe_mxfp4_occupancy(n));
+  return MONO_OK;
+}
+int occ_attn(int* n) {
   HIP_TRY(mono::attn::attn_occupancy(n));
   return MONO_OK;
 }
@@ -198,10 +202,17 @@ extern "C" int mono_moe_create(const mono_moe_config* cfg, mono_moe** out) {
   if (c.router != MONO_ROUTER_SIGMOID_BIAS && c.router != MONO_ROUTER_SOFTMAX)
     return fail(MONO_EINVAL, "unknown router %d", c.router);
   const MoeGeom geo{c.hidden, c.n_experts, c.top_k, c.inter};
-  if (c.weight_format == MONO_WEIGHT_FP8_BLOCK128 && !moe_fp8_supported(geo))
+  const bool fp8 = c.weight_format == MONO_WEIGHT_FP8_BLOCK128;
+  if (fp8 && (!moe_fp8_supported(geo) || c.router != MONO_ROUTER_SIGMOID_BIAS))
     return fail(MONO_EINVAL,
-                "FP8 MoE geometry H=%d E=%d top_k=%d I=%d has no compiled kernel (built: H=7168 E=256 top_k=8 I=512)",
-                c.hidden, c.n_experts, c.top_k, c.inter);
+                "FP8 MoE geometry H=%d E=%d top_k=%d I=%d router %d has no compiled kernel (built: H=7168 E=256 "
+                "top_k=8 I=512, sigmoid + bias router)",
+                c.hidden, c.n_experts, c.top_k, c.inter, c.router);
+  if (!fp8 && (!moe_mxfp4_supported(geo) || c.router != MONO_ROUTER_SOFTMAX))
+    return fail(MONO_EINVAL,
+                "MXFP4 MoE geometry H=%d E=%d top_k=%d I=%d router %d has no compiled kernel (built: H=3072 E=256 "
+                "top_k=8 I=384, softmax router)",
+                c.hidden, c.n_experts, c.top_k, c.inter, c.router);
   if (int rc = check_device(c.device)) return rc;
   const size_t H = c.hidden, E = c.n_experts, I = c.inter;
   const size_t max_act = (size_t)std::min(c.max_rows * c.top_k, c.n_experts) + 1;
@@ -214,7 +225,7 @@ extern "C" int mono_moe_create(const mono_moe_config* cfg, mono_moe** out) {
   mono_moe* m = new mono_moe();
   m->magic = MOE_MAGIC;
   m->cfg = c;
-  if (int rc = m->init(c.device, cv.off, o_guard, moe_occupancy, "MoE")) {
+  if (int rc = m->init(c.device, cv.off, o_guard, fp8 ? occ_moe_fp8 : occ_moe_mxfp4, "MoE")) {
     (void)m->release();
     delete m;
     return rc;
@@ -265,10 +276,21 @@ extern "C" int mono_moe_fp8_forward(mono_moe* m, const mono_moe_fp8_args* args, 
 }
 
 extern "C" int mono_moe_mxfp4_forward(mono_moe* m, const mono_moe_mxfp4_args* args, void* stream) {
-  (void)m;
-  (void)args;
-  (void)stream;
-  return fail(MONO_EINVAL, "mono_moe_mxfp4_forward: not built yet");
+  using namespace mono::moe;
+  if (!args) return fail(MONO_EINVAL, "mono_moe_mxfp4_forward: args is NULL");
+  if (int rc = check_moe(m, args->rows)) return rc;
+  if (m->cfg.weight_format != MONO_WEIGHT_MXFP4 || m->cfg.router != MONO_ROUTER_SOFTMAX)
+    return fail(MONO_ESTATE, "this runtime was created for another weight format / router");
+  REQUIRE_PTR(args->x);
+  REQUIRE_PTR(args->logits);
+  REQUIRE_PTR(args->w13);
+  REQUIRE_PTR(args->s13);
+  REQUIRE_PTR(args->w2);
+  REQUIRE_PTR(args->s2);
+  REQUIRE_PTR(args->out);
+  hipError_t e = moe_mxfp4_forward(*args, m->grid, m->mail, m->guard, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(MONO_EHIP, "launching the MXFP4 MoE: %s", hipGetErrorString(e));
+  return ok();
 }
 
 extern "C" int mono_moe_set_deadline(mono_moe* m, double seconds) {
@@ -316,7 +338,7 @@ extern "C" int mono_attn_create(const mono_attn_config* cfg, mono_attn** out) {
   mono_attn* a = new mono_attn();
   a->magic = ATTN_MAGIC;
   a->cfg = c;
-  if (int rc = a->init(c.device, cv.off, o_guard, attn_occupancy, "attention")) {
+  if (int rc = a->init(c.device, cv.off, o_guard, occ_attn, "attention")) {
     (void)a->release();
     delete a;
     return rc;

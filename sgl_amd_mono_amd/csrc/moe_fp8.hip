@@ -37,6 +37,7 @@
 // contiguous HBM. Each workgroup issues a task's weight loads before it waits on or
 // reduces the previous task, so weights stream while mailboxes are polled.
 #include "common.h"
+#include "moe_common.h"
 #include "moe_ops.h"
 #include "moe_plan.h"
 #include "sync.h"
@@ -79,17 +80,9 @@ struct Lds {
   f32x4 red[2][FW][WAVE];           // cross-wave sums
   uint8_t bq[MAX_ROWS][I];          // a down task's FP8 mid
   float coef[MAX_ROWS][IB];         // its block scale x route weight
-  int32_t expert[MAX_ACT];          // the plan: expert id of each slot
-  uint32_t rowmask[MAX_ACT];        // rows each slot serves
-  int32_t dmap[E];                  // slot of a picked expert
-  int32_t pick_id[MAX_ROWS][TOPK];
-  float pick_w[MAX_ROWS][TOPK];
-  int32_t rowslot[MAX_ROWS][NSLOT]; // a row's slots in plan order
-  uint32_t used[E];
+  PlanLds<E, TOPK> plan;
   uint32_t rkey[E];
   float rraw[E];
-  int32_t wcount[FW];
-  int32_t n_act;
   uint32_t tag;
   uint32_t err;
 };
@@ -114,47 +107,6 @@ struct Args {
   Mail mail;
   GuardArgs guard;
 };
-
-MONO_DEV uint32_t radix_key(float f) {
-  const uint32_t b = __float_as_uint(f);
-  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-}
-
-// Sort a lane's 4 (key desc, id asc) candidates.
-MONO_DEV void sort4(uint32_t (&k)[4], int (&id)[4], float (&raw)[4]) {
-  const int pairs[5][2] = {{0, 1}, {2, 3}, {0, 2}, {1, 3}, {1, 2}};
-#pragma unroll
-  for (int p = 0; p < 5; ++p) {
-    const int x = pairs[p][0], y = pairs[p][1];
-    const bool first = (k[x] > k[y]) || (k[x] == k[y] && id[x] < id[y]);
-    if (!first) {
-      uint32_t tk = k[x]; k[x] = k[y]; k[y] = tk;
-      int ti = id[x]; id[x] = id[y]; id[y] = ti;
-      float tr = raw[x]; raw[x] = raw[y]; raw[y] = tr;
-    }
-  }
-}
-
-// The 32 bytes lane (g, r) holds of 128-k block kb of 16-row group rg of a shuffled
-// [N, K] E4M3 matrix at wb (kdiv32 = K / 32): k = 128 kb + 32 g + [0, 32) of row
-// 16 rg + r, as two nontemporal dwordx4 loads 256 bytes apart.
-MONO_DEV i32x8 ld_shuf(const uint8_t* wb, int kdiv32, int rg, int kb, int g, int r) {
-  const uint8_t* p = wb + (size_t)(rg * kdiv32 + kb * 4 + g) * 512 + r * 16;
-  const u32x4 lo = ld_nt_u32x4(p), hi = ld_nt_u32x4(p + 256);
-  i32x8 v;
-  v[0] = lo[0]; v[1] = lo[1]; v[2] = lo[2]; v[3] = lo[3];
-  v[4] = hi[0]; v[5] = hi[1]; v[6] = hi[2]; v[7] = hi[3];
-  return v;
-}
-
-// 32 bytes of an LDS row as one MFMA operand
-MONO_DEV i32x8 lds32(const uint8_t* p) {
-  const u32x4 lo = *reinterpret_cast<const u32x4*>(p), hi = *reinterpret_cast<const u32x4*>(p + 16);
-  i32x8 v;
-  v[0] = lo[0]; v[1] = lo[1]; v[2] = lo[2]; v[3] = lo[3];
-  v[4] = hi[0]; v[5] = hi[1]; v[6] = hi[2]; v[7] = hi[3];
-  return v;
-}
 
 // bf16(a * rstd * gamma) of 8 consecutive k as one bf16 MFMA operand
 // (stage_x_rmsnorm, kernel.py:1367-1400)
@@ -299,27 +251,9 @@ class Step {
         key[i] = L.rkey[id[i]];
         raw[i] = L.rraw[id[i]];
       }
-      sort4(key, id, raw);
-      float my_raw = 0.f;  // lane k < TOPK: the raw score and id of pick k
-      int my_id = 0;
-      for (int k = 0; k < TOPK; ++k) {
-        const uint32_t m = wave_umax(key[0]);
-        const uint32_t cand = key[0] == m ? 0xffffu - (uint32_t)id[0] : 0u;
-        const int expert = min((int)(0xffffu - wave_umax(cand)), E - 1);
-        const bool hit = key[0] == m && id[0] == expert;
-        const uint64_t bal = __ballot(hit);
-        const int src = __ffsll((long long)bal) - 1;
-        const float rv = __shfl(raw[0], src, WAVE);
-        if (lane == k) {
-          my_raw = rv;
-          my_id = expert;
-        }
-        if (hit) {
-          key[0] = key[1]; key[1] = key[2]; key[2] = key[3]; key[3] = 0u;
-          id[0] = id[1]; id[1] = id[2]; id[2] = id[3]; id[3] = 0xffff;
-          raw[0] = raw[1]; raw[1] = raw[2]; raw[2] = raw[3]; raw[3] = 0.f;
-        }
-      }
+      float my_raw;  // lane k < TOPK: the raw score and id of pick k
+      int my_id;
+      wave_topk<TOPK>(key, id, raw, E, my_id, my_raw);
       // sum of the picks' raw scores in the butterfly order of lanes 0..7
       float tot = lane < TOPK ? my_raw : 0.f;
 #pragma unroll
@@ -385,72 +319,9 @@ class Step {
 
   // ---------------------------------------------------------------- plan
   MONO_DEV bool load_plan() {
-    bool ok = true;
-    for (int e = tid; e < E; e += FT) L.used[e] = 0u;
-    if (tid < S * 2 * MAX_TOPK) {
-      const int s = tid / (2 * MAX_TOPK), k = tid % (2 * MAX_TOPK);
-      if (k % MAX_TOPK < TOPK) {
-        uint32_t v = 0;
-        ok = poll_word(&A.mail.rsel[s * 2 * MAX_TOPK + k], v, W_PICKS, gd);
-        if (k < MAX_TOPK) L.pick_id[s][k] = (int)v;
-        else L.pick_w[s][k - MAX_TOPK] = __uint_as_float(v);
-      }
-    }
-    if (!block_all(ok)) return false;
-    if (tid < S * TOPK) {
-      const int s = tid / TOPK, k = tid % TOPK;
-      atomicOr(&L.used[L.pick_id[s][k]], 1u << s);
-    }
-    __syncthreads();
-    // slot 0: the shared expert (id E) over every row; slots 1..: used experts ascending
-    const bool f = tid < E && L.used[tid] != 0u;
-    const uint64_t bal = __ballot(f);
-    const int before = __popcll(bal & ((1ull << lane) - 1ull));
-    if (lane == 0) L.wcount[wave] = __popcll(bal);
-    __syncthreads();
-    int off = 1;
-    for (int w = 0; w < wave; ++w) off += L.wcount[w];
-    if (f) {
-      const int d = off + before;
-      L.expert[d] = tid;
-      L.rowmask[d] = L.used[tid];
-      L.dmap[tid] = d;
-    }
-    if (tid == 0) {
-      L.expert[0] = E;
-      L.rowmask[0] = (1u << S) - 1u;
-      int n = 1;
-      for (int w = 0; w < FW; ++w) n += L.wcount[w];
-      L.n_act = n;
-    }
-    __syncthreads();
-    if (tid < S) {
-      int sl[NSLOT];
-      sl[0] = 0;
-      for (int k = 0; k < TOPK; ++k) {
-        const int d = L.dmap[L.pick_id[tid][k]];
-        int j = k + 1;
-        while (j > 1 && sl[j - 1] > d) {
-          sl[j] = sl[j - 1];
-          --j;
-        }
-        sl[j] = d;
-      }
-      for (int k = 0; k < NSLOT; ++k) L.rowslot[tid][k] = sl[k];
-    }
-    __syncthreads();
+    if (!build_plan<E, TOPK, FT>(L.plan, A.mail.rsel, S, W_PICKS, gd)) return false;
     plan_ready = true;
     return true;
-  }
-
-  MONO_DEV float route_weight(int d, int s) const {
-    if (d == 0) return 1.0f;
-    const int e = L.expert[d];
-    float w = 0.f;
-#pragma unroll
-    for (int k = 0; k < TOPK; ++k)
-      if (L.pick_id[s][k] == e) w = L.pick_w[s][k];
-    return w;
   }
 
   // ---------------------------------------------------------------- task list
@@ -459,7 +330,7 @@ class Step {
     ok = true;
     if (T < NT) return K_UP;  // the shared expert's tiles need no plan
     if (!plan_ready && !(ok = load_plan())) return K_NONE;
-    const int n_up = L.n_act * NT, n_dn = L.n_act * DN_GROUPS;
+    const int n_up = L.plan.n_act * NT, n_dn = L.plan.n_act * DN_GROUPS;
     if (T < n_up) return K_UP;
     if (T < n_up + n_dn) return K_DOWN;
     if (T < n_up + n_dn + FIN_TASKS) return K_FINAL;
@@ -472,7 +343,7 @@ class Step {
     const i32x8 zero = {};
     if (kind == K_UP) {
       const int d = T / NT, c = T % NT;
-      const int e = d == 0 ? E : L.expert[d];
+      const int e = d == 0 ? E : L.plan.expert[d];
       const uint8_t* wb = A.w13 + (size_t)e * (2 * I) * H;
 #pragma unroll
       for (int j = 0; j < UP_KBW; ++j) {
@@ -481,9 +352,9 @@ class Step {
         W[2 * j + 1] = ld_shuf(wb, H / 32, NT + c, kb, g, r);   // up rows I + 16c..
       }
     } else if (kind == K_DOWN) {
-      const int j = T - L.n_act * NT;
+      const int j = T - L.plan.n_act * NT;
       const int d = j / DN_GROUPS, grp = j % DN_GROUPS;
-      const uint8_t* wb = A.w2 + (size_t)L.expert[d] * H * I;
+      const uint8_t* wb = A.w2 + (size_t)L.plan.expert[d] * H * I;
       const int rg0 = (grp * DN_ROWS + wave * 32) / 16;
 #pragma unroll
       for (int t = 0; t < 2; ++t)
@@ -531,7 +402,7 @@ class Step {
   // ---------------------------------------------------------------- up
   MONO_DEV void up_compute(int T, f32x4& ag, f32x4& au) {
     const int d = T / NT, c = T % NT;
-    const int e = d == 0 ? E : L.expert[d];
+    const int e = d == 0 ? E : L.plan.expert[d];
     const float* sg = A.s13 + ((size_t)e * (2 * I / 128) + c / 8) * KB;
     const float* su = A.s13 + ((size_t)e * (2 * I / 128) + I / 128 + c / 8) * KB;
     ag = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -551,7 +422,7 @@ class Step {
 
   MONO_DEV void up_publish(int T, const f32x4& ag, const f32x4& au) {
     const int d = T / NT, c = T % NT;
-    const uint32_t mask = d == 0 ? (1u << S) - 1u : L.rowmask[d];
+    const uint32_t mask = d == 0 ? (1u << S) - 1u : L.plan.rowmask[d];
     L.red[0][wave][lane] = ag;
     L.red[1][wave][lane] = au;
     __syncthreads();
@@ -571,10 +442,10 @@ class Step {
 
   // ---------------------------------------------------------------- down
   MONO_DEV bool down_compute(int T, f32x4 (&acc)[2]) {
-    const int j = T - L.n_act * NT;
+    const int j = T - L.plan.n_act * NT;
     const int d = j / DN_GROUPS, grp = j % DN_GROUPS;
-    const int e = L.expert[d];
-    const uint32_t mask = L.rowmask[d];
+    const int e = L.plan.expert[d];
+    const uint32_t mask = L.plan.rowmask[d];
     // thread (row s, 16-channel group cg) polls its 16 contiguous mid words; 8 groups
     // (8 consecutive lanes) make a 128-channel quantisation block
     constexpr int CG = 16;
@@ -601,7 +472,7 @@ class Step {
       }
       *reinterpret_cast<u32x4*>(&L.bq[s][cg * CG]) = packed;
       if ((cg % (128 / CG)) == 0)
-        L.coef[s][cg / (128 / CG)] = in ? (nz ? am * (1.0f / FP8_MAX) : 1.0f) * route_weight(d, s) : 0.f;
+        L.coef[s][cg / (128 / CG)] = in ? (nz ? am * (1.0f / FP8_MAX) : 1.0f) * route_weight(L.plan, d, s) : 0.f;
     }
     __syncthreads();
     const float* ws = A.s2 + ((size_t)e * (H / 128) + (grp * DN_ROWS + wave * 32) / 128) * IB;
@@ -620,9 +491,9 @@ class Step {
   }
 
   MONO_DEV void down_publish(int T, const f32x4 (&acc)[2]) {
-    const int j = T - L.n_act * NT;
+    const int j = T - L.plan.n_act * NT;
     const int d = j / DN_GROUPS, grp = j % DN_GROUPS;
-    const uint32_t mask = L.rowmask[d];
+    const uint32_t mask = L.plan.rowmask[d];
     if ((mask >> r) & 1u) {
 #pragma unroll
       for (int t = 0; t < 2; ++t)
@@ -637,12 +508,12 @@ class Step {
 
   // ---------------------------------------------------------------- final
   MONO_DEV bool final_task(int T) {
-    const int f = T - L.n_act * (NT + DN_GROUPS);
+    const int f = T - L.plan.n_act * (NT + DN_GROUPS);
     bool ok = true;
     if (tid < S * FIN_ROWS) {
       const int s = tid / FIN_ROWS, h = f * FIN_ROWS + tid % FIN_ROWS;
       const uint64_t* base = &A.mail.ypart[(size_t)s * H + h];
-      const int32_t* slots = L.rowslot[s];
+      const int32_t* slots = L.plan.rowslot[s];
       uint32_t v[NSLOT];
       ok = poll_words<NSLOT>([base, slots](int k) { return base + (size_t)slots[k] * MAX_ROWS * H; }, v,
                              (1u << NSLOT) - 1u, W_YPART, gd);

@@ -29,5 +29,10 @@ hipError_t moe_fp8_occupancy(int* blocks_per_cu);
 // Enqueue the one persistent launch on `st` with `grid` workgroups (one a CU).
 hipError_t moe_fp8_forward(const MoeFp8Args& g, int grid, const Mail& mail, const GuardArgs& guard, hipStream_t st);
 
+bool moe_mxfp4_supported(const MoeGeom& geo);
+hipError_t moe_mxfp4_occupancy(int* blocks_per_cu);
+hipError_t moe_mxfp4_forward(const mono_moe_mxfp4_args& g, int grid, const Mail& mail, const GuardArgs& guard,
+                             hipStream_t st);
+
 }  // namespace moe
 }  // namespace mono

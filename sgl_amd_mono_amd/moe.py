@@ -53,10 +53,10 @@ class Fp8MoeWeights:
 
 @dataclass
 class Mxfp4MoeWeights:
-    w13: torch.Tensor  # uint8 [E+1, 2I, H/2] packed E2M1
+    w13: torch.Tensor  # uint8 [E+1, 2I, H/2] packed E2M1, AITER (16, 16) layout
     s13: torch.Tensor  # uint8 [E+1, 2I, H/32] E8M0
-    w2: torch.Tensor  # uint8 [E+1, H, I/2]
-    s2: torch.Tensor  # uint8 [E+1, H, I/32]
+    w2: torch.Tensor  # uint8 [E+1, H, I/2] packed E2M1, AITER (16, 16) layout
+    s2: torch.Tensor  # uint8 [E+1, H, I/32] E8M0
 
 
 FP8_TYPES = (torch.float8_e4m3fn, torch.uint8)

@@ -54,15 +54,16 @@ def rows_bf16(rows: int, hidden: int, device, seed: int) -> torch.Tensor:
 
 
 def mxfp4_moe_weights(geo: MoeGeometry, device, seed: int = 0) -> Mxfp4MoeWeights:
-    """MXFP4 experts: uniform random E2M1 code bytes, E8M0 scales uniform in [119, 123)
-    (test_minimax_m31_ffn.py:47-51: 'e8m0 codes around 2^-7')."""
+    """MXFP4 experts: uniform random E2M1 code bytes in AITER's (16, 16) layout, E8M0
+    scales uniform in [119, 123) (test_minimax_m31_ffn.py:47-51: 'e8m0 codes around
+    2^-7')."""
     H, E, I = geo.hidden, geo.n_experts, geo.inter
     g = _gen(device, seed)
     u8 = dict(generator=g, device=device, dtype=torch.uint8)
     return Mxfp4MoeWeights(
-        w13=torch.randint(0, 256, (E + 1, 2 * I, H // 2), **u8),
+        w13=shuffle_16x16(torch.randint(0, 256, (E + 1, 2 * I, H // 2), **u8)),
         s13=torch.randint(119, 123, (E + 1, 2 * I, H // 32), **u8),
-        w2=torch.randint(0, 256, (E + 1, H, I // 2), **u8),
+        w2=shuffle_16x16(torch.randint(0, 256, (E + 1, H, I // 2), **u8)),
         s2=torch.randint(119, 123, (E + 1, H, I // 32), **u8),
     )
 
