@@ -20,7 +20,9 @@
  *   - Glm53LayerOp.launch(h, caches, cos, sin, step)    glm53/gfx950/runner.py:240-321
  *       (rt.dispatch of 42 raw data_ptr() ints + stream)
  *       -> mono_moe_fp8_forward  (its MoE half, stages 8-10, kernel.py:4199-5187)
- *       -> mono_attn_forward     (its sparse-attention half, kernel.py:2684-4123)
+ *       -> mono_front_forward    (its projections up to the index query, kernel.py:1367-2443)
+       -> mono_attn_forward     (its sparse-attention half, kernel.py:2684-4123)
+       -> mono_back_forward     (W_UV, o_proj and the residual, kernel.py:3975-4197)
  *   - minimax_m31 FFN launch, A16W4 experts              minimax_m31/ffn.py:1182-1378
  *       -> mono_moe_mxfp4_forward
  *   - guard error words read back by tests              common/guard.py:16-30,100-241
@@ -209,6 +211,97 @@ int mono_attn_set_deadline(mono_attn* attn, double seconds);
 int mono_attn_read_errors(mono_attn* attn, int32_t* words);
 int mono_attn_clear_errors(mono_attn* attn);
 int mono_attn_set_fault(mono_attn* attn, int32_t site);
+
+/* ---------------------------------------------------------------- projections
+ * The attention block's projections around the sparse-attention phase, one GPU's
+ * TP=4 share of a DeepSeek-V3.2-shaped layer (hidden 7168, q_lora 1536, kv_lora 512,
+ * 32 heads of 128 nope + 64 rope dims, value dim 128, FP4 indexer of 64 heads x 128).
+ *
+ * mono_front_forward: one persistent launch (glm53/gfx950/kernel.py:1367-2443 with the
+ * FP4 indexer of deepseek_v4/gfx950/kernels/stages/indexer.py:236-408): input RMSNorm,
+ * q_a | kv_a and index key / head-weight projections, q_a RMSNorm, q_b + RoPE, the
+ * absorbed query W_UK^T q_nope, KV RMSNorm + k_pe RoPE + the FP8 MLA cache row, the
+ * index key (LayerNorm, RoPE, Hadamard, FP4) into the index plane, and the index
+ * query (RoPE, Hadamard, FP4) and head weights: exactly mono_attn_args' inputs.
+ *
+ * mono_back_forward: one persistent launch (kernel.py:3975-4197 after the split
+ * merge): o = W_UV o_lat per head, then a = h + W_o o (the TP all-reduce is a local
+ * residual add).
+ *
+ * FP8 matrices are E4M3 in AITER's (16, 16) layout ([N/16, K/32, 2, 16, 16] bytes)
+ * with f32 128 x 128 block scales, row-major [ceil(N/128), K/128]; they are widened
+ * exactly to bf16 and multiplied with bf16 activations, f32 accumulation. */
+typedef struct mono_proj mono_proj;
+
+typedef struct {
+  int device;
+  int max_rows; /* widest step, 1..16 */
+} mono_proj_config;
+
+typedef struct {
+  const void* g_in;   /* bf16 [7168] input RMSNorm weight */
+  const void* w_qkv;  /* e4m3 [2112, 7168]: q_a 1536 | kv latent 512 | k_pe 64 */
+  const float* s_qkv; /* [17, 56] */
+  const void* w_ik;   /* e4m3 [128, 7168] index key */
+  const float* s_ik;  /* [1, 56] */
+  const void* w_iw;   /* bf16 [64, 7168] index head weights, (16, 16) layout of its bytes */
+  const void* g_q;    /* bf16 [1536] q_a RMSNorm weight */
+  const void* g_kv;   /* bf16 [512] KV RMSNorm weight */
+  const float* g_ik;  /* f32 [128] index key LayerNorm weight */
+  const float* b_ik;  /* f32 [128] index key LayerNorm bias */
+  const void* w_qb;   /* e4m3 [6144, 1536]: rows h*192 + (nope 0..127 | pe 128..191) */
+  const float* s_qb;  /* [48, 12] */
+  const void* w_iq;   /* e4m3 [8192, 1536]: rows h*128 + d */
+  const float* s_iq;  /* [64, 12] */
+  const void* w_uk;   /* e4m3 [16384, 128]: rows h*512 + c, W_UK^T (q_lat = W q_nope) */
+  const float* s_uk;  /* [128, 1] */
+  const void* w_uv;   /* e4m3 [4096, 512]: rows h*128 + v */
+  const float* s_uv;  /* [32, 4] */
+  const void* w_o;    /* e4m3 [7168, 4096] */
+  const float* s_o;   /* [56, 32] */
+} mono_proj_weights;
+
+typedef struct {
+  const void* h;             /* bf16 [rows, 7168] residual stream */
+  const int32_t* seq_lens;   /* [rows] keys of a row counting this step's token, which
+                                sits at position seq_len - 1; a row outside
+                                [1, min(max_pos, pt_stride * 64)] is a pad row: it
+                                writes no cache row */
+  const int32_t* page_table; /* [rows, pt_stride] */
+  int pt_stride;
+  int n_pages;               /* pages of the caches (a page id >= n_pages: pad row) */
+  const float* rope_cos;     /* f32 [max_pos, 32] */
+  const float* rope_sin;     /* f32 [max_pos, 32] */
+  int max_pos;
+  void* ikv;                 /* u8 [n_pages, 4, 64, 16] index plane, written in place */
+  void* iks;                 /* u8 [n_pages, 4, 64] */
+  void* kv;                  /* u8 [n_pages * 64, 576] MLA cache, written in place */
+  float* kv_scale;           /* f32 [n_pages * 64] */
+  void* q;                   /* out bf16 [rows, 32, 576] q_lat | q_pe */
+  void* iq;                  /* out u8 [rows, 64, 64] E2M1 index query */
+  void* iqs;                 /* out u8 [rows, 64, 4] E8M0 */
+  void* iw;                  /* out bf16 [rows, 64] index head weights */
+  int rows;
+} mono_front_args;
+
+typedef struct {
+  const void* o_lat; /* bf16 [rows, 32, 512] the attention phase's output */
+  const void* h;     /* bf16 [rows, 7168] residual stream */
+  void* a;           /* out bf16 [rows, 7168] h + W_o W_UV o_lat */
+  void* o;           /* optional out bf16 [rows, 4096] W_UV o_lat (NULL: not written) */
+  int rows;
+} mono_back_args;
+
+/* Wait sites of the projection launches: 0 stage-A partials, 1 q_an, 2 q_nope,
+ * 3 raw index query, 4 W_UV output. */
+int mono_proj_create(const mono_proj_config* cfg, mono_proj** out);
+int mono_proj_destroy(mono_proj* proj);
+int mono_front_forward(mono_proj* proj, const mono_proj_weights* w, const mono_front_args* args, void* stream);
+int mono_back_forward(mono_proj* proj, const mono_proj_weights* w, const mono_back_args* args, void* stream);
+int mono_proj_set_deadline(mono_proj* proj, double seconds);
+int mono_proj_read_errors(mono_proj* proj, int32_t* words);
+int mono_proj_clear_errors(mono_proj* proj);
+int mono_proj_set_fault(mono_proj* proj, int32_t site);
 
 #ifdef __cplusplus
 }

@@ -56,6 +56,33 @@ class AttnArgs(C.Structure):
     ]
 
 
+class ProjConfig(C.Structure):
+    _fields_ = [("device", _I32), ("max_rows", _I32)]
+
+
+PROJ_WEIGHT_FIELDS = (
+    "g_in", "w_qkv", "s_qkv", "w_ik", "s_ik", "w_iw", "g_q", "g_kv", "g_ik", "b_ik",
+    "w_qb", "s_qb", "w_iq", "s_iq", "w_uk", "s_uk", "w_uv", "s_uv", "w_o", "s_o",
+)
+
+
+class ProjWeights(C.Structure):
+    _fields_ = [(n, _VP) for n in PROJ_WEIGHT_FIELDS]
+
+
+class FrontArgs(C.Structure):
+    _fields_ = [
+        ("h", _VP), ("seq_lens", _VP), ("page_table", _VP), ("pt_stride", _I32), ("n_pages", _I32),
+        ("rope_cos", _VP), ("rope_sin", _VP), ("max_pos", _I32),
+        ("ikv", _VP), ("iks", _VP), ("kv", _VP), ("kv_scale", _VP),
+        ("q", _VP), ("iq", _VP), ("iqs", _VP), ("iw", _VP), ("rows", _I32),
+    ]
+
+
+class BackArgs(C.Structure):
+    _fields_ = [("o_lat", _VP), ("h", _VP), ("a", _VP), ("o", _VP), ("rows", _I32)]
+
+
 # entry point -> (restype, argtypes); every name include/mono.h declares
 SIGNATURES = {
     "mono_abi_version": (C.c_int, []),
@@ -75,11 +102,20 @@ SIGNATURES = {
     "mono_attn_read_errors": (C.c_int, [_VP, C.POINTER(C.c_int32)]),
     "mono_attn_clear_errors": (C.c_int, [_VP]),
     "mono_attn_set_fault": (C.c_int, [_VP, C.c_int32]),
+    "mono_proj_create": (C.c_int, [C.POINTER(ProjConfig), C.POINTER(_VP)]),
+    "mono_proj_destroy": (C.c_int, [_VP]),
+    "mono_front_forward": (C.c_int, [_VP, C.POINTER(ProjWeights), C.POINTER(FrontArgs), _VP]),
+    "mono_back_forward": (C.c_int, [_VP, C.POINTER(ProjWeights), C.POINTER(BackArgs), _VP]),
+    "mono_proj_set_deadline": (C.c_int, [_VP, C.c_double]),
+    "mono_proj_read_errors": (C.c_int, [_VP, C.POINTER(C.c_int32)]),
+    "mono_proj_clear_errors": (C.c_int, [_VP]),
+    "mono_proj_set_fault": (C.c_int, [_VP, C.c_int32]),
 }
 GUARD_WORDS = 4
 # wait sites of the launches (guard word 1 = site + 1)
 MOE_SITES = {0: "router logits", 1: "route picks", 2: "expert mid activations", 3: "expert outputs"}
 ATTN_SITES = {0: "index scores", 1: "selected slots", 2: "split partials", 3: "top-k team"}
+PROJ_SITES = {0: "stage-A partial sums", 1: "normed q_a", 2: "q_nope", 3: "raw index query", 4: "W_UV output"}
 
 _lock = threading.Lock()
 _lib = None

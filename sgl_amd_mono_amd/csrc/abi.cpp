@@ -16,6 +16,7 @@
 #include "attn_ops.h"
 #include "mono.h"
 #include "moe_ops.h"
+#include "proj_ops.h"
 
 namespace {
 
@@ -127,8 +128,14 @@ struct mono_attn : RuntimeBase {
   mono::attn::Mail mail;
 };
 
+struct mono_proj : RuntimeBase {
+  mono_proj_config cfg;
+  mono::proj::Mail mail;
+};
+
 static const uint32_t MOE_MAGIC = 0x6d6f6531u;
 static const uint32_t ATTN_MAGIC = 0x6174746eu;
+static const uint32_t PROJ_MAGIC = 0x70726f6au;
 
 namespace {
 
@@ -138,6 +145,13 @@ int occ_moe_fp8(int* n) {
 }
 int occ_moe_mxfp4(int* n) {
   HIP_TRY(mono::moe::moe_mxfp4_occupancy(n));
+  return MONO_OK;
+}
+int occ_proj(int* n) {
+  int a = 0, b = 0;
+  HIP_TRY(mono::proj::front_occupancy(&a));
+  HIP_TRY(mono::proj::back_occupancy(&b));
+  *n = std::min(a, b);
   return MONO_OK;
 }
 int occ_attn(int* n) {
@@ -414,4 +428,128 @@ extern "C" int mono_attn_read_errors(mono_attn* a, int32_t* words) {
 extern "C" int mono_attn_clear_errors(mono_attn* a) {
   if (!live(a, ATTN_MAGIC)) return fail(MONO_ESTATE, "not a live attention runtime");
   return guard_clear(a);
+}
+
+// ------------------------------------------------------------------ projection runtime
+
+extern "C" int mono_proj_create(const mono_proj_config* cfg, mono_proj** out) {
+  using namespace mono::proj;
+  if (!cfg || !out) return fail(MONO_EINVAL, "mono_proj_create: cfg and out must be non-NULL");
+  *out = nullptr;
+  const mono_proj_config& c = *cfg;
+  if (c.max_rows < 1 || c.max_rows > MAX_ROWS)
+    return fail(MONO_EINVAL, "max_rows must be in [1, %d], got %d", MAX_ROWS, c.max_rows);
+  if (int rc = check_device(c.device)) return rc;
+  Carve cv;
+  const size_t o_guard = cv.take(mono::G_WORDS * 4);
+  size_t o_mb[5];
+  for (int i = 0; i < 5; ++i) o_mb[i] = cv.take(MAIL_WORDS[i] * 8);
+  mono_proj* p = new mono_proj();
+  p->magic = PROJ_MAGIC;
+  p->cfg = c;
+  if (int rc = p->init(c.device, cv.off, o_guard, occ_proj, "projection")) {
+    (void)p->release();
+    delete p;
+    return rc;
+  }
+  p->mail.guard = p->guard.words;
+  p->mail.pa = reinterpret_cast<uint64_t*>(p->at(o_mb[0]));
+  p->mail.qan = reinterpret_cast<uint64_t*>(p->at(o_mb[1]));
+  p->mail.qnope = reinterpret_cast<uint64_t*>(p->at(o_mb[2]));
+  p->mail.iqraw = reinterpret_cast<uint64_t*>(p->at(o_mb[3]));
+  p->mail.ob = reinterpret_cast<uint64_t*>(p->at(o_mb[4]));
+  *out = p;
+  return ok();
+}
+
+extern "C" int mono_proj_destroy(mono_proj* p) {
+  if (!p) return ok();
+  if (!live(p, PROJ_MAGIC)) return fail(MONO_ESTATE, "mono_proj_destroy: not a live projection runtime");
+  const int rc = p->release();
+  delete p;
+  return rc ? rc : ok();
+}
+
+static int check_proj(const mono_proj* p, const mono_proj_weights* w, int rows) {
+  if (!live(p, PROJ_MAGIC)) return fail(MONO_ESTATE, "not a live projection runtime");
+  if (!w) return fail(MONO_EINVAL, "weights is NULL");
+  if (rows < 1 || rows > p->cfg.max_rows)
+    return fail(MONO_EINVAL, "rows must be in [1, %d] (the runtime's max_rows), got %d", p->cfg.max_rows, rows);
+  return check_device(p->device);
+}
+
+extern "C" int mono_front_forward(mono_proj* p, const mono_proj_weights* w, const mono_front_args* args,
+                                  void* stream) {
+  if (!args) return fail(MONO_EINVAL, "mono_front_forward: args is NULL");
+  if (int rc = check_proj(p, w, args->rows)) return rc;
+  REQUIRE_PTR(w->g_in);
+  REQUIRE_PTR(w->w_qkv);
+  REQUIRE_PTR(w->s_qkv);
+  REQUIRE_PTR(w->w_ik);
+  REQUIRE_PTR(w->s_ik);
+  REQUIRE_PTR(w->w_iw);
+  REQUIRE_PTR(w->g_q);
+  REQUIRE_PTR(w->g_kv);
+  REQUIRE_PTR(w->g_ik);
+  REQUIRE_PTR(w->b_ik);
+  REQUIRE_PTR(w->w_qb);
+  REQUIRE_PTR(w->s_qb);
+  REQUIRE_PTR(w->w_iq);
+  REQUIRE_PTR(w->s_iq);
+  REQUIRE_PTR(w->w_uk);
+  REQUIRE_PTR(w->s_uk);
+  REQUIRE_PTR(args->h);
+  REQUIRE_PTR(args->seq_lens);
+  REQUIRE_PTR(args->page_table);
+  REQUIRE_PTR(args->rope_cos);
+  REQUIRE_PTR(args->rope_sin);
+  REQUIRE_PTR(args->ikv);
+  REQUIRE_PTR(args->iks);
+  REQUIRE_PTR(args->kv);
+  REQUIRE_PTR(args->kv_scale);
+  REQUIRE_PTR(args->q);
+  REQUIRE_PTR(args->iq);
+  REQUIRE_PTR(args->iqs);
+  REQUIRE_PTR(args->iw);
+  if (args->pt_stride < 1) return fail(MONO_EINVAL, "pt_stride must be positive, got %d", args->pt_stride);
+  if (args->n_pages < 1) return fail(MONO_EINVAL, "n_pages must be positive, got %d", args->n_pages);
+  if (args->max_pos < 1) return fail(MONO_EINVAL, "max_pos must be positive, got %d", args->max_pos);
+  hipError_t e = mono::proj::front_forward(*w, *args, p->grid, p->mail, p->guard, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(MONO_EHIP, "launching the front projections: %s", hipGetErrorString(e));
+  return ok();
+}
+
+extern "C" int mono_back_forward(mono_proj* p, const mono_proj_weights* w, const mono_back_args* args, void* stream) {
+  if (!args) return fail(MONO_EINVAL, "mono_back_forward: args is NULL");
+  if (int rc = check_proj(p, w, args->rows)) return rc;
+  REQUIRE_PTR(w->w_uv);
+  REQUIRE_PTR(w->s_uv);
+  REQUIRE_PTR(w->w_o);
+  REQUIRE_PTR(w->s_o);
+  REQUIRE_PTR(args->o_lat);
+  REQUIRE_PTR(args->h);
+  REQUIRE_PTR(args->a);
+  hipError_t e = mono::proj::back_forward(*w, *args, p->grid, p->mail, p->guard, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(MONO_EHIP, "launching the output projections: %s", hipGetErrorString(e));
+  return ok();
+}
+
+extern "C" int mono_proj_set_deadline(mono_proj* p, double seconds) {
+  if (!live(p, PROJ_MAGIC)) return fail(MONO_ESTATE, "not a live projection runtime");
+  return guard_set_deadline(p, seconds);
+}
+
+extern "C" int mono_proj_set_fault(mono_proj* p, int32_t site) {
+  if (!live(p, PROJ_MAGIC)) return fail(MONO_ESTATE, "not a live projection runtime");
+  return guard_set_fault(p, site);
+}
+
+extern "C" int mono_proj_read_errors(mono_proj* p, int32_t* words) {
+  if (!live(p, PROJ_MAGIC)) return fail(MONO_ESTATE, "not a live projection runtime");
+  return guard_read(p, words);
+}
+
+extern "C" int mono_proj_clear_errors(mono_proj* p) {
+  if (!live(p, PROJ_MAGIC)) return fail(MONO_ESTATE, "not a live projection runtime");
+  return guard_clear(p);
 }

@@ -1,0 +1,198 @@
+// Back of the attention block on gfx950 as ONE persistent launch (one 512-thread
+// workgroup per CU, tasks dealt round-robin, tagged mailboxes between the stages):
+//   U  (head): o[:, h] = bf16(W_UV[h] o_lat[:, h]), 8 row groups of 16, one a wave,
+//      K = 512 in 4 steps -> mailbox ob (bf16 pairs)
+//   O  (32-row tile) of W_o [7168, 4096]: 4 waves a row group, 8 128-k steps a wave,
+//      against o staged in LDS; a = bf16(h + W_o o)
+// (glm53/gfx950/kernel.py:3975-4197; the attention TP reduce there is the local
+// residual add here.)
+#include "common.h"
+#include "proj_common.h"
+#include "proj_ops.h"
+#include "sync.h"
+
+namespace mono {
+namespace proj {
+
+namespace {
+
+constexpr int FT = 512;
+constexpr int FW = FT / WAVE;
+constexpr int O_K = HEADS * VDIM;         // 4096
+constexpr int NT_O = HIDDEN / 32;         // 224 tiles of 32 rows
+constexpr int XU = KV_LORA + 8;
+constexpr int XO = O_K + 8;
+constexpr int W_OB = 4;
+
+struct Lds {
+  union {
+    uint16_t xu[MAX_ROWS][XU];
+    uint16_t xo[MAX_ROWS][XO];
+  } u;
+  f32x4 red[FW][WAVE];
+  uint32_t tag;
+  uint32_t err;
+};
+
+struct Args {
+  mono_proj_weights w;
+  mono_back_args a;
+  Mail mail;
+  GuardArgs guard;
+};
+
+class Back {
+ public:
+  MONO_DEV Back(const Args& args, Lds& l) : W(args.w), A(args.a), M(args.mail), L(l) {
+    tid = threadIdx.x;
+    lane = tid % WAVE;
+    wave = tid / WAVE;
+    g = lane / 16;
+    r = lane % 16;
+    G = gridDim.x;
+    S = A.rows;
+    guard_args = args.guard;
+  }
+
+  MONO_DEV void run() {
+    if (tid == 0) {
+      const uint32_t ticket = __hip_atomic_fetch_add(&guard_args.words[G_TICKET], 1u, __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT);
+      L.tag = ticket / (uint32_t)G + 1u;
+      L.err = ld_agent_u32(&guard_args.words[G_ERROR]);
+    }
+    __syncthreads();
+    if (L.err != 0) return;
+    gd.a = guard_args;
+    gd.tag = L.tag;
+    gd.deadline = now_ticks() + guard_args.deadline_ticks;
+    for (int T = blockIdx.x; T < HEADS + NT_O; T += G) {
+      if (T < HEADS) {
+        stage_u(T);
+      } else if (!stage_o(T - HEADS)) {
+        return;
+      }
+    }
+  }
+
+ private:
+  const mono_proj_weights& W;
+  const mono_back_args& A;
+  const Mail& M;
+  Lds& L;
+  GuardArgs guard_args;
+  Guard gd;
+  int tid, lane, wave, g, r, G, S;
+
+  MONO_DEV void stage_u(int h) {
+    u32x4 WR[8];
+    float SC[4];
+    const int rg = (VDIM / 16) * h + wave;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      ld_fp8_tile(static_cast<const uint8_t*>(W.w_uv), KV_LORA / 32, rg, j, g, r, WR[2 * j], WR[2 * j + 1]);
+      SC[j] = W.s_uv[(rg * 16 / 128) * (KV_LORA / 128) + j];
+    }
+    const uint16_t* olat = static_cast<const uint16_t*>(A.o_lat);
+    for (int f = tid; f < S * (KV_LORA / 8); f += FT) {
+      const int s = f / (KV_LORA / 8), p = f % (KV_LORA / 8);
+      *reinterpret_cast<u32x4*>(&L.u.xu[s][8 * p]) = ld_u32x4(olat + ((size_t)s * HEADS + h) * KV_LORA + 8 * p);
+    }
+    __syncthreads();
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc += SC[j] * step_fp8(join(WR[2 * j], WR[2 * j + 1]), &L.u.xu[r][128 * j + 32 * g]);
+    if (r < S) {
+      const int v = h * VDIM + 16 * wave + 4 * g;  // output channel of o
+      const uint32_t w0 = pack_bf16x2(acc[0], acc[1]), w1 = pack_bf16x2(acc[2], acc[3]);
+      mb_put(&M.ob[(size_t)r * (O_K / 2) + v / 2], w0, gd.tag);
+      mb_put(&M.ob[(size_t)r * (O_K / 2) + v / 2 + 1], w1, gd.tag);
+      if (A.o) {
+        u32x2 o;
+        o[0] = w0;
+        o[1] = w1;
+        *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(A.o) + (size_t)r * O_K + v) = o;
+      }
+    }
+    __syncthreads();  // the next task rewrites the LDS
+  }
+
+  MONO_DEV bool stage_o(int t) {
+    u32x4 WR[16];
+    float SC[8];
+    const int rg = 2 * t + wave / 4;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int ks = (wave % 4) * 8 + j;
+      ld_fp8_tile(static_cast<const uint8_t*>(W.w_o), O_K / 32, rg, ks, g, r, WR[2 * j], WR[2 * j + 1]);
+      SC[j] = W.s_o[(rg * 16 / 128) * (O_K / 128) + ks];
+    }
+    // o of every row: S x 2048 bf16 pairs
+    const int total = S * (O_K / 2);
+    for (int base = 0; base < total; base += FT * 8) {
+      uint32_t v[8];
+      uint32_t pending = 0;
+#pragma unroll
+      for (int q = 0; q < 8; ++q)
+        if (base + tid + FT * q < total) pending |= 1u << q;
+      const uint64_t* ob = M.ob + base + tid;
+      const bool ok = poll_words<8>([ob](int q) { return ob + FT * q; }, v, pending, W_OB, gd);
+      if (!block_all(ok)) return false;
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const int w = base + tid + FT * q;
+        if (w < total) *reinterpret_cast<uint32_t*>(&L.u.xo[w / (O_K / 2)][2 * (w % (O_K / 2))]) = v[q];
+      }
+    }
+    __syncthreads();
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int ks = (wave % 4) * 8 + j;
+      acc += SC[j] * step_fp8(join(WR[2 * j], WR[2 * j + 1]), &L.u.xo[r][128 * ks + 32 * g]);
+    }
+    L.red[wave][lane] = acc;
+    __syncthreads();
+    {
+      const int rgl = tid / 256, l = (tid / 4) % WAVE, i = tid % 4;
+      float y = 0.f;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) y += L.red[4 * rgl + k][l][i];
+      const int s = l % 16, row = 32 * t + 16 * rgl + 4 * (l / 16) + i;
+      if (s < S) {
+        const size_t at = (size_t)s * HIDDEN + row;
+        const float hv = bf16_bits_to_f32(static_cast<const uint16_t*>(A.h)[at]);
+        static_cast<uint16_t*>(A.a)[at] = f32_to_bf16_bits(__fadd_rn(hv, y));
+      }
+    }
+    __syncthreads();
+    return true;
+  }
+};
+
+__global__ __launch_bounds__(FT, 1) void k_back(Args args) {
+  __shared__ Lds lds;
+  Back b(args, lds);
+  b.run();
+}
+
+}  // namespace
+
+hipError_t back_occupancy(int* blocks_per_cu) {
+  return hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, k_back, FT, 0);
+}
+
+hipError_t back_forward(const mono_proj_weights& w, const mono_back_args& a, int grid, const Mail& mail,
+                        const GuardArgs& guard, hipStream_t st) {
+  if (a.rows < 1 || a.rows > MAX_ROWS || grid < 1) return hipErrorInvalidConfiguration;
+  Args args;
+  args.w = w;
+  args.a = a;
+  args.mail = mail;
+  args.guard = guard;
+  k_back<<<grid, FT, 0, st>>>(args);
+  return hipGetLastError();
+}
+
+}  // namespace proj
+}  // namespace mono

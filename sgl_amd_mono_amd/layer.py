@@ -1,0 +1,192 @@
+"""Host side of the attention block's projections (and, through them, the whole layer).
+
+``ProjRuntime`` owns the projection launches' mailboxes and guard, as the reference's
+``Glm53Runtime`` owns its scratch (sgl_amd_mono/glm53/gfx950/runner.py:133-215);
+``front`` and ``back`` check SGLang-shaped tensors and dispatch raw pointers as
+``Glm53LayerOp.launch`` does (runner.py:240-321):
+
+* ``front``: rows h -> the attention phase's inputs (q, FP4 index query + scales,
+  index head weights), writing this step's MLA cache row and FP4 index key in place.
+* ``back``: the attention output o_lat -> a = h + W_o W_UV o_lat.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass, fields
+
+import torch
+
+from . import _lib
+from .attn import AttnCaches
+from .runtime import Runtime, need
+
+HIDDEN, Q_LORA, KV_LORA, PE_DIM = 7168, 1536, 512, 64
+HEADS, NOPE_DIM, V_DIM = 32, 128, 128
+QK_DIM = NOPE_DIM + PE_DIM
+INDEX_HEADS, INDEX_DIM = 64, 128
+N_QKV = Q_LORA + KV_LORA + PE_DIM
+MAX_ROWS = 16
+
+
+def _blocks(n: int) -> int:
+    return -(-n // 128)
+
+
+# name -> (shape, dtype); FP8 matrices are E4M3 bytes in AITER's (16, 16) layout with
+# f32 [ceil(N/128), K/128] block scales; w_iw is bf16 whose bytes are (16, 16)-shuffled
+WEIGHT_SPECS = {
+    "g_in": ((HIDDEN,), torch.bfloat16),
+    "w_qkv": ((N_QKV, HIDDEN), torch.uint8),
+    "s_qkv": ((_blocks(N_QKV), HIDDEN // 128), torch.float32),
+    "w_ik": ((INDEX_DIM, HIDDEN), torch.uint8),
+    "s_ik": ((1, HIDDEN // 128), torch.float32),
+    "w_iw": ((INDEX_HEADS, HIDDEN), torch.bfloat16),
+    "g_q": ((Q_LORA,), torch.bfloat16),
+    "g_kv": ((KV_LORA,), torch.bfloat16),
+    "g_ik": ((INDEX_DIM,), torch.float32),
+    "b_ik": ((INDEX_DIM,), torch.float32),
+    "w_qb": ((HEADS * QK_DIM, Q_LORA), torch.uint8),
+    "s_qb": ((HEADS * QK_DIM // 128, Q_LORA // 128), torch.float32),
+    "w_iq": ((INDEX_HEADS * INDEX_DIM, Q_LORA), torch.uint8),
+    "s_iq": ((INDEX_HEADS * INDEX_DIM // 128, Q_LORA // 128), torch.float32),
+    "w_uk": ((HEADS * KV_LORA, NOPE_DIM), torch.uint8),
+    "s_uk": ((HEADS * KV_LORA // 128, 1), torch.float32),
+    "w_uv": ((HEADS * V_DIM, KV_LORA), torch.uint8),
+    "s_uv": ((HEADS * V_DIM // 128, KV_LORA // 128), torch.float32),
+    "w_o": ((HIDDEN, HEADS * V_DIM), torch.uint8),
+    "s_o": ((HIDDEN // 128, HEADS * V_DIM // 128), torch.float32),
+}
+
+
+@dataclass
+class ProjWeights:
+    """One layer's attention-block projection weights (device tensors, read in place)."""
+
+    g_in: torch.Tensor
+    w_qkv: torch.Tensor
+    s_qkv: torch.Tensor
+    w_ik: torch.Tensor
+    s_ik: torch.Tensor
+    w_iw: torch.Tensor
+    g_q: torch.Tensor
+    g_kv: torch.Tensor
+    g_ik: torch.Tensor
+    b_ik: torch.Tensor
+    w_qb: torch.Tensor
+    s_qb: torch.Tensor
+    w_iq: torch.Tensor
+    s_iq: torch.Tensor
+    w_uk: torch.Tensor
+    s_uk: torch.Tensor
+    w_uv: torch.Tensor
+    s_uv: torch.Tensor
+    w_o: torch.Tensor
+    s_o: torch.Tensor
+
+    def check(self, device) -> None:
+        for f in fields(self):
+            shape, dtype = WEIGHT_SPECS[f.name]
+            need(getattr(self, f.name), f.name, shape, dtype, device)
+
+    def c_struct(self) -> _lib.ProjWeights:
+        return _lib.ProjWeights(**{n: _lib.ptr(getattr(self, n)) for n in _lib.PROJ_WEIGHT_FIELDS})
+
+    def nbytes(self) -> int:
+        return sum(getattr(self, f.name).numel() * getattr(self, f.name).element_size() for f in fields(self))
+
+
+@dataclass
+class FrontOut:
+    """The attention phase's inputs for one step."""
+
+    q: torch.Tensor  # bf16 [rows, 32, 576]
+    iq: torch.Tensor  # u8 [rows, 64, 64]
+    iqs: torch.Tensor  # u8 [rows, 64, 4]
+    iw: torch.Tensor  # bf16 [rows, 64]
+
+    @staticmethod
+    def empty(rows: int, device) -> "FrontOut":
+        return FrontOut(
+            q=torch.empty(rows, HEADS, KV_LORA + PE_DIM, dtype=torch.bfloat16, device=device),
+            iq=torch.empty(rows, INDEX_HEADS, INDEX_DIM // 2, dtype=torch.uint8, device=device),
+            iqs=torch.empty(rows, INDEX_HEADS, INDEX_DIM // 32, dtype=torch.uint8, device=device),
+            iw=torch.empty(rows, INDEX_HEADS, dtype=torch.bfloat16, device=device),
+        )
+
+
+class ProjRuntime(Runtime):
+    """The C library's projection handle for a widest step ``max_rows`` (<= 16)."""
+
+    PREFIX = "mono_proj"
+    SITES = _lib.PROJ_SITES
+    KIND = "projection"
+
+    def __init__(self, max_rows: int, device=None):
+        super().__init__(device)
+        self.max_rows = max_rows
+        self._create(_lib.ProjConfig(device=self.device.index, max_rows=max_rows))
+
+    def _rows(self, t: torch.Tensor, name: str) -> int:
+        if t.dim() != 2 or not 1 <= t.shape[0] <= self.max_rows:
+            raise ValueError(f"{name}: expected [rows <= {self.max_rows}, {HIDDEN}], got {tuple(t.shape)}")
+        return t.shape[0]
+
+    def front(self, h: torch.Tensor, seq_lens: torch.Tensor, page_table: torch.Tensor, caches: AttnCaches,
+              w: ProjWeights, rope_cos: torch.Tensor, rope_sin: torch.Tensor, out: FrontOut | None = None,
+              check_weights: bool = True) -> FrontOut:
+        """Rows ``h`` [rows, 7168] bf16 whose new tokens sit at ``seq_lens - 1`` ->
+        FrontOut; writes each row's MLA cache row and FP4 index key in place."""
+        dev = self.device
+        S = self._rows(h, "h")
+        need(h, "h", (S, HIDDEN), torch.bfloat16, dev)
+        need(seq_lens, "seq_lens", (S,), torch.int32, dev)
+        if page_table.dim() != 2 or page_table.shape[0] < S:
+            raise ValueError(f"page_table: expected [>= {S}, pages], got {tuple(page_table.shape)}")
+        need(page_table, "page_table", tuple(page_table.shape), torch.int32, dev)
+        pages = caches.ikv.shape[0]
+        need(caches.ikv, "ikv", (pages, 4, 64, 16), torch.uint8, dev)
+        need(caches.iks, "iks", (pages, 4, 64), torch.uint8, dev)
+        need(caches.kv, "kv", (pages * 64, KV_LORA + PE_DIM), torch.uint8, dev)
+        need(caches.kv_scale, "kv_scale", (pages * 64,), torch.float32, dev)
+        if rope_cos.dim() != 2 or rope_cos.shape[1] != PE_DIM // 2:
+            raise ValueError(f"rope_cos: expected [max_pos, {PE_DIM // 2}], got {tuple(rope_cos.shape)}")
+        need(rope_cos, "rope_cos", tuple(rope_cos.shape), torch.float32, dev)
+        need(rope_sin, "rope_sin", tuple(rope_cos.shape), torch.float32, dev)
+        if check_weights:
+            w.check(dev)
+        out = FrontOut.empty(S, dev) if out is None else out
+        need(out.q, "q", (S, HEADS, KV_LORA + PE_DIM), torch.bfloat16, dev)
+        need(out.iq, "iq", (S, INDEX_HEADS, INDEX_DIM // 2), torch.uint8, dev)
+        need(out.iqs, "iqs", (S, INDEX_HEADS, INDEX_DIM // 32), torch.uint8, dev)
+        need(out.iw, "iw", (S, INDEX_HEADS), torch.bfloat16, dev)
+        P = _lib.ptr
+        args = _lib.FrontArgs(
+            h=P(h), seq_lens=P(seq_lens), page_table=P(page_table), pt_stride=page_table.shape[1],
+            n_pages=pages, rope_cos=P(rope_cos), rope_sin=P(rope_sin), max_pos=rope_cos.shape[0],
+            ikv=P(caches.ikv), iks=P(caches.iks), kv=P(caches.kv), kv_scale=P(caches.kv_scale),
+            q=P(out.q), iq=P(out.iq), iqs=P(out.iqs), iw=P(out.iw), rows=S,
+        )  # fmt: skip
+        ws = w.c_struct()
+        _lib.check(_lib.lib().mono_front_forward(self._h, C.byref(ws), C.byref(args), self._stream()))
+        return out
+
+    def back(self, o_lat: torch.Tensor, h: torch.Tensor, w: ProjWeights, a: torch.Tensor | None = None,
+             o: torch.Tensor | None = None, check_weights: bool = True) -> torch.Tensor:
+        """a = h + W_o W_UV o_lat [rows, 7168] bf16 (``o``, if given, receives W_UV o_lat
+        [rows, 4096] bf16)."""
+        dev = self.device
+        S = self._rows(h, "h")
+        need(h, "h", (S, HIDDEN), torch.bfloat16, dev)
+        need(o_lat, "o_lat", (S, HEADS, KV_LORA), torch.bfloat16, dev)
+        if check_weights:
+            w.check(dev)
+        a = torch.empty_like(h) if a is None else a
+        need(a, "a", (S, HIDDEN), torch.bfloat16, dev)
+        if o is not None:
+            need(o, "o", (S, HEADS * V_DIM), torch.bfloat16, dev)
+        P = _lib.ptr
+        args = _lib.BackArgs(o_lat=P(o_lat), h=P(h), a=P(a), o=P(o), rows=S)
+        ws = w.c_struct()
+        _lib.check(_lib.lib().mono_back_forward(self._h, C.byref(ws), C.byref(args), self._stream()))
+        return a

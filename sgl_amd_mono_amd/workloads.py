@@ -120,3 +120,51 @@ def attn_case(ctx_lens, device, seed: int = 0, max_ctx: int = 32768, spare_pages
         seq_lens=torch.tensor([int(n) for n in ctx_lens], dtype=torch.int32, device=device),
     )
     return step, AttnCaches(ikv=ikv, iks=iks, kv=kv, kv_scale=kv_scale)
+
+
+def _fp8_matrix(n: int, k: int, g: torch.Generator, device):
+    """E4M3 codes of N(0, 1) samples in the (16, 16) layout and f32 128 x 128 block
+    scales ~U(0.5, 2) / (1.25 sqrt(K)), so a GEMV of unit-variance rows gives outputs
+    of about unit variance."""
+    codes = shuffle_16x16(fp8_codes((n, k), g, device))
+    s = (torch.rand(-(-n // 128), k // 128, generator=g, device=device) * 1.5 + 0.5) / (1.25 * k**0.5)
+    return codes, s
+
+
+def proj_weights(device, seed: int = 0):
+    """One layer's attention-block projection weights (sgl_amd_mono_amd.layer.WEIGHT_SPECS):
+    FP8 matrices as ``_fp8_matrix``, RMSNorm weights 1 + 0.1 N(0, 1) bf16, the index
+    key LayerNorm weight 1 + 0.1 N(0, 1) and bias 0.1 N(0, 1) f32, the index head-weight
+    matrix N(0, 1/7168) bf16 (its bytes (16, 16)-shuffled)."""
+    from .layer import HEADS, HIDDEN, INDEX_DIM, INDEX_HEADS, KV_LORA, N_QKV, NOPE_DIM, Q_LORA, QK_DIM, V_DIM
+    from .layer import ProjWeights
+
+    g = _gen(device, seed)
+
+    def norm(n):
+        return (1.0 + 0.1 * torch.randn(n, generator=g, device=device)).to(torch.bfloat16)
+
+    w = {}
+    w["g_in"] = norm(HIDDEN)
+    w["w_qkv"], w["s_qkv"] = _fp8_matrix(N_QKV, HIDDEN, g, device)
+    w["w_ik"], w["s_ik"] = _fp8_matrix(INDEX_DIM, HIDDEN, g, device)
+    iw = (torch.randn(INDEX_HEADS, HIDDEN, generator=g, device=device) * HIDDEN**-0.5).to(torch.bfloat16)
+    w["w_iw"] = shuffle_16x16(iw.view(torch.uint8)).view(torch.bfloat16)
+    w["g_q"] = norm(Q_LORA)
+    w["g_kv"] = norm(KV_LORA)
+    w["g_ik"] = 1.0 + 0.1 * torch.randn(INDEX_DIM, generator=g, device=device)
+    w["b_ik"] = 0.1 * torch.randn(INDEX_DIM, generator=g, device=device)
+    w["w_qb"], w["s_qb"] = _fp8_matrix(HEADS * QK_DIM, Q_LORA, g, device)
+    w["w_iq"], w["s_iq"] = _fp8_matrix(INDEX_HEADS * INDEX_DIM, Q_LORA, g, device)
+    w["w_uk"], w["s_uk"] = _fp8_matrix(HEADS * KV_LORA, NOPE_DIM, g, device)
+    w["w_uv"], w["s_uv"] = _fp8_matrix(HEADS * V_DIM, KV_LORA, g, device)
+    w["w_o"], w["s_o"] = _fp8_matrix(HIDDEN, HEADS * V_DIM, g, device)
+    return ProjWeights(**w)
+
+
+def rope_tables(max_pos: int, device, dim: int = 64, theta: float = 10000.0):
+    """RoPE cos / sin f32 [max_pos, dim / 2]: angle = pos * theta^(-2i / dim), formed
+    in f64."""
+    inv = theta ** (-torch.arange(0, dim, 2, dtype=torch.float64) / dim)
+    ang = torch.arange(max_pos, dtype=torch.float64)[:, None] * inv[None]
+    return torch.cos(ang).float().to(device), torch.sin(ang).float().to(device)
