@@ -1,23 +1,27 @@
 """Benchmark of the decoder-layer path on one MI355X (gfx950).
 
-``python bench.py [--steps K] [--warmup W] [--rows 8] [--workload moe_fp8]`` prints one
+``python bench.py [--workload layer] [--steps K] [--warmup W] [--rows 8]`` prints one
 JSON line. A step is one pass of the hot path over one batch of synthetic decode rows
 whose inputs and weights are already resident in HBM:
 
-* ``moe_fp8`` (default; BASELINE config 2 at 8 rows): the FP8 routed + shared MoE half
-  of the decoder layer (RMSNorm, router, top-8, W8A8 experts, residual) through
-  ``mono_moe_fp8_forward``.
+* ``layer`` (default): 61 stacked, independently seeded decoder
+  layers at 8 rows over 32768-key contexts, each layer the four persistent launches
+  front -> sparse attention -> back -> FP8 MoE; one step runs every layer once and is
+  replayed from a HIP graph. ``value`` is microseconds per layer.
+* ``moe_fp8`` (BASELINE config 2 at 8 rows): the FP8 routed + shared MoE half of the
+  layer (RMSNorm, router, top-8, W8A8 experts, residual) through ``mono_moe_fp8_forward``.
 * ``moe_mxfp4``: the MXFP4 A16W4 routed + shared MoE behind a
   softmax router through ``mono_moe_mxfp4_forward``.
 * ``attn``: FP4 index scores over ``--ctx`` keys a row, the exact
   top-2048 and sparse MLA decode, through ``mono_attn_forward``.
 
-Weight sets and activation batches rotate from step to step so every step streams its
-experts from HBM rather than from the 256 MB Infinity Cache. The timed region is K
-steps bracketed by ``torch.cuda.synchronize()``; HIP events on the launch stream time
-each step. ``roofline`` prices the algorithmic bytes of a step (distinct experts read
+Weights never repeat within ~1.5 GB of streamed bytes (rotating weight sets for the
+single-phase workloads; 61 distinct layers for ``layer``), so every step streams from
+HBM rather than from the 256 MB Infinity Cache. The timed region is K steps bracketed
+by ``torch.cuda.synchronize()``; HIP events on the launch stream time each step.
+``roofline`` prices the dominant kernel's algorithmic bytes (distinct experts read
 once, the router once, activations in and out) against 8 TB/s. ``cpu_baseline`` times
-the CPU oracle's restatement of the same step on this host (rank 0 only, a bounded
+the CPU oracle's restatement of the same work on this host (rank 0 only, a bounded
 sample) as a reported baseline.
 
 Only one GPU is used: ``--gpus`` above 1 exits with a message.
@@ -429,22 +433,249 @@ def cpu_baseline_attn(args, case):
                         f"host '{cpu_model()}', os.cpu_count()={os.cpu_count()}"))
 
 
-WORKLOADS = {"moe_fp8": bench_moe_fp8, "moe_mxfp4": bench_moe_mxfp4, "attn": bench_attn}
+# ------------------------------------------------------------------ full layer (config 5)
+def proj_bytes(w, names) -> int:
+    return sum(getattr(w, n).numel() * getattr(w, n).element_size() for n in names)
+
+
+FRONT_W = ("g_in", "w_qkv", "s_qkv", "w_ik", "s_ik", "w_iw", "g_q", "g_kv", "g_ik", "b_ik", "w_qb", "s_qb",
+           "w_iq", "s_iq", "w_uk", "s_uk")
+BACK_W = ("w_uv", "s_uv", "w_o", "s_o")
+PHASES = ("front", "attn", "back", "moe")
+
+
+def bench_layer(args, dev):
+    """``--layers`` (61) stacked, independently seeded decoder layers
+    at ``--rows`` (8) rows, every row a ``--ctx``-key (32768) request whose new token is
+    its last. One step runs all layers once; it is captured in a HIP graph (244
+    persistent launches) and replayed, so host dispatch is off the timed path. The value
+    is microseconds per layer. A second timed region runs the same step eagerly with a
+    HIP event between every two phases; its per-phase averages give the breakdown and
+    the MoE kernel's launch duration for ``roofline``."""
+    import torch
+
+    from sgl_amd_mono_amd import workloads
+    from sgl_amd_mono_amd.layer import LayerRuntime, LayerWeights
+    from sgl_amd_mono_amd.moe import FP8_MOE
+
+    L, S, ctx = args.layers, args.rows, args.ctx
+    lens = [ctx] * S
+    log(f"generating {L} layers (seeds 1000 l + 7) of weights and {S} x {ctx}-key caches on {dev}")
+    t0 = time.perf_counter()
+    layers = []
+    for l in range(L):
+        seed = 1000 * l + 7
+        w = LayerWeights(proj=workloads.proj_weights(dev, seed=seed),
+                         moe=workloads.fp8_moe_weights(FP8_MOE, dev, seed=seed + 1))
+        step, caches = workloads.attn_case(lens, dev, seed=seed + 2, max_ctx=ctx)
+        layers.append((w, step, caches))
+    cos, sin = workloads.rope_tables(ctx, dev)
+    torch.cuda.synchronize()
+    log(f"generated in {time.perf_counter() - t0:.1f} s; {torch.cuda.memory_allocated(dev) / 1e9:.1f} GB allocated")
+    rt = LayerRuntime(S, ctx, dev)
+    x_in = workloads.rows_bf16(S, 7168, dev, seed=5)
+    xb = [torch.empty_like(x_in), torch.empty_like(x_in)]
+
+    def run_step(marks=None):
+        x = x_in
+        for l, (w, step, caches) in enumerate(layers):
+            hook = None if marks is None else (lambda i, l=l: marks(l, i))
+            x = rt.forward(x, step.seq_lens, step.page_table, caches, w, cos, sin, out=xb[l % 2],
+                           check_weights=False, on_phase=hook)
+        return x
+
+    # validation pass: routing per layer (distinct experts), and the weights' shapes
+    distinct = []
+    x = x_in
+    for l, (w, step, caches) in enumerate(layers):
+        w.proj.check(rt.device)
+        x, it = rt.forward(x, step.seq_lens, step.page_table, caches, w, cos, sin, out=xb[l % 2], keep=True)
+        distinct.append(len(set(it["topk_ids"].flatten().tolist())) + 1)
+    torch.cuda.synchronize()
+    rt.check_errors()
+
+    for _ in range(max(args.warmup, 1)):
+        run_step()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        run_step()
+    torch.cuda.synchronize()
+    for _ in range(2):
+        graph.replay()
+    torch.cuda.synchronize()
+    rt.check_errors()
+
+    stream = torch.cuda.current_stream(dev)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
+    log(f"timing {args.steps} graph replays of {L} layers")
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ev[0].record(stream)
+    for i in range(args.steps):
+        graph.replay()
+        ev[i + 1].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    rt.check_errors()
+    per = [ev[i].elapsed_time(ev[i + 1]) * 1e3 for i in range(args.steps)]  # us a step
+    step_us = ev[0].elapsed_time(ev[-1]) * 1e3 / args.steps
+    us = step_us / L
+
+    # eager pass with phase events: the breakdown and the MoE launch durations
+    n_eager = max(1, min(3, args.steps))
+    pev = [[[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(L)] for _ in range(n_eager)]
+    torch.cuda.synchronize()
+    for k in range(n_eager):
+        x = x_in
+        for l, (w, step, caches) in enumerate(layers):
+            pev[k][l][0].record(stream)
+            x = rt.forward(x, step.seq_lens, step.page_table, caches, w, cos, sin, out=xb[l % 2],
+                           check_weights=False, on_phase=lambda i, l=l, k=k: pev[k][l][i + 1].record(stream))
+    torch.cuda.synchronize()
+    rt.check_errors()
+    ph = {p: [] for p in PHASES}
+    for k in range(n_eager):
+        for l in range(L):
+            for i, p in enumerate(PHASES):
+                ph[p].append(pev[k][l][i].elapsed_time(pev[k][l][i + 1]) * 1e3)
+    ph_us = {p: statistics.fmean(v) for p, v in ph.items()}
+    eager_layer_us = sum(ph_us.values())
+
+    w0 = layers[0][0]
+    moe_fixed = 256 * 7168 * 2 + 256 * 4 + 7168 * 2 + 2 * S * 7168 * 2
+    moe_b = [d * fp8_expert_bytes(FP8_MOE) + moe_fixed for d in distinct]
+    phase_bytes = {
+        "front": proj_bytes(w0.proj, FRONT_W) + S * 7168 * 2 + S * (576 + 4 + 68) + S * (32 * 576 * 2 + 64 * 68 + 128),
+        "attn": attn_step_bytes(lens),
+        "back": proj_bytes(w0.proj, BACK_W) + S * (32 * 512 * 2 + 2 * 7168 * 2),
+        "moe": statistics.fmean(moe_b),
+    }
+    moe_durs = ph["moe"]
+    moe_achieved = statistics.fmean(
+        b / (t * 1e-6) for b, t in zip([moe_b[l] for _ in range(n_eager) for l in range(L)], moe_durs)) / 1e9
+    layer_bytes = sum(phase_bytes.values())
+    log(f"{us:.2f} us/layer ({step_us / 1e3:.3f} ms a {L}-layer step, median {statistics.median(per) / L:.2f}), "
+        f"{layer_bytes / (us * 1e-6) / 1e9:.0f} GB/s over the layer; eager phases "
+        + ", ".join(f"{p} {ph_us[p]:.1f}" for p in PHASES) + f" us; MoE {moe_achieved:.0f} GB/s; wall {wall:.2f} s")
+
+    cpu = None
+    if args.cpu_seconds > 0:
+        cpu = cpu_baseline_layer(args, layers[0], x_in, cos, sin)
+    rt.close()
+    return dict(
+        value=us, unit="us",
+        ms_per_step=step_us / 1e3,
+        dtype="fp8_e4m3 weights (bf16 / fp8 MFMA, f32 accumulate), fp4 index, fp8 kv",
+        config=dict(workload="BASELINE config 5: full fused decoder layer, one GPU's TP=4 share, 61 stacked layers",
+                    rows=S, context=ctx, layers=L, hidden=7168, heads=32, experts=256, top_k=8, shared_experts=1,
+                    inter=512, launches_per_layer=4, graph=True),
+        extra=dict(
+            us_per_layer_median=statistics.median(per) / L, us_per_layer_min=min(per) / L,
+            us_per_layer_max=max(per) / L, rows_per_s=S / (us * 1e-6), step_wall_s=wall / args.steps,
+            layer_algorithmic_bytes=layer_bytes, layer_achieved_gbs=layer_bytes / (us * 1e-6) / 1e9,
+            phases_us_eager=ph_us, eager_layer_us=eager_layer_us,
+            phases_algorithmic_bytes=phase_bytes,
+            phases_achieved_gbs={p: phase_bytes[p] / (ph_us[p] * 1e-6) / 1e9 for p in PHASES},
+            distinct_experts_mean=statistics.fmean(distinct),
+        ),
+        roofline=dict(
+            bound="hbm", achieved=moe_achieved, peak=HBM_PEAK_GBS, unit="GB/s", frac=moe_achieved / HBM_PEAK_GBS,
+            traffic=None, kernel="k_moe_fp8 (the MoE phase: 86% of the layer's bytes)",
+            bytes_per_launch=statistics.fmean(moe_b), avg_launch_us=statistics.fmean(moe_durs),
+        ),
+        cpu_baseline=cpu,
+    )
+
+
+def cpu_baseline_layer(args, layer, x_in, cos, sin):
+    """One layer of the CPU oracle chain (oracle.layer.front, oracle.attention,
+    oracle.layer.back, oracle.moe.fp8_moe_block) at the same rows, on this host."""
+    import torch
+
+    from oracle import attention as oatt
+    from oracle import codecs as ocodecs
+    from oracle import layer as ol
+    from oracle import moe as omoe
+    from sgl_amd_mono_amd.layer import WEIGHT_SPECS
+    from sgl_amd_mono_amd.moe import FP8_MOE
+
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    w, step, caches = layer
+
+    class Lazy:
+        def __init__(self, t, shuffled=False):
+            self.t, self.shuffled, self.c = t, shuffled, {}
+
+        def __getitem__(self, e):
+            if e not in self.c:
+                x = self.t[e].cpu()
+                self.c[e] = ocodecs.aiter_unshuffle(x) if self.shuffled else x
+            return self.c[e]
+
+    pw = {}
+    for name in WEIGHT_SPECS:
+        t = getattr(w.proj, name).cpu()
+        if name == "w_iw":
+            t = ocodecs.aiter_unshuffle(t.view(torch.uint8)).view(torch.bfloat16)
+        elif name.startswith("w_"):
+            t = ocodecs.aiter_unshuffle(t)
+        pw[name] = t
+    m = w.moe
+    mw = dict(g_post=m.g_post.cpu(), w_router=m.w_router.cpu(), bias=m.bias.cpu(), w13=Lazy(m.w13, True),
+              s13=Lazy(m.s13), w2=Lazy(m.w2, True), s2=Lazy(m.s2))
+    c = {k: v.cpu() for k, v in vars(caches).items()}
+    seq, pt = step.seq_lens.cpu(), step.page_table.cpu()
+    h = x_in.cpu()
+    cs, sn = cos.cpu(), sin.cpu()
+
+    def one():
+        f = ol.front(h, seq.long() - 1, pt, pw, cs, sn)
+        ol.write_caches(f, c["ikv"], c["iks"], c["kv"], c["kv_scale"])
+        sc = oatt.index_scores(f["iq"], f["iqs"], f["iw"], c["ikv"], c["iks"], pt, seq, args.ctx)
+        sel = oatt.select_topk(sc, seq, pt)
+        o_lat = oatt.sparse_mla(f["q"], c["kv"], c["kv_scale"], sel).to(torch.bfloat16)
+        a = ol.back(o_lat, h, pw)["a"]
+        return omoe.fp8_moe_block(a, mw["g_post"], mw["w_router"], mw["bias"], mw["w13"], mw["s13"], mw["w2"],
+                                  mw["s2"], eps=FP8_MOE.eps, top_k=FP8_MOE.top_k, inter=FP8_MOE.inter)["out"]
+
+    one()  # warm-up: fetches the experts this layer's routing touches
+    times = []
+    t_end = time.perf_counter() + args.cpu_seconds
+    while (len(times) < 3 or time.perf_counter() < t_end) and len(times) < 20:
+        t = time.perf_counter()
+        one()
+        times.append((time.perf_counter() - t) * 1e6)
+    med = statistics.median(times)
+    log(f"cpu oracle: {med:.0f} us a layer, median of {len(times)} on {threads} threads")
+    return dict(value=med, unit="us", cores=torch.get_num_threads(), kind="port",
+                sample=(f"one layer (layer 0) of the oracle chain front + index scores + top-2048 + sparse MLA + "
+                        f"back + FP8 MoE (f32 torch restatement) at {args.rows} rows x {args.ctx} keys, "
+                        f"{len(times)} runs, median; x {args.layers} layers would be {med * args.layers / 1e6:.1f} s "
+                        f"a step; host '{cpu_model()}', os.cpu_count()={os.cpu_count()}"))
+
+
+WORKLOADS = {"layer": bench_layer, "moe_fp8": bench_moe_fp8, "moe_mxfp4": bench_moe_mxfp4, "attn": bench_attn}
+DEFAULT_STEPS = {"layer": 20, "moe_fp8": 200, "moe_mxfp4": 200, "attn": 200}
 
 
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--steps", type=int, default=None, help="timed steps (default: 20 for layer, else 200)")
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--rows", type=int, default=8)
-    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="moe_fp8")
+    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="layer")
+    ap.add_argument("--layers", type=int, default=61, help="stacked layers (layer workload)")
     ap.add_argument("--sets", type=int, default=2, help="weight sets rotated over the steps")
     ap.add_argument("--batches", type=int, default=16, help="activation batches rotated")
     ap.add_argument("--ctx", type=int, default=32768, help="keys a row (attn workload)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="wall budget of the CPU baseline sample (0 skips it)")
     args = ap.parse_args()
+    if args.steps is None:
+        args.steps = DEFAULT_STEPS[args.workload]
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:

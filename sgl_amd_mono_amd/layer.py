@@ -19,6 +19,7 @@ import torch
 
 from . import _lib
 from .attn import AttnCaches
+from .moe import Fp8MoeWeights
 from .runtime import Runtime, need
 
 HIDDEN, Q_LORA, KV_LORA, PE_DIM = 7168, 1536, 512, 64
@@ -190,3 +191,83 @@ class ProjRuntime(Runtime):
         ws = w.c_struct()
         _lib.check(_lib.lib().mono_back_forward(self._h, C.byref(ws), C.byref(args), self._stream()))
         return a
+
+
+@dataclass
+class LayerWeights:
+    """One decoder layer: the attention block's projections and the FP8 MoE."""
+
+    proj: ProjWeights
+    moe: Fp8MoeWeights
+
+
+class LayerRuntime:
+    """One GPU's TP=4 share of a DeepSeek-V3.2-shaped decoder layer with an FP4 indexer
+    four persistent launches on the caller's stream, each phase's
+    outputs in scratch this runtime owns (the reference launches the same body as one
+    grid, glm53/gfx950/kernel.py:6-45, with the TP all-reduces that are local residual
+    adds here):
+
+        front (mono_front_forward) -> sparse attention (mono_attn_forward)
+          -> back (mono_back_forward) -> FP8 MoE + residual (mono_moe_fp8_forward)
+
+    No call synchronises with the host, so a caller may capture a step in a HIP graph.
+    """
+
+    def __init__(self, max_rows: int = 8, max_ctx: int = 32768, device=None):
+        from .attn import AttnRuntime
+        from .moe import FP8_MOE, MoeRuntime
+
+        if not 1 <= max_rows <= MAX_ROWS:
+            raise ValueError(f"max_rows must be in [1, {MAX_ROWS}], got {max_rows}")
+        self.proj = ProjRuntime(max_rows, device)
+        self.device = self.proj.device
+        self.attn = AttnRuntime(max_rows, max_ctx, device=self.device)
+        self.moe = MoeRuntime(FP8_MOE, max_rows, self.device)
+        self.max_rows, self.max_ctx = max_rows, max_ctx
+        self._front = FrontOut.empty(max_rows, self.device)
+        self._o_lat = torch.empty(max_rows, HEADS, KV_LORA, dtype=torch.bfloat16, device=self.device)
+        self._a = torch.empty(max_rows, HIDDEN, dtype=torch.bfloat16, device=self.device)
+
+    def close(self) -> None:
+        for rt in (self.proj, self.attn, self.moe):
+            rt.close()
+
+    def forward(self, h: torch.Tensor, seq_lens: torch.Tensor, page_table: torch.Tensor, caches: AttnCaches,
+                w: LayerWeights, rope_cos: torch.Tensor, rope_sin: torch.Tensor, out: torch.Tensor | None = None,
+                check_weights: bool = True, keep: bool = False, on_phase=None):
+        """x_out [rows, 7168] bf16 = the layer applied to rows ``h`` whose new tokens sit
+        at ``seq_lens - 1`` (this step's cache rows are written in place). ``keep``
+        also returns the intermediates (front outputs, the index scores and selected
+        slots, o_lat, a, the MoE routing and sum) as copies. ``on_phase(i)`` (if given)
+        is called after the launch of phase i is enqueued (0 front, 1 attention, 2 back,
+        3 MoE), e.g. to record timing events between the phases."""
+        from .attn import AttnStep
+
+        S = h.shape[0] if h.dim() == 2 else -1
+        if not 1 <= S <= self.max_rows:
+            raise ValueError(f"h: expected [rows <= {self.max_rows}, {HIDDEN}], got {tuple(h.shape)}")
+        fo = FrontOut(q=self._front.q[:S], iq=self._front.iq[:S], iqs=self._front.iqs[:S], iw=self._front.iw[:S])
+        mark = on_phase if on_phase is not None else (lambda i: None)
+        self.proj.front(h, seq_lens, page_table, caches, w.proj, rope_cos, rope_sin, out=fo,
+                        check_weights=check_weights)
+        mark(0)
+        step = AttnStep(iq=fo.iq, iqs=fo.iqs, iw=fo.iw, q=fo.q, page_table=page_table, seq_lens=seq_lens)
+        if not keep:
+            o_lat = self.attn.forward(step, caches, out=self._o_lat[:S])
+            mark(1)
+            a = self.proj.back(o_lat, h, w.proj, a=self._a[:S], check_weights=check_weights)
+            mark(2)
+            x = self.moe.forward_fp8(a, w.moe, out=out)
+            mark(3)
+            return x
+        o_lat, adbg = self.attn.forward(step, caches, out=self._o_lat[:S], debug=True)
+        a = self.proj.back(o_lat, h, w.proj, a=self._a[:S], check_weights=check_weights)
+        x, dbg = self.moe.forward_fp8(a, w.moe, out=out, debug=True)
+        inter = dict(q=fo.q.clone(), iq=fo.iq.clone(), iqs=fo.iqs.clone(), iw=fo.iw.clone(), o_lat=o_lat.clone(),
+                     a=a.clone(), index_scores=adbg["scores"], topk_slots=adbg["topk"], **dbg)
+        return x, inter
+
+    def check_errors(self) -> None:
+        for rt in (self.proj, self.attn, self.moe):
+            rt.check_errors()

@@ -39,9 +39,10 @@ def fp8_moe_weights(geo: MoeGeometry, device, seed: int = 0) -> Fp8MoeWeights:
     g_post = (1.0 + 0.1 * torch.randn(H, generator=g, device=device)).to(torch.bfloat16)
     w13 = torch.empty(E + 1, 2 * I, H, dtype=torch.uint8, device=device)
     w2 = torch.empty(E + 1, H, I, dtype=torch.uint8, device=device)
-    for e in range(E + 1):  # one expert at a time keeps the f32 temporaries small
-        w13[e] = shuffle_16x16(fp8_codes((2 * I, H), g, device))
-        w2[e] = shuffle_16x16(fp8_codes((H, I), g, device))
+    for e0 in range(0, E + 1, 32):  # 32 experts at a time bound the f32 temporaries
+        e1 = min(e0 + 32, E + 1)
+        w13[e0:e1] = shuffle_16x16(fp8_codes((e1 - e0, 2 * I, H), g, device))
+        w2[e0:e1] = shuffle_16x16(fp8_codes((e1 - e0, H, I), g, device))
     s13 = (torch.rand(E + 1, 2 * I // 128, H // 128, generator=g, device=device) * 1.5 + 0.5) / 448.0
     s2 = (torch.rand(E + 1, H // 128, I // 128, generator=g, device=device) * 1.5 + 0.5) / 448.0
     return Fp8MoeWeights(g_post=g_post, w_router=w_router, bias=bias, w13=w13, s13=s13, w2=w2, s2=s2)

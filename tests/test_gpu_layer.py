@@ -1,0 +1,111 @@
+"""The whole decoder layer on the GPU: two stacked, independently
+seeded layers at 8 rows over 32768-key contexts, each phase checked against the CPU
+oracle on the inputs the device handed it (the same teacher-forced comparison the
+phase tests make), so the test pins how the layer runtime wires the phases together:
+
+* front: q (q_lat | q_pe) and the index head weights against oracle.layer.front;
+* attention: the exact top-2048 of the device's index scores bit-exact, o_lat against
+  oracle.attention.sparse_mla over that selection and the caches front wrote;
+* back: a against oracle.layer.back on the device's o_lat;
+* MoE: routing bit-exact on the device's scores, x_out against oracle.moe.fp8_moe_block.
+"""
+
+import pytest
+import torch
+
+from oracle import attention as oatt
+from oracle import codecs as ocodecs
+from oracle import layer as ol
+from oracle import moe as omoe
+from oracle import topk as otopk
+from sgl_amd_mono_amd import workloads
+from sgl_amd_mono_amd.layer import WEIGHT_SPECS, LayerRuntime, LayerWeights
+from sgl_amd_mono_amd.moe import FP8_MOE
+
+pytestmark = pytest.mark.gpu
+
+ROWS, CTX, LAYERS = 8, 32768, 2
+
+
+class CpuExperts:
+    def __init__(self, t, shuffled=False):
+        self.t, self.shuffled, self.cache = t, shuffled, {}
+
+    def __getitem__(self, e):
+        if e not in self.cache:
+            x = self.t[e].cpu()
+            self.cache[e] = ocodecs.aiter_unshuffle(x) if self.shuffled else x
+        return self.cache[e]
+
+
+def _cpu_proj(w):
+    out = {}
+    for name in WEIGHT_SPECS:
+        t = getattr(w, name).cpu()
+        if name == "w_iw":
+            t = ocodecs.aiter_unshuffle(t.view(torch.uint8)).view(torch.bfloat16)
+        elif name.startswith("w_"):
+            t = ocodecs.aiter_unshuffle(t)
+        out[name] = t
+    return out
+
+
+def _close(got, want, what):
+    got, want = got.float(), want.float()
+    err = (got - want).abs()
+    rel = float((got - want).norm() / want.norm().clamp_min(1e-30))
+    print(f"  {what}: max err {float(err.max()):.3e}, rel {rel:.3e}", flush=True)
+    assert bool((err <= 2e-2 + 1e-2 * want.abs()).all()), what
+    assert rel <= 1e-2, what
+
+
+def test_two_layers_phase_by_phase(gpu_device):
+    rt = LayerRuntime(ROWS, CTX, gpu_device)
+    cos, sin = workloads.rope_tables(CTX, gpu_device)
+    lens = [CTX, 9000, 2049, 300, CTX - 5, 2048, 16000, 64]  # new tokens at len - 1
+    x = workloads.rows_bf16(ROWS, ol.HIDDEN, gpu_device, seed=5)
+    try:
+        for layer in range(LAYERS):
+            seed = 1000 * layer + 7  # per-layer seeds (test/kernels/glm53/check_layer.py:84)
+            print(f"[layer {layer}] weights", flush=True)
+            w = LayerWeights(proj=workloads.proj_weights(gpu_device, seed=seed),
+                             moe=workloads.fp8_moe_weights(FP8_MOE, gpu_device, seed=seed + 1))
+            step, caches = workloads.attn_case(lens, gpu_device, seed=seed + 2, max_ctx=CTX)
+            x_out, it = rt.forward(x, step.seq_lens, step.page_table, caches, w, cos, sin, keep=True)
+            torch.cuda.synchronize()
+            rt.check_errors()
+            h = x.cpu()
+            pos = step.seq_lens.cpu().long() - 1
+            pt = step.page_table.cpu()
+
+            f = ol.front(h, pos, pt, _cpu_proj(w.proj), cos.cpu(), sin.cpu())
+            _close(it["q"].cpu(), f["q"], "front q")
+            _close(it["iw"].cpu(), f["iw"], "front iw")
+
+            c = {k: v.cpu() for k, v in vars(caches).items()}
+            scores, sel = it["index_scores"].cpu(), it["topk_slots"].cpu()
+            ref_scores = oatt.index_scores(it["iq"].cpu(), it["iqs"].cpu(), it["iw"].cpu(), c["ikv"], c["iks"], pt,
+                                           step.seq_lens.cpu(), CTX)
+            for s, n in enumerate(lens):
+                d = float((scores[s, :n] - ref_scores[s, :n]).abs().max())
+                assert d <= 1e-4 * float(ref_scores[s, :n].abs().max()) + 1e-6, (s, d)
+            assert torch.equal(sel, oatt.select_topk(scores, step.seq_lens.cpu(), pt))
+            o_ref = oatt.sparse_mla(it["q"].cpu(), c["kv"], c["kv_scale"], sel)
+            _close(it["o_lat"].cpu(), o_ref, "attention o_lat")
+
+            b = ol.back(it["o_lat"].cpu(), h, _cpu_proj(w.proj))
+            _close(it["a"].cpu(), b["a"], "back a")
+
+            m = w.moe
+            ids_ref, w_ref = otopk.router_top8(it["scores"].cpu(), m.bias.cpu(), FP8_MOE.top_k, FP8_MOE.route_scale)
+            assert torch.equal(it["topk_ids"].cpu().long(), ids_ref)
+            ref = omoe.fp8_moe_block(
+                it["a"].cpu(), m.g_post.cpu(), m.w_router.cpu(), m.bias.cpu(), CpuExperts(m.w13, True),
+                CpuExperts(m.s13), CpuExperts(m.w2, True), CpuExperts(m.s2), eps=FP8_MOE.eps, top_k=FP8_MOE.top_k,
+                inter=FP8_MOE.inter, ids=ids_ref, weights=w_ref,
+            )  # fmt: skip
+            _close(x_out.cpu(), ref["out"], "moe x_out")
+            x = x_out.clone()
+            del w, caches
+    finally:
+        rt.close()
