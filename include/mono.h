@@ -282,6 +282,10 @@ typedef struct {
   void* iqs;                 /* out u8 [rows, 64, 4] E8M0 */
   void* iw;                  /* out bf16 [rows, 64] index head weights */
   int rows;
+  int64_t* timeline;         /* optional i64 [tasks, 4] per task: start, inputs-ready, end
+                                ticks (s_memrealtime, 100 MHz), workgroup << 8 | stage
+                                (0 A, 1 B, 2 C, 3 D, 4 E); tasks = 140 (rows <= 8) or
+                                280, + 272 + 9 rows */
 } mono_front_args;
 
 typedef struct {
@@ -290,6 +294,7 @@ typedef struct {
   void* a;           /* out bf16 [rows, 7168] h + W_o W_UV o_lat */
   void* o;           /* optional out bf16 [rows, 4096] W_UV o_lat (NULL: not written) */
   int rows;
+  int64_t* timeline; /* optional i64 [256, 4] as in mono_front_args (stage 0 U, 1 O) */
 } mono_back_args;
 
 /* Wait sites of the projection launches: 0 stage-A partials, 1 q_an, 2 q_nope,

@@ -75,12 +75,12 @@ class FrontArgs(C.Structure):
         ("h", _VP), ("seq_lens", _VP), ("page_table", _VP), ("pt_stride", _I32), ("n_pages", _I32),
         ("rope_cos", _VP), ("rope_sin", _VP), ("max_pos", _I32),
         ("ikv", _VP), ("iks", _VP), ("kv", _VP), ("kv_scale", _VP),
-        ("q", _VP), ("iq", _VP), ("iqs", _VP), ("iw", _VP), ("rows", _I32),
+        ("q", _VP), ("iq", _VP), ("iqs", _VP), ("iw", _VP), ("rows", _I32), ("timeline", _VP),
     ]
 
 
 class BackArgs(C.Structure):
-    _fields_ = [("o_lat", _VP), ("h", _VP), ("a", _VP), ("o", _VP), ("rows", _I32)]
+    _fields_ = [("o_lat", _VP), ("h", _VP), ("a", _VP), ("o", _VP), ("rows", _I32), ("timeline", _VP)]
 
 
 # entry point -> (restype, argtypes); every name include/mono.h declares

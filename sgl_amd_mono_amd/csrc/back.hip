@@ -67,11 +67,13 @@ class Back {
     gd.tag = L.tag;
     gd.deadline = now_ticks() + guard_args.deadline_ticks;
     for (int T = blockIdx.x; T < HEADS + NT_O; T += G) {
+      const uint64_t t0 = now_ticks();
       if (T < HEADS) {
         stage_u(T);
       } else if (!stage_o(T - HEADS)) {
         return;
       }
+      stamp(T, t0, T < HEADS ? 0 : 1);
     }
   }
 
@@ -83,6 +85,18 @@ class Back {
   GuardArgs guard_args;
   Guard gd;
   int tid, lane, wave, g, r, G, S;
+  uint64_t waited = 0;
+
+  // timeline row of task T: start, inputs-ready and end ticks, workgroup << 8 | stage
+  MONO_DEV void stamp(int T, uint64_t t0, int kind) const {
+    if (A.timeline && tid == 0) {
+      int64_t* tl = A.timeline + (size_t)T * 4;
+      tl[0] = (int64_t)t0;
+      tl[1] = (int64_t)waited;
+      tl[2] = (int64_t)now_ticks();
+      tl[3] = ((int64_t)blockIdx.x << 8) | kind;
+    }
+  }
 
   MONO_DEV void stage_u(int h) {
     u32x4 WR[8];
@@ -99,6 +113,7 @@ class Back {
       *reinterpret_cast<u32x4*>(&L.u.xu[s][8 * p]) = ld_u32x4(olat + ((size_t)s * HEADS + h) * KV_LORA + 8 * p);
     }
     __syncthreads();
+    waited = now_ticks();
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc += SC[j] * step_fp8(join(WR[2 * j], WR[2 * j + 1]), &L.u.xu[r][128 * j + 32 * g]);
@@ -127,24 +142,31 @@ class Back {
       ld_fp8_tile(static_cast<const uint8_t*>(W.w_o), O_K / 32, rg, ks, g, r, WR[2 * j], WR[2 * j + 1]);
       SC[j] = W.s_o[(rg * 16 / 128) * (O_K / 128) + ks];
     }
-    // o of every row: S x 2048 bf16 pairs
+    // one hint word a head (W_UV task): its last pair of the last row
+    const uint64_t* oh = M.ob + (size_t)(S - 1) * (O_K / 2);
+    if (!hint_wait(HEADS, [oh](int i) { return oh + (size_t)i * (VDIM / 2) + VDIM / 2 - 1; }, W_OB, gd)) return false;
+    // o of every row: S x 2048 bf16 pairs, thread t words t + 512 q (coalesced), 4 rows a
+    // sweep
+    constexpr int B = 16;
     const int total = S * (O_K / 2);
-    for (int base = 0; base < total; base += FT * 8) {
-      uint32_t v[8];
+    for (int base = 0; base < total; base += FT * B) {
+      uint32_t v[B];
       uint32_t pending = 0;
 #pragma unroll
-      for (int q = 0; q < 8; ++q)
+      for (int q = 0; q < B; ++q)
         if (base + tid + FT * q < total) pending |= 1u << q;
       const uint64_t* ob = M.ob + base + tid;
-      const bool ok = poll_words<8>([ob](int q) { return ob + FT * q; }, v, pending, W_OB, gd);
+      const auto at = [ob](int q) { return ob + FT * q; };
+      const bool ok = poll_words<B, decltype(at), true>(at, v, pending, W_OB, gd);
       if (!block_all(ok)) return false;
 #pragma unroll
-      for (int q = 0; q < 8; ++q) {
+      for (int q = 0; q < B; ++q) {
         const int w = base + tid + FT * q;
         if (w < total) *reinterpret_cast<uint32_t*>(&L.u.xo[w / (O_K / 2)][2 * (w % (O_K / 2))]) = v[q];
       }
     }
     __syncthreads();
+    waited = now_ticks();
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < 8; ++j) {

@@ -31,32 +31,37 @@ constexpr int FW = FT / WAVE;
 
 constexpr int A_TILES = (N_QKV + ID) / 16;   // FP8 tiles of stage A
 constexpr int W_TILES = IH / 16;             // bf16 tiles of stage A
-constexpr int NT_A = (A_TILES + W_TILES) * KP;
-constexpr int A_STEPS = HIDDEN / 128 / KP;   // 128-k steps a K part
-constexpr int A_KW = HIDDEN / KP;            // k of a part
-constexpr int XA = A_KW + 8;                 // LDS row stride (bf16): rows 4 banks apart
+constexpr int KPW = 4;                       // K parts of a bf16 tile
 constexpr int QB_TILES = HEADS * QK / 64;
 constexpr int NT_C = QB_TILES + IH * ID / 64;
+constexpr int XA_ELEMS = MAX_ROWS * (HIDDEN / 2 + 8);  // 8 rows of K or 16 rows of K / 2
 constexpr int XC = Q_LORA + 8;
 constexpr int XD = NOPE + 8;
 constexpr int ROW_PIECES = HIDDEN / 8;       // 16-byte pieces of an input row
-constexpr int PART_PIECES = ROW_PIECES / KP;
+constexpr int RPL = ROW_PIECES / WAVE;       // pieces a lane holds of a row
+constexpr int MAX_STEPS_W = 7;               // 128-k steps a wave of a stage-A tile, at most
 constexpr float EPS = 1e-6f;
 constexpr float LN_EPS = 1e-6f;
 constexpr float INDEX_W_SCALE = 0.011048543456039804f;  // 128^-1/2 * 64^-1/2
-static_assert(A_STEPS == 3 * FW + 4 && PART_PIECES % WAVE == 0 && ROW_PIECES % WAVE == 0, "stage A split");
+static_assert(ROW_PIECES % WAVE == 0 && KPW <= MAX_PARTS, "stage A split");
+
+// FP8 tiles of stage A are split in K in kp_fp8(S) parts: whole (8 rows of K fit the
+// LDS) up to 8 rows, halves above
+MONO_DEV int kp_fp8(int S) { return S <= 8 ? 1 : 2; }
+MONO_DEV int nt_a(int S) { return A_TILES * kp_fp8(S) + W_TILES * KPW; }
 
 enum { W_PA = 0, W_QAN = 1, W_QNOPE = 2, W_IQRAW = 3 };
 
 struct Lds {
   union {
-    uint16_t xa[MAX_ROWS][XA];
+    uint16_t xa[XA_ELEMS];  // stage A rows, stride = the part's k + 8
     uint16_t xc[MAX_ROWS][XC];
     uint16_t xd[MAX_ROWS][XD];
-    float row[KP][N_A];
+    float row[MAX_PARTS][N_A];
   } u;
   f32x4 red[FW][WAVE];
   float stat[FW][2];
+  uint16_t gin[HIDDEN];  // the input RMSNorm weight, loaded once a launch
   uint32_t tag;
   uint32_t err;
 };
@@ -93,23 +98,34 @@ class Front {
     gd.a = guard_args;
     gd.tag = L.tag;
     gd.deadline = now_ticks() + guard_args.deadline_ticks;
+    for (int p = tid; p < ROW_PIECES; p += FT)
+      *reinterpret_cast<u32x4*>(&L.gin[8 * p]) = ld_u32x4(static_cast<const uint16_t*>(W.g_in) + 8 * p);
+    __syncthreads();
     for (int T = blockIdx.x;; T += G) {
-      int t = T;
+      relane();
+      int t = T, kind;
       bool ok = true;
-      if (t < NT_A) {
+      const uint64_t t0 = now_ticks();
+      if (t < nt_a(S)) {
+        kind = 0;
         stage_a(t);
-      } else if ((t -= NT_A) < S) {
+      } else if ((t -= nt_a(S)) < S) {
+        kind = 1;
         ok = stage_b(t);
       } else if ((t -= S) < NT_C) {
+        kind = 2;
         ok = stage_c(t);
       } else if ((t -= NT_C) < HEADS) {
+        kind = 3;
         ok = stage_d(t);
       } else if ((t -= HEADS) < S * (IH / FW)) {
+        kind = 4;
         ok = stage_e(t);
       } else {
         break;
       }
       if (!ok) return;
+      stamp(T, t0, kind);
     }
   }
 
@@ -121,6 +137,32 @@ class Front {
   GuardArgs guard_args;
   Guard gd;
   int tid, lane, wave, g, r, G, S;
+  uint64_t waited = 0;
+
+  // Re-derive the thread's coordinates through an opaque copy at every task, so the
+  // compiler cannot hoist each stage's per-thread address arithmetic out of the task
+  // loop (held across all stages, it spills).
+  MONO_DEV void relane() {
+    int t = (int)threadIdx.x;
+    asm volatile("" : "+v"(t));
+    tid = t;
+    lane = t % WAVE;
+    wave = __builtin_amdgcn_readfirstlane(t / WAVE);  // wave-uniform: scalar branches
+    g = lane / 16;
+    r = lane % 16;
+  }
+
+  // timeline row of task T: start, inputs-ready and end ticks, workgroup << 8 | stage
+  MONO_DEV void stamp(int T, uint64_t t0, int kind) const {
+    if (A.timeline && tid == 0) {
+      int64_t* tl = A.timeline + (size_t)T * 4;
+      tl[0] = (int64_t)t0;
+      tl[1] = (int64_t)waited;
+      tl[2] = (int64_t)now_ticks();
+      tl[3] = ((int64_t)blockIdx.x << 8) | kind;
+    }
+  }
+  MONO_DEV void mark_waited() { waited = now_ticks(); }
 
   // ------------------------------------------------------------ row helpers
   // position of row s's new token and its cache slot (-1: a pad row writes nothing)
@@ -157,47 +199,61 @@ class Front {
   }
 
   // ------------------------------------------------------------ stage A
+  // A tile's weights go out first as one uninterrupted burst of loads (vector memory
+  // completes in order, so nothing that must be waited for may sit between them); the
+  // rows then go to LDS by DMA (global_load_lds, no registers) and are normed in place.
   MONO_DEV void stage_a(int t) {
-    const int tile = t / KP, part = t % KP;
-    const bool bf16w = tile >= A_TILES;
-    const int nj = wave < A_STEPS - 3 * FW ? 4 : 3;
-    u32x4 WR[16];
-    float SC[4];
+    const int kp = kp_fp8(S);
+    const bool bf16w = t >= A_TILES * kp;
+    const int u = bf16w ? t - A_TILES * kp : t;
+    const int parts = bf16w ? KPW : kp;
+    const int tile = u / parts, part = u % parts;
+    const int steps = HIDDEN / 128 / parts;  // 128-k steps of the part
+    const int kw = steps * 128;
+    const int nj = (steps - wave + FW - 1) / FW;  // this wave's steps: wave + 8 j
+    // staged rows: k in [sk0, sk0 + skw), the FP8 part or the half holding a bf16 quarter
+    const int spart = bf16w ? part / (KPW / kp) : part;
+    const int skw = HIDDEN / kp, sk0 = spart * skw, sstride = skw + 8;
+    const int koff = part * kw - sk0;
+
+    // 1. weights (every load unconditional: surplus steps repeat the wave's last one
+    // and are not computed; a load under a condition is waited for at the join)
+    u32x4 WR[2 * MAX_STEPS_W];
+    float SC[MAX_STEPS_W];
     if (!bf16w) {
       const bool qkv = tile < N_QKV / 16;
       const uint8_t* wb = static_cast<const uint8_t*>(qkv ? W.w_qkv : W.w_ik);
       const float* sb = qkv ? W.s_qkv : W.s_ik;
       const int rg = qkv ? tile : tile - N_QKV / 16;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int ks = part * A_STEPS + wave + FW * j;
-        if (j < nj) {
-          ld_fp8_tile(wb, HIDDEN / 32, rg, ks, g, r, WR[2 * j], WR[2 * j + 1]);
-          SC[j] = sb[(rg * 16 / 128) * (HIDDEN / 128) + ks];
-        } else {
-          WR[2 * j] = WR[2 * j + 1] = u32x4{0u, 0u, 0u, 0u};
-          SC[j] = 0.f;
-        }
+      for (int j = 0; j < MAX_STEPS_W; ++j) {
+        const int ks = part * steps + wave + FW * min(j, nj - 1);
+        ld_fp8_tile(wb, HIDDEN / 32, rg, ks, g, r, WR[2 * j], WR[2 * j + 1]);
+        SC[j] = sb[(rg * 16 / 128) * (HIDDEN / 128) + ks];
       }
     } else {
       const uint8_t* wb = static_cast<const uint8_t*>(W.w_iw);
-      const int rg = tile - A_TILES;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int ks = part * A_STEPS + wave + FW * j;
+      for (int j = 0; j < MAX_STEPS_W / 2; ++j) {
+        const int ks = part * steps + wave + FW * min(j, nj - 1);
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-          WR[4 * j + q] = j < nj ? ld_bf16_tile(wb, HIDDEN * 2 / 32, rg, ks, g, r, q) : u32x4{0u, 0u, 0u, 0u};
+        for (int q = 0; q < 4; ++q) WR[4 * j + q] = ld_bf16_tile(wb, HIDDEN * 2 / 32, tile, ks, g, r, q);
       }
+#pragma unroll
+      for (int q = 4 * (MAX_STEPS_W / 2); q < 2 * MAX_STEPS_W; ++q) WR[q] = u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int j = 0; j < MAX_STEPS_W; ++j) SC[j] = 0.f;
     }
-    stage_rows(part);
-    __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
+    stage_rows(sk0, skw, sstride);
+    mark_waited();
 
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    const int rr = min(r, S - 1);  // rows past the step: copies of the last, dropped below
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      if (j < nj) {
-        const uint16_t* brow = &L.u.xa[r][128 * (wave + FW * j) + 32 * g];
+    for (int j = 0; j < MAX_STEPS_W; ++j) {
+      if (j < nj && (!bf16w || j < MAX_STEPS_W / 2)) {
+        const uint16_t* brow = &L.u.xa[rr * sstride + koff + 128 * (wave + FW * j) + 32 * g];
         if (!bf16w) {
           acc += SC[j] * step_fp8(join(WR[2 * j], WR[2 * j + 1]), brow);
         } else {
@@ -213,78 +269,138 @@ class Front {
       float v = 0.f;
 #pragma unroll
       for (int w = 0; w < FW; ++w) v += L.red[w][l][i];
-      const int s = l % 16, row = tile * 16 + 4 * (l / 16) + i;
+      const int s = l % 16, row = (bf16w ? A_TILES * 16 : 0) + tile * 16 + 4 * (l / 16) + i;
       if (s < S) mb_putf(&M.pa[((size_t)part * MAX_ROWS + s) * N_A + row], v, gd.tag);
     }
     __syncthreads();  // the next task rewrites the LDS
   }
 
-  // Input RMSNorm (glm53/gfx950/kernel.py:1367-1398): wave w takes rows w, w + 8: the
-  // whole row's squares (deterministic wave sum), then bf16(x rstd gamma) of the K
-  // part into LDS.
-  MONO_DEV void stage_rows(int part) {
-    const uint16_t* gamma = static_cast<const uint16_t*>(W.g_in);
-    for (int s = wave; s < S; s += FW) {
-      const uint16_t* hrow = static_cast<const uint16_t*>(A.h) + (size_t)s * HIDDEN;
-      u32x4 mine[PART_PIECES / WAVE], other[PART_PIECES / WAVE];
+  // Input RMSNorm (glm53/gfx950/kernel.py:1367-1398) into LDS: wave w takes rows w, w + 8.
+  // k in [k0, k0 + kw) goes to LDS by DMA (lane l's 16 bytes land at the wave's base +
+  // 16 l), the rest of the row (rows > 8 only) into registers for the sum of squares;
+  // then each row's squares are summed (deterministic wave sum) and the staged part
+  // scaled in place to bf16(x rstd gamma).
+  MONO_DEV void stage_rows(int k0, int kw, int stride) {
+    const uint16_t* hbase = static_cast<const uint16_t*>(A.h);
+    const int m0 = k0 / (8 * WAVE), mw = kw / (8 * WAVE);  // staged 1 KB pieces a row
+    u32x4 ov[2][RPL / 2];  // the unstaged half of up to two rows (kp = 2)
+    for (int s = wave, n = 0; s < S; s += FW, ++n) {
+      const uint16_t* hrow = hbase + (size_t)s * HIDDEN;
+      for (int m = 0; m < mw; ++m)
+        __builtin_amdgcn_global_load_lds(hrow + 8 * (lane + WAVE * (m0 + m)), &L.u.xa[s * stride + 8 * WAVE * m], 16, 0, 0);
+      if (mw < RPL) {
+        const int mo = m0 == 0 ? RPL / 2 : 0;
 #pragma unroll
-      for (int m = 0; m < PART_PIECES / WAVE; ++m) {
-        mine[m] = ld_u32x4(hrow + 8 * (part * PART_PIECES + lane + WAVE * m));
-        other[m] = ld_u32x4(hrow + 8 * ((1 - part) * PART_PIECES + lane + WAVE * m));
-      }
-      float ss = 0.f;
-#pragma unroll
-      for (int m = 0; m < PART_PIECES / WAVE; ++m) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float a0 = bf16_lo(mine[m][e]), a1 = bf16_hi(mine[m][e]);
-          const float b0 = bf16_lo(other[m][e]), b1 = bf16_hi(other[m][e]);
-          ss += a0 * a0 + a1 * a1 + b0 * b0 + b1 * b1;
+        for (int m = 0; m < RPL / 2; ++m) {
+          const u32x4 x = ld_u32x4(hrow + 8 * (lane + WAVE * (mo + m)));
+          if (n == 0) ov[0][m] = x;
+          else ov[1][m] = x;
         }
-        __builtin_amdgcn_sched_barrier(0);  // one piece at a time: the rest stay packed
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    for (int s = wave, n = 0; s < S; s += FW, ++n) {
+      float ss = 0.f;
+      for (int m = 0; m < mw; ++m) {
+        const u32x4 x = *reinterpret_cast<const u32x4*>(&L.u.xa[s * stride + 8 * (lane + WAVE * m)]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ss += bf16_lo(x[e]) * bf16_lo(x[e]) + bf16_hi(x[e]) * bf16_hi(x[e]);
+      }
+      if (mw < RPL) {
+#pragma unroll
+        for (int m = 0; m < RPL / 2; ++m) {
+          const u32x4 x = n == 0 ? ov[0][m] : ov[1][m];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) ss += bf16_lo(x[e]) * bf16_lo(x[e]) + bf16_hi(x[e]) * bf16_hi(x[e]);
+        }
       }
       ss = wave_sum(ss);
       const float rstd = 1.0f / sqrtf(ss / (float)HIDDEN + EPS);
-#pragma unroll
-      for (int m = 0; m < PART_PIECES / WAVE; ++m) {
-        const int pc = lane + WAVE * m;
-        const u32x4 gw = ld_u32x4(gamma + 8 * (part * PART_PIECES + pc));
+      for (int m = 0; m < mw; ++m) {
+        u32x4* px = reinterpret_cast<u32x4*>(&L.u.xa[s * stride + 8 * (lane + WAVE * m)]);
+        const u32x4 x = *px;
+        const u32x4 gw = *reinterpret_cast<const u32x4*>(&L.gin[k0 + 8 * (lane + WAVE * m)]);
         u32x4 o;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const float y0 = mul_rn(mul_rn(bf16_lo(mine[m][e]), rstd), bf16_lo(gw[e]));
-          const float y1 = mul_rn(mul_rn(bf16_hi(mine[m][e]), rstd), bf16_hi(gw[e]));
+          const float y0 = mul_rn(mul_rn(bf16_lo(x[e]), rstd), bf16_lo(gw[e]));
+          const float y1 = mul_rn(mul_rn(bf16_hi(x[e]), rstd), bf16_hi(gw[e]));
           o[e] = pack_bf16x2(y0, y1);
         }
-        *reinterpret_cast<u32x4*>(&L.u.xa[s][8 * pc]) = o;
-        __builtin_amdgcn_sched_barrier(0);
+        *px = o;
       }
     }
+    __syncthreads();
   }
 
   // ------------------------------------------------------------ stage B
   MONO_DEV bool stage_b(int s) {
-    constexpr int NW = KP * N_A / FT;
-    static_assert(KP * N_A % FT == 0, "row words");
+    constexpr int NW = (2 * (N_QKV + ID) + KPW * IH + FT - 1) / FT;  // words a thread polls, at most
+    const int kp = kp_fp8(S);
+    const int n_fp8 = kp * (N_QKV + ID), total = n_fp8 + KPW * IH;
+    // everything but the partial sums is loaded before the wait
+    const int slot = slot_of(s), pr = rope_row(s);
+    const float cl = A.rope_cos[(size_t)pr * (PE_DIM / 2) + tid % (PE_DIM / 2)];
+    const float sl = A.rope_sin[(size_t)pr * (PE_DIM / 2) + tid % (PE_DIM / 2)];
+    const uint16_t* gq = static_cast<const uint16_t*>(W.g_q);
+    const uint32_t gq0 = *reinterpret_cast<const uint32_t*>(gq + 2 * tid);
+    const uint32_t gq1 = *reinterpret_cast<const uint32_t*>(gq + 2 * min(tid + FT, Q_LORA / 2 - 1));
+    const float gkv = bf16_bits_to_f32(static_cast<const uint16_t*>(W.g_kv)[tid]);
+    const float gik0 = W.g_ik[2 * lane], gik1 = W.g_ik[2 * lane + 1];
+    const float bik0 = W.b_ik[2 * lane], bik1 = W.b_ik[2 * lane + 1];
     {
+      // one hint word a stage-A task: its last output row of row s
+      const uint64_t* pah = M.pa;
+      const int na = nt_a(S);
+      const bool hok = hint_wait(
+          na,
+          [pah, s, kp](int i) {
+            const bool bw = i >= A_TILES * kp;
+            const int u = bw ? i - A_TILES * kp : i, parts = bw ? KPW : kp;
+            const int tile = u / parts, part = u % parts;
+            const int row = (bw ? A_TILES * 16 : 0) + tile * 16 + 15;
+            return pah + ((size_t)part * MAX_ROWS + s) * N_A + row;
+          },
+          W_PA, gd);
+      if (!hok) return false;
       uint32_t v[NW];
+      uint32_t pending = 0;
+#pragma unroll
+      for (int m = 0; m < NW; ++m)
+        if (tid + FT * m < total) pending |= 1u << m;
       const uint64_t* pa = M.pa;
       const int t0 = tid;
-      const bool ok = poll_words<NW>(
-          [pa, t0, s](int m) {
-            const int w = t0 + FT * m, part = w / N_A, col = w % N_A;
-            return pa + ((size_t)part * MAX_ROWS + s) * N_A + col;
-          },
-          v, (1u << NW) - 1u, W_PA, gd);
+      const auto at = [pa, t0, s, kp, n_fp8](int m) {
+        const int w = t0 + FT * m;
+        int part, col;
+        if (w < n_fp8) {
+          part = w / (N_QKV + ID);
+          col = w % (N_QKV + ID);
+        } else {
+          part = (w - n_fp8) / IH;
+          col = N_QKV + ID + (w - n_fp8) % IH;
+        }
+        return pa + ((size_t)part * MAX_ROWS + s) * N_A + col;
+      };
+      const bool ok = poll_words<NW>(at, v, pending, W_PA, gd);
       if (!block_all(ok)) return false;
+      mark_waited();
 #pragma unroll
       for (int m = 0; m < NW; ++m) {
         const int w = tid + FT * m;
-        L.u.row[w / N_A][w % N_A] = __uint_as_float(v[m]);
+        if (w < n_fp8) L.u.row[w / (N_QKV + ID)][w % (N_QKV + ID)] = __uint_as_float(v[m]);
+        else if (w < total) L.u.row[(w - n_fp8) / IH][N_QKV + ID + (w - n_fp8) % IH] = __uint_as_float(v[m]);
       }
     }
     __syncthreads();
-    for (int c = tid; c < N_A; c += FT) L.u.row[0][c] = L.u.row[0][c] + L.u.row[1][c];
+    // the K parts summed in part order
+    for (int c = tid; c < N_A; c += FT) {
+      const int np = c < N_QKV + ID ? kp : KPW;
+      float v = L.u.row[0][c];
+      for (int p = 1; p < np; ++p) v += L.u.row[p][c];
+      L.u.row[0][c] = v;
+    }
     __syncthreads();
     const float* row = L.u.row[0];
 
@@ -297,24 +413,24 @@ class Front {
     const float rk = 1.0f / sqrtf(ss[1] / (float)KV_LORA + EPS);
 
     // q_an, published as bf16 pairs
-    const uint16_t* gq = static_cast<const uint16_t*>(W.g_q);
-    for (int j = tid; j < Q_LORA / 2; j += FT) {
-      const uint32_t gw = *reinterpret_cast<const uint32_t*>(gq + 2 * j);
-      const float y0 = mul_rn(mul_rn(row[2 * j], rq), bf16_lo(gw));
-      const float y1 = mul_rn(mul_rn(row[2 * j + 1], rq), bf16_hi(gw));
-      mb_put(&M.qan[(size_t)s * (Q_LORA / 2) + j], pack_bf16x2(y0, y1), gd.tag);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int j = tid + FT * h;
+      if (j < Q_LORA / 2) {
+        const uint32_t gw = h == 0 ? gq0 : gq1;
+        const float y0 = mul_rn(mul_rn(row[2 * j], rq), bf16_lo(gw));
+        const float y1 = mul_rn(mul_rn(row[2 * j + 1], rq), bf16_hi(gw));
+        mb_put(&M.qan[(size_t)s * (Q_LORA / 2) + j], pack_bf16x2(y0, y1), gd.tag);
+      }
     }
 
     // KV row: bf16 latent and RoPE'd k_pe, one power-of-two E4M3 scale
-    const int slot = slot_of(s), pr = rope_row(s);
-    const float c0 = tid < PE_DIM / 2 ? A.rope_cos[(size_t)pr * (PE_DIM / 2) + tid] : 0.f;
-    const float s0 = tid < PE_DIM / 2 ? A.rope_sin[(size_t)pr * (PE_DIM / 2) + tid] : 0.f;
-    const float kvn = bf16_round(mul_rn(mul_rn(kv, rk), bf16_bits_to_f32(static_cast<const uint16_t*>(W.g_kv)[tid])));
+    const float kvn = bf16_round(mul_rn(mul_rn(kv, rk), gkv));
     float p0 = 0.f, p1 = 0.f;
     if (tid < PE_DIM / 2) {
       p0 = row[Q_LORA + KV_LORA + 2 * tid];
       p1 = row[Q_LORA + KV_LORA + 2 * tid + 1];
-      rope_pair(p0, p1, c0, s0);
+      rope_pair(p0, p1, cl, sl);
       p0 = bf16_round(p0);
       p1 = bf16_round(p1);
     }
@@ -347,10 +463,9 @@ class Front {
       const float mean = wave_sum(v0 + v1) / (float)ID;
       const float d0 = sub_rn(v0, mean), d1 = sub_rn(v1, mean);
       const float rs = 1.0f / sqrtf(wave_sum(d0 * d0 + d1 * d1) / (float)ID + LN_EPS);
-      float y0 = add_rn(mul_rn(mul_rn(d0, rs), W.g_ik[2 * lane]), W.b_ik[2 * lane]);
-      float y1 = add_rn(mul_rn(mul_rn(d1, rs), W.g_ik[2 * lane + 1]), W.b_ik[2 * lane + 1]);
-      if (lane < PE_DIM / 2)
-        rope_pair(y0, y1, A.rope_cos[(size_t)pr * (PE_DIM / 2) + lane], A.rope_sin[(size_t)pr * (PE_DIM / 2) + lane]);
+      float y0 = add_rn(mul_rn(mul_rn(d0, rs), gik0), bik0);
+      float y1 = add_rn(mul_rn(mul_rn(d1, rs), gik1), bik1);
+      if (lane < PE_DIM / 2) rope_pair(y0, y1, cl, sl);
       uint32_t e8;
       const uint32_t byte = index_vec_fp4(y0, y1, lane, e8);
       if (slot >= 0) {
@@ -372,27 +487,27 @@ class Front {
   }
 
   // ------------------------------------------------------------ stage C
-  // poll S rows of n words (bf16 pairs) from `mb` (row stride `stride` words) into
-  // LDS rows of `xs` (stride `xstride` bf16)
-  template <int XS>
+  // Poll S rows of n words (bf16 pairs) from `mb` (rows `stride` words apart) into LDS
+  // rows of `xs`. Thread t takes words t + 512 q of the S x n range: each poll
+  // instruction of a wave covers 512 contiguous bytes (the loads coalesce).
+  template <int XS, int B>
   MONO_DEV bool stage_pairs(const uint64_t* mb, int n, size_t stride, uint16_t (*xs)[XS], int site) {
     const int total = S * n;
-    for (int base = 0; base < total; base += FT * 8) {
-      uint32_t v[8];
+    for (int base = 0; base < total; base += FT * B) {
+      uint32_t v[B];
       uint32_t pending = 0;
 #pragma unroll
-      for (int q = 0; q < 8; ++q)
+      for (int q = 0; q < B; ++q)
         if (base + tid + FT * q < total) pending |= 1u << q;
       const int t0 = base + tid;
-      const bool ok = poll_words<8>(
-          [mb, t0, n, stride](int q) {
-            const int w = t0 + FT * q;
-            return mb + (size_t)(w / n) * stride + w % n;
-          },
-          v, pending, site, gd);
+      const auto at = [mb, t0, n, stride](int q) {
+        const int w = t0 + FT * q;
+        return mb + (size_t)(w / n) * stride + w % n;
+      };
+      const bool ok = poll_words<B, decltype(at), true>(at, v, pending, site, gd);
       if (!block_all(ok)) return false;
 #pragma unroll
-      for (int q = 0; q < 8; ++q) {
+      for (int q = 0; q < B; ++q) {
         const int w = t0 + FT * q;
         if (w < total) *reinterpret_cast<uint32_t*>(&xs[w / n][2 * (w % n)]) = v[q];
       }
@@ -413,8 +528,20 @@ class Front {
       ld_fp8_tile(wb, Q_LORA / 32, rg, ks, g, r, WR[2 * j], WR[2 * j + 1]);
       SC[j] = sb[(rg * 16 / 128) * (Q_LORA / 128) + ks];
     }
-    if (!stage_pairs<XC>(M.qan, Q_LORA / 2, Q_LORA / 2, L.u.xc, W_QAN)) return false;
+    // this thread's output pair (after the wave-pair reduction) and, for a q_pe tile,
+    // its RoPE factors, loaded before the wait
+    const int rgl = tid / 128, l = (tid / 2) % WAVE, pi = tid % 2;
+    const int ch = 16 * rgl + 4 * (l / 16) + 2 * pi, so = l % 16;
+    const int qrow = 64 * c + ch, qd = qrow % QK;
+    const int prc = rope_row(min(so, S - 1)), ic = max(qd - NOPE, 0) / 2;
+    const float rc = A.rope_cos[(size_t)prc * (PE_DIM / 2) + ic];
+    const float rs = A.rope_sin[(size_t)prc * (PE_DIM / 2) + ic];
+    const uint64_t* qh = M.qan;
+    if (!hint_wait(S, [qh](int i) { return qh + (size_t)i * (Q_LORA / 2) + Q_LORA / 2 - 1; }, W_QAN, gd))
+      return false;
+    if (!stage_pairs<XC, 16>(M.qan, Q_LORA / 2, Q_LORA / 2, L.u.xc, W_QAN)) return false;
     __syncthreads();
+    mark_waited();
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < 6; ++j) {
@@ -424,19 +551,18 @@ class Front {
     L.red[wave][lane] = acc;
     __syncthreads();
     {
-      const int rgl = tid / 128, l = (tid / 2) % WAVE, pi = tid % 2;
       const float v0 = L.red[2 * rgl][l][2 * pi] + L.red[2 * rgl + 1][l][2 * pi];
       const float v1 = L.red[2 * rgl][l][2 * pi + 1] + L.red[2 * rgl + 1][l][2 * pi + 1];
-      const int ch = 16 * rgl + 4 * (l / 16) + 2 * pi, s = l % 16;
+      const int s = so;
       if (s < S) {
         if (qb) {
-          const int row = 64 * c + ch, head = row / QK, d = row % QK;
+          const int row = qrow, head = row / QK, d = qd;
           if (d < NOPE) {
             mb_put(&M.qnope[((size_t)s * HEADS + head) * (NOPE / 2) + d / 2], pack_bf16x2(v0, v1), gd.tag);
           } else {
-            const int i = (d - NOPE) / 2, pr = rope_row(s);
+            const int i = (d - NOPE) / 2;
             float x0 = v0, x1 = v1;
-            rope_pair(x0, x1, A.rope_cos[(size_t)pr * (PE_DIM / 2) + i], A.rope_sin[(size_t)pr * (PE_DIM / 2) + i]);
+            rope_pair(x0, x1, rc, rs);
             *reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(A.q) + ((size_t)s * HEADS + head) * (KV_LORA + PE_DIM) +
                                          KV_LORA + 2 * i) = pack_bf16x2(x0, x1);
           }
@@ -460,9 +586,12 @@ class Front {
       ld_fp8_tile(static_cast<const uint8_t*>(W.w_uk), NOPE / 32, rg, 0, g, r, WR[2 * j], WR[2 * j + 1]);
       SC[j] = W.s_uk[rg * 16 / 128];
     }
-    if (!stage_pairs<XD>(M.qnope + (size_t)h * (NOPE / 2), NOPE / 2, (size_t)HEADS * (NOPE / 2), L.u.xd, W_QNOPE))
+    const uint64_t* nh = M.qnope + ((size_t)(S - 1) * HEADS + h) * (NOPE / 2);
+    if (!hint_wait(2, [nh](int i) { return nh + 32 * i + 31; }, W_QNOPE, gd)) return false;
+    if (!stage_pairs<XD, 16>(M.qnope + (size_t)h * (NOPE / 2), NOPE / 2, (size_t)HEADS * (NOPE / 2), L.u.xd, W_QNOPE))
       return false;
     __syncthreads();
+    mark_waited();
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const f32x4 v = SC[j] * step_fp8(join(WR[2 * j], WR[2 * j + 1]), &L.u.xd[r][32 * g]);
@@ -481,14 +610,18 @@ class Front {
   // ------------------------------------------------------------ stage E
   MONO_DEV bool stage_e(int e) {
     const int s = e / (IH / FW), head = (e % (IH / FW)) * FW + wave;
+    const int pr = rope_row(s);
+    const float rc = A.rope_cos[(size_t)pr * (PE_DIM / 2) + lane % (PE_DIM / 2)];
+    const float rs = A.rope_sin[(size_t)pr * (PE_DIM / 2) + lane % (PE_DIM / 2)];
+    const uint64_t* ih = M.iqraw + ((size_t)s * IH + (e % (IH / FW)) * FW) * (ID / 2);
+    if (!hint_wait(2 * FW, [ih](int i) { return ih + (size_t)(i / 2) * (ID / 2) + 32 * (i % 2) + 31; }, W_IQRAW, gd))
+      return false;
     uint32_t v;
     const bool ok = poll_word(&M.iqraw[((size_t)s * IH + head) * (ID / 2) + lane], v, W_IQRAW, gd);
     if (!block_all(ok)) return false;
+    mark_waited();
     float a = bf16_lo(v), b = bf16_hi(v);
-    if (lane < PE_DIM / 2) {
-      const int pr = rope_row(s);
-      rope_pair(a, b, A.rope_cos[(size_t)pr * (PE_DIM / 2) + lane], A.rope_sin[(size_t)pr * (PE_DIM / 2) + lane]);
-    }
+    if (lane < PE_DIM / 2) rope_pair(a, b, rc, rs);
     uint32_t e8;
     const uint32_t byte = index_vec_fp4(a, b, lane, e8);
     static_cast<uint8_t*>(A.iq)[((size_t)s * IH + head) * (ID / 2) + lane] = (uint8_t)byte;

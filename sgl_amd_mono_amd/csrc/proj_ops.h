@@ -15,18 +15,18 @@ constexpr int HEADS = 32, NOPE = 128, QK = NOPE + PE_DIM, VDIM = 128;
 constexpr int IH = 64, ID = 128;
 constexpr int N_QKV = Q_LORA + KV_LORA + PE_DIM;  // 2112 rows of q_a | kv_a
 constexpr int N_A = N_QKV + ID + IH;              // stage-A outputs a row: q_a | kv_a | index k | index w
-constexpr int KP = 2;                             // K parts of a stage-A tile
+constexpr int MAX_PARTS = 4;                      // K parts of a stage-A tile, at most
 
 // Mailboxes of one projection runtime (tagged 64-bit words, see sync.h).
 struct Mail {
-  uint64_t* pa;     // [KP][MAX_ROWS][N_A]           stage-A partial sums, f32
+  uint64_t* pa;     // [MAX_PARTS][MAX_ROWS][N_A]    stage-A partial sums, f32
   uint64_t* qan;    // [MAX_ROWS][Q_LORA / 2]        normed q_a, bf16 pairs
   uint64_t* qnope;  // [MAX_ROWS][HEADS][NOPE / 2]   q_nope, bf16 pairs
   uint64_t* iqraw;  // [MAX_ROWS][IH][ID / 2]        raw index query, bf16 pairs
   uint64_t* ob;     // [MAX_ROWS][HEADS * VDIM / 2]  W_UV o_lat, bf16 pairs
   uint32_t* guard;  // [G_WORDS]
 };
-constexpr size_t MAIL_WORDS[5] = {(size_t)KP * MAX_ROWS * N_A, (size_t)MAX_ROWS * Q_LORA / 2,
+constexpr size_t MAIL_WORDS[5] = {(size_t)MAX_PARTS * MAX_ROWS * N_A, (size_t)MAX_ROWS * Q_LORA / 2,
                                   (size_t)MAX_ROWS * HEADS * NOPE / 2, (size_t)MAX_ROWS * IH * ID / 2,
                                   (size_t)MAX_ROWS * HEADS * VDIM / 2};
 

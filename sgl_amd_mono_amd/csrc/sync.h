@@ -54,6 +54,10 @@ MONO_DEV void mb_putf(uint64_t* p, float v, uint32_t tag) { mb_put(p, __float_as
 MONO_DEV uint64_t mb_load(const uint64_t* p) {
   return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// A plain (L2-cacheable) load of a mailbox word. Only a first pass after a hint wait
+// uses it: a line cached before its producer wrote it returns an old tag, and that word
+// is then polled with agent-scope loads, so a stale copy is never taken for data.
+MONO_DEV uint64_t mb_load_cached(const uint64_t* p) { return *p; }
 MONO_DEV uint32_t ld_agent_u32(const uint32_t* p) {
   return __hip_atomic_load(const_cast<uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -85,13 +89,35 @@ struct Guard {
 // Poll the mailbox words at(j) of this lane whose bit j is set in `pending` until each
 // carries `tag`; their payloads go to v[j]. `at` computes an address from its index,
 // so callers hold no arrays of pointers. False if the guard expired first.
-template <int N, class At>
+//
+// The first pass loads every pending word. While words are missing, a spin loads only
+// the first missing one (the probe) and sweeps the rest once the probe has arrived: a
+// waiting workgroup then costs one load a thread a spin, not one a word, so early
+// waiters do not flood the memory system the producers are streaming through.
+//
+// CACHED_FIRST: the first pass uses plain cacheable loads (after a hint wait has seen the
+// producers finish, so many workgroups reading one broadcast payload share the L2 of
+// their XCD instead of each fetching it from memory).
+template <int N, class At, bool CACHED_FIRST = false>
 MONO_DEV bool poll_words(At at, uint32_t (&v)[N], uint32_t pending, int site, const Guard& g) {
   if (pending && site == g.a.fault_site) {  // host-forced fault: the wait fails at once
     g.fail(site);
     return false;
   }
-  for (uint32_t spin = 1;; ++spin) {
+  if (CACHED_FIRST) {
+    uint64_t w[N];
+#pragma unroll
+    for (int j = 0; j < N; ++j)
+      if ((pending >> j) & 1u) w[j] = mb_load_cached(at(j));
+#pragma unroll
+    for (int j = 0; j < N; ++j)
+      if (((pending >> j) & 1u) && (uint32_t)(w[j] >> 32) == g.tag) {
+        v[j] = (uint32_t)w[j];
+        pending &= ~(1u << j);
+      }
+    if (!pending) return true;
+  }
+  const auto sweep = [&]() {
     uint64_t w[N];
 #pragma unroll
     for (int j = 0; j < N; ++j)
@@ -102,12 +128,27 @@ MONO_DEV bool poll_words(At at, uint32_t (&v)[N], uint32_t pending, int site, co
         v[j] = (uint32_t)w[j];
         pending &= ~(1u << j);
       }
-    if (!pending) return true;
-    // the deadline after the 1st, 33rd, ... poll; other workgroups' failures after the
+  };
+  sweep();
+  for (uint32_t spin = 1; pending; ++spin) {
+    uint64_t probe = 0;
+    bool sent = false;
+#pragma unroll
+    for (int j = 0; j < N; ++j)
+      if (!sent && ((pending >> j) & 1u)) {
+        probe = mb_load(at(j));
+        sent = true;
+      }
+    if ((uint32_t)(probe >> 32) == g.tag) {
+      sweep();
+      continue;
+    }
+    // the deadline after the 1st, 33rd, ... miss; other workgroups' failures after the
     // 32nd, 64th, ... (that check is a memory round trip, kept off the first retry)
     if (spin % POLL_CHECK <= 1 && g.expired(site, spin % POLL_CHECK == 0)) return false;
     __builtin_amdgcn_s_sleep(1);
   }
+  return true;
 }
 
 MONO_DEV bool poll_word(const uint64_t* p, uint32_t& v, int site, const Guard& g) {
@@ -115,6 +156,21 @@ MONO_DEV bool poll_word(const uint64_t* p, uint32_t& v, int site, const Guard& g
   const bool ok = poll_words<1>([p](int) { return p; }, vs, 1u, site, g);
   v = vs[0];
   return ok;
+}
+
+// Wait until each of n hint words carries the tag: thread i < n polls at(i), one word
+// that producer i of the awaited data writes with (or after) the rest of its share,
+// while the other threads wait at the barrier. The full poll that follows then mostly
+// finds every word in place on its first pass; meanwhile a waiting workgroup costs n
+// loads a spin instead of one a payload word. Workgroup-uniform result.
+template <class At>
+MONO_DEV bool hint_wait(int n, At at, int site, const Guard& g) {
+  bool ok = true;
+  for (int i = threadIdx.x; i < n; i += blockDim.x) {
+    uint32_t v;
+    ok = poll_word(at(i), v, site, g) && ok;
+  }
+  return __syncthreads_and(ok ? 1 : 0) != 0;
 }
 
 // Workgroup-uniform AND of a per-thread flag (a full barrier).

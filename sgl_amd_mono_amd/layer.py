@@ -28,6 +28,14 @@ QK_DIM = NOPE_DIM + PE_DIM
 INDEX_HEADS, INDEX_DIM = 64, 128
 N_QKV = Q_LORA + KV_LORA + PE_DIM
 MAX_ROWS = 16
+FRONT_TASKS_FIXED = 224 + 32 + 16  # stage C, D and bf16 stage-A tasks; B and E add 1 + 8 a row
+
+
+def front_tasks(rows: int) -> int:
+    """Tasks of one front launch: 140 FP8 stage-A tiles whole (rows <= 8) or in K
+    halves, 16 bf16 tile quarters, a row task and 8 index-query tasks a row, 224 + 32."""
+    return 140 * (1 if rows <= 8 else 2) + FRONT_TASKS_FIXED + 9 * rows
+BACK_TASKS = 32 + 224
 
 
 def _blocks(n: int) -> int:
@@ -135,9 +143,11 @@ class ProjRuntime(Runtime):
 
     def front(self, h: torch.Tensor, seq_lens: torch.Tensor, page_table: torch.Tensor, caches: AttnCaches,
               w: ProjWeights, rope_cos: torch.Tensor, rope_sin: torch.Tensor, out: FrontOut | None = None,
-              check_weights: bool = True) -> FrontOut:
+              check_weights: bool = True, timeline: torch.Tensor | None = None) -> FrontOut:
         """Rows ``h`` [rows, 7168] bf16 whose new tokens sit at ``seq_lens - 1`` ->
-        FrontOut; writes each row's MLA cache row and FP4 index key in place."""
+        FrontOut; writes each row's MLA cache row and FP4 index key in place.
+        ``timeline`` (int64 [front_tasks(rows), 4]) receives each task's start,
+        inputs-ready and end ticks and workgroup << 8 | stage."""
         dev = self.device
         S = self._rows(h, "h")
         need(h, "h", (S, HIDDEN), torch.bfloat16, dev)
@@ -166,14 +176,17 @@ class ProjRuntime(Runtime):
             h=P(h), seq_lens=P(seq_lens), page_table=P(page_table), pt_stride=page_table.shape[1],
             n_pages=pages, rope_cos=P(rope_cos), rope_sin=P(rope_sin), max_pos=rope_cos.shape[0],
             ikv=P(caches.ikv), iks=P(caches.iks), kv=P(caches.kv), kv_scale=P(caches.kv_scale),
-            q=P(out.q), iq=P(out.iq), iqs=P(out.iqs), iw=P(out.iw), rows=S,
+            q=P(out.q), iq=P(out.iq), iqs=P(out.iqs), iw=P(out.iw), rows=S, timeline=P(timeline),
         )  # fmt: skip
+        if timeline is not None:
+            need(timeline, "timeline", (front_tasks(S), 4), torch.int64, dev)
         ws = w.c_struct()
         _lib.check(_lib.lib().mono_front_forward(self._h, C.byref(ws), C.byref(args), self._stream()))
         return out
 
     def back(self, o_lat: torch.Tensor, h: torch.Tensor, w: ProjWeights, a: torch.Tensor | None = None,
-             o: torch.Tensor | None = None, check_weights: bool = True) -> torch.Tensor:
+             o: torch.Tensor | None = None, check_weights: bool = True,
+             timeline: torch.Tensor | None = None) -> torch.Tensor:
         """a = h + W_o W_UV o_lat [rows, 7168] bf16 (``o``, if given, receives W_UV o_lat
         [rows, 4096] bf16)."""
         dev = self.device
@@ -187,7 +200,9 @@ class ProjRuntime(Runtime):
         if o is not None:
             need(o, "o", (S, HEADS * V_DIM), torch.bfloat16, dev)
         P = _lib.ptr
-        args = _lib.BackArgs(o_lat=P(o_lat), h=P(h), a=P(a), o=P(o), rows=S)
+        if timeline is not None:
+            need(timeline, "timeline", (BACK_TASKS, 4), torch.int64, dev)
+        args = _lib.BackArgs(o_lat=P(o_lat), h=P(h), a=P(a), o=P(o), rows=S, timeline=P(timeline))
         ws = w.c_struct()
         _lib.check(_lib.lib().mono_back_forward(self._h, C.byref(ws), C.byref(args), self._stream()))
         return a
