@@ -21,6 +21,7 @@ from . import _lib
 from .runtime import Runtime, need
 
 IH, ID, NH, DQK, DV, PAGE, TOPK = 64, 128, 32, 576, 512, 64, 2048
+SPLITS = 32  # split tasks a row (64 selected tokens each)
 SOFTMAX_SCALE = (128 + 64) ** -0.5  # (qk_nope + qk_rope)^-1/2, glm53/gfx950/config.py:171-173
 
 
@@ -64,7 +65,7 @@ class AttnRuntime(Runtime):
     def n_tasks(self, rows: int) -> int:
         """Tasks of one launch over ``rows`` rows (the timeline's length)."""
         n_score = -(-rows * (self.max_ctx // 1024) // 16) * 16  # padded to whole top-k teams
-        return n_score + rows * 16 + rows * 16 + rows * (NH // 2)
+        return n_score + rows * 16 + rows * SPLITS + rows * (NH // 2)
 
     def forward(self, step: AttnStep, caches: AttnCaches, out: torch.Tensor | None = None,
                 debug: bool = False, timeline: torch.Tensor | None = None):

@@ -347,7 +347,7 @@ extern "C" int mono_attn_create(const mono_attn_config* cfg, mono_attn** out) {
   const size_t o_sel = cv.take(R * TOPK * 8);
   const size_t o_hist = cv.take(R * PASSES * TEAM * 256 * 8);
   const size_t o_cnt = cv.take(R * TEAM * 2 * 8);
-  const size_t o_part = cv.take(R * SPLITS * NH * DV * 8);
+  const size_t o_part = cv.take(R * SPLITS * NH * (DV / 2) * 8);
   const size_t o_ml = cv.take(R * SPLITS * NH * 2 * 8);
   mono_attn* a = new mono_attn();
   a->magic = ATTN_MAGIC;

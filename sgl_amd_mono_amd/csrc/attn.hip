@@ -74,10 +74,16 @@ struct SplitLds {
   float alpha[NH];
 };
 
+struct MergeLds {
+  float w[2][SPLITS];  // each split's weight e^(m_j - M), 0 for an empty split
+  float den[2];        // sum_j w_j l_j
+};
+
 struct Lds {
   union {
     TopkLds t;
     SplitLds sp;
+    MergeLds mg;
   } u;
   int32_t scan[AW];
   uint32_t tag;
@@ -486,23 +492,18 @@ class Step {
   static constexpr int GATHER = (SUB * (DQK / 16) + AT - 1) / AT;  // 16-byte loads a thread a sub-tile
 
   // Issue sub-tile st's cache-row loads: consecutive lanes read consecutive 16-byte
-  // chunks of a row.
+  // chunks of a row. Every load is unconditional (an empty slot or a surplus chunk
+  // reads row 0 and is masked later): a load under a condition is waited for at the
+  // join, which would serialize the gather's round trips.
   MONO_DEV void gather_load(const SplitLds& P, int st, u32x4 (&gv)[GATHER], float& gs) {
 #pragma unroll
     for (int i = 0; i < GATHER; ++i) {
-      const int f = tid + i * AT;
-      gv[i] = u32x4{0u, 0u, 0u, 0u};
-      if (f < SUB * (DQK / 16)) {
-        const int t = f / (DQK / 16), c = f % (DQK / 16);
-        const int slot = P.slot[st * SUB + t];
-        if (slot >= 0) gv[i] = ld_nt_u32x4(A.kv + (size_t)slot * DQK + c * 16);
-      }
+      const int f = min(tid + i * AT, SUB * (DQK / 16) - 1);
+      const int t = f / (DQK / 16), c = f % (DQK / 16);
+      const int slot = max(P.slot[st * SUB + t], 0);
+      gv[i] = ld_nt_u32x4(A.kv + (size_t)slot * DQK + c * 16);
     }
-    gs = 0.f;
-    if (tid < SUB) {
-      const int slot = P.slot[st * SUB + tid];
-      if (slot >= 0) gs = A.kv_scale[slot];
-    }
+    gs = A.kv_scale[max(P.slot[st * SUB + tid % SUB], 0)];
   }
 
   // bf16 column d of 8 consecutive rows from t0: a p.v operand (8 tokens of one dim).
@@ -518,28 +519,32 @@ class Step {
     return __builtin_bit_cast(bf16x8, w);
   }
 
-  // Store the gathered rows widened to bf16, row-major (swizzled).
-  MONO_DEV void gather_store(SplitLds& P, const u32x4 (&gv)[GATHER], float gs) {
+  // Store the gathered rows of sub-tile st widened to bf16, row-major (swizzled); the
+  // rows of empty slots as zeros (their loads read row 0).
+  MONO_DEV void gather_store(SplitLds& P, int st, const u32x4 (&gv)[GATHER], float gs) {
 #pragma unroll
     for (int i = 0; i < GATHER; ++i) {
       const int f = tid + i * AT;
       if (f < SUB * (DQK / 16)) {
         const int t = f / (DQK / 16), c = f % (DQK / 16);
-        u32x4 lo, hi;
+        const bool live = P.slot[st * SUB + t] >= 0;
+        u32x4 lo = {0u, 0u, 0u, 0u}, hi = {0u, 0u, 0u, 0u};
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
           const u32x2 a = fp8x4_bf16(gv[i][q]), b = fp8x4_bf16(gv[i][q + 2]);
-          lo[2 * q] = a[0];
-          lo[2 * q + 1] = a[1];
-          hi[2 * q] = b[0];
-          hi[2 * q + 1] = b[1];
+          if (live) {
+            lo[2 * q] = a[0];
+            lo[2 * q + 1] = a[1];
+            hi[2 * q] = b[0];
+            hi[2 * q + 1] = b[1];
+          }
         }
         // dims 16c .. 16c + 15 are dwords 8c .. 8c + 7: one swizzled 8-dword block
         *reinterpret_cast<u32x4*>(&P.kvb[kv_at(t, 8 * c)]) = lo;
         *reinterpret_cast<u32x4*>(&P.kvb[kv_at(t, 8 * c) + 4]) = hi;
       }
     }
-    if (tid < SUB) P.kvs[tid] = gs;
+    if (tid < SUB) P.kvs[tid] = P.slot[st * SUB + tid] >= 0 ? gs : 0.f;
   }
 
   MONO_DEV bool split_task(int s, int j) {
@@ -560,8 +565,8 @@ class Step {
       u32x4 qv[QL];
 #pragma unroll
       for (int i = 0; i < QL; ++i) {
-        const int f = tid + i * AT;
-        if (f < NH * DQK / 8) qv[i] = ld_u32x4(A.q + (size_t)s * NH * DQK + (size_t)f * 8);
+        const int f = min(tid + i * AT, NH * DQK / 8 - 1);  // unconditional (see gather_load)
+        qv[i] = ld_u32x4(A.q + (size_t)s * NH * DQK + (size_t)f * 8);
       }
 #pragma unroll
       for (int i = 0; i < QL; ++i) {
@@ -597,18 +602,30 @@ class Step {
 
 #pragma unroll 1
     for (int st = 0; st < nsub; ++st) {
-      gather_store(P, gv, gs);
+      gather_store(P, st, gv, gs);
       __syncthreads();
       if (st + 1 < nsub) gather_load(P, st + 1, gv, gs);  // in flight while this sub-tile computes
       // logits of 16 heads x 16 tokens a wave: K = 576 in 18 bf16 steps
       {
-        f32x4 d = {0.f, 0.f, 0.f, 0.f};
+        // two accumulators and operands read a step ahead: the LDS reads of step ks + 1
+        // overlap the MFMA of step ks
+        f32x4 d0 = {0.f, 0.f, 0.f, 0.f}, d1 = d0;
+        const uint16_t* qrow = &P.q[16 * ht + r][8 * g];
+        bf16x8 qa = *reinterpret_cast<const bf16x8*>(qrow);
+        bf16x8 kb = *reinterpret_cast<const bf16x8*>(&P.kvb[kv_at(16 * tt + r, 4 * g)]);
 #pragma unroll
         for (int ks = 0; ks < DQK / 32; ++ks) {
-          const bf16x8 qa = *reinterpret_cast<const bf16x8*>(&P.q[16 * ht + r][32 * ks + 8 * g]);
-          const bf16x8 kb = *reinterpret_cast<const bf16x8*>(&P.kvb[kv_at(16 * tt + r, 16 * ks + 4 * g)]);
-          d = mfma_bf16(qa, kb, d);
+          bf16x8 qn = qa, kn = kb;
+          if (ks + 1 < DQK / 32) {
+            qn = *reinterpret_cast<const bf16x8*>(qrow + 32 * (ks + 1));
+            kn = *reinterpret_cast<const bf16x8*>(&P.kvb[kv_at(16 * tt + r, 16 * (ks + 1) + 4 * g)]);
+          }
+          if (ks % 2 == 0) d0 = mfma_bf16(qa, kb, d0);
+          else d1 = mfma_bf16(qa, kb, d1);
+          qa = qn;
+          kb = kn;
         }
+        const f32x4 d = d0 + d1;
         const int t = 16 * tt + r;
         const bool valid = st * SUB + t < cnt && P.slot[st * SUB + t] >= 0;
         const float sc = P.kvs[t] * A.scale;
@@ -643,27 +660,30 @@ class Step {
       }
 #pragma unroll
       for (int kt = 0; kt < SUB / 32; ++kt) {
-        bf16x8 pa[2];
+        bf16x8 pa[2], vb[4];  // every operand of the k step read before its MFMAs
 #pragma unroll
         for (int a = 0; a < 2; ++a) pa[a] = *reinterpret_cast<const bf16x8*>(&P.pb[16 * a + r][32 * kt + 8 * g]);
 #pragma unroll
-        for (int b = 0; b < 4; ++b) {
-          const bf16x8 vb = column8(P, 32 * kt + 8 * g, 16 * (4 * wave + b) + r);
+        for (int b = 0; b < 4; ++b) vb[b] = column8(P, 32 * kt + 8 * g, 16 * (4 * wave + b) + r);
 #pragma unroll
-          for (int a = 0; a < 2; ++a) acc[a][b] = mfma_bf16(pa[a], vb, acc[a][b]);
-        }
+        for (int b = 0; b < 4; ++b)
+#pragma unroll
+          for (int a = 0; a < 2; ++a) acc[a][b] = mfma_bf16(pa[a], vb[b], acc[a][b]);
       }
       __syncthreads();
     }
     const size_t pb = ((size_t)s * SPLITS + j) * NH;
+    // bf16 pairs (the reference's split partials, kernel.py:4040-4066): lane r holds dim
+    // 16 n + r, its neighbour r ^ 1 the other half of the pair
 #pragma unroll
     for (int a = 0; a < 2; ++a)
 #pragma unroll
       for (int b = 0; b < 4; ++b)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
+          const float mine = acc[a][b][i], other = dpp_f<DPP_XOR1>(mine);
           const int h = 16 * a + 4 * g + i, dim = 16 * (4 * wave + b) + r;
-          mb_putf(&A.mail.part[(pb + h) * DV + dim], acc[a][b][i], gd.tag);
+          if ((r & 1) == 0) mb_put(&A.mail.part[(pb + h) * (DV / 2) + dim / 2], pack_bf16x2(mine, other), gd.tag);
         }
     if (lane < 4) {
       const float m = lane == 0 ? m_run[0] : lane == 1 ? m_run[1] : lane == 2 ? m_run[2] : m_run[3];
@@ -677,37 +697,48 @@ class Step {
 
   // ---------------------------------------------------------------- merge
   MONO_DEV bool merge_task(int s, int hp) {
-    const int h = 2 * hp + tid / 256, d0 = (tid % 256) * 2;
+    static_assert(SPLITS <= WAVE, "a lane a split");
+    MergeLds& Q = L.u.mg;
+    const int hh = tid / 256, h = 2 * hp + hh, d0 = (tid % 256) * 2;
     const size_t rb = (size_t)s * SPLITS;
-    uint32_t ml[2 * SPLITS];
-    const uint64_t* mlp = &A.mail.ml[(rb * NH + h) * 2];
-    bool ok = poll_words<2 * SPLITS>([mlp](int q) { return mlp + (size_t)(q / 2) * NH * 2 + q % 2; }, ml,
-                                     0xffffffffu >> (32 - 2 * SPLITS), W_PART, gd);
-    float M = NEG_INF;
+    // the split weights: lane j of waves 0 and 4 (heads 2 hp, 2 hp + 1) takes split j
+    bool ok = true;
+    if (wave % 4 == 0) {
+      float m = NEG_INF, l = 0.f;
+      if (lane < SPLITS) {
+        uint32_t v[2];
+        const uint64_t* mlp = &A.mail.ml[((rb + lane) * NH + h) * 2];
+        ok = poll_words<2>([mlp](int q) { return mlp + q; }, v, 3u, W_PART, gd);
+        m = __uint_as_float(v[0]);
+        l = __uint_as_float(v[1]);
+      }
+      const bool live = l > 0.f;
+      const float M = wave_max(live ? m : NEG_INF);
+      const float w = live ? hw_exp(m - M) : 0.f;
+      const float den = wave_sum(w * l);
+      if (lane < SPLITS) Q.w[hh][lane] = w;
+      if (lane == 0) Q.den[hh] = den;
+    }
+    if (!block_all(ok)) return false;
     uint32_t live = 0;
 #pragma unroll
-    for (int j = 0; j < SPLITS; ++j) {
-      if (__uint_as_float(ml[2 * j + 1]) > 0.f) {
-        M = fmaxf(M, __uint_as_float(ml[2 * j]));
-        live |= 0x3u << (2 * j);
-      }
-    }
-    uint32_t av[2 * SPLITS];
-    const uint64_t* ap = &A.mail.part[(rb * NH + h) * DV + d0];
-    if (ok) ok = poll_words<2 * SPLITS>([ap](int q) { return ap + (size_t)(q / 2) * NH * DV + q % 2; }, av, live, W_PART, gd);
-    float o[2] = {0.f, 0.f}, den = 0.f;
+    for (int j = 0; j < SPLITS; ++j) live |= (Q.w[hh][j] > 0.f ? 1u : 0u) << j;
+    uint32_t av[SPLITS];
+    const uint64_t* ap = &A.mail.part[(rb * NH + h) * (DV / 2) + d0 / 2];
+    ok = poll_words<SPLITS>([ap](int q) { return ap + (size_t)q * NH * (DV / 2); }, av, live, W_PART, gd);
+    float o[2] = {0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < SPLITS; ++j) {
-      if ((live >> (2 * j)) & 1u) {
-        const float w = hw_exp(__uint_as_float(ml[2 * j]) - M);
-        den += w * __uint_as_float(ml[2 * j + 1]);
-#pragma unroll
-        for (int i = 0; i < 2; ++i) o[i] += w * __uint_as_float(av[2 * j + i]);
+      if ((live >> j) & 1u) {
+        const float w = Q.w[hh][j];
+        o[0] += w * bf16_lo(av[j]);
+        o[1] += w * bf16_hi(av[j]);
       }
     }
+    const float den = Q.den[hh];
     const float inv = den > 0.f ? 1.0f / den : 0.f;
     if (ok) *reinterpret_cast<uint32_t*>(A.out + ((size_t)s * NH + h) * DV + d0) = pack_bf16x2(o[0] * inv, o[1] * inv);
-    return block_all(ok);
+    return block_all(ok);  // also: the next task may rewrite the LDS weights
   }
 };
 

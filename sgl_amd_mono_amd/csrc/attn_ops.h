@@ -19,7 +19,7 @@ constexpr int TOPK = 2048;      // tokens a row attends
 constexpr int MAX_ROWS = 64;
 constexpr int MAX_CTX = 32768;  // keys a row the one-workgroup top-k holds in LDS
 constexpr int CHUNK = 1024;     // keys a score task
-constexpr int SPLITS = 16;      // attention splits a row
+constexpr int SPLITS = 32;      // attention splits a row (64 selected tokens each)
 constexpr int SPLIT = TOPK / SPLITS;
 constexpr int TEAM = 16;        // workgroups selecting one row's top-k together
 constexpr int PASSES = 4;       // 8-bit radix digits of a 32-bit key
@@ -30,7 +30,7 @@ struct Mail {
   uint64_t* sel;    // [max_rows][TOPK]               selected slots, i32
   uint64_t* hist;   // [max_rows][PASSES][TEAM][256]  a team member's digit histogram
   uint64_t* cnt;    // [max_rows][TEAM][2]            a member's keys above / at the threshold
-  uint64_t* part;   // [max_rows][SPLITS][NH][DV]     a split's unnormalised output, f32
+  uint64_t* part;   // [max_rows][SPLITS][NH][DV / 2] a split's unnormalised output, bf16 pairs
   uint64_t* ml;     // [max_rows][SPLITS][NH][2]      a split's max logit and sum
   uint32_t* guard;  // [G_WORDS]
   int max_ctx;
