@@ -345,7 +345,9 @@ extern "C" int mono_attn_create(const mono_attn_config* cfg, mono_attn** out) {
   const size_t o_guard = cv.take(mono::G_WORDS * 4);
   const size_t o_score = cv.take(R * c.max_ctx * 8);
   const size_t o_sel = cv.take(R * TOPK * 8);
+  const size_t o_hist1 = cv.take(R * (c.max_ctx / CHUNK) * 256 * 8);
   const size_t o_hist = cv.take(R * PASSES * TEAM * 256 * 8);
+  const size_t o_cand = cv.take(R * CMAX * 8);
   const size_t o_cnt = cv.take(R * TEAM * 2 * 8);
   const size_t o_part = cv.take(R * SPLITS * NH * (DV / 2) * 8);
   const size_t o_ml = cv.take(R * SPLITS * NH * 2 * 8);
@@ -365,7 +367,9 @@ extern "C" int mono_attn_create(const mono_attn_config* cfg, mono_attn** out) {
   a->mail.guard = a->guard.words;
   a->mail.score = reinterpret_cast<uint64_t*>(a->at(o_score));
   a->mail.sel = reinterpret_cast<uint64_t*>(a->at(o_sel));
+  a->mail.hist1 = reinterpret_cast<uint64_t*>(a->at(o_hist1));
   a->mail.hist = reinterpret_cast<uint64_t*>(a->at(o_hist));
+  a->mail.cand = reinterpret_cast<uint64_t*>(a->at(o_cand));
   a->mail.cnt = reinterpret_cast<uint64_t*>(a->at(o_cnt));
   a->mail.part = reinterpret_cast<uint64_t*>(a->at(o_part));
   a->mail.ml = reinterpret_cast<uint64_t*>(a->at(o_ml));

@@ -14,18 +14,21 @@
 //          plane the B operand of v_mfma_scale_f32_16x16x128_f8f6f4 with FP4 formats:
 //          the plane's E8M0 bytes are the MFMA's per-lane B scales as they lie (a
 //          lane's dword holds its key's scale for the page's four 16-key tiles).
-//          score = sum_h w_h relu(q_h . k) -> mailbox score
+//          score = sum_h w_h relu(q_h . k) -> mailbox score, and the task's histogram
+//          of the keys' leading 8-bit digits -> mailbox hist1
 //   topk   (row, member of a team of 16): the row's scores as order-preserving u32
 //          keys, 2048 a member; an MSB-first 8-bit radix select of the 2048th largest
-//          key, each digit from the sum of the members' histograms (mailbox hist; a
-//          wave's most common digits go in as one atomic); then a stable compaction
-//          from the members' counts (mailbox cnt): every key above it and the lowest
-//          positions equal to it, ascending -> cache slots
-//          (page_table[p / 64] * 64 + p % 64) -> mailbox sel (glm53/check.py:100-117)
-//   split  (row, 128 selected tokens): 2 sub-tiles of 64 tokens gathered from the FP8
+//          key: digit 1 from the chunk histograms, digit 2 from the sum of the members'
+//          histograms (mailbox hist; a wave's most common digits go in as one atomic).
+//          The keys sharing both digits with the threshold (mailbox cand) are ranked by
+//          every member; a crowded bin (ties) takes digits 3 and 4 the same way as digit
+//          2 and a stable compaction from the members' counts (mailbox cnt). Every key
+//          above the threshold and the lowest positions equal to it, ascending -> cache
+//          slots (page_table[p / 64] * 64 + p % 64) -> mailbox sel (glm53/check.py:100-117)
+//   split  (row, 64 selected tokens): sub-tiles of 64 tokens gathered from the FP8
 //          cache and widened exactly to bf16 in LDS, bf16 MFMA 16x16x32 for q.k and
 //          p.v, the per-token scale folded into the logit and the probability, online
-//          softmax -> mailboxes part, ml
+//          softmax -> mailboxes part (bf16 pairs), ml
 //   merge  (row, 2 heads): out = sum_j e^(m_j - M) acc_j / sum_j e^(m_j - M) l_j, bf16
 #include "attn_ops.h"
 #include "common.h"
@@ -41,7 +44,6 @@ constexpr int AW = AT / WAVE;
 constexpr int KPM = MAX_CTX / TEAM;          // keys a top-k team member owns
 constexpr int KPT = KPM / AT;                // keys a thread of a member holds
 constexpr int SUB = 64;                      // tokens a split sub-tile
-constexpr int NSUB = SPLIT / SUB;
 constexpr int Q_STRIDE = DQK + 8;            // bf16 a q row in LDS
 // dwords a cached row in LDS, as bf16 pairs: 16-byte aligned rows; the swizzle below
 // spreads a p.v column (8 rows, 8 apart for the 4 lane groups) over the banks
@@ -55,13 +57,20 @@ static_assert(AT == NH * DV / 32, "a merge task covers 2 heads");
 
 enum { W_SCORE = 0, W_SEL = 1, W_PART = 2, W_TEAM = 3 };
 
+struct ScoreLds {
+  uint32_t hist[256];  // the task's leading-digit histogram
+};
+
 struct TopkLds {
   int32_t pt[TOPK / PAGE];  // a short row's page table
+  uint32_t key[KPM];        // this member's keys, position order
   uint32_t hist[256];       // this member's digit histogram
   uint32_t tot[256];        // the team's
+  uint32_t pre[256];        // the members' before this one
+  uint32_t cu[CMAX];        // the team's threshold candidates, 0 past the last
   int32_t cnt[TEAM][2];     // the team's keys above / at the threshold
-  uint32_t digit;
-  int32_t above;
+  uint32_t digit, uT;
+  int32_t above, pre_above;
 };
 
 struct SplitLds {
@@ -81,6 +90,7 @@ struct MergeLds {
 
 struct Lds {
   union {
+    ScoreLds sc;
     TopkLds t;
     SplitLds sp;
     MergeLds mg;
@@ -233,7 +243,7 @@ class Step {
   // 16 ht ..), its head weights, and 128 keys = 2 pages = 8 tiles of 16 keys (lane
   // (g, r) holds chunk g of key 16 t + r) with their pages' E8M0 dwords.
   struct ScoreOps {
-    int s, k0, n;
+    int s, c, k0, n;
     u32x4 qa[IH / 16];
     int qsc[IH / 16];
     uint32_t w2[IH / 16][2];
@@ -243,7 +253,8 @@ class Step {
 
   MONO_DEV void score_load(int T, ScoreOps& o) {
     o.s = T / CH;
-    o.k0 = (T % CH) * CHUNK + wave * KEYS_WAVE;
+    o.c = T % CH;
+    o.k0 = o.c * CHUNK + wave * KEYS_WAVE;
     o.n = row_len(o.s);
     if (o.k0 >= o.n) return;
 #pragma unroll
@@ -266,38 +277,60 @@ class Step {
       o.ks[i] = *reinterpret_cast<const uint32_t*>(A.iks + (size_t)(pg[i] * 4 + g) * PAGE + r * 4);
   }
 
+  // The wave's 128 scores -> mailbox score (lane (g, r) ends with keys k0 + 16 g + r and
+  // k0 + 64 + 16 g + r, so each store covers 64 consecutive positions), then the task's
+  // histogram of their leading key digits -> mailbox hist1 (the top-k's first radix
+  // pass). Every wave reaches the two barriers; a wave past the row computes nothing.
   MONO_DEV void score_compute(const ScoreOps& o) {
-    if (o.k0 >= o.n) return;  // wave-uniform; no barrier in the score stage
-    float wv[IH / 16][4];
-#pragma unroll
-    for (int ht = 0; ht < IH / 16; ++ht) {
-      wv[ht][0] = bf16_lo(o.w2[ht][0]);
-      wv[ht][1] = bf16_hi(o.w2[ht][0]);
-      wv[ht][2] = bf16_lo(o.w2[ht][1]);
-      wv[ht][3] = bf16_hi(o.w2[ht][1]);
-    }
-#pragma unroll
-    for (int kt = 0; kt < KTILES; ++kt) {
-      float part = 0.f;
+    const bool live = o.k0 < o.n;  // wave-uniform
+    float sc[2] = {0.f, 0.f};
+    if (live) {
+      float wv[IH / 16][4];
 #pragma unroll
       for (int ht = 0; ht < IH / 16; ++ht) {
-        f32x4 d;
-        switch (kt % 4) {
-          case 0: d = mfma_fp4_opb<0>(o.qa[ht], o.kb[kt], o.qsc[ht], (int)o.ks[kt / 4]); break;
-          case 1: d = mfma_fp4_opb<1>(o.qa[ht], o.kb[kt], o.qsc[ht], (int)o.ks[kt / 4]); break;
-          case 2: d = mfma_fp4_opb<2>(o.qa[ht], o.kb[kt], o.qsc[ht], (int)o.ks[kt / 4]); break;
-          default: d = mfma_fp4_opb<3>(o.qa[ht], o.kb[kt], o.qsc[ht], (int)o.ks[kt / 4]); break;
-        }
+        wv[ht][0] = bf16_lo(o.w2[ht][0]);
+        wv[ht][1] = bf16_hi(o.w2[ht][0]);
+        wv[ht][2] = bf16_lo(o.w2[ht][1]);
+        wv[ht][3] = bf16_hi(o.w2[ht][1]);
+      }
 #pragma unroll
-        for (int i = 0; i < 4; ++i) part += wv[ht][i] * fmaxf(d[i], 0.f);
+      for (int kt = 0; kt < KTILES; ++kt) {
+        float part = 0.f;
+#pragma unroll
+        for (int ht = 0; ht < IH / 16; ++ht) {
+          f32x4 d;
+          switch (kt % 4) {
+            case 0: d = mfma_fp4_opb<0>(o.qa[ht], o.kb[kt], o.qsc[ht], (int)o.ks[kt / 4]); break;
+            case 1: d = mfma_fp4_opb<1>(o.qa[ht], o.kb[kt], o.qsc[ht], (int)o.ks[kt / 4]); break;
+            case 2: d = mfma_fp4_opb<2>(o.qa[ht], o.kb[kt], o.qsc[ht], (int)o.ks[kt / 4]); break;
+            default: d = mfma_fp4_opb<3>(o.qa[ht], o.kb[kt], o.qsc[ht], (int)o.ks[kt / 4]); break;
+          }
+#pragma unroll
+          for (int i = 0; i < 4; ++i) part += wv[ht][i] * fmaxf(d[i], 0.f);
+        }
+        part += __shfl_xor(part, 16, WAVE);  // every lane group now holds key 16 kt + r's sum
+        part += __shfl_xor(part, 32, WAVE);
+        if (kt % 4 == g) sc[kt / 4] = part;
       }
-      part += __shfl_xor(part, 16, WAVE);
-      part += __shfl_xor(part, 32, WAVE);
-      const int pos = o.k0 + kt * 16 + r;
-      if (g == 0 && pos < o.n) {
-        mb_putf(&A.mail.score[(size_t)o.s * A.mail.max_ctx + pos], part, gd.tag);
-        if (A.scores) A.scores[(size_t)o.s * A.mail.max_ctx + pos] = part;
+    }
+    bool kl[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int pos = o.k0 + 64 * i + 16 * g + r;
+      kl[i] = live && pos < o.n;
+      if (kl[i]) {
+        mb_putf(&A.mail.score[(size_t)o.s * A.mail.max_ctx + pos], sc[i], gd.tag);
+        if (A.scores) A.scores[(size_t)o.s * A.mail.max_ctx + pos] = sc[i];
       }
+    }
+    uint32_t* hist = L.u.sc.hist;
+    __syncthreads();  // the previous task's histogram is published and cleared
+#pragma unroll
+    for (int i = 0; i < 2; ++i) hist_add(hist, kl[i], radix_key(sc[i]) >> 24);
+    __syncthreads();
+    if (tid < 256) {
+      if (o.c * CHUNK < o.n) mb_put(&A.mail.hist1[((size_t)o.s * CH + o.c) * 256 + tid], hist[tid], gd.tag);
+      hist[tid] = 0u;
     }
   }
 
@@ -305,6 +338,7 @@ class Step {
   // before the previous task computes.
   MONO_DEV void score_stage(int T0, int n_score) {
     if (T0 >= n_score) return;
+    if (tid < 256) L.u.sc.hist[tid] = 0u;
     ScoreOps cur, nxt;
     score_load(T0, cur);
     for (int T = T0; T < n_score; T += G) {
@@ -315,6 +349,7 @@ class Step {
       stamp(T, t0, 0);
       if (more) cur = nxt;
     }
+    __syncthreads();  // the top-k tasks reuse the LDS
   }
 
   // ---------------------------------------------------------------- top-k
@@ -358,8 +393,9 @@ class Step {
   }
 
   // Pick the next digit from a 256-bin histogram (wave 0): the highest digit d with
-  // (keys above d) < need <= (keys above d) + hist[d]; writes K.digit and K.above.
-  MONO_DEV void pick_digit(TopkLds& K, const uint32_t* hist, int need) {
+  // (keys above d) < need <= (keys above d) + hist[d] -> K.digit, K.above; with `pre`,
+  // also K.pre_above = the sum of pre over the bins above d.
+  MONO_DEV void pick_digit(TopkLds& K, const uint32_t* hist, int need, const uint32_t* pre) {
     if (wave != 0) return;
     int c[4], tot = 0;  // lane l holds bins 255 - 4l .. 252 - 4l, highest first
 #pragma unroll
@@ -374,27 +410,78 @@ class Step {
       if (lane >= o) incl += y;
     }
     const int excl = incl - tot;
-    if (excl < need && need <= incl) {
-      int run = excl;
+    const bool mine = excl < need && need <= incl;
+    int dg = 0, ab = 0, run = excl;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        if (run + c[j] >= need) {
-          K.digit = (uint32_t)(255 - 4 * lane - j);
-          K.above = run;
-          break;
-        }
-        run += c[j];
+    for (int j = 0; j < 4; ++j) {
+      if (mine && dg == 0 && run + c[j] >= need) {
+        dg = 256 + 255 - 4 * lane - j;  // + 256: found
+        ab = run;
       }
+      run += c[j];
+    }
+    const uint64_t who = __ballot(mine);
+    const int src = who ? __ffsll((long long)who) - 1 : 0;
+    dg = __shfl(dg, src, WAVE) & 0xff;
+    ab = __shfl(ab, src, WAVE);
+    if (pre) {
+      int x = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) x += 255 - 4 * lane - j > dg ? (int)pre[255 - 4 * lane - j] : 0;
+#pragma unroll
+      for (int o = 1; o < WAVE; o <<= 1) x += __shfl_xor(x, o, WAVE);
+      if (lane == 0) K.pre_above = x;
+    }
+    if (lane == 0) {
+      K.digit = (uint32_t)dg;
+      K.above = ab;
     }
   }
 
+  // One exchanged radix pass: member m's histogram of the digit at `shift` over its keys
+  // matching prefix under mask -> mailbox hist; the team's sum -> K.tot and the sum over
+  // the members before m -> K.pre. Workgroup-uniform result.
+  MONO_DEV bool exchange_hist(int s, int m, int pass, const uint32_t (&key)[KPT], int cnt, uint32_t prefix,
+                              uint32_t mask, int shift) {
+    TopkLds& K = L.u.t;
+    if (tid < 256) K.hist[tid] = 0u;
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < KPT; ++q) hist_add(K.hist, q < cnt && (key[q] & mask) == prefix, (key[q] >> shift) & 0xffu);
+    __syncthreads();
+    uint64_t* hb = &A.mail.hist[((size_t)s * PASSES + pass) * TEAM * 256];
+    bool ok = true;
+    if (tid < 256) {
+      mb_put(&hb[m * 256 + tid], K.hist[tid], gd.tag);
+      uint32_t v[TEAM];
+      const uint64_t* col = hb + tid;
+      ok = poll_words<TEAM>([col](int j) { return col + j * 256; }, v, (1u << TEAM) - 1u, W_TEAM, gd);
+      uint32_t t = 0, p = 0;
+#pragma unroll
+      for (int j = 0; j < TEAM; ++j) {
+        t += v[j];
+        p += j < m ? v[j] : 0u;
+      }
+      K.tot[tid] = t;
+      K.pre[tid] = p;
+    }
+    return block_all(ok);
+  }
+
+  // a threshold candidate's rank word: larger first = score desc, position asc (the
+  // candidates share their keys' upper 16 bits)
+  MONO_DEV static uint32_t cand_word(uint32_t key, int pos) { return (key << 16) | (uint32_t)(0x7fff - pos); }
+
   // Member m of row s's top-k team. The team selects the exact top-TOPK of the row
   // (score desc, position asc) -> cache slots, ascending. Member m owns positions
-  // [m KPM, (m + 1) KPM), KPT of them in each thread's registers. Per 8-bit digit,
-  // MSB first, each member publishes its histogram of the live keys and sums the
-  // team's (every member computes the same digit); then members publish their counts
-  // above / at the threshold T and each writes its selected slots at its offset: keys
-  // above T, and the lowest positions equal to T.
+  // [m KPM, (m + 1) KPM), KPT of them in each thread's registers. An MSB-first 8-bit
+  // radix select of the threshold key: digit 1 from the score tasks' chunk histograms,
+  // digit 2 from the members' exchanged histograms. The keys left sharing both digits
+  // with the threshold (the candidates, few unless scores tie) are exchanged as (low
+  // key bits, position) and every member ranks them all; a crowded threshold bin
+  // instead takes digits 3 and 4 the same way as digit 2 and then the members' counts
+  // above / at the threshold (mailbox cnt). Each member writes its selected slots at
+  // its offset in position order.
   MONO_DEV bool topk_member(int s, int m) {
     TopkLds& K = L.u.t;
     const int n = row_len(s);
@@ -403,88 +490,157 @@ class Step {
         for (int i = tid; i < TOPK / PAGE; i += AT) K.pt[i] = i * PAGE < n ? page_of(s, i * PAGE) : 0;
         __syncthreads();
         for (int j = tid; j < TOPK; j += AT) publish_sel(s, j, j < n ? K.pt[j / PAGE] * PAGE + j % PAGE : -1);
+        __syncthreads();  // the next task may rewrite the LDS page table
       }
       return true;
     }
     const int p0 = m * KPM + tid * KPT;
     const int cnt = min(max(n - p0, 0), KPT);
     const int page = cnt > 0 ? page_of(s, p0) : 0;  // a thread's keys share one page
-    uint32_t key[KPT];
     bool ok;
-    {
-      uint32_t v[KPT];
-      const uint64_t* base = &A.mail.score[(size_t)s * A.mail.max_ctx + p0];
-      ok = poll_words<KPT>([base](int q) { return base + q; }, v, (1u << cnt) - 1u, W_SCORE, gd);
+    // threads 0..255: bin tid of every scored chunk's histogram; 256..: the member's
+    // scores (coalesced) -> LDS keys
+    if (tid < 256) {
+      constexpr int NCH = MAX_CTX / CHUNK, CPM = KPM / CHUNK;
+      const int nch = (n + CHUNK - 1) / CHUNK;
+      uint32_t v[NCH];
+      const uint64_t* col = &A.mail.hist1[(size_t)s * CH * 256 + tid];
+      ok = poll_words<NCH>([col](int c) { return col + c * 256; }, v, nch >= NCH ? ~0u : (1u << nch) - 1u, W_SCORE,
+                           gd);
+      uint32_t t = 0, p = 0;
 #pragma unroll
-      for (int q = 0; q < KPT; ++q) key[q] = radix_key(__uint_as_float(v[q]));
+      for (int c = 0; c < NCH; ++c) {
+        t += c < nch ? v[c] : 0u;
+        p += c < nch && c < CPM * m ? v[c] : 0u;
+      }
+      K.tot[tid] = t;
+      K.pre[tid] = p;
+    } else {
+      constexpr int NW = KPM / (AT - 256);
+      const int i0 = tid - 256;
+      uint32_t v[NW], pend = 0;
+#pragma unroll
+      for (int q = 0; q < NW; ++q) {
+        v[q] = 0u;
+        pend |= (m * KPM + i0 + 256 * q < n ? 1u : 0u) << q;
+      }
+      const uint64_t* base = &A.mail.score[(size_t)s * A.mail.max_ctx + m * KPM + i0];
+      ok = poll_words<NW>([base](int q) { return base + 256 * q; }, v, pend, W_SCORE, gd);
+#pragma unroll
+      for (int q = 0; q < NW; ++q) K.key[i0 + 256 * q] = radix_key(__uint_as_float(v[q]));
     }
     if (!block_all(ok)) return false;
     mark_waited();
-    uint32_t prefix = 0, mask = 0;
-    int need = TOPK;
+    uint32_t key[KPT];
+    {
+      static_assert(KPT == 4, "a thread's keys are one 16-byte LDS read");
+      const u32x4 k4 = *reinterpret_cast<const u32x4*>(&K.key[tid * KPT]);
+#pragma unroll
+      for (int q = 0; q < KPT; ++q) key[q] = k4[q];
+    }
+    pick_digit(K, K.tot, TOPK, K.pre);
+    __syncthreads();
+    int need = TOPK - K.above, above_before = K.pre_above;
+    uint32_t prefix = K.digit << 24, mask = 0xff000000u;
+    if (!exchange_hist(s, m, 1, key, cnt, prefix, mask, 16)) return false;
+    pick_digit(K, K.tot, need, K.pre);
+    __syncthreads();
+    need -= K.above;
+    above_before += K.pre_above;
+    prefix |= K.digit << 16;
+    mask |= 0x00ff0000u;
+    const int n_cand = (int)K.tot[K.digit], cand_before = (int)K.pre[K.digit];
+    int sel_before;
+    uint32_t uT = 0;  // candidates: the lowest selected rank word
+    bool cand = n_cand <= CMAX;  // team-uniform
+    if (cand) {
+      const uint32_t P16 = prefix >> 16;
+      int c_my = 0;
+#pragma unroll
+      for (int q = 0; q < KPT; ++q) c_my += (q < cnt && (key[q] >> 16) == P16) ? 1 : 0;
+      int idx = cand_before + block_excl_scan(c_my);
+      uint64_t* cb = &A.mail.cand[(size_t)s * CMAX];
+#pragma unroll
+      for (int q = 0; q < KPT; ++q)
+        if (q < cnt && (key[q] >> 16) == P16) mb_put(&cb[idx++], cand_word(key[q], p0 + q), gd.tag);
+      static_assert(CMAX == AT, "a thread a candidate");
+      uint32_t u = 0;
+      ok = true;
+      if (tid < n_cand) ok = poll_word(&cb[tid], u, W_TEAM, gd);
+      K.cu[tid] = u;
+      if (!block_all(ok)) return false;
+      if (wave * WAVE < n_cand) {  // wave-uniform
+        int rank = 0;              // candidates ranked before this thread's
+        for (int j = 0; j < n_cand; j += 4) {
+          const u32x4 x = *reinterpret_cast<const u32x4*>(&K.cu[j]);
+          rank += (x[0] > u ? 1 : 0) + (x[1] > u ? 1 : 0) + (x[2] > u ? 1 : 0) + (x[3] > u ? 1 : 0);
+        }
+        if (tid < n_cand && rank == need - 1) K.uT = u;
+      }
+      __syncthreads();
+      uT = K.uT;
+      sel_before = above_before + __syncthreads_count(tid < cand_before && u >= uT);
+    } else {
 #pragma unroll 1
-    for (int pass = 0; pass < PASSES; ++pass) {
-      const int shift = 24 - 8 * pass;
-      if (tid < 256) K.hist[tid] = 0u;
-      __syncthreads();
+      for (int pass = 2; pass < PASSES; ++pass) {
+        const int shift = 24 - 8 * pass;
+        __syncthreads();  // K.digit and K.tot are read
+        if (!exchange_hist(s, m, pass, key, cnt, prefix, mask, shift)) return false;
+        pick_digit(K, K.tot, need, nullptr);
+        __syncthreads();
+        need -= K.above;
+        prefix |= K.digit << shift;
+        mask |= 0xffu << shift;
+      }
+      // the team's counts above / at T, then this member's offset
+      int c_gt = 0, c_eq = 0;
 #pragma unroll
-      for (int q = 0; q < KPT; ++q) hist_add(K.hist, q < cnt && (key[q] & mask) == prefix, (key[q] >> shift) & 0xffu);
-      __syncthreads();
-      uint64_t* hb = &A.mail.hist[((size_t)s * PASSES + pass) * TEAM * 256];
-      if (tid < 256) {
-        mb_put(&hb[m * 256 + tid], K.hist[tid], gd.tag);
-        uint32_t v[TEAM];
-        const uint64_t* col = hb + tid;
-        ok = poll_words<TEAM>([col](int j) { return col + j * 256; }, v, (1u << TEAM) - 1u, W_TEAM, gd);
-        uint32_t t = 0;
-#pragma unroll
-        for (int j = 0; j < TEAM; ++j) t += v[j];
-        K.tot[tid] = t;
+      for (int q = 0; q < KPT; ++q) {
+        c_gt += (q < cnt && key[q] > prefix) ? 1 : 0;
+        c_eq += (q < cnt && key[q] == prefix) ? 1 : 0;
+      }
+      const int gt_in = block_excl_scan(c_gt), eq_in = block_excl_scan(c_eq);
+      if (tid == AT - 1) {  // the last thread's inclusive sums are the member's totals
+        mb_put(&A.mail.cnt[((size_t)s * TEAM + m) * 2], (uint32_t)(gt_in + c_gt), gd.tag);
+        mb_put(&A.mail.cnt[((size_t)s * TEAM + m) * 2 + 1], (uint32_t)(eq_in + c_eq), gd.tag);
+      }
+      ok = true;
+      if (tid < 2 * TEAM) {
+        uint32_t v = 0;
+        ok = poll_word(&A.mail.cnt[(size_t)s * TEAM * 2 + tid], v, W_TEAM, gd);
+        K.cnt[tid / 2][tid % 2] = (int)v;
       }
       if (!block_all(ok)) return false;
-      pick_digit(K, K.tot, need);
-      __syncthreads();
-      need -= K.above;
-      prefix |= K.digit << shift;
-      mask |= 0xffu << shift;
-      __syncthreads();
-    }
-    // the team's counts above / at T, then this member's offsets
-    const uint32_t T = prefix;
-    int c_gt = 0, c_eq = 0;
-#pragma unroll
-    for (int q = 0; q < KPT; ++q) {
-      c_gt += (q < cnt && key[q] > T) ? 1 : 0;
-      c_eq += (q < cnt && key[q] == T) ? 1 : 0;
-    }
-    const int gt_in = block_excl_scan(c_gt), eq_in = block_excl_scan(c_eq);
-    if (tid == AT - 1) {  // the last thread's inclusive sums are the member's totals
-      mb_put(&A.mail.cnt[((size_t)s * TEAM + m) * 2], (uint32_t)(gt_in + c_gt), gd.tag);
-      mb_put(&A.mail.cnt[((size_t)s * TEAM + m) * 2 + 1], (uint32_t)(eq_in + c_eq), gd.tag);
-    }
-    if (tid < 2 * TEAM) {
-      uint32_t v = 0;
-      ok = poll_word(&A.mail.cnt[(size_t)s * TEAM * 2 + tid], v, W_TEAM, gd);
-      K.cnt[tid / 2][tid % 2] = (int)v;
-    }
-    if (!block_all(ok)) return false;
-    int sel_before = 0, eq_before = 0;  // over the members before m, in position order
-    for (int j = 0; j < m; ++j) {
-      const int take_j = min(max(need - eq_before, 0), K.cnt[j][1]);
-      sel_before += K.cnt[j][0] + take_j;
-      eq_before += K.cnt[j][1];
-    }
-    const int take = min(max(need - (eq_before + eq_in), 0), c_eq);
-    int idx = sel_before + block_excl_scan(c_gt + take);
-    int te = 0;
-#pragma unroll
-    for (int q = 0; q < KPT; ++q) {
-      const bool eq = key[q] == T;
-      if (q < cnt && (key[q] > T || (eq && te < take)) && idx < TOPK) {
-        te += eq ? 1 : 0;
-        publish_sel(s, idx++, page * PAGE + (p0 + q) % PAGE);
+      int eq_before = 0;  // over the members before m, in position order
+      sel_before = 0;
+      for (int j = 0; j < m; ++j) {
+        const int take_j = min(max(need - eq_before, 0), K.cnt[j][1]);
+        sel_before += K.cnt[j][0] + take_j;
+        eq_before += K.cnt[j][1];
       }
+      // this thread's share of the keys equal to T: the lowest positions first
+      uT = (uint32_t)min(max(need - (eq_before + eq_in), 0), c_eq);
     }
+    // the selected keys in position order: above the threshold prefix, and the
+    // threshold's share (candidates ranked at or above uT / the first uT equal to T)
+    bool take[KPT];
+    int c_take = 0, te = 0;
+#pragma unroll
+    for (int q = 0; q < KPT; ++q) {
+      if (cand) {
+        const uint32_t hi = key[q] >> 16;
+        take[q] = q < cnt && (hi > (prefix >> 16) || (hi == (prefix >> 16) && cand_word(key[q], p0 + q) >= uT));
+      } else {
+        const bool eq = q < cnt && key[q] == prefix;
+        take[q] = (q < cnt && key[q] > prefix) || (eq && te < (int)uT);
+        te += eq ? 1 : 0;
+      }
+      c_take += take[q] ? 1 : 0;
+    }
+    int idx = sel_before + block_excl_scan(c_take);
+#pragma unroll
+    for (int q = 0; q < KPT; ++q)
+      if (take[q] && idx < TOPK) publish_sel(s, idx++, page * PAGE + (p0 + q) % PAGE);
     return true;
   }
 

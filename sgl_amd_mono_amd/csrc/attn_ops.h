@@ -23,12 +23,15 @@ constexpr int SPLITS = 32;      // attention splits a row (64 selected tokens ea
 constexpr int SPLIT = TOPK / SPLITS;
 constexpr int TEAM = 16;        // workgroups selecting one row's top-k together
 constexpr int PASSES = 4;       // 8-bit radix digits of a 32-bit key
+constexpr int CMAX = 512;       // threshold candidates a row exchanged as (key, position)
 
 // Mailboxes of one attention runtime (tagged 64-bit words, see sync.h).
 struct Mail {
   uint64_t* score;  // [max_rows][max_ctx]           index scores, f32
   uint64_t* sel;    // [max_rows][TOPK]               selected slots, i32
+  uint64_t* hist1;  // [max_rows][max_ctx / CHUNK][256] a score chunk's leading-digit histogram
   uint64_t* hist;   // [max_rows][PASSES][TEAM][256]  a team member's digit histogram
+  uint64_t* cand;   // [max_rows][CMAX]               threshold candidates (low key bits, position)
   uint64_t* cnt;    // [max_rows][TEAM][2]            a member's keys above / at the threshold
   uint64_t* part;   // [max_rows][SPLITS][NH][DV / 2] a split's unnormalised output, bf16 pairs
   uint64_t* ml;     // [max_rows][SPLITS][NH][2]      a split's max logit and sum

@@ -33,9 +33,28 @@ def rt(gpu_device):
     r.close()
 
 
-def _check(rt, ctx, seed, gpu_device):
-    print(f"[attn] rows={len(ctx)} seed={seed} ctx={ctx[:8]}...", flush=True)
+def _crowding(scores, ctx):
+    """For each row longer than 2048: how many of its keys share the 2048th largest
+    key's upper 16 bits (the device exchanges them when at most 512, else takes two
+    more radix digits)."""
+    out = []
+    for s, n in enumerate(ctx):
+        if n <= 2048:
+            continue
+        b = scores[s, :n].contiguous().view(torch.int32).long() & 0xFFFFFFFF
+        key = torch.where(b >= 2**31, b ^ 0xFFFFFFFF, b | 2**31)
+        t = key.sort(descending=True).values[2047]
+        out.append(int(((key >> 16) == (t >> 16)).sum()))
+    return out
+
+
+def _check(rt, ctx, seed, gpu_device, period=0):
+    print(f"[attn] rows={len(ctx)} seed={seed} period={period} ctx={ctx[:8]}...", flush=True)
     step, caches = workloads.attn_case(ctx, gpu_device, seed=seed)
+    if period:  # every page of the index plane a copy of page p % period: repeated scores
+        src = torch.arange(caches.ikv.shape[0], device=gpu_device) % period
+        caches.ikv.copy_(caches.ikv[src].clone())
+        caches.iks.copy_(caches.iks[src].clone())
     out, dbg = rt.forward(step, caches, debug=True)
     torch.cuda.synchronize()
     rt.check_errors()
@@ -49,6 +68,7 @@ def _check(rt, ctx, seed, gpu_device):
         scale = ref_scores[s, :n].abs().max().item()
         assert d <= SCORE_REL * scale + 1e-6, (s, d, scale)
     want_sel = oatt.select_topk(scores, st["seq_lens"], st["page_table"])
+    print(f"[attn] keys sharing the threshold's upper 16 bits: {_crowding(scores, ctx)}", flush=True)
     assert torch.equal(sel, want_sel), [s for s in range(len(ctx)) if not torch.equal(sel[s], want_sel[s])]
     ref = oatt.sparse_mla(st["q"], c["kv"], c["kv_scale"], sel)
     got = out.cpu().float()
@@ -74,6 +94,15 @@ def test_attn_48_rows_mixed_contexts(rt, gpu_device):
     ctx = torch.randint(1, 12000, (48,), generator=g).tolist()
     ctx[0], ctx[1], ctx[2] = 32768, 2048, 2049
     _check(rt, ctx, 2, gpu_device)
+
+
+@pytest.mark.parametrize("period", [1, 6])
+def test_attn_repeated_scores(rt, gpu_device, period):
+    """Index planes whose pages repeat every `period` pages: each score recurs about
+    n / (64 period) times in a row, so the keys sharing the threshold's upper 16 bits
+    tie in whole groups (512 copies at period 1 and 32768 keys: exactly the largest
+    candidate exchange), and the lowest positions of the threshold score are taken."""
+    _check(rt, [32768, 20000, 9000, 4100, 2049], 5, gpu_device, period=period)
 
 
 def test_attn_ties_take_lowest_positions(rt, gpu_device):
