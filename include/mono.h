@@ -206,7 +206,8 @@ typedef struct {
 int mono_attn_forward(mono_attn* attn, const mono_attn_args* args, void* stream);
 
 /* Guard controls of an attention runtime (as the MoE runtime's). Wait sites: 0 index
- * scores, 1 selected slots, 2 split partials, 3 top-k team histograms and counts. */
+ * scores (a row's score chunks), 1 selected slots, 2 split partials, 3 top-k team
+ * histograms and candidates. */
 int mono_attn_set_deadline(mono_attn* attn, double seconds);
 int mono_attn_read_errors(mono_attn* attn, int32_t* words);
 int mono_attn_clear_errors(mono_attn* attn);

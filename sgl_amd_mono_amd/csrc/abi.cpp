@@ -345,8 +345,9 @@ extern "C" int mono_attn_create(const mono_attn_config* cfg, mono_attn** out) {
   const size_t o_guard = cv.take(mono::G_WORDS * 4);
   const size_t o_score = cv.take(R * c.max_ctx * 8);
   const size_t o_sel = cv.take(R * TOPK * 8);
-  const size_t o_hist1 = cv.take(R * (c.max_ctx / CHUNK) * 256 * 8);
-  const size_t o_hist = cv.take(R * PASSES * TEAM * 256 * 8);
+  const size_t o_rowh = cv.take(2 * R * ROWH * 4);
+  const size_t o_cdone = cv.take(R * (c.max_ctx / CHUNK) * 8);
+  const size_t o_hist = cv.take(R * PASSES * TEAM * HW * 8);
   const size_t o_cand = cv.take(R * CMAX * 8);
   const size_t o_cnt = cv.take(R * TEAM * 2 * 8);
   const size_t o_part = cv.take(R * SPLITS * NH * (DV / 2) * 8);
@@ -367,13 +368,15 @@ extern "C" int mono_attn_create(const mono_attn_config* cfg, mono_attn** out) {
   a->mail.guard = a->guard.words;
   a->mail.score = reinterpret_cast<uint64_t*>(a->at(o_score));
   a->mail.sel = reinterpret_cast<uint64_t*>(a->at(o_sel));
-  a->mail.hist1 = reinterpret_cast<uint64_t*>(a->at(o_hist1));
+  a->mail.rowh = reinterpret_cast<uint32_t*>(a->at(o_rowh));
+  a->mail.cdone = reinterpret_cast<uint64_t*>(a->at(o_cdone));
   a->mail.hist = reinterpret_cast<uint64_t*>(a->at(o_hist));
   a->mail.cand = reinterpret_cast<uint64_t*>(a->at(o_cand));
   a->mail.cnt = reinterpret_cast<uint64_t*>(a->at(o_cnt));
   a->mail.part = reinterpret_cast<uint64_t*>(a->at(o_part));
   a->mail.ml = reinterpret_cast<uint64_t*>(a->at(o_ml));
   a->mail.max_ctx = c.max_ctx;
+  a->mail.max_rows = c.max_rows;
   *out = a;
   return ok();
 }
@@ -431,7 +434,11 @@ extern "C" int mono_attn_read_errors(mono_attn* a, int32_t* words) {
 
 extern "C" int mono_attn_clear_errors(mono_attn* a) {
   if (!live(a, ATTN_MAGIC)) return fail(MONO_ESTATE, "not a live attention runtime");
-  return guard_clear(a);
+  if (int rc = guard_clear(a)) return rc;
+  // a failed launch may have left row histograms uncleared for its successor
+  HIP_TRY(hipMemset(a->mail.rowh, 0, 2 * (size_t)a->cfg.max_rows * mono::attn::ROWH * sizeof(uint32_t)));
+  HIP_TRY(hipDeviceSynchronize());
+  return ok();
 }
 
 // ------------------------------------------------------------------ projection runtime

@@ -68,6 +68,7 @@ struct TopkLds {
   uint32_t tot[256];        // the team's
   uint32_t pre[256];        // the members' before this one
   uint32_t cu[CMAX];        // the team's threshold candidates, 0 past the last
+  int32_t xw[TEAM];         // the members' keys above the first digit
   int32_t cnt[TEAM][2];     // the team's keys above / at the threshold
   uint32_t digit, uT;
   int32_t above, pre_above;
@@ -175,6 +176,10 @@ class Step {
     gd.a = A.guard;
     gd.tag = L.tag;
     gd.deadline = now_ticks() + A.guard.deadline_ticks;
+    for (int s = blockIdx.x; s < A.mail.max_rows; s += G) {  // the next launch's row histograms
+      uint32_t* nx = row_hist(gd.tag + 1u, s);
+      if (tid < ROWH) __hip_atomic_store(&nx[tid], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     // score tasks padded to a multiple of TEAM so no top-k team straddles a round
     const int n_score = (A.rows * CH + TEAM - 1) / TEAM * TEAM, n_topk = A.rows * TEAM;
     const int n_split = A.rows * SPLITS, n_merge = A.rows * (NH / 2);
@@ -213,6 +218,11 @@ class Step {
   uint64_t waited = 0;
 
   MONO_DEV int row_len(int s) const { return min(max(A.seq_lens[s], 0), A.mail.max_ctx); }
+  // row s's leading-digit histogram of the launch with this tag: launches alternate
+  // between two copies, and each launch clears the copy its successor uses
+  MONO_DEV uint32_t* row_hist(uint32_t tag, int s) const {
+    return A.mail.rowh + ((size_t)(tag & 1u) * A.mail.max_rows + s) * ROWH;
+  }
   MONO_DEV int page_of(int s, int p) const {
     const int pg = A.pt[(size_t)s * A.pt_stride + p / PAGE];
     return min(max(pg, 0), A.n_pages - 1);
@@ -279,8 +289,9 @@ class Step {
 
   // The wave's 128 scores -> mailbox score (lane (g, r) ends with keys k0 + 16 g + r and
   // k0 + 64 + 16 g + r, so each store covers 64 consecutive positions), then the task's
-  // histogram of their leading key digits -> mailbox hist1 (the top-k's first radix
-  // pass). Every wave reaches the two barriers; a wave past the row computes nothing.
+  // histogram of their leading key digits, added into the row's histogram (the top-k's
+  // first radix pass) before the chunk is marked done (mailbox cdone). Every wave
+  // reaches the barriers; a wave past the row computes nothing.
   MONO_DEV void score_compute(const ScoreOps& o) {
     const bool live = o.k0 < o.n;  // wave-uniform
     float sc[2] = {0.f, 0.f};
@@ -324,14 +335,19 @@ class Step {
       }
     }
     uint32_t* hist = L.u.sc.hist;
-    __syncthreads();  // the previous task's histogram is published and cleared
+    __syncthreads();  // the previous task's histogram is added and cleared
 #pragma unroll
     for (int i = 0; i < 2; ++i) hist_add(hist, kl[i], radix_key(sc[i]) >> 24);
     __syncthreads();
-    if (tid < 256) {
-      if (o.c * CHUNK < o.n) mb_put(&A.mail.hist1[((size_t)o.s * CH + o.c) * 256 + tid], hist[tid], gd.tag);
-      hist[tid] = 0u;
+    if (o.c * CHUNK < o.n) {  // workgroup-uniform
+      uint32_t* rh = row_hist(gd.tag, o.s);
+      if (tid < 256 && hist[tid] != 0u)
+        __hip_atomic_fetch_add(&rh[tid], hist[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __builtin_amdgcn_s_waitcnt(0);  // every add is performed before the chunk is marked done
+      __syncthreads();
+      if (tid == 0) mb_put(&A.mail.cdone[(size_t)o.s * CH + o.c], 0u, gd.tag);
     }
+    if (tid < 256) hist[tid] = 0u;
   }
 
   // The workgroup's score tasks T0, T0 + G, ... < n_score, each task's loads issued
@@ -355,12 +371,7 @@ class Step {
   // ---------------------------------------------------------------- top-k
   // exclusive prefix sum of v over the workgroup (a full barrier)
   MONO_DEV int block_excl_scan(int v) {
-    int incl = v;
-#pragma unroll
-    for (int o = 1; o < WAVE; o <<= 1) {
-      const int y = __shfl_up(incl, o, WAVE);
-      if (lane >= o) incl += y;
-    }
+    const int incl = wave_incl_scan(v);
     if (lane == WAVE - 1) L.scan[wave] = incl;
     __syncthreads();
     int before = 0;
@@ -375,21 +386,18 @@ class Step {
     if (A.topk) A.topk[(size_t)s * TOPK + j] = slot;
   }
 
-  // Count a key digit into hist, aggregating heavy hitters: the wave's two most common
-  // leading digits go in as one atomic each (scores share sign and exponent bits, so
-  // the first digits pile onto few bins), the rest lane by lane.
+  // Count a key digit into an LDS histogram: the lanes sharing the first live lane's
+  // digit (scores share sign and exponent bits, so leading digits pile onto few bins)
+  // as one atomic, every other live lane as a plain atomic (the LDS resolves spread
+  // addresses quickly; a wave of same-address atomics would serialize).
   MONO_DEV void hist_add(uint32_t* hist, bool live, uint32_t d) {
-    uint64_t act = __ballot(live);
-#pragma unroll
-    for (int it = 0; it < 2; ++it) {
-      if (act == 0) break;
-      const int leader = __ffsll((long long)act) - 1;
-      const uint32_t dl = __shfl(d, leader, WAVE);
-      const uint64_t m = __ballot(live && d == dl) & act;
-      if (lane == leader) atomicAdd(&hist[dl], (uint32_t)__popcll(m));
-      act &= ~m;
-    }
-    if ((act >> lane) & 1ull) atomicAdd(&hist[d], 1u);
+    const uint64_t act = __ballot(live);
+    if (act == 0) return;  // wave-uniform
+    const int first = __builtin_ctzll(act);
+    const uint32_t d0 = (uint32_t)__builtin_amdgcn_readlane((int)d, first);
+    const uint64_t same = __ballot(live && d == d0);
+    if (live && d != d0) atomicAdd(&hist[d], 1u);
+    if (lane == first) atomicAdd(&hist[d0], (uint32_t)__popcll(same));
   }
 
   // Pick the next digit from a 256-bin histogram (wave 0): the highest digit d with
@@ -403,12 +411,7 @@ class Step {
       c[j] = (int)hist[255 - 4 * lane - j];
       tot += c[j];
     }
-    int incl = tot;
-#pragma unroll
-    for (int o = 1; o < WAVE; o <<= 1) {
-      const int y = __shfl_up(incl, o, WAVE);
-      if (lane >= o) incl += y;
-    }
+    const int incl = wave_incl_scan(tot);
     const int excl = incl - tot;
     const bool mine = excl < need && need <= incl;
     int dg = 0, ab = 0, run = excl;
@@ -422,14 +425,13 @@ class Step {
     }
     const uint64_t who = __ballot(mine);
     const int src = who ? __ffsll((long long)who) - 1 : 0;
-    dg = __shfl(dg, src, WAVE) & 0xff;
-    ab = __shfl(ab, src, WAVE);
+    dg = __builtin_amdgcn_readlane(dg, src) & 0xff;
+    ab = __builtin_amdgcn_readlane(ab, src);
     if (pre) {
       int x = 0;
 #pragma unroll
       for (int j = 0; j < 4; ++j) x += 255 - 4 * lane - j > dg ? (int)pre[255 - 4 * lane - j] : 0;
-#pragma unroll
-      for (int o = 1; o < WAVE; o <<= 1) x += __shfl_xor(x, o, WAVE);
+      x = wave_sum_i(x);
       if (lane == 0) K.pre_above = x;
     }
     if (lane == 0) {
@@ -439,31 +441,43 @@ class Step {
   }
 
   // One exchanged radix pass: member m's histogram of the digit at `shift` over its keys
-  // matching prefix under mask -> mailbox hist; the team's sum -> K.tot and the sum over
-  // the members before m -> K.pre. Workgroup-uniform result.
+  // matching prefix under mask -> mailbox hist as 128 words of two 16-bit bins (a member
+  // holds at most KPM keys), plus `count` as word 128 when count >= 0; the team's sum
+  // -> K.tot, the sum over the members before m -> K.pre, the members' counts -> K.xw.
+  // Workgroup-uniform result.
   MONO_DEV bool exchange_hist(int s, int m, int pass, const uint32_t (&key)[KPT], int cnt, uint32_t prefix,
-                              uint32_t mask, int shift) {
+                              uint32_t mask, int shift, int count) {
+    static_assert(KPM < 65536, "16-bit bins");
     TopkLds& K = L.u.t;
     if (tid < 256) K.hist[tid] = 0u;
     __syncthreads();
 #pragma unroll
     for (int q = 0; q < KPT; ++q) hist_add(K.hist, q < cnt && (key[q] & mask) == prefix, (key[q] >> shift) & 0xffu);
     __syncthreads();
-    uint64_t* hb = &A.mail.hist[((size_t)s * PASSES + pass) * TEAM * 256];
+    uint64_t* hb = &A.mail.hist[((size_t)s * PASSES + pass) * TEAM * HW];
     bool ok = true;
-    if (tid < 256) {
-      mb_put(&hb[m * 256 + tid], K.hist[tid], gd.tag);
+    if (tid < 128) {
+      mb_put(&hb[m * HW + tid], K.hist[2 * tid] | (K.hist[2 * tid + 1] << 16), gd.tag);
       uint32_t v[TEAM];
       const uint64_t* col = hb + tid;
-      ok = poll_words<TEAM>([col](int j) { return col + j * 256; }, v, (1u << TEAM) - 1u, W_TEAM, gd);
-      uint32_t t = 0, p = 0;
+      const auto at = [col](int j) { return col + j * HW; };
+      ok = poll_words<TEAM, decltype(at), false, false>(at, v, (1u << TEAM) - 1u, W_TEAM, gd);
+      uint32_t t = 0, p = 0;  // two 16-bit sums side by side (at most TEAM KPM keys)
 #pragma unroll
       for (int j = 0; j < TEAM; ++j) {
         t += v[j];
         p += j < m ? v[j] : 0u;
       }
-      K.tot[tid] = t;
-      K.pre[tid] = p;
+      K.tot[2 * tid] = t & 0xffffu;
+      K.tot[2 * tid + 1] = t >> 16;
+      K.pre[2 * tid] = p & 0xffffu;
+      K.pre[2 * tid + 1] = p >> 16;
+    } else if (count >= 0 && tid < 128 + TEAM) {
+      const int j = tid - 128;
+      if (j == m) mb_put(&hb[m * HW + 128], (uint32_t)count, gd.tag);
+      uint32_t v = 0;
+      ok = poll_word(&hb[j * HW + 128], v, W_TEAM, gd);
+      K.xw[j] = (int)v;
     }
     return block_all(ok);
   }
@@ -497,25 +511,13 @@ class Step {
     const int p0 = m * KPM + tid * KPT;
     const int cnt = min(max(n - p0, 0), KPT);
     const int page = cnt > 0 ? page_of(s, p0) : 0;  // a thread's keys share one page
-    bool ok;
-    // threads 0..255: bin tid of every scored chunk's histogram; 256..: the member's
-    // scores (coalesced) -> LDS keys
-    if (tid < 256) {
-      constexpr int NCH = MAX_CTX / CHUNK, CPM = KPM / CHUNK;
-      const int nch = (n + CHUNK - 1) / CHUNK;
-      uint32_t v[NCH];
-      const uint64_t* col = &A.mail.hist1[(size_t)s * CH * 256 + tid];
-      ok = poll_words<NCH>([col](int c) { return col + c * 256; }, v, nch >= NCH ? ~0u : (1u << nch) - 1u, W_SCORE,
-                           gd);
-      uint32_t t = 0, p = 0;
-#pragma unroll
-      for (int c = 0; c < NCH; ++c) {
-        t += c < nch ? v[c] : 0u;
-        p += c < nch && c < CPM * m ? v[c] : 0u;
-      }
-      K.tot[tid] = t;
-      K.pre[tid] = p;
-    } else {
+    bool ok = true;
+    // thread c < (scored chunks) waits for chunk c's counts in the row histogram,
+    // threads 256.. poll the member's scores (coalesced) -> LDS keys
+    if (tid < (n + CHUNK - 1) / CHUNK) {
+      uint32_t v;
+      ok = poll_word(&A.mail.cdone[(size_t)s * CH + tid], v, W_SCORE, gd);
+    } else if (tid >= 256) {
       constexpr int NW = KPM / (AT - 256);
       const int i0 = tid - 256;
       uint32_t v[NW], pend = 0;
@@ -525,12 +527,13 @@ class Step {
         pend |= (m * KPM + i0 + 256 * q < n ? 1u : 0u) << q;
       }
       const uint64_t* base = &A.mail.score[(size_t)s * A.mail.max_ctx + m * KPM + i0];
-      ok = poll_words<NW>([base](int q) { return base + 256 * q; }, v, pend, W_SCORE, gd);
+      const auto at = [base](int q) { return base + 256 * q; };
+      ok = poll_words<NW, decltype(at), false, false>(at, v, pend, W_SCORE, gd);
 #pragma unroll
       for (int q = 0; q < NW; ++q) K.key[i0 + 256 * q] = radix_key(__uint_as_float(v[q]));
     }
     if (!block_all(ok)) return false;
-    mark_waited();
+    if (tid < 256) K.tot[tid] = ld_agent_u32(&row_hist(gd.tag, s)[tid]);
     uint32_t key[KPT];
     {
       static_assert(KPT == 4, "a thread's keys are one 16-byte LDS read");
@@ -538,15 +541,28 @@ class Step {
 #pragma unroll
       for (int q = 0; q < KPT; ++q) key[q] = k4[q];
     }
-    pick_digit(K, K.tot, TOPK, K.pre);
     __syncthreads();
-    int need = TOPK - K.above, above_before = K.pre_above;
-    uint32_t prefix = K.digit << 24, mask = 0xff000000u;
-    if (!exchange_hist(s, m, 1, key, cnt, prefix, mask, 16)) return false;
+    mark_waited();
+    pick_digit(K, K.tot, TOPK, nullptr);
+    __syncthreads();
+    int need = TOPK - K.above;
+    const uint32_t d1 = K.digit;
+    uint32_t prefix = d1 << 24, mask = 0xff000000u;
+    int above1 = 0;  // this member's keys above digit 1
+#pragma unroll
+    for (int q = 0; q < KPT; ++q) above1 += (q < cnt && (key[q] >> 24) > d1) ? 1 : 0;
+    above1 = wave_sum_i(above1);
+    if (lane == 0) L.scan[wave] = above1;
+    __syncthreads();
+    above1 = 0;
+#pragma unroll
+    for (int w = 0; w < AW; ++w) above1 += L.scan[w];
+    if (!exchange_hist(s, m, 1, key, cnt, prefix, mask, 16, above1)) return false;
     pick_digit(K, K.tot, need, K.pre);
     __syncthreads();
     need -= K.above;
-    above_before += K.pre_above;
+    int above_before = K.pre_above;  // the earlier members' keys above the threshold's upper 16 bits
+    for (int j = 0; j < m; ++j) above_before += K.xw[j];
     prefix |= K.digit << 16;
     mask |= 0x00ff0000u;
     const int n_cand = (int)K.tot[K.digit], cand_before = (int)K.pre[K.digit];
@@ -585,7 +601,7 @@ class Step {
       for (int pass = 2; pass < PASSES; ++pass) {
         const int shift = 24 - 8 * pass;
         __syncthreads();  // K.digit and K.tot are read
-        if (!exchange_hist(s, m, pass, key, cnt, prefix, mask, shift)) return false;
+        if (!exchange_hist(s, m, pass, key, cnt, prefix, mask, shift, -1)) return false;
         pick_digit(K, K.tot, need, nullptr);
         __syncthreads();
         need -= K.above;

@@ -17,26 +17,31 @@ constexpr int DV = 512;         // latent dims attended as values
 constexpr int PAGE = 64;        // tokens a cache page
 constexpr int TOPK = 2048;      // tokens a row attends
 constexpr int MAX_ROWS = 64;
-constexpr int MAX_CTX = 32768;  // keys a row the one-workgroup top-k holds in LDS
+constexpr int MAX_CTX = 32768;  // keys a row at most (2048 a top-k team member)
 constexpr int CHUNK = 1024;     // keys a score task
 constexpr int SPLITS = 32;      // attention splits a row (64 selected tokens each)
 constexpr int SPLIT = TOPK / SPLITS;
 constexpr int TEAM = 16;        // workgroups selecting one row's top-k together
 constexpr int PASSES = 4;       // 8-bit radix digits of a 32-bit key
 constexpr int CMAX = 512;       // threshold candidates a row exchanged as (key, position)
+constexpr int HW = 136;         // words a member's histogram: 128 of two 16-bit bins, 1 count
+constexpr int ROWH = 256;       // words a row histogram
 
 // Mailboxes of one attention runtime (tagged 64-bit words, see sync.h).
 struct Mail {
   uint64_t* score;  // [max_rows][max_ctx]           index scores, f32
   uint64_t* sel;    // [max_rows][TOPK]               selected slots, i32
-  uint64_t* hist1;  // [max_rows][max_ctx / CHUNK][256] a score chunk's leading-digit histogram
-  uint64_t* hist;   // [max_rows][PASSES][TEAM][256]  a team member's digit histogram
+  uint32_t* rowh;   // [2][max_rows][ROWH]           leading-digit histogram of a row's scores
+                    //                                 (untagged counts; launch parity tag & 1)
+  uint64_t* cdone;  // [max_rows][max_ctx / CHUNK]   a score chunk's counts are in rowh
+  uint64_t* hist;   // [max_rows][PASSES][TEAM][HW]   a team member's digit histogram, packed
   uint64_t* cand;   // [max_rows][CMAX]               threshold candidates (low key bits, position)
   uint64_t* cnt;    // [max_rows][TEAM][2]            a member's keys above / at the threshold
   uint64_t* part;   // [max_rows][SPLITS][NH][DV / 2] a split's unnormalised output, bf16 pairs
   uint64_t* ml;     // [max_rows][SPLITS][NH][2]      a split's max logit and sum
   uint32_t* guard;  // [G_WORDS]
   int max_ctx;
+  int max_rows;
 };
 
 struct AttnArgs : mono_attn_args {

@@ -88,6 +88,21 @@ MONO_DEV uint32_t wave_umax(uint32_t v) {
   return max(a, b);
 }
 
+// Inclusive prefix sum over the wave, lane 0 first: DPP row shifts inside each 16-lane
+// row (Hillis-Steele), then two row broadcasts carry the sums of row 0 and of rows
+// 0..1 into the rows after them. Lanes whose DPP source lies outside the row add 0.
+MONO_DEV int wave_incl_scan(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);  // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false);  // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false);  // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false);  // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);  // row_bcast:15 -> rows 1, 3
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);  // row_bcast:31 -> rows 2, 3
+  return v;
+}
+// integer sum over the wave (wave-uniform)
+MONO_DEV int wave_sum_i(int v) { return __builtin_amdgcn_readlane(wave_incl_scan(v), WAVE - 1); }
+
 // max over groups of `WIDTH` consecutive lanes (WIDTH a power of two <= 16)
 template <int WIDTH>
 MONO_DEV float group_max(float v) {

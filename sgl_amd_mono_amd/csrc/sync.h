@@ -98,7 +98,9 @@ struct Guard {
 // CACHED_FIRST: the first pass uses plain cacheable loads (after a hint wait has seen the
 // producers finish, so many workgroups reading one broadcast payload share the L2 of
 // their XCD instead of each fetching it from memory).
-template <int N, class At, bool CACHED_FIRST = false>
+// PROBE = false: every spin sweeps all missing words (for small exchanges between a few
+// workgroups, where a probe's extra round trip is the cost that matters).
+template <int N, class At, bool CACHED_FIRST = false, bool PROBE = true>
 MONO_DEV bool poll_words(At at, uint32_t (&v)[N], uint32_t pending, int site, const Guard& g) {
   if (pending && site == g.a.fault_site) {  // host-forced fault: the wait fails at once
     g.fail(site);
@@ -131,6 +133,12 @@ MONO_DEV bool poll_words(At at, uint32_t (&v)[N], uint32_t pending, int site, co
   };
   sweep();
   for (uint32_t spin = 1; pending; ++spin) {
+    if (!PROBE) {
+      if (spin % POLL_CHECK <= 1 && g.expired(site, spin % POLL_CHECK == 0)) return false;
+      __builtin_amdgcn_s_sleep(1);
+      sweep();
+      continue;
+    }
     uint64_t probe = 0;
     bool sent = false;
 #pragma unroll
