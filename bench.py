@@ -494,6 +494,8 @@ def bench_layer(args, dev):
     torch.cuda.synchronize()
     rt.check_errors()
 
+    if args.pmc_pass:
+        return pmc_pass(args, dev, run_step, distinct)
     for _ in range(max(args.warmup, 1)):
         run_step()
     torch.cuda.synchronize()
@@ -552,6 +554,7 @@ def bench_layer(args, dev):
         "moe": statistics.fmean(moe_b),
     }
     moe_durs = ph["moe"]
+    traffic = read_traffic("k_moe_fp8")
     moe_achieved = statistics.fmean(
         b / (t * 1e-6) for b, t in zip([moe_b[l] for _ in range(n_eager) for l in range(L)], moe_durs)) / 1e9
     layer_bytes = sum(phase_bytes.values())
@@ -581,11 +584,53 @@ def bench_layer(args, dev):
         ),
         roofline=dict(
             bound="hbm", achieved=moe_achieved, peak=HBM_PEAK_GBS, unit="GB/s", frac=moe_achieved / HBM_PEAK_GBS,
-            traffic=None, kernel="k_moe_fp8 (the MoE phase: 86% of the layer's bytes)",
+            traffic=traffic, kernel="k_moe_fp8 (the MoE phase: 86% of the layer's bytes)",
             bytes_per_launch=statistics.fmean(moe_b), avg_launch_us=statistics.fmean(moe_durs),
         ),
         cpu_baseline=cpu,
     )
+
+
+CALIB_BYTES = 1 << 30  # the calibration copy of a PMC pass: 1 GiB read, 1 GiB written
+TRAFFIC_FILE = ROOT / "profiles" / "traffic_layer_8rows.md"
+
+
+def pmc_pass(args, dev, run_step, distinct):
+    """For ``rocprofv3 --pmc FETCH_SIZE`` / ``--pmc WRITE_SIZE`` runs: ``--steps`` eager
+    layer steps (every dispatch seen by the profiler; no graph) and then one device copy
+    of CALIB_BYTES, whose counter reading calibrates the counter in bytes. Prints one
+    JSON line naming what ran."""
+    import torch
+
+    from sgl_amd_mono_amd.moe import FP8_MOE
+
+    for _ in range(args.steps):
+        run_step()
+    src = torch.empty(CALIB_BYTES // 4, dtype=torch.float32, device=dev).fill_(1.0)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    moe_fixed = 256 * 7168 * 2 + 256 * 4 + 7168 * 2 + 2 * args.rows * 7168 * 2
+    print(json.dumps({"pmc_pass": True, "steps": args.steps, "layers": args.layers, "rows": args.rows,
+                      "calib_copy_bytes": CALIB_BYTES,
+                      "moe_algorithmic_bytes_mean": statistics.fmean(
+                          d * fp8_expert_bytes(FP8_MOE) + moe_fixed for d in distinct)}), flush=True)
+    return None
+
+
+def read_traffic(kernel: str):
+    """HBM bytes a launch of `kernel` (fetched + written) from the committed PMC summary,
+    whose lines `traffic <kernel> <bytes>` come from two rocprofv3 --pmc runs calibrated
+    by a copy of known size; None when the summary is absent."""
+    try:
+        for line in TRAFFIC_FILE.read_text().splitlines():
+            f = line.strip().strip("`").split()
+            if len(f) == 3 and f[0] == "traffic" and f[1] == kernel:
+                return float(f[2])
+    except OSError:
+        return None
+    return None
 
 
 def cpu_baseline_layer(args, layer, x_in, cos, sin):
@@ -673,6 +718,8 @@ def main() -> int:
     ap.add_argument("--ctx", type=int, default=32768, help="keys a row (attn workload)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="wall budget of the CPU baseline sample (0 skips it)")
+    ap.add_argument("--pmc-pass", action="store_true",
+                    help="layer workload: eager steps plus a calibration copy, for rocprofv3 --pmc runs")
     args = ap.parse_args()
     if args.steps is None:
         args.steps = DEFAULT_STEPS[args.workload]
@@ -694,6 +741,8 @@ def main() -> int:
     torch.cuda.set_device(dev)
     log(f"device {torch.cuda.get_device_properties(dev).gcnArchName}, workload {args.workload}")
     r = WORKLOADS[args.workload](args, dev)
+    if r is None:  # a PMC pass printed its own line
+        return 0
     line = {
         "metric": METRIC,
         "value": round(r["value"], 3),
