@@ -48,7 +48,7 @@ MONO_DEV void wave_topk(uint32_t (&key)[4], int (&id)[4], float (&raw)[4], int n
     const bool hit = key[0] == m && id[0] == pick;
     const uint64_t bal = __ballot(hit);
     const int src = __ffsll((long long)bal) - 1;
-    const float rv = __shfl(raw[0], src, WAVE);
+    const float rv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, raw[0]), src));
     if (lane == k) {
       my_raw = rv;
       my_id = pick;

@@ -230,8 +230,8 @@ class Step {
     if (tid < E) {
       const uint64_t* base = &A.mail.rlog[(size_t)s * E + tid];
       uint32_t v[RK];
-      ok = poll_words<RK>([base](int ks) { return base + (size_t)ks * MAX_ROWS * E; }, v, (1u << RK) - 1u,
-                          W_LOGITS, gd);
+      const auto at = [base](int ks) { return base + (size_t)ks * MAX_ROWS * E; };
+      ok = poll_words<RK, decltype(at), false, false>(at, v, (1u << RK) - 1u, W_LOGITS, gd);
       float lg = 0.f;
 #pragma unroll
       for (int ks = 0; ks < RK; ++ks) lg += __uint_as_float(v[ks]);
@@ -256,8 +256,7 @@ class Step {
       wave_topk<TOPK>(key, id, raw, E, my_id, my_raw);
       // sum of the picks' raw scores in the butterfly order of lanes 0..7
       float tot = lane < TOPK ? my_raw : 0.f;
-#pragma unroll
-      for (int o = 1; o < TOPK; o <<= 1) tot += __shfl_xor(tot, o, WAVE);
+      tot = row_reduce<TOPK>(tot, OpAdd());
       const float w = my_raw * (hw_rcp(tot) * A.route_scale);
       if (lane < TOPK) {
         mb_put(&A.mail.rsel[s * 2 * MAX_TOPK + lane], (uint32_t)my_id, gd.tag);
@@ -273,20 +272,19 @@ class Step {
   // Lane quantises 8 consecutive k of a row; 16 lanes make a 128-block.
   MONO_DEV void quant_rows() {
     constexpr int PER_ROW = H / (8 * WAVE);  // wave passes a row
+    constexpr int QU = 4;                    // passes a wave has in flight
     const int npass = S * PER_ROW;
-    for (int p0 = wave; p0 < npass; p0 += FW * 2) {
-      u32x4 av[2], gv[2];
+    for (int p0 = wave; p0 < npass; p0 += FW * QU) {
+      u32x4 av[QU], gv[QU];
 #pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const int p = p0 + u * FW;
-        if (p < npass) {
-          const int s = p / PER_ROW, k = ((p % PER_ROW) * WAVE + lane) * 8;
-          av[u] = ld_u32x4(A.a + (size_t)s * H + k);
-          gv[u] = ld_u32x4(A.g_post + k);
-        }
+      for (int u = 0; u < QU; ++u) {  // unconditional (clamped) loads: no serialising joins
+        const int p = min(p0 + u * FW, npass - 1);
+        const int s = p / PER_ROW, k = ((p % PER_ROW) * WAVE + lane) * 8;
+        av[u] = ld_u32x4(A.a + (size_t)s * H + k);
+        gv[u] = ld_u32x4(A.g_post + k);
       }
 #pragma unroll
-      for (int u = 0; u < 2; ++u) {
+      for (int u = 0; u < QU; ++u) {
         const int p = p0 + u * FW;
         if (p >= npass) continue;  // wave-uniform
         const int s = p / PER_ROW, k = ((p % PER_ROW) * WAVE + lane) * 8;
