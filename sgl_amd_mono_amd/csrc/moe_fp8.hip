@@ -200,16 +200,15 @@ class Step {
 
   MONO_DEV void router(int t, const u32x4 (&wr)[RSTEP]) {
     const int et = t % (E / 16), ks = t / (E / 16);
-    const bool live = r < S;
-    const float rj = live ? L.rstd[r] : 0.f;
-    const uint16_t* arow = A.a + (size_t)(live ? r : 0) * H;
+    // columns r >= S compute on row S - 1 and are dropped: every load unconditional
+    const int rr = min(r, S - 1);
+    const float rj = L.rstd[rr];
+    const uint16_t* arow = A.a + (size_t)rr * H;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int st = 0; st < RSTEP; ++st) {
       const int k = ks * (H / RK) + wave * RKW + st * 32 + g * 8;
-      bf16x8 b = {};
-      if (live) b = normed8(arow + k, A.g_post + k, rj);
-      acc = mfma_bf16(__builtin_bit_cast(bf16x8, wr[st]), b, acc);
+      acc = mfma_bf16(__builtin_bit_cast(bf16x8, wr[st]), normed8(arow + k, A.g_post + k, rj), acc);
     }
     L.red[0][wave][lane] = acc;
     __syncthreads();
@@ -227,6 +226,7 @@ class Step {
   // ---------------------------------------------------------------- route
   MONO_DEV bool route(int s) {
     bool ok = true;
+    const float bias = A.bias[min(tid, E - 1)];  // before the wait: no round trip after it
     if (tid < E) {
       const uint64_t* base = &A.mail.rlog[(size_t)s * E + tid];
       uint32_t v[RK];
@@ -237,7 +237,7 @@ class Step {
       for (int ks = 0; ks < RK; ++ks) lg += __uint_as_float(v[ks]);
       const float raw = sigmoid(lg);
       L.rraw[tid] = raw;
-      L.rkey[tid] = radix_key(raw + A.bias[tid]);
+      L.rkey[tid] = radix_key(raw + bias);
       if (A.scores && ok) A.scores[s * E + tid] = raw;
     }
     if (!block_all(ok)) return false;
