@@ -3,11 +3,13 @@
 //
 // The reference's stages 1-4 (glm53/gfx950/kernel.py:1367-2443) with the FP4
 // indexer of deepseek_v4/gfx950/kernels/stages/indexer.py:236-408:
-//   A  (tile of 16 rows, K half) of [W_qkv (2112) | W_ik (128)] FP8 and W_iw (64)
-//      bf16 against the input-RMSNormed rows: every task sums each row's squares over
-//      the whole row (one wave a row), stages its K half as bf16(x rstd gamma) in LDS,
-//      and runs 3-4 128-k steps a wave -> partial sums (mailbox pa)
-//   B  (row): the two halves summed; q_a RMSNorm -> q_an (bf16 pairs); KV RMSNorm +
+//   A  (tile of 16 rows, K part) of [W_qkv (2112) | W_ik (128)] FP8 (whole K up to 8
+//      rows, halves above) and W_iw (64) bf16 (K quarters) against the input-RMSNormed
+//      rows: the weight burst goes out first; every task stages its rows by DMA into
+//      LDS, sums each row's squares over the whole row (one wave a row), scales its K
+//      part to bf16(x rstd gamma) in place and runs its 128-k steps -> partial sums
+//      (mailbox pa)
+//   B  (row): the K parts summed in order; q_a RMSNorm -> q_an (bf16 pairs); KV RMSNorm +
 //      k_pe RoPE -> one power-of-two-scaled E4M3 row into the MLA cache; index key
 //      LayerNorm + RoPE + Hadamard + FP4 into the index plane; head weights
 //   C  (64-row tile) of W_qb (6144) and W_iq (8192) against q_an: q_nope (bf16 pairs),
