@@ -350,8 +350,9 @@ extern "C" int mono_attn_create(const mono_attn_config* cfg, mono_attn** out) {
   const size_t o_hist = cv.take(R * PASSES * TEAM * HW * 8);
   const size_t o_cand = cv.take(R * CMAX * 8);
   const size_t o_cnt = cv.take(R * TEAM * 2 * 8);
-  const size_t o_part = cv.take(R * SPLITS * NH * (DV / 2) * 8);
-  const size_t o_ml = cv.take(R * SPLITS * NH * 2 * 8);
+  const size_t o_part = cv.take(R * SPLITS * NH * DV * 2);
+  const size_t o_ml = cv.take(R * SPLITS * NH * 2 * 4);
+  const size_t o_sdone = cv.take(R * SPLITS * 8);
   mono_attn* a = new mono_attn();
   a->magic = ATTN_MAGIC;
   a->cfg = c;
@@ -373,8 +374,9 @@ extern "C" int mono_attn_create(const mono_attn_config* cfg, mono_attn** out) {
   a->mail.hist = reinterpret_cast<uint64_t*>(a->at(o_hist));
   a->mail.cand = reinterpret_cast<uint64_t*>(a->at(o_cand));
   a->mail.cnt = reinterpret_cast<uint64_t*>(a->at(o_cnt));
-  a->mail.part = reinterpret_cast<uint64_t*>(a->at(o_part));
-  a->mail.ml = reinterpret_cast<uint64_t*>(a->at(o_ml));
+  a->mail.part = reinterpret_cast<uint16_t*>(a->at(o_part));
+  a->mail.ml = reinterpret_cast<float*>(a->at(o_ml));
+  a->mail.sdone = reinterpret_cast<uint64_t*>(a->at(o_sdone));
   a->mail.max_ctx = c.max_ctx;
   a->mail.max_rows = c.max_rows;
   *out = a;

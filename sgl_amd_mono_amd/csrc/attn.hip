@@ -28,8 +28,10 @@
 //   split  (row, 64 selected tokens): sub-tiles of 64 tokens gathered from the FP8
 //          cache and widened exactly to bf16 in LDS, bf16 MFMA 16x16x32 for q.k and
 //          p.v, the per-token scale folded into the logit and the probability, online
-//          softmax -> mailboxes part (bf16 pairs), ml
-//   merge  (row, 2 heads): out = sum_j e^(m_j - M) acc_j / sum_j e^(m_j - M) l_j, bf16
+//          softmax -> the split's partials (bf16, 32 KB in one contiguous run) and
+//          (m, l), then its done word (mailbox sdone)
+//   merge  (row, 2 heads): once every split of the row is done,
+//          out = sum_j e^(m_j - M) acc_j / sum_j e^(m_j - M) l_j, bf16
 #include "attn_ops.h"
 #include "common.h"
 #include "sync.h"
@@ -52,6 +54,8 @@ constexpr int PB_STRIDE = SUB + 8;           // bf16 a probability row in LDS
 constexpr int KEYS_WAVE = CHUNK / AW;        // 128 keys a wave of a score task
 constexpr int KTILES = KEYS_WAVE / 16;
 constexpr float NEG_INF = -__builtin_huge_valf();
+constexpr int BUF_DWORD3 = 0x00020000;       // raw buffer resource word 3 (gfx9)
+constexpr int SC1 = 16;                      // buffer cache policy: device-coherent
 static_assert(KPM % AT == 0 && PAGE % KPT == 0 && TEAM <= 16 && KEYS_WAVE % PAGE == 0 && SPLIT % SUB == 0, "tiling");
 static_assert(AT == NH * DV / 32, "a merge task covers 2 heads");
 
@@ -727,9 +731,10 @@ class Step {
     const size_t mlb = ((size_t)s * SPLITS + j) * NH;
     if (cnt == 0) {  // an empty split contributes nothing to the merge
       if (tid < NH) {
-        mb_putf(&A.mail.ml[(mlb + tid) * 2], NEG_INF, gd.tag);
-        mb_putf(&A.mail.ml[(mlb + tid) * 2 + 1], 0.f, gd.tag);
+        st_agent_f32(&A.mail.ml[(mlb + tid) * 2], NEG_INF);
+        st_agent_f32(&A.mail.ml[(mlb + tid) * 2 + 1], 0.f);
       }
+      split_done(s, j);
       return true;
     }
     {
@@ -844,9 +849,12 @@ class Step {
       }
       __syncthreads();
     }
-    const size_t pb = ((size_t)s * SPLITS + j) * NH;
-    // bf16 pairs (the reference's split partials, kernel.py:4040-4066): lane r holds dim
-    // 16 n + r, its neighbour r ^ 1 the other half of the pair
+    // the partials (bf16, the reference's split partials, kernel.py:4040-4066) staged as
+    // [head][dim] in LDS (lane r holds dim 16 n + r, its neighbour r ^ 1 the other half
+    // of a pair), then stored as the split's contiguous 32 KB by 16-byte
+    // device-coherent stores; then (m, l); then the split's done word
+    uint32_t* ot = P.kvb;  // free after the last P.V step's barrier
+    static_assert(sizeof(P.kvb) >= NH * DV * 2, "partial staging");
 #pragma unroll
     for (int a = 0; a < 2; ++a)
 #pragma unroll
@@ -855,16 +863,35 @@ class Step {
         for (int i = 0; i < 4; ++i) {
           const float mine = acc[a][b][i], other = dpp_f<DPP_XOR1>(mine);
           const int h = 16 * a + 4 * g + i, dim = 16 * (4 * wave + b) + r;
-          if ((r & 1) == 0) mb_put(&A.mail.part[(pb + h) * (DV / 2) + dim / 2], pack_bf16x2(mine, other), gd.tag);
+          if ((r & 1) == 0) ot[(h * DV + dim) / 2] = pack_bf16x2(mine, other);
         }
+    __syncthreads();
+    {
+      const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+          A.mail.part + ((size_t)s * SPLITS + j) * NH * DV, 0, NH * DV * 2, BUF_DWORD3);
+      constexpr int CH16 = NH * DV * 2 / 16;  // 16-byte chunks of the split's partials
+#pragma unroll
+      for (int q = 0; q < CH16 / AT; ++q) {
+        const int c = tid + AT * q;
+        __builtin_amdgcn_raw_buffer_store_b128(*reinterpret_cast<const u32x4*>(&ot[4 * c]), rs, 16 * c, 0, SC1);
+      }
+    }
     if (lane < 4) {
       const float m = lane == 0 ? m_run[0] : lane == 1 ? m_run[1] : lane == 2 ? m_run[2] : m_run[3];
       const float l = lane == 0 ? l_run[0] : lane == 1 ? l_run[1] : lane == 2 ? l_run[2] : l_run[3];
       const int h = 4 * wave + lane;
-      mb_putf(&A.mail.ml[(mlb + h) * 2], m, gd.tag);
-      mb_putf(&A.mail.ml[(mlb + h) * 2 + 1], l, gd.tag);
+      st_agent_f32(&A.mail.ml[(mlb + h) * 2], m);
+      st_agent_f32(&A.mail.ml[(mlb + h) * 2 + 1], l);
     }
+    split_done(s, j);  // its barrier also frees the staging LDS for the next task
     return true;
+  }
+
+  // every store of the split performed (each thread waits for its own), then its done word
+  MONO_DEV void split_done(int s, int j) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid == 0) mb_put(&A.mail.sdone[(size_t)s * SPLITS + j], 0u, gd.tag);
   }
 
   // ---------------------------------------------------------------- merge
@@ -873,17 +900,19 @@ class Step {
     MergeLds& Q = L.u.mg;
     const int hh = tid / 256, h = 2 * hp + hh, d0 = (tid % 256) * 2;
     const size_t rb = (size_t)s * SPLITS;
-    // the split weights: lane j of waves 0 and 4 (heads 2 hp, 2 hp + 1) takes split j
+    // every split of the row done: lane j of wave 0 polls split j's word
     bool ok = true;
+    if (wave == 0 && lane < SPLITS) {
+      uint32_t v;
+      ok = poll_word(&A.mail.sdone[rb + lane], v, W_PART, gd);
+    }
+    if (!block_all(ok)) return false;
+    mark_waited();
+    // the split weights: lane j of waves 0 and 4 (heads 2 hp, 2 hp + 1) takes split j
     if (wave % 4 == 0) {
-      float m = NEG_INF, l = 0.f;
-      if (lane < SPLITS) {
-        uint32_t v[2];
-        const uint64_t* mlp = &A.mail.ml[((rb + lane) * NH + h) * 2];
-        ok = poll_words<2>([mlp](int q) { return mlp + q; }, v, 3u, W_PART, gd);
-        m = __uint_as_float(v[0]);
-        l = __uint_as_float(v[1]);
-      }
+      const int jl = min(lane, SPLITS - 1);
+      const float m = ld_agent_f32(&A.mail.ml[((rb + jl) * NH + h) * 2]);
+      const float l = lane < SPLITS ? ld_agent_f32(&A.mail.ml[((rb + jl) * NH + h) * 2 + 1]) : 0.f;
       const bool live = l > 0.f;
       const float M = wave_max(live ? m : NEG_INF);
       const float w = live ? hw_exp(m - M) : 0.f;
@@ -891,26 +920,27 @@ class Step {
       if (lane < SPLITS) Q.w[hh][lane] = w;
       if (lane == 0) Q.den[hh] = den;
     }
-    if (!block_all(ok)) return false;
-    uint32_t live = 0;
-#pragma unroll
-    for (int j = 0; j < SPLITS; ++j) live |= (Q.w[hh][j] > 0.f ? 1u : 0u) << j;
+    // the channel pair of every split (unconditional loads; an empty split's words are
+    // read and ignored)
     uint32_t av[SPLITS];
-    const uint64_t* ap = &A.mail.part[(rb * NH + h) * (DV / 2) + d0 / 2];
-    ok = poll_words<SPLITS>([ap](int q) { return ap + (size_t)q * NH * (DV / 2); }, av, live, W_PART, gd);
+#pragma unroll
+    for (int j = 0; j < SPLITS; ++j)
+      av[j] = ld_agent_u32(reinterpret_cast<const uint32_t*>(&A.mail.part[((rb + j) * NH + h) * DV + d0]));
+    __syncthreads();
     float o[2] = {0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < SPLITS; ++j) {
-      if ((live >> j) & 1u) {
-        const float w = Q.w[hh][j];
+      const float w = Q.w[hh][j];
+      if (w > 0.f) {
         o[0] += w * bf16_lo(av[j]);
         o[1] += w * bf16_hi(av[j]);
       }
     }
     const float den = Q.den[hh];
     const float inv = den > 0.f ? 1.0f / den : 0.f;
-    if (ok) *reinterpret_cast<uint32_t*>(A.out + ((size_t)s * NH + h) * DV + d0) = pack_bf16x2(o[0] * inv, o[1] * inv);
-    return block_all(ok);  // also: the next task may rewrite the LDS weights
+    *reinterpret_cast<uint32_t*>(A.out + ((size_t)s * NH + h) * DV + d0) = pack_bf16x2(o[0] * inv, o[1] * inv);
+    __syncthreads();  // the next task may rewrite the LDS weights
+    return true;
   }
 };
 

@@ -37,8 +37,10 @@ struct Mail {
   uint64_t* hist;   // [max_rows][PASSES][TEAM][HW]   a team member's digit histogram, packed
   uint64_t* cand;   // [max_rows][CMAX]               threshold candidates (low key bits, position)
   uint64_t* cnt;    // [max_rows][TEAM][2]            a member's keys above / at the threshold
-  uint64_t* part;   // [max_rows][SPLITS][NH][DV / 2] a split's unnormalised output, bf16 pairs
-  uint64_t* ml;     // [max_rows][SPLITS][NH][2]      a split's max logit and sum
+  uint16_t* part;   // [max_rows][SPLITS][NH][DV]     a split's unnormalised output, bf16
+                    //                                 (untagged; read after sdone)
+  float* ml;        // [max_rows][SPLITS][NH][2]      a split's max logit and sum (untagged)
+  uint64_t* sdone;  // [max_rows][SPLITS]             a split's part and ml are stored
   uint32_t* guard;  // [G_WORDS]
   int max_ctx;
   int max_rows;

@@ -61,6 +61,11 @@ MONO_DEV uint64_t mb_load_cached(const uint64_t* p) { return *p; }
 MONO_DEV uint32_t ld_agent_u32(const uint32_t* p) {
   return __hip_atomic_load(const_cast<uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// device-coherent plain data (read after the tagged word that announces it)
+MONO_DEV float ld_agent_f32(const float* p) { return __uint_as_float(ld_agent_u32(reinterpret_cast<const uint32_t*>(p))); }
+MONO_DEV void st_agent_f32(float* p, float v) {
+  __hip_atomic_store(reinterpret_cast<uint32_t*>(p), __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 struct Guard {
   GuardArgs a;
