@@ -343,7 +343,7 @@ extern "C" int mono_attn_create(const mono_attn_config* cfg, mono_attn** out) {
   const size_t R = c.max_rows;
   Carve cv;
   const size_t o_guard = cv.take(mono::G_WORDS * 4);
-  const size_t o_score = cv.take(R * c.max_ctx * 8);
+  const size_t o_score = cv.take(R * c.max_ctx * 4);
   const size_t o_sel = cv.take(R * TOPK * 8);
   const size_t o_rowh = cv.take(2 * R * ROWH * 4);
   const size_t o_cdone = cv.take(R * (c.max_ctx / CHUNK) * 8);
@@ -367,7 +367,7 @@ extern "C" int mono_attn_create(const mono_attn_config* cfg, mono_attn** out) {
     return fail(MONO_ESTATE, "the attention launch needs a CU count divisible by %d, got %d", TEAM, a->grid);
   }
   a->mail.guard = a->guard.words;
-  a->mail.score = reinterpret_cast<uint64_t*>(a->at(o_score));
+  a->mail.score = reinterpret_cast<uint32_t*>(a->at(o_score));
   a->mail.sel = reinterpret_cast<uint64_t*>(a->at(o_sel));
   a->mail.rowh = reinterpret_cast<uint32_t*>(a->at(o_rowh));
   a->mail.cdone = reinterpret_cast<uint64_t*>(a->at(o_cdone));

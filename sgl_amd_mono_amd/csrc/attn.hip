@@ -67,7 +67,6 @@ struct ScoreLds {
 
 struct TopkLds {
   int32_t pt[TOPK / PAGE];  // a short row's page table
-  uint32_t key[KPM];        // this member's keys, position order
   uint32_t hist[256];       // this member's digit histogram
   uint32_t tot[256];        // the team's
   uint32_t pre[256];        // the members' before this one
@@ -334,7 +333,8 @@ class Step {
       const int pos = o.k0 + 64 * i + 16 * g + r;
       kl[i] = live && pos < o.n;
       if (kl[i]) {
-        mb_putf(&A.mail.score[(size_t)o.s * A.mail.max_ctx + pos], sc[i], gd.tag);
+        __hip_atomic_store(&A.mail.score[(size_t)o.s * A.mail.max_ctx + pos], __float_as_uint(sc[i]), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
         if (A.scores) A.scores[(size_t)o.s * A.mail.max_ctx + pos] = sc[i];
       }
     }
@@ -516,35 +516,24 @@ class Step {
     const int cnt = min(max(n - p0, 0), KPT);
     const int page = cnt > 0 ? page_of(s, p0) : 0;  // a thread's keys share one page
     bool ok = true;
-    // thread c < (scored chunks) waits for chunk c's counts in the row histogram,
-    // threads 256.. poll the member's scores (coalesced) -> LDS keys
+    // thread c < (scored chunks) waits for chunk c's scores and counts (done word)
     if (tid < (n + CHUNK - 1) / CHUNK) {
       uint32_t v;
       ok = poll_word(&A.mail.cdone[(size_t)s * CH + tid], v, W_SCORE, gd);
-    } else if (tid >= 256) {
-      constexpr int NW = KPM / (AT - 256);
-      const int i0 = tid - 256;
-      uint32_t v[NW], pend = 0;
-#pragma unroll
-      for (int q = 0; q < NW; ++q) {
-        v[q] = 0u;
-        pend |= (m * KPM + i0 + 256 * q < n ? 1u : 0u) << q;
-      }
-      const uint64_t* base = &A.mail.score[(size_t)s * A.mail.max_ctx + m * KPM + i0];
-      const auto at = [base](int q) { return base + 256 * q; };
-      ok = poll_words<NW, decltype(at), false, false>(at, v, pend, W_SCORE, gd);
-#pragma unroll
-      for (int q = 0; q < NW; ++q) K.key[i0 + 256 * q] = radix_key(__uint_as_float(v[q]));
     }
     if (!block_all(ok)) return false;
-    if (tid < 256) K.tot[tid] = ld_agent_u32(&row_hist(gd.tag, s)[tid]);
+    // then a thread's KPT consecutive scores: one 16-byte device-coherent load (the
+    // buffer reads zeros past the row), and the row histogram
     uint32_t key[KPT];
     {
-      static_assert(KPT == 4, "a thread's keys are one 16-byte LDS read");
-      const u32x4 k4 = *reinterpret_cast<const u32x4*>(&K.key[tid * KPT]);
+      static_assert(KPT == 4, "a thread's keys are one 16-byte load");
+      const __amdgpu_buffer_rsrc_t rs =
+          __builtin_amdgcn_make_buffer_rsrc(A.mail.score + (size_t)s * A.mail.max_ctx, 0, n * 4, BUF_DWORD3);
+      const u32x4 k4 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, p0 * 4, 0, SC1));
 #pragma unroll
-      for (int q = 0; q < KPT; ++q) key[q] = k4[q];
+      for (int q = 0; q < KPT; ++q) key[q] = radix_key(__uint_as_float(k4[q]));
     }
+    if (tid < 256) K.tot[tid] = ld_agent_u32(&row_hist(gd.tag, s)[tid]);
     __syncthreads();
     mark_waited();
     pick_digit(K, K.tot, TOPK, nullptr);

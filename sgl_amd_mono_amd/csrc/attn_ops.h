@@ -29,11 +29,12 @@ constexpr int ROWH = 256;       // words a row histogram
 
 // Mailboxes of one attention runtime (tagged 64-bit words, see sync.h).
 struct Mail {
-  uint64_t* score;  // [max_rows][max_ctx]           index scores, f32
+  uint32_t* score;  // [max_rows][max_ctx]           index scores, f32 (untagged; read after cdone)
   uint64_t* sel;    // [max_rows][TOPK]               selected slots, i32
   uint32_t* rowh;   // [2][max_rows][ROWH]           leading-digit histogram of a row's scores
                     //                                 (untagged counts; launch parity tag & 1)
-  uint64_t* cdone;  // [max_rows][max_ctx / CHUNK]   a score chunk's counts are in rowh
+  uint64_t* cdone;  // [max_rows][max_ctx / CHUNK]   a score chunk's scores are stored and
+                    //                                 its counts are in rowh
   uint64_t* hist;   // [max_rows][PASSES][TEAM][HW]   a team member's digit histogram, packed
   uint64_t* cand;   // [max_rows][CMAX]               threshold candidates (low key bits, position)
   uint64_t* cnt;    // [max_rows][TEAM][2]            a member's keys above / at the threshold
