@@ -56,6 +56,7 @@ constexpr int KB = H / 128;          // 128-k blocks of a hidden row
 constexpr int IB = I / 128;          // 128-k blocks of a mid row
 constexpr int NT = I / 16;           // up tiles a slot
 constexpr int UP_KBW = KB / FW;      // k blocks a wave of an up tile
+constexpr int UP_H0 = 4;             // of them in an up tile's first half (W[0..7]); the rest W[8..13]
 constexpr int RK = 14;               // router K slices
 constexpr int RKW = H / RK / FW;     // k a wave of a router task
 constexpr int RSTEP = RKW / 32;      // bf16 MFMA steps a wave of a router task
@@ -132,7 +133,6 @@ class Step {
     r = lane % 16;
     G = gridDim.x;
     S = a.rows;
-    plan_ready = false;
   }
 
   MONO_DEV void run() {
@@ -168,8 +168,8 @@ class Step {
   Lds& L;
   Guard gd;
   int tid, lane, wave, g, r, G, S;
-  bool plan_ready;
   i32x8 W[14];  // weights of the next task: an up tile (14) or a down task (8)
+  float SC[2 * UP_KBW];  // an up tile's block scales (gate, up a k block), read with each half
 
   // ---------------------------------------------------------------- norm
   MONO_DEV void norm_stats() {
@@ -316,18 +316,11 @@ class Step {
   }
 
   // ---------------------------------------------------------------- plan
-  MONO_DEV bool load_plan() {
-    if (!build_plan<E, TOPK, FT>(L.plan, A.mail.rsel, S, W_PICKS, gd)) return false;
-    plan_ready = true;
-    return true;
-  }
+  MONO_DEV bool load_plan() { return build_plan<E, TOPK, FT>(L.plan, A.mail.rsel, S, W_PICKS, gd); }
 
   // ---------------------------------------------------------------- task list
-  // kind of task T (loads the plan first when T needs it); K_NONE past the list
-  MONO_DEV int classify(int T, bool& ok) {
-    ok = true;
-    if (T < NT) return K_UP;  // the shared expert's tiles need no plan
-    if (!plan_ready && !(ok = load_plan())) return K_NONE;
+  // kind of task T (the plan is loaded); K_NONE past the list
+  MONO_DEV int classify(int T) const {
     const int n_up = L.plan.n_act * NT, n_dn = L.plan.n_act * DN_GROUPS;
     if (T < n_up) return K_UP;
     if (T < n_up + n_dn) return K_DOWN;
@@ -340,15 +333,8 @@ class Step {
   MONO_DEV void load_task(int kind, int T) {
     const i32x8 zero = {};
     if (kind == K_UP) {
-      const int d = T / NT, c = T % NT;
-      const int e = d == 0 ? E : L.plan.expert[d];
-      const uint8_t* wb = A.w13 + (size_t)e * (2 * I) * H;
-#pragma unroll
-      for (int j = 0; j < UP_KBW; ++j) {
-        const int kb = wave * UP_KBW + j;
-        W[2 * j] = ld_shuf(wb, H / 32, c, kb, g, r);            // gate rows 16c..
-        W[2 * j + 1] = ld_shuf(wb, H / 32, NT + c, kb, g, r);   // up rows I + 16c..
-      }
+      load_up<0>(T);
+      load_up<1>(T);
     } else if (kind == K_DOWN) {
       const int j = T - L.plan.n_act * NT;
       const int d = j / DN_GROUPS, grp = j % DN_GROUPS;
@@ -370,20 +356,46 @@ class Step {
   // task's weight loads, then publish the task's results while those loads fly.
   MONO_DEV void tasks() {
     int T = blockIdx.x;
-    bool ok;
-    int kind = classify(T, ok);
-    if (!ok) return;
-    load_task(kind, T);
+    // a shared-expert tile needs no plan: its loads go out before the plan is read
+    if (T < NT) load_task(K_UP, T);
+    if (!load_plan()) return;
+    int kind = classify(T);
+    if (T >= NT) load_task(kind, T);
+    // consecutive up tiles, half by half: the next tile's first half goes out once this
+    // tile's first half is consumed, its second half once this second half is, so one
+    // half is always streaming while the other computes (vector memory returns in
+    // order: consuming a half waits only for loads issued before it)
+    while (kind == K_UP) {
+      f32x4 ag = {0.f, 0.f, 0.f, 0.f}, au = ag;
+      const int T2 = T + G;
+      up_half<0>(ag, au);
+      const int kind2 = classify(T2);
+      if (kind2 != K_UP) {
+        up_half<1>(ag, au);
+        load_task(kind2, T2);
+        up_publish(T, ag, au);
+        T = T2;
+        kind = kind2;
+        break;
+      }
+      load_up<0>(T2);
+      up_half<1>(ag, au);
+      load_up<1>(T2);
+      up_publish(T, ag, au);
+      T = T2;
+    }
     while (kind != K_NONE) {
       f32x4 acc[2];
-      if (kind == K_UP) {
-        up_compute(T, acc[0], acc[1]);
-      } else if (kind == K_DOWN) {
+      if (kind == K_DOWN) {
         if (!down_compute(T, acc)) return;
+      } else if (kind == K_UP) {
+        acc[0] = f32x4{0.f, 0.f, 0.f, 0.f};
+        acc[1] = acc[0];
+        up_half<0>(acc[0], acc[1]);
+        up_half<1>(acc[0], acc[1]);
       }
       const int T2 = T + G;
-      const int kind2 = classify(T2, ok);
-      if (!ok) return;
+      const int kind2 = classify(T2);
       load_task(kind2, T2);
       if (kind == K_UP) {
         up_publish(T, acc[0], acc[1]);
@@ -398,23 +410,44 @@ class Step {
   }
 
   // ---------------------------------------------------------------- up
-  MONO_DEV void up_compute(int T, f32x4& ag, f32x4& au) {
+  // Half HALF of up tile T (the wave's k blocks 0..3 or 4..6) into W, its block scales
+  // into SC first.
+  template <int HALF>
+  MONO_DEV void load_up(int T) {
+    constexpr int J0 = HALF == 0 ? 0 : UP_H0, J1 = HALF == 0 ? UP_H0 : UP_KBW;
     const int d = T / NT, c = T % NT;
-    const int e = d == 0 ? E : L.plan.expert[d];
-    const float* sg = A.s13 + ((size_t)e * (2 * I / 128) + c / 8) * KB;
-    const float* su = A.s13 + ((size_t)e * (2 * I / 128) + I / 128 + c / 8) * KB;
-    ag = f32x4{0.f, 0.f, 0.f, 0.f};
-    au = ag;
+    const int e = __builtin_amdgcn_readfirstlane(d == 0 ? E : L.plan.expert[d]);
+    {  // the half's scales: scalar loads (one value a wave), apart from the vector queue
+      const int wv = __builtin_amdgcn_readfirstlane(wave);
+      const float* sg = A.s13 + ((size_t)e * (2 * I / 128) + c / 8) * KB + wv * UP_KBW;
 #pragma unroll
-    for (int j = 0; j < UP_KBW; ++j) {
+      for (int j = J0; j < J1; ++j) {
+        SC[2 * j] = sg[j];
+        SC[2 * j + 1] = sg[(I / 128) * KB + j];
+      }
+    }
+    const uint8_t* wb = A.w13 + (size_t)e * (2 * I) * H;
+#pragma unroll
+    for (int j = J0; j < J1; ++j) {
+      const int kb = wave * UP_KBW + j;
+      W[2 * j] = ld_shuf(wb, H / 32, c, kb, g, r);
+      W[2 * j + 1] = ld_shuf(wb, H / 32, NT + c, kb, g, r);
+    }
+  }
+  // Half HALF of the up tile in W: FP8 x FP8 MFMA, block scale x activation scale.
+  template <int HALF>
+  MONO_DEV void up_half(f32x4& ag, f32x4& au) {
+    constexpr int J0 = HALF == 0 ? 0 : UP_H0, J1 = HALF == 0 ? UP_H0 : UP_KBW;
+#pragma unroll
+    for (int j = J0; j < J1; ++j) {
       const int kb = wave * UP_KBW + j;
       const i32x8 b = lds32(&L.xq[r][kb * 128 + g * 32]);
       const float xsj = L.xs[r][kb];
       const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
       const f32x4 cg = mfma_fp8(W[2 * j], b, zero);
       const f32x4 cu = mfma_fp8(W[2 * j + 1], b, zero);
-      ag += cg * (sg[kb] * xsj);
-      au += cu * (su[kb] * xsj);
+      ag += cg * (SC[2 * j] * xsj);
+      au += cu * (SC[2 * j + 1] * xsj);
     }
   }
 
