@@ -120,18 +120,20 @@ MONO_DEV bool build_plan(PlanLds<E, TOPK>& P, const uint64_t* rsel, int S, int s
     P.n_act = n;
   }
   __syncthreads();
-  if (tid < S) {  // a row's slots, ascending: insertion into the LDS row itself
-    int32_t* sl = P.rowslot[tid];
-    sl[0] = 0;
-    for (int k = 0; k < TOPK; ++k) {
-      const int d = P.dmap[P.pick_id[tid][k]];
-      int j = k + 1;
-      while (j > 1 && sl[j - 1] > d) {
-        sl[j] = sl[j - 1];
-        --j;
-      }
-      sl[j] = d;
-    }
+  // a row's slots, ascending: thread (s, k) places pick k's slot at its rank among the
+  // row's picks (equal slots ranked by k, so every place of the row is written once)
+  static_assert(THREADS >= MAX_ROWS * TOPK, "one thread a pick");
+  if (tid < S * TOPK) {
+    const int s = tid / TOPK, k = tid % TOPK;
+    int dd[TOPK];
+#pragma unroll
+    for (int k2 = 0; k2 < TOPK; ++k2) dd[k2] = P.dmap[P.pick_id[s][k2]];
+    const int d = dd[k];
+    int rank = 0;
+#pragma unroll
+    for (int k2 = 0; k2 < TOPK; ++k2) rank += (dd[k2] < d || (dd[k2] == d && k2 < k)) ? 1 : 0;
+    P.rowslot[s][1 + rank] = d;
+    if (k == 0) P.rowslot[s][0] = 0;
   }
   __syncthreads();
   return true;

@@ -9,7 +9,8 @@
 //
 // Work, in the order each workgroup walks it:
 //   ticket   one atomic add a workgroup -> the launch's tag (sync.h)
-//   norm     every workgroup: the RMSNorm statistics of all rows (kernel.py:1367-1415)
+//   norm     every workgroup: the RMSNorm statistics of all rows (kernel.py:1367-1415);
+//            wave w keeps row w in registers for xq
 //   router   task t < 16 * RK on workgroup t: 16 experts x a 512-wide K slice of the
 //            bf16 router GEMV on the bf16-rounded normed rows (MFMA 16x16x32 bf16)
 //            -> partial logits (mailbox rlog)
@@ -17,7 +18,8 @@
 //            the f32 bits of (score + bias) with lowest-id ties, weights = score / sum
 //            x route_scale (kernel.py:1575-1629) -> the row's picks (mailbox rsel)
 //   xq       every workgroup: per-128 FP8 quantisation of the normed rows into LDS
-//            (amax / 448 with a hardware reciprocal, kernel.py:1440-1450)
+//            (amax / 448 with a hardware reciprocal, kernel.py:1440-1450), after the
+//            router and route so that neither waits for it
 //   plan     every workgroup, before its first routed tile: the distinct experts of
 //            the step; slot 0 is the shared expert (weight 1), slots 1.. the picked
 //            experts by ascending id
@@ -66,6 +68,7 @@ constexpr int DN_GROUPS = H / DN_ROWS;
 constexpr int FIN_ROWS = 32;
 constexpr int FIN_TASKS = H / FIN_ROWS;
 constexpr int NSLOT = TOPK + 1;      // slots a row uses: the shared expert and its picks
+constexpr int PER_ROW = H / (8 * WAVE);  // 16-byte loads a lane makes of a hidden row
 static_assert(KB % FW == 0 && RKW % 32 == 0 && H % (RK * FW) == 0, "tiling");
 static_assert(UP_KBW * 2 <= 14 && 2 * IB <= 14, "weight registers");
 static_assert(FT == MAX_ROWS * (I / 16), "a down task's thread owns 16 mid channels of one row");
@@ -152,13 +155,14 @@ class Step {
     gd.tag = L.tag;
     gd.deadline = now_ticks() + A.guard.deadline_ticks;
 
-    norm_stats();
+    u32x4 ar[PER_ROW];  // wave w's row w, kept for the quantisation
+    norm_stats(ar);
     __syncthreads();
     if (rt < ROUTER_TASKS) router(rt, wr);
     if ((int)blockIdx.x >= G - S) {
       if (!route(G - 1 - (int)blockIdx.x)) return;
     }
-    quant_rows();
+    quant_rows(ar);
     __syncthreads();
     tasks();
   }
@@ -172,22 +176,33 @@ class Step {
   float SC[2 * UP_KBW];  // an up tile's block scales (gate, up a k block), read with each half
 
   // ---------------------------------------------------------------- norm
-  MONO_DEV void norm_stats() {
-    for (int s = wave; s < S; s += FW) {
-      const uint16_t* row = A.a + (size_t)s * H;
-      float ss = 0.f;
+  // Wave w reads row w (lane: 8 consecutive k of each 512) into registers, which it
+  // keeps for the quantisation; row w + 8 is read for its statistics.
+  MONO_DEV void norm_stats(u32x4 (&ar)[PER_ROW]) {
+    const uint16_t* row0 = A.a + (size_t)min(wave, S - 1) * H;
 #pragma unroll
-      for (int j = 0; j < H / 8 / WAVE; ++j) {
-        const u32x4 w = ld_u32x4(row + (j * WAVE + lane) * 8);
+    for (int j = 0; j < PER_ROW; ++j) ar[j] = ld_u32x4(row0 + (j * WAVE + lane) * 8);
+    if (wave + FW < S) {
+      u32x4 w[PER_ROW];
+      const uint16_t* row = A.a + (size_t)(wave + FW) * H;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const float lo = bf16_lo(w[q]), hi = bf16_hi(w[q]);
-          ss += lo * lo + hi * hi;
-        }
-      }
-      ss = wave_sum(ss);
-      if (lane == 0) L.rstd[s] = hw_rsq(ss * (1.0f / H) + A.eps);
+      for (int j = 0; j < PER_ROW; ++j) w[j] = ld_u32x4(row + (j * WAVE + lane) * 8);
+      row_rstd(wave + FW, w);
     }
+    if (wave < S) row_rstd(wave, ar);
+  }
+
+  MONO_DEV void row_rstd(int s, const u32x4 (&w)[PER_ROW]) {
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < PER_ROW; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float lo = bf16_lo(w[j][q]), hi = bf16_hi(w[j][q]);
+        ss += lo * lo + hi * hi;
+      }
+    ss = wave_sum(ss);
+    if (lane == 0) L.rstd[s] = hw_rsq(ss * (1.0f / H) + A.eps);
   }
 
   // ---------------------------------------------------------------- router
@@ -269,49 +284,55 @@ class Step {
   }
 
   // ---------------------------------------------------------------- xq
-  // Lane quantises 8 consecutive k of a row; 16 lanes make a 128-block.
-  MONO_DEV void quant_rows() {
-    constexpr int PER_ROW = H / (8 * WAVE);  // wave passes a row
-    constexpr int QU = 4;                    // passes a wave has in flight
-    const int npass = S * PER_ROW;
-    for (int p0 = wave; p0 < npass; p0 += FW * QU) {
-      u32x4 av[QU], gv[QU];
+  // Lane quantises 8 consecutive k of a row; 16 lanes make a 128-block. Row w comes
+  // from the registers the norm filled; row w + 8 is read again.
+  MONO_DEV void quant_rows(u32x4 (&ar)[PER_ROW]) {
+    static_assert(MAX_ROWS <= 2 * FW, "two rows a wave at most");
+    u32x4 gr[PER_ROW];
 #pragma unroll
-      for (int u = 0; u < QU; ++u) {  // unconditional (clamped) loads: no serialising joins
-        const int p = min(p0 + u * FW, npass - 1);
-        const int s = p / PER_ROW, k = ((p % PER_ROW) * WAVE + lane) * 8;
-        av[u] = ld_u32x4(A.a + (size_t)s * H + k);
-        gv[u] = ld_u32x4(A.g_post + k);
+    for (int j = 0; j < PER_ROW; ++j) gr[j] = ld_u32x4(A.g_post + (j * WAVE + lane) * 8);
+    if (wave < S) quant_row(wave, ar, gr);
+    if (wave + FW < S) {
+      const uint16_t* row = A.a + (size_t)(wave + FW) * H;
+#pragma unroll
+      for (int j = 0; j < PER_ROW; ++j) {
+        ar[j] = ld_u32x4(row + (j * WAVE + lane) * 8);
+        // gamma's bf16 -> f32 unpacking is redone for this row: shared with the first
+        // row it would hold twice gamma's registers
+        asm volatile("" : "+v"(gr[j]));
       }
+      quant_row(wave + FW, ar, gr);
+    }
+  }
+
+  MONO_DEV void quant_row(int s, const u32x4 (&av)[PER_ROW], const u32x4 (&gv)[PER_ROW]) {
+    const float rj = L.rstd[s];
 #pragma unroll
-      for (int u = 0; u < QU; ++u) {
-        const int p = p0 + u * FW;
-        if (p >= npass) continue;  // wave-uniform
-        const int s = p / PER_ROW, k = ((p % PER_ROW) * WAVE + lane) * 8;
-        const float rj = L.rstd[s];
-        float x[8];
+    for (int j = 0; j < PER_ROW; ++j) {
+      const int k = (j * WAVE + lane) * 8;
+      float x[8];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          x[2 * q] = bf16_lo(av[u][q]) * rj * bf16_lo(gv[u][q]);
-          x[2 * q + 1] = bf16_hi(av[u][q]) * rj * bf16_hi(gv[u][q]);
-        }
-        float m = 0.f;
-#pragma unroll
-        for (int q = 0; q < 8; ++q) m = fmaxf(m, fabsf(x[q]));
-        const float amax = group_max<16>(m);
-        const bool nz = amax > 0.f;
-        const float inv = nz ? hw_rcp(amax) * FP8_MAX : 1.0f;
-        u32x2 packed;
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          float q4[4];
-#pragma unroll
-          for (int q = 0; q < 4; ++q) q4[q] = fminf(fmaxf(x[4 * h + q] * inv, -FP8_MAX), FP8_MAX);
-          packed[h] = fp8x4_pack(q4[0], q4[1], q4[2], q4[3]);
-        }
-        *reinterpret_cast<u32x2*>(&L.xq[s][k]) = packed;
-        if ((lane % 16) == 0) L.xs[s][k / 128] = nz ? amax * (1.0f / FP8_MAX) : 1.0f;
+      for (int q = 0; q < 4; ++q) {
+        x[2 * q] = bf16_lo(av[j][q]) * rj * bf16_lo(gv[j][q]);
+        x[2 * q + 1] = bf16_hi(av[j][q]) * rj * bf16_hi(gv[j][q]);
       }
+      float m = 0.f;
+#pragma unroll
+      for (int q = 0; q < 8; ++q) m = fmaxf(m, fabsf(x[q]));
+      const float amax = group_max<16>(m);
+      const bool nz = amax > 0.f;
+      const float inv = nz ? hw_rcp(amax) * FP8_MAX : 1.0f;
+      u32x2 packed;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        float q4[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) q4[q] = fminf(fmaxf(x[4 * h + q] * inv, -FP8_MAX), FP8_MAX);
+        packed[h] = fp8x4_pack(q4[0], q4[1], q4[2], q4[3]);
+      }
+      *reinterpret_cast<u32x2*>(&L.xq[s][k]) = packed;
+      if ((lane % 16) == 0) L.xs[s][k / 128] = nz ? amax * (1.0f / FP8_MAX) : 1.0f;
+      __builtin_amdgcn_sched_barrier(0);  // one chunk at a time: no interleaved live ranges
     }
   }
 
