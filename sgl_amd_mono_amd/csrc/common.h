@@ -180,6 +180,11 @@ MONO_DEV u32x4 ld_nt_u32x4(const void* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
 }
 MONO_DEV u32x4 ld_u32x4(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+// Data no launch writes (weights and their scales) read at a wave-uniform address
+// through the constant address space: a scalar load into SGPRs, outside the in-order
+// vector memory queue.
+typedef const __attribute__((address_space(4))) float const_f32;
+MONO_DEV float ld_const_f32(const float* p) { return *(const_f32*)p; }
 // 32 bytes (two dwordx4) straight into one MFMA operand tuple
 MONO_DEV i32x8 ld_nt_i32x8(const void* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const i32x8*>(p));

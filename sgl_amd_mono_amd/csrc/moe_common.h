@@ -146,8 +146,10 @@ MONO_DEV float route_weight(const PlanLds<E, TOPK>& P, int d, int s) {
   const int e = P.expert[d];
   float w = 0.f;
 #pragma unroll
-  for (int k = 0; k < TOPK; ++k)
-    if (P.pick_id[s][k] == e) w = P.pick_w[s][k];
+  for (int k = 0; k < TOPK; ++k) {  // unconditional reads: no branch a pick
+    const float wk = P.pick_w[s][k];
+    w = P.pick_id[s][k] == e ? wk : w;
+  }
   return w;
 }
 

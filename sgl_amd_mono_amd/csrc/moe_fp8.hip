@@ -63,15 +63,17 @@ constexpr int RK = 14;               // router K slices
 constexpr int RKW = H / RK / FW;     // k a wave of a router task
 constexpr int RSTEP = RKW / 32;      // bf16 MFMA steps a wave of a router task
 constexpr int ROUTER_TASKS = (E / 16) * RK;
-constexpr int DN_ROWS = 256;         // output rows of a down task (8 waves x 2 tiles)
+constexpr int DN_ROWS = 448;         // output rows of a down task: 28 16-row tiles x 4 k blocks
 constexpr int DN_GROUPS = H / DN_ROWS;
+constexpr int DN_PAIR = DN_ROWS / 16 / (FW / 2);  // row tiles of a wave pair
 constexpr int FIN_ROWS = 32;
 constexpr int FIN_TASKS = H / FIN_ROWS;
 constexpr int NSLOT = TOPK + 1;      // slots a row uses: the shared expert and its picks
 constexpr int PER_ROW = H / (8 * WAVE);  // 16-byte loads a lane makes of a hidden row
 static_assert(KB % FW == 0 && RKW % 32 == 0 && H % (RK * FW) == 0, "tiling");
-static_assert(UP_KBW * 2 <= 14 && 2 * IB <= 14, "weight registers");
-static_assert(FT == MAX_ROWS * (I / 16), "a down task's thread owns 16 mid channels of one row");
+static_assert(UP_KBW * 2 == 14 && DN_PAIR * IB == 2 * 14 && H % DN_ROWS == 0, "14 weight tiles a wave");
+static_assert(IB == 4 && DN_PAIR == 7, "a wave pair's row tiles: 3 whole and half of one each");
+static_assert(I == 8 * WAVE && MAX_ROWS <= 2 * FW, "a down task's wave reads one or two mid rows, 8 channels a lane");
 static_assert(MAX_ROWS * FIN_ROWS <= FT, "a final task's thread owns one (row, output)");
 
 // wait sites (guard error word = site + 1)
@@ -357,16 +359,7 @@ class Step {
       load_up<0>(T);
       load_up<1>(T);
     } else if (kind == K_DOWN) {
-      const int j = T - L.plan.n_act * NT;
-      const int d = j / DN_GROUPS, grp = j % DN_GROUPS;
-      const uint8_t* wb = A.w2 + (size_t)L.plan.expert[d] * H * I;
-      const int rg0 = (grp * DN_ROWS + wave * 32) / 16;
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int kb = 0; kb < IB; ++kb) W[t * IB + kb] = ld_shuf(wb, I / 32, rg0 + t, kb, g, r);
-#pragma unroll
-      for (int q = 2 * IB; q < 14; ++q) W[q] = zero;
+      load_down(T);
     } else {
 #pragma unroll
       for (int q = 0; q < 14; ++q) W[q] = zero;
@@ -406,7 +399,7 @@ class Step {
       T = T2;
     }
     while (kind != K_NONE) {
-      f32x4 acc[2];
+      f32x4 acc[4];
       if (kind == K_DOWN) {
         if (!down_compute(T, acc)) return;
       } else if (kind == K_UP) {
@@ -443,8 +436,8 @@ class Step {
       const float* sg = A.s13 + ((size_t)e * (2 * I / 128) + c / 8) * KB + wv * UP_KBW;
 #pragma unroll
       for (int j = J0; j < J1; ++j) {
-        SC[2 * j] = sg[j];
-        SC[2 * j + 1] = sg[(I / 128) * KB + j];
+        SC[2 * j] = ld_const_f32(sg + j);
+        SC[2 * j + 1] = ld_const_f32(sg + (I / 128) * KB + j);
       }
     }
     const uint8_t* wb = A.w13 + (size_t)e * (2 * I) * H;
@@ -493,69 +486,111 @@ class Step {
   }
 
   // ---------------------------------------------------------------- down
-  MONO_DEV bool down_compute(int T, f32x4 (&acc)[2]) {
-    const int j = T - L.plan.n_act * NT;
+  // A down task (slot d, group grp) makes output rows grp * 448 .. + 448: 28 row tiles
+  // of 16 x 4 128-k blocks = 112 weight tiles, 14 a wave. Wave pair p owns row tiles
+  // 7p .. 7p + 6, i.e. tiles n = 0..27 of the pair in (row tile, k block) order: wave 2p
+  // holds n = 0..13 (row tiles 0-2 whole, k blocks 0-1 of row tile 3), wave 2p + 1
+  // n = 14..27; row tile 3's two halves meet in LDS.
+  MONO_DEV void load_down(int T) {
+    const int j = __builtin_amdgcn_readfirstlane(T - L.plan.n_act * NT);
     const int d = j / DN_GROUPS, grp = j % DN_GROUPS;
-    const int e = L.plan.expert[d];
+    const int e = __builtin_amdgcn_readfirstlane(L.plan.expert[d]);
+    const int wv = __builtin_amdgcn_readfirstlane(wave);
+    const int n0 = (wv & 1) * 14, rt0 = grp * (DN_ROWS / 16) + (wv >> 1) * DN_PAIR;
+    {  // block scales: scalar loads, apart from the vector queue
+      const float* sb = A.s2 + (size_t)e * (H / 128) * IB;
+#pragma unroll
+      for (int i = 0; i < 14; ++i) {
+        const int n = n0 + i, rt = rt0 + n / IB;
+        SC[i] = ld_const_f32(sb + (rt / 8) * IB + n % IB);
+      }
+    }
+    const uint8_t* wb = A.w2 + (size_t)e * H * I;
+#pragma unroll
+    for (int i = 0; i < 14; ++i) {
+      const int n = n0 + i;
+      W[i] = ld_shuf(wb, I / 32, rt0 + n / IB, n % IB, g, r);
+    }
+  }
+
+  MONO_DEV bool down_compute(int T, f32x4 (&acc)[4]) {
+    const int j = T - L.plan.n_act * NT;
+    const int d = j / DN_GROUPS;
     const uint32_t mask = L.plan.rowmask[d];
-    // thread (row s, 16-channel group cg) polls its 16 contiguous mid words; 8 groups
-    // (8 consecutive lanes) make a 128-channel quantisation block
-    constexpr int CG = 16;
-    const int s = tid / (I / CG), cg = tid % (I / CG);
-    const bool in = s < MAX_ROWS && ((mask >> s) & 1u);
-    const uint64_t* base = &A.mail.mid[((size_t)d * MAX_ROWS + (in ? s : 0)) * I + cg * CG];
-    uint32_t v[CG];
-    const bool ok = poll_words<CG>([base](int q) { return base + q; }, v, in ? 0xffffu : 0u, W_MID, gd);
-    if (!block_all(ok)) return false;
-    float m = 0.f;
+    // wave w polls row w's mid (then row w + 8 when S > 8), lane l its 8 contiguous
+    // channels 8l .. 8l + 7; 16 lanes make a 128-channel quantisation block
+    constexpr int CG = I / WAVE;
+    bool ok = true;
+    for (int s = wave; s < S; s += FW) {  // wave-uniform trip count
+      const bool in = (mask >> s) & 1u;
+      const uint64_t* base = &A.mail.mid[((size_t)d * MAX_ROWS + s) * I + lane * CG];
+      uint32_t v[CG];
 #pragma unroll
-    for (int q = 0; q < CG; ++q) m = fmaxf(m, in ? fabsf(__uint_as_float(v[q])) : 0.f);
-    const float am = group_max<128 / CG>(m);
-    const bool nz = am > 0.f;
-    const float inv = nz ? hw_rcp(am) * FP8_MAX : 1.0f;
-    if (s < MAX_ROWS) {
-      u32x4 packed;
+      for (int q = 0; q < CG; ++q) v[q] = 0u;
+      ok = poll_words<CG>([base](int q) { return base + q; }, v, in ? (1u << CG) - 1u : 0u, W_MID, gd) && ok;
+      float m = 0.f;
 #pragma unroll
-      for (int h = 0; h < 4; ++h) {
+      for (int q = 0; q < CG; ++q) m = fmaxf(m, fabsf(__uint_as_float(v[q])));
+      const float am = group_max<128 / CG>(m);
+      const bool nz = am > 0.f;
+      const float inv = nz ? hw_rcp(am) * FP8_MAX : 1.0f;
+      u32x2 packed;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
         float q4[4];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) q4[q] = in ? fminf(fmaxf(__uint_as_float(v[4 * h + q]) * inv, -FP8_MAX), FP8_MAX) : 0.f;
+        for (int q = 0; q < 4; ++q) q4[q] = fminf(fmaxf(__uint_as_float(v[4 * h + q]) * inv, -FP8_MAX), FP8_MAX);
         packed[h] = fp8x4_pack(q4[0], q4[1], q4[2], q4[3]);
       }
-      *reinterpret_cast<u32x4*>(&L.bq[s][cg * CG]) = packed;
-      if ((cg % (128 / CG)) == 0)
-        L.coef[s][cg / (128 / CG)] = in ? (nz ? am * (1.0f / FP8_MAX) : 1.0f) * route_weight(L.plan, d, s) : 0.f;
+      *reinterpret_cast<u32x2*>(&L.bq[s][lane * CG]) = packed;
+      if ((lane % (128 / CG)) == 0)
+        L.coef[s][lane / (128 / CG)] = in ? (nz ? am * (1.0f / FP8_MAX) : 1.0f) * route_weight(L.plan, d, s) : 0.f;
     }
-    __syncthreads();
-    const float* ws = A.s2 + ((size_t)e * (H / 128) + (grp * DN_ROWS + wave * 32) / 128) * IB;
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int kb = 0; kb < IB; ++kb) {
-        const i32x8 bb = lds32(&L.bq[r][kb * 128 + g * 32]);
-        const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-        const f32x4 c = mfma_fp8(W[t * IB + kb], bb, zero);
-        acc[t] += c * (ws[kb] * L.coef[r][kb]);
-      }
-    }
+    if (!block_all(ok)) return false;
+    if (__builtin_amdgcn_readfirstlane(wave) & 1)
+      down_mfma<1>(acc);
+    else
+      down_mfma<0>(acc);
     return true;
   }
 
-  MONO_DEV void down_publish(int T, const f32x4 (&acc)[2]) {
+  // acc[a]: the wave's a-th row tile (pair row tile a + 3 ODD)
+  template <int ODD>
+  MONO_DEV void down_mfma(f32x4 (&acc)[4]) {
+#pragma unroll
+    for (int a = 0; a < 4; ++a) acc[a] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < 14; ++i) {
+      const int n = ODD * 14 + i, a = n / IB - 3 * ODD, kb = n % IB;
+      const i32x8 bb = lds32(&L.bq[r][kb * 128 + g * 32]);
+      const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+      const f32x4 c = mfma_fp8(W[i], bb, zero);
+      acc[a] += c * (SC[i] * L.coef[r][kb]);
+    }
+  }
+
+  MONO_DEV void down_publish(int T, f32x4 (&acc)[4]) {
     const int j = T - L.plan.n_act * NT;
     const int d = j / DN_GROUPS, grp = j % DN_GROUPS;
     const uint32_t mask = L.plan.rowmask[d];
+    const int wv = __builtin_amdgcn_readfirstlane(wave);
+    const int odd = wv & 1, rt0 = grp * (DN_ROWS / 16) + (wv >> 1) * DN_PAIR;
+    // the pair's row tile 3: the odd wave's k blocks 2-3 join the even wave's 0-1
+    if (odd) L.red[0][wv][lane] = acc[0];
+    __syncthreads();
+    if (!odd) acc[3] += L.red[0][wv + 1][lane];
     if ((mask >> r) & 1u) {
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
+      for (int a = 0; a < 4; ++a) {
+        if (odd && a == 0) continue;  // wave-uniform
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const int h = grp * DN_ROWS + wave * 32 + t * 16 + 4 * g + i;
-          mb_putf(&A.mail.ypart[((size_t)d * MAX_ROWS + r) * H + h], acc[t][i], gd.tag);
+          const int h = (rt0 + a + 3 * odd) * 16 + 4 * g + i;
+          mb_putf(&A.mail.ypart[((size_t)d * MAX_ROWS + r) * H + h], acc[a][i], gd.tag);
         }
+      }
     }
-    __syncthreads();  // the next down task rewrites bq / coef / amax
+    __syncthreads();  // the next down task rewrites bq / coef / red
   }
 
   // ---------------------------------------------------------------- final
