@@ -457,6 +457,9 @@ extern "C" int mono_proj_create(const mono_proj_config* cfg, mono_proj** out) {
   const size_t o_guard = cv.take(mono::G_WORDS * 4);
   size_t o_mb[5];
   for (int i = 0; i < 5; ++i) o_mb[i] = cv.take(MAIL_WORDS[i] * 8);
+  const size_t o_odone = cv.take((size_t)mono::proj::HEADS * 8);
+  const size_t o_xn = cv.take((size_t)mono::proj::MAX_ROWS * mono::proj::HIDDEN * 2);
+  const size_t o_xdone = cv.take((size_t)mono::proj::MAX_ROWS * 8);
   mono_proj* p = new mono_proj();
   p->magic = PROJ_MAGIC;
   p->cfg = c;
@@ -470,7 +473,10 @@ extern "C" int mono_proj_create(const mono_proj_config* cfg, mono_proj** out) {
   p->mail.qan = reinterpret_cast<uint64_t*>(p->at(o_mb[1]));
   p->mail.qnope = reinterpret_cast<uint64_t*>(p->at(o_mb[2]));
   p->mail.iqraw = reinterpret_cast<uint64_t*>(p->at(o_mb[3]));
-  p->mail.ob = reinterpret_cast<uint64_t*>(p->at(o_mb[4]));
+  p->mail.ob = reinterpret_cast<uint32_t*>(p->at(o_mb[4]));
+  p->mail.odone = reinterpret_cast<uint64_t*>(p->at(o_odone));
+  p->mail.xn = reinterpret_cast<uint32_t*>(p->at(o_xn));
+  p->mail.xdone = reinterpret_cast<uint64_t*>(p->at(o_xdone));
   *out = p;
   return ok();
 }

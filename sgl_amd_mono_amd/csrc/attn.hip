@@ -54,8 +54,6 @@ constexpr int PB_STRIDE = SUB + 8;           // bf16 a probability row in LDS
 constexpr int KEYS_WAVE = CHUNK / AW;        // 128 keys a wave of a score task
 constexpr int KTILES = KEYS_WAVE / 16;
 constexpr float NEG_INF = -__builtin_huge_valf();
-constexpr int BUF_DWORD3 = 0x00020000;       // raw buffer resource word 3 (gfx9)
-constexpr int SC1 = 16;                      // buffer cache policy: device-coherent
 static_assert(KPM % AT == 0 && PAGE % KPT == 0 && TEAM <= 16 && KEYS_WAVE % PAGE == 0 && SPLIT % SUB == 0, "tiling");
 static_assert(AT == NH * DV / 32, "a merge task covers 2 heads");
 

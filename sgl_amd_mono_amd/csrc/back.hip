@@ -1,7 +1,7 @@
 // Back of the attention block on gfx950 as ONE persistent launch (one 512-thread
 // workgroup per CU, tasks dealt round-robin, tagged mailboxes between the stages):
 //   U  (head): o[:, h] = bf16(W_UV[h] o_lat[:, h]), 8 row groups of 16, one a wave,
-//      K = 512 in 4 steps -> mailbox ob (bf16 pairs)
+//      K = 512 in 4 steps -> ob (untagged bf16 pairs) and the head's done word
 //   O  (32-row tile) of W_o [7168, 4096]: 4 waves a row group, 8 128-k steps a wave,
 //      against o staged in LDS; a = bf16(h + W_o o)
 // (glm53/gfx950/kernel.py:3975-4197; the attention TP reduce there is the local
@@ -119,17 +119,16 @@ class Back {
     for (int j = 0; j < 4; ++j) acc += SC[j] * step_fp8(join(WR[2 * j], WR[2 * j + 1]), &L.u.xu[r][128 * j + 32 * g]);
     if (r < S) {
       const int v = h * VDIM + 16 * wave + 4 * g;  // output channel of o
-      const uint32_t w0 = pack_bf16x2(acc[0], acc[1]), w1 = pack_bf16x2(acc[2], acc[3]);
-      mb_put(&M.ob[(size_t)r * (O_K / 2) + v / 2], w0, gd.tag);
-      mb_put(&M.ob[(size_t)r * (O_K / 2) + v / 2 + 1], w1, gd.tag);
-      if (A.o) {
-        u32x2 o;
-        o[0] = w0;
-        o[1] = w1;
-        *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(A.o) + (size_t)r * O_K + v) = o;
-      }
+      u32x2 o;
+      o[0] = pack_bf16x2(acc[0], acc[1]);
+      o[1] = pack_bf16x2(acc[2], acc[3]);
+      __builtin_amdgcn_raw_buffer_store_b64(o, coherent_rsrc(M.ob, MAX_ROWS * (O_K / 2) * 4),
+                                            ((size_t)r * (O_K / 2) + v / 2) * 4, 0, SC1);
+      if (A.o) *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(A.o) + (size_t)r * O_K + v) = o;
     }
-    __syncthreads();  // the next task rewrites the LDS
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();  // the head's o is stored (and the next task rewrites the LDS)
+    if (tid == 0) mb_put(&M.odone[h], 0u, gd.tag);
   }
 
   MONO_DEV bool stage_o(int t) {
@@ -142,28 +141,20 @@ class Back {
       ld_fp8_tile(static_cast<const uint8_t*>(W.w_o), O_K / 32, rg, ks, g, r, WR[2 * j], WR[2 * j + 1]);
       SC[j] = W.s_o[(rg * 16 / 128) * (O_K / 128) + ks];
     }
-    // one hint word a head (W_UV task): its last pair of the last row
-    const uint64_t* oh = M.ob + (size_t)(S - 1) * (O_K / 2);
-    if (!hint_wait(HEADS, [oh](int i) { return oh + (size_t)i * (VDIM / 2) + VDIM / 2 - 1; }, W_OB, gd)) return false;
-    // o of every row: S x 2048 bf16 pairs, thread t words t + 512 q (coalesced), 4 rows a
-    // sweep
-    constexpr int B = 16;
-    const int total = S * (O_K / 2);
-    for (int base = 0; base < total; base += FT * B) {
-      uint32_t v[B];
-      uint32_t pending = 0;
+    // every head's done word, then o of every row in one pass: thread t 16-byte units
+    // t + 512 q (row q; rows past S read as 0 and are not kept)
+    const uint64_t* od = M.odone;
+    if (!hint_wait(HEADS, [od](int i) { return od + i; }, W_OB, gd)) return false;
+    {
+      const __amdgpu_buffer_rsrc_t rs = coherent_rsrc(M.ob, S * (O_K / 2) * 4);
+      static_assert(O_K / 8 == FT, "a row of o is one 16-byte unit a thread");
+      u32x4 v[MAX_ROWS];
 #pragma unroll
-      for (int q = 0; q < B; ++q)
-        if (base + tid + FT * q < total) pending |= 1u << q;
-      const uint64_t* ob = M.ob + base + tid;
-      const auto at = [ob](int q) { return ob + FT * q; };
-      const bool ok = poll_words<B, decltype(at), true>(at, v, pending, W_OB, gd);
-      if (!block_all(ok)) return false;
+      for (int q = 0; q < MAX_ROWS; ++q)
+        v[q] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, (q * FT + tid) * 16, 0, SC1));
 #pragma unroll
-      for (int q = 0; q < B; ++q) {
-        const int w = base + tid + FT * q;
-        if (w < total) *reinterpret_cast<uint32_t*>(&L.u.xo[w / (O_K / 2)][2 * (w % (O_K / 2))]) = v[q];
-      }
+      for (int q = 0; q < MAX_ROWS; ++q)
+        if (q < S) *reinterpret_cast<u32x4*>(&L.u.xo[q][8 * tid]) = v[q];
     }
     __syncthreads();
     waited = now_ticks();

@@ -3,12 +3,13 @@
 //
 // The reference's stages 1-4 (glm53/gfx950/kernel.py:1367-2443) with the FP4
 // indexer of deepseek_v4/gfx950/kernels/stages/indexer.py:236-408:
+//   N  (row): the input RMSNorm, bf16(x rstd gamma), once -> xn (untagged) and the
+//      row's done word
 //   A  (tile of 16 rows, K part) of [W_qkv (2112) | W_ik (128)] FP8 (whole K up to 8
-//      rows, halves above) and W_iw (64) bf16 (K quarters) against the input-RMSNormed
-//      rows: the weight burst goes out first; every task stages its rows by DMA into
-//      LDS, sums each row's squares over the whole row (one wave a row), scales its K
-//      part to bf16(x rstd gamma) in place and runs its 128-k steps -> partial sums
-//      (mailbox pa)
+//      rows, halves above) and W_iw (64) bf16 (K quarters) against the normed rows:
+//      the weight burst goes out first, then the rows' done words are awaited and the
+//      task's K part of every row arrives by DMA into LDS; its 128-k steps -> partial
+//      sums (mailbox pa)
 //   B  (row): the K parts summed in order; q_a RMSNorm -> q_an (bf16 pairs); KV RMSNorm +
 //      k_pe RoPE -> one power-of-two-scaled E4M3 row into the MLA cache; index key
 //      LayerNorm + RoPE + Hadamard + FP4 into the index plane; head weights
@@ -52,7 +53,7 @@ static_assert(ROW_PIECES % WAVE == 0 && KPW <= MAX_PARTS, "stage A split");
 MONO_DEV int kp_fp8(int S) { return S <= 8 ? 1 : 2; }
 MONO_DEV int nt_a(int S) { return A_TILES * kp_fp8(S) + W_TILES * KPW; }
 
-enum { W_PA = 0, W_QAN = 1, W_QNOPE = 2, W_IQRAW = 3 };
+enum { W_PA = 0, W_QAN = 1, W_QNOPE = 2, W_IQRAW = 3, W_XN = 4 };
 
 struct Lds {
   union {
@@ -108,9 +109,12 @@ class Front {
       int t = T, kind;
       bool ok = true;
       const uint64_t t0 = now_ticks();
-      if (t < nt_a(S)) {
+      if (t < S) {
+        kind = 5;
+        norm_row(t);
+      } else if ((t -= S) < nt_a(S)) {
         kind = 0;
-        stage_a(t);
+        ok = stage_a(t);
       } else if ((t -= nt_a(S)) < S) {
         kind = 1;
         ok = stage_b(t);
@@ -203,8 +207,8 @@ class Front {
   // ------------------------------------------------------------ stage A
   // A tile's weights go out first as one uninterrupted burst of loads (vector memory
   // completes in order, so nothing that must be waited for may sit between them); the
-  // rows then go to LDS by DMA (global_load_lds, no registers) and are normed in place.
-  MONO_DEV void stage_a(int t) {
+  // normed rows then go to LDS by DMA (global_load_lds, no registers).
+  MONO_DEV bool stage_a(int t) {
     const int kp = kp_fp8(S);
     const bool bf16w = t >= A_TILES * kp;
     const int u = bf16w ? t - A_TILES * kp : t;
@@ -247,7 +251,7 @@ class Front {
       for (int j = 0; j < MAX_STEPS_W; ++j) SC[j] = 0.f;
     }
     __builtin_amdgcn_sched_barrier(0);
-    stage_rows(sk0, skw, sstride);
+    if (!load_rows(sk0, skw, sstride)) return false;
     mark_waited();
 
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -275,65 +279,63 @@ class Front {
       if (s < S) mb_putf(&M.pa[((size_t)part * MAX_ROWS + s) * N_A + row], v, gd.tag);
     }
     __syncthreads();  // the next task rewrites the LDS
+    return true;
   }
 
-  // Input RMSNorm (glm53/gfx950/kernel.py:1367-1398) into LDS: wave w takes rows w, w + 8.
-  // k in [k0, k0 + kw) goes to LDS by DMA (lane l's 16 bytes land at the wave's base +
-  // 16 l), the rest of the row (rows > 8 only) into registers for the sum of squares;
-  // then each row's squares are summed (deterministic wave sum) and the staged part
-  // scaled in place to bf16(x rstd gamma).
-  MONO_DEV void stage_rows(int k0, int kw, int stride) {
-    const uint16_t* hbase = static_cast<const uint16_t*>(A.h);
-    const int m0 = k0 / (8 * WAVE), mw = kw / (8 * WAVE);  // staged 1 KB pieces a row
-    u32x4 ov[2][RPL / 2];  // the unstaged half of up to two rows (kp = 2)
-    for (int s = wave, n = 0; s < S; s += FW, ++n) {
-      const uint16_t* hrow = hbase + (size_t)s * HIDDEN;
-      for (int m = 0; m < mw; ++m)
-        __builtin_amdgcn_global_load_lds(hrow + 8 * (lane + WAVE * (m0 + m)), &L.u.xa[s * stride + 8 * WAVE * m], 16, 0, 0);
-      if (mw < RPL) {
-        const int mo = m0 == 0 ? RPL / 2 : 0;
+  // Stage N, row s: the input RMSNorm (glm53/gfx950/kernel.py:1367-1398) once for every
+  // stage-A task. Wave 0 sums the
+  // row's squares (lane pieces lane + 64 m in order, then the wave sum); every thread
+  // writes bf16(x rstd gamma) of its pieces to xn with device-coherent stores; after
+  // they complete, the row's done word.
+  MONO_DEV void norm_row(int s) {
+    const uint16_t* hrow = static_cast<const uint16_t*>(A.h) + (size_t)s * HIDDEN;
+    if (wave == 0) {
+      u32x4 x[RPL];
 #pragma unroll
-        for (int m = 0; m < RPL / 2; ++m) {
-          const u32x4 x = ld_u32x4(hrow + 8 * (lane + WAVE * (mo + m)));
-          if (n == 0) ov[0][m] = x;
-          else ov[1][m] = x;
-        }
+      for (int m = 0; m < RPL; ++m) x[m] = ld_u32x4(hrow + 8 * (lane + WAVE * m));
+      float ss = 0.f;
+#pragma unroll
+      for (int m = 0; m < RPL; ++m)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ss += bf16_lo(x[m][e]) * bf16_lo(x[m][e]) + bf16_hi(x[m][e]) * bf16_hi(x[m][e]);
+      ss = wave_sum(ss);
+      if (lane == 0) L.stat[0][0] = 1.0f / sqrtf(ss / (float)HIDDEN + EPS);
+    }
+    __syncthreads();
+    mark_waited();
+    const float rstd = L.stat[0][0];
+    const __amdgpu_buffer_rsrc_t rs = coherent_rsrc(M.xn + (size_t)s * (HIDDEN / 2), HIDDEN * 2);
+    for (int p = tid; p < ROW_PIECES; p += FT) {
+      const u32x4 x = ld_u32x4(hrow + 8 * p);
+      const u32x4 gw = *reinterpret_cast<const u32x4*>(&L.gin[8 * p]);
+      u32x4 o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float y0 = mul_rn(mul_rn(bf16_lo(x[e]), rstd), bf16_lo(gw[e]));
+        const float y1 = mul_rn(mul_rn(bf16_hi(x[e]), rstd), bf16_hi(gw[e]));
+        o[e] = pack_bf16x2(y0, y1);
       }
+      __builtin_amdgcn_raw_buffer_store_b128(o, rs, p * 16, 0, SC1);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();  // the row is stored (and L.stat is free again)
+    if (tid == 0) mb_put(&M.xdone[s], 0u, gd.tag);
+  }
+
+  // The task's K part [k0, k0 + kw) of every normed row into LDS (row stride `stride`),
+  // once every row's done word is in: device-coherent DMA, 1 KB a wave instruction.
+  MONO_DEV bool load_rows(int k0, int kw, int stride) {
+    const uint64_t* xd = M.xdone;
+    if (!hint_wait(S, [xd](int i) { return xd + i; }, W_XN, gd)) return false;
+    const int m0 = k0 / (8 * WAVE), mw = kw / (8 * WAVE);  // 1 KB pieces a row
+    for (int s = wave; s < S; s += FW) {
+      const uint16_t* row = reinterpret_cast<const uint16_t*>(M.xn) + (size_t)s * HIDDEN;
+      for (int m = 0; m < mw; ++m)
+        __builtin_amdgcn_global_load_lds(row + 8 * (lane + WAVE * (m0 + m)), &L.u.xa[s * stride + 8 * WAVE * m], 16, 0, SC1);
     }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    for (int s = wave, n = 0; s < S; s += FW, ++n) {
-      float ss = 0.f;
-      for (int m = 0; m < mw; ++m) {
-        const u32x4 x = *reinterpret_cast<const u32x4*>(&L.u.xa[s * stride + 8 * (lane + WAVE * m)]);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) ss += bf16_lo(x[e]) * bf16_lo(x[e]) + bf16_hi(x[e]) * bf16_hi(x[e]);
-      }
-      if (mw < RPL) {
-#pragma unroll
-        for (int m = 0; m < RPL / 2; ++m) {
-          const u32x4 x = n == 0 ? ov[0][m] : ov[1][m];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) ss += bf16_lo(x[e]) * bf16_lo(x[e]) + bf16_hi(x[e]) * bf16_hi(x[e]);
-        }
-      }
-      ss = wave_sum(ss);
-      const float rstd = 1.0f / sqrtf(ss / (float)HIDDEN + EPS);
-      for (int m = 0; m < mw; ++m) {
-        u32x4* px = reinterpret_cast<u32x4*>(&L.u.xa[s * stride + 8 * (lane + WAVE * m)]);
-        const u32x4 x = *px;
-        const u32x4 gw = *reinterpret_cast<const u32x4*>(&L.gin[k0 + 8 * (lane + WAVE * m)]);
-        u32x4 o;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float y0 = mul_rn(mul_rn(bf16_lo(x[e]), rstd), bf16_lo(gw[e]));
-          const float y1 = mul_rn(mul_rn(bf16_hi(x[e]), rstd), bf16_hi(gw[e]));
-          o[e] = pack_bf16x2(y0, y1);
-        }
-        *px = o;
-      }
-    }
-    __syncthreads();
+    return true;
   }
 
   // ------------------------------------------------------------ stage B

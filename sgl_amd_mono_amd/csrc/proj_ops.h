@@ -23,7 +23,12 @@ struct Mail {
   uint64_t* qan;    // [MAX_ROWS][Q_LORA / 2]        normed q_a, bf16 pairs
   uint64_t* qnope;  // [MAX_ROWS][HEADS][NOPE / 2]   q_nope, bf16 pairs
   uint64_t* iqraw;  // [MAX_ROWS][IH][ID / 2]        raw index query, bf16 pairs
-  uint64_t* ob;     // [MAX_ROWS][HEADS * VDIM / 2]  W_UV o_lat, bf16 pairs
+  uint32_t* xn;     // [MAX_ROWS][HIDDEN / 2]        input-RMSNormed rows, bf16 pairs
+                    //                                (untagged; read after xdone)
+  uint64_t* xdone;  // [MAX_ROWS]                    row s of xn is stored
+  uint32_t* ob;     // [MAX_ROWS][HEADS * VDIM / 2]  W_UV o_lat, bf16 pairs (untagged; read
+                    //                                after odone)
+  uint64_t* odone;  // [HEADS]                       a head's ob is stored
   uint32_t* guard;  // [G_WORDS]
 };
 constexpr size_t MAIL_WORDS[5] = {(size_t)MAX_PARTS * MAX_ROWS * N_A, (size_t)MAX_ROWS * Q_LORA / 2,

@@ -67,6 +67,16 @@ MONO_DEV void st_agent_f32(float* p, float v) {
   __hip_atomic_store(reinterpret_cast<uint32_t*>(p), __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Untagged data behind a tagged done word: the producer stores it with device-coherent
+// buffer stores, waits for them (s_waitcnt 0) and a barrier, then puts the done word;
+// the consumer polls the done word, then reads the data with device-coherent loads.
+// Bytes past the resource's size read as 0 and are not stored.
+constexpr int BUF_DWORD3 = 0x00020000;  // raw buffer resource word 3 (gfx9)
+constexpr int SC1 = 16;                 // buffer cache policy: device-coherent
+MONO_DEV __amdgpu_buffer_rsrc_t coherent_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, bytes, BUF_DWORD3);
+}
+
 struct Guard {
   GuardArgs a;
   uint64_t deadline;  // absolute s_memrealtime tick

@@ -33,8 +33,9 @@ FRONT_TASKS_FIXED = 224 + 32 + 16  # stage C, D and bf16 stage-A tasks; B and E 
 
 def front_tasks(rows: int) -> int:
     """Tasks of one front launch: 140 FP8 stage-A tiles whole (rows <= 8) or in K
-    halves, 16 bf16 tile quarters, a row task and 8 index-query tasks a row, 224 + 32."""
-    return 140 * (1 if rows <= 8 else 2) + FRONT_TASKS_FIXED + 9 * rows
+    halves, 16 bf16 tile quarters, two row tasks (norm, stage B) and 8 index-query
+    tasks a row, 224 + 32."""
+    return 140 * (1 if rows <= 8 else 2) + FRONT_TASKS_FIXED + 10 * rows
 BACK_TASKS = 32 + 224
 
 
