@@ -128,7 +128,7 @@ class Back {
     }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();  // the head's o is stored (and the next task rewrites the LDS)
-    if (tid == 0) mb_put(&M.odone[h], 0u, gd.tag);
+    put_done(M.odone, h, gd.tag);
   }
 
   MONO_DEV bool stage_o(int t) {
@@ -143,7 +143,7 @@ class Back {
     }
     // every head's done word, then o of every row in one pass: thread t 16-byte units
     // t + 512 q (row q; rows past S read as 0 and are not kept)
-    const uint64_t* od = M.odone;
+    const uint64_t* od = done_copy(M.odone);
     if (!hint_wait(HEADS, [od](int i) { return od + i; }, W_OB, gd)) return false;
     {
       const __amdgpu_buffer_rsrc_t rs = coherent_rsrc(M.ob, S * (O_K / 2) * 4);

@@ -276,9 +276,11 @@ class Front {
 #pragma unroll
       for (int w = 0; w < FW; ++w) v += L.red[w][l][i];
       const int s = l % 16, row = (bf16w ? A_TILES * 16 : 0) + tile * 16 + 4 * (l / 16) + i;
-      if (s < S) mb_putf(&M.pa[((size_t)part * MAX_ROWS + s) * N_A + row], v, gd.tag);
+      if (s < S) st_agent_f32(reinterpret_cast<float*>(&M.pa[((size_t)part * MAX_ROWS + s) * N_A + row]), v);
     }
-    __syncthreads();  // the next task rewrites the LDS
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();  // the partials are stored (and the next task rewrites the LDS)
+    if (tid == 0) mb_put(&M.adone[t], 0u, gd.tag);
     return true;
   }
 
@@ -319,13 +321,13 @@ class Front {
     }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();  // the row is stored (and L.stat is free again)
-    if (tid == 0) mb_put(&M.xdone[s], 0u, gd.tag);
+    put_done(M.xdone, s, gd.tag);
   }
 
   // The task's K part [k0, k0 + kw) of every normed row into LDS (row stride `stride`),
   // once every row's done word is in: device-coherent DMA, 1 KB a wave instruction.
   MONO_DEV bool load_rows(int k0, int kw, int stride) {
-    const uint64_t* xd = M.xdone;
+    const uint64_t* xd = done_copy(M.xdone);
     if (!hint_wait(S, [xd](int i) { return xd + i; }, W_XN, gd)) return false;
     const int m0 = k0 / (8 * WAVE), mw = kw / (8 * WAVE);  // 1 KB pieces a row
     for (int s = wave; s < S; s += FW) {
@@ -354,29 +356,13 @@ class Front {
     const float gik0 = W.g_ik[2 * lane], gik1 = W.g_ik[2 * lane + 1];
     const float bik0 = W.b_ik[2 * lane], bik1 = W.b_ik[2 * lane + 1];
     {
-      // one hint word a stage-A task: its last output row of row s
-      const uint64_t* pah = M.pa;
-      const int na = nt_a(S);
-      const bool hok = hint_wait(
-          na,
-          [pah, s, kp](int i) {
-            const bool bw = i >= A_TILES * kp;
-            const int u = bw ? i - A_TILES * kp : i, parts = bw ? KPW : kp;
-            const int tile = u / parts, part = u % parts;
-            const int row = (bw ? A_TILES * 16 : 0) + tile * 16 + 15;
-            return pah + ((size_t)part * MAX_ROWS + s) * N_A + row;
-          },
-          W_PA, gd);
-      if (!hok) return false;
-      uint32_t v[NW];
-      uint32_t pending = 0;
+      // every stage-A task's done word, then row s's partials in one pass
+      const uint64_t* ad = M.adone;
+      if (!hint_wait(nt_a(S), [ad](int i) { return ad + i; }, W_PA, gd)) return false;
+      mark_waited();
 #pragma unroll
-      for (int m = 0; m < NW; ++m)
-        if (tid + FT * m < total) pending |= 1u << m;
-      const uint64_t* pa = M.pa;
-      const int t0 = tid;
-      const auto at = [pa, t0, s, kp, n_fp8](int m) {
-        const int w = t0 + FT * m;
+      for (int m = 0; m < NW; ++m) {
+        const int w = tid + FT * m;
         int part, col;
         if (w < n_fp8) {
           part = w / (N_QKV + ID);
@@ -385,16 +371,7 @@ class Front {
           part = (w - n_fp8) / IH;
           col = N_QKV + ID + (w - n_fp8) % IH;
         }
-        return pa + ((size_t)part * MAX_ROWS + s) * N_A + col;
-      };
-      const bool ok = poll_words<NW>(at, v, pending, W_PA, gd);
-      if (!block_all(ok)) return false;
-      mark_waited();
-#pragma unroll
-      for (int m = 0; m < NW; ++m) {
-        const int w = tid + FT * m;
-        if (w < n_fp8) L.u.row[w / (N_QKV + ID)][w % (N_QKV + ID)] = __uint_as_float(v[m]);
-        else if (w < total) L.u.row[(w - n_fp8) / IH][N_QKV + ID + (w - n_fp8) % IH] = __uint_as_float(v[m]);
+        if (w < total) L.u.row[part][col] = ld_agent_f32(reinterpret_cast<const float*>(&M.pa[((size_t)part * MAX_ROWS + s) * N_A + col]));
       }
     }
     __syncthreads();
@@ -424,9 +401,13 @@ class Front {
         const uint32_t gw = h == 0 ? gq0 : gq1;
         const float y0 = mul_rn(mul_rn(row[2 * j], rq), bf16_lo(gw));
         const float y1 = mul_rn(mul_rn(row[2 * j + 1], rq), bf16_hi(gw));
-        mb_put(&M.qan[(size_t)s * (Q_LORA / 2) + j], pack_bf16x2(y0, y1), gd.tag);
+        __hip_atomic_store(&M.qan[(size_t)s * (Q_LORA / 2) + j], pack_bf16x2(y0, y1), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
       }
     }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();  // row s of q_an is stored
+    put_done(M.qdone, s, gd.tag);
 
     // KV row: bf16 latent and RoPE'd k_pe, one power-of-two E4M3 scale
     const float kvn = bf16_round(mul_rn(mul_rn(kv, rk), gkv));
@@ -491,34 +472,6 @@ class Front {
   }
 
   // ------------------------------------------------------------ stage C
-  // Poll S rows of n words (bf16 pairs) from `mb` (rows `stride` words apart) into LDS
-  // rows of `xs`. Thread t takes words t + 512 q of the S x n range: each poll
-  // instruction of a wave covers 512 contiguous bytes (the loads coalesce).
-  template <int XS, int B>
-  MONO_DEV bool stage_pairs(const uint64_t* mb, int n, size_t stride, uint16_t (*xs)[XS], int site) {
-    const int total = S * n;
-    for (int base = 0; base < total; base += FT * B) {
-      uint32_t v[B];
-      uint32_t pending = 0;
-#pragma unroll
-      for (int q = 0; q < B; ++q)
-        if (base + tid + FT * q < total) pending |= 1u << q;
-      const int t0 = base + tid;
-      const auto at = [mb, t0, n, stride](int q) {
-        const int w = t0 + FT * q;
-        return mb + (size_t)(w / n) * stride + w % n;
-      };
-      const bool ok = poll_words<B, decltype(at), true>(at, v, pending, site, gd);
-      if (!block_all(ok)) return false;
-#pragma unroll
-      for (int q = 0; q < B; ++q) {
-        const int w = t0 + FT * q;
-        if (w < total) *reinterpret_cast<uint32_t*>(&xs[w / n][2 * (w % n)]) = v[q];
-      }
-    }
-    return true;
-  }
-
   MONO_DEV bool stage_c(int c) {
     const bool qb = c < QB_TILES;
     const uint8_t* wb = static_cast<const uint8_t*>(qb ? W.w_qb : W.w_iq);
@@ -540,10 +493,21 @@ class Front {
     const int prc = rope_row(min(so, S - 1)), ic = max(qd - NOPE, 0) / 2;
     const float rc = A.rope_cos[(size_t)prc * (PE_DIM / 2) + ic];
     const float rs = A.rope_sin[(size_t)prc * (PE_DIM / 2) + ic];
-    const uint64_t* qh = M.qan;
-    if (!hint_wait(S, [qh](int i) { return qh + (size_t)i * (Q_LORA / 2) + Q_LORA / 2 - 1; }, W_QAN, gd))
-      return false;
-    if (!stage_pairs<XC, 16>(M.qan, Q_LORA / 2, Q_LORA / 2, L.u.xc, W_QAN)) return false;
+    const uint64_t* qdn = done_copy(M.qdone);
+    if (!hint_wait(S, [qdn](int i) { return qdn + i; }, W_QAN, gd)) return false;
+    {  // q_an of every row in one pass of 16-byte device-coherent loads (192 a row)
+      constexpr int UR = Q_LORA / 8, NU = (MAX_ROWS * UR + FT - 1) / FT;
+      const __amdgpu_buffer_rsrc_t rsq = coherent_rsrc(M.qan, S * (Q_LORA / 2) * 4);
+      u32x4 v[NU];
+#pragma unroll
+      for (int q = 0; q < NU; ++q)
+        v[q] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsq, (tid + FT * q) * 16, 0, SC1));
+#pragma unroll
+      for (int q = 0; q < NU; ++q) {
+        const int u = tid + FT * q;
+        if (u < S * UR) *reinterpret_cast<u32x4*>(&L.u.xc[u / UR][8 * (u % UR)]) = v[q];
+      }
+    }
     __syncthreads();
     mark_waited();
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -562,7 +526,8 @@ class Front {
         if (qb) {
           const int row = qrow, head = row / QK, d = qd;
           if (d < NOPE) {
-            mb_put(&M.qnope[((size_t)s * HEADS + head) * (NOPE / 2) + d / 2], pack_bf16x2(v0, v1), gd.tag);
+            __hip_atomic_store(&M.qnope[((size_t)s * HEADS + head) * (NOPE / 2) + d / 2], pack_bf16x2(v0, v1),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
           } else {
             const int i = (d - NOPE) / 2;
             float x0 = v0, x1 = v1;
@@ -572,11 +537,14 @@ class Front {
           }
         } else {
           const int row = 64 * (c - QB_TILES) + ch, head = row / ID, d = row % ID;
-          mb_put(&M.iqraw[((size_t)s * IH + head) * (ID / 2) + d / 2], pack_bf16x2(v0, v1), gd.tag);
+          __hip_atomic_store(&M.iqraw[((size_t)s * IH + head) * (ID / 2) + d / 2], pack_bf16x2(v0, v1),
+                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
       }
     }
-    __syncthreads();
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();  // the tile's outputs are stored
+    if (tid == 0) mb_put(&M.cdone[c], 0u, gd.tag);
     return true;
   }
 
@@ -590,10 +558,14 @@ class Front {
       ld_fp8_tile(static_cast<const uint8_t*>(W.w_uk), NOPE / 32, rg, 0, g, r, WR[2 * j], WR[2 * j + 1]);
       SC[j] = W.s_uk[rg * 16 / 128];
     }
-    const uint64_t* nh = M.qnope + ((size_t)(S - 1) * HEADS + h) * (NOPE / 2);
-    if (!hint_wait(2, [nh](int i) { return nh + 32 * i + 31; }, W_QNOPE, gd)) return false;
-    if (!stage_pairs<XD, 16>(M.qnope + (size_t)h * (NOPE / 2), NOPE / 2, (size_t)HEADS * (NOPE / 2), L.u.xd, W_QNOPE))
-      return false;
+    // head h's q_nope comes from q_b tiles 3h and 3h + 1 (QK = 192 rows a head)
+    static_assert(QK == 3 * 64 && NOPE == 2 * 64, "q_nope of a head = two q_b tiles");
+    const uint64_t* cd = M.cdone + 3 * h;
+    if (!hint_wait(2, [cd](int i) { return cd + i; }, W_QNOPE, gd)) return false;
+    for (int w = tid; w < S * (NOPE / 2); w += FT) {
+      const int s = w / (NOPE / 2), p = w % (NOPE / 2);
+      *reinterpret_cast<uint32_t*>(&L.u.xd[s][2 * p]) = ld_agent_u32(&M.qnope[((size_t)s * HEADS + h) * (NOPE / 2) + p]);
+    }
     __syncthreads();
     mark_waited();
 #pragma unroll
@@ -617,13 +589,12 @@ class Front {
     const int pr = rope_row(s);
     const float rc = A.rope_cos[(size_t)pr * (PE_DIM / 2) + lane % (PE_DIM / 2)];
     const float rs = A.rope_sin[(size_t)pr * (PE_DIM / 2) + lane % (PE_DIM / 2)];
-    const uint64_t* ih = M.iqraw + ((size_t)s * IH + (e % (IH / FW)) * FW) * (ID / 2);
-    if (!hint_wait(2 * FW, [ih](int i) { return ih + (size_t)(i / 2) * (ID / 2) + 32 * (i % 2) + 31; }, W_IQRAW, gd))
-      return false;
-    uint32_t v;
-    const bool ok = poll_word(&M.iqraw[((size_t)s * IH + head) * (ID / 2) + lane], v, W_IQRAW, gd);
-    if (!block_all(ok)) return false;
+    // index heads 8j .. 8j + 7 come from W_iq tiles 16j .. 16j + 15 (two a head)
+    static_assert(ID == 2 * 64, "a raw index query head = two W_iq tiles");
+    const uint64_t* cd = M.cdone + QB_TILES + 2 * (e % (IH / FW)) * FW;
+    if (!hint_wait(2 * FW, [cd](int i) { return cd + i; }, W_IQRAW, gd)) return false;
     mark_waited();
+    const uint32_t v = ld_agent_u32(&M.iqraw[((size_t)s * IH + head) * (ID / 2) + lane]);
     float a = bf16_lo(v), b = bf16_hi(v);
     if (lane < PE_DIM / 2) rope_pair(a, b, rc, rs);
     uint32_t e8;

@@ -16,19 +16,25 @@ constexpr int IH = 64, ID = 128;
 constexpr int N_QKV = Q_LORA + KV_LORA + PE_DIM;  // 2112 rows of q_a | kv_a
 constexpr int N_A = N_QKV + ID + IH;              // stage-A outputs a row: q_a | kv_a | index k | index w
 constexpr int MAX_PARTS = 4;                      // K parts of a stage-A tile, at most
+constexpr int MAX_A_TASKS = 2 * (N_QKV + ID) / 16 + MAX_PARTS * IH / 16;  // stage-A tasks, at most
+constexpr int C_TASKS = HEADS * QK / 64 + IH * ID / 64;                   // stage-C tiles
 
-// Mailboxes of one projection runtime (tagged 64-bit words, see sync.h).
+// Mailboxes of one projection runtime: untagged data, each read after its producers'
+// tagged done words (see sync.h).
 struct Mail {
-  uint64_t* pa;     // [MAX_PARTS][MAX_ROWS][N_A]    stage-A partial sums, f32
-  uint64_t* qan;    // [MAX_ROWS][Q_LORA / 2]        normed q_a, bf16 pairs
-  uint64_t* qnope;  // [MAX_ROWS][HEADS][NOPE / 2]   q_nope, bf16 pairs
-  uint64_t* iqraw;  // [MAX_ROWS][IH][ID / 2]        raw index query, bf16 pairs
+  uint32_t* pa;     // [MAX_PARTS][MAX_ROWS][N_A]    stage-A partial sums, f32
+  uint64_t* adone;  // [MAX_A_TASKS]                 a stage-A task's partials are stored
+  uint32_t* qan;    // [MAX_ROWS][Q_LORA / 2]        normed q_a, bf16 pairs
+  uint64_t* qdone;  // [MAX_ROWS], replicated        row s of qan is stored
+  uint32_t* qnope;  // [MAX_ROWS][HEADS][NOPE / 2]   q_nope, bf16 pairs
+  uint32_t* iqraw;  // [MAX_ROWS][IH][ID / 2]        raw index query, bf16 pairs
+  uint64_t* cdone;  // [C_TASKS]                     a stage-C tile's outputs are stored
   uint32_t* xn;     // [MAX_ROWS][HIDDEN / 2]        input-RMSNormed rows, bf16 pairs
                     //                                (untagged; read after xdone)
-  uint64_t* xdone;  // [MAX_ROWS]                    row s of xn is stored
+  uint64_t* xdone;  // [MAX_ROWS], replicated        row s of xn is stored
   uint32_t* ob;     // [MAX_ROWS][HEADS * VDIM / 2]  W_UV o_lat, bf16 pairs (untagged; read
                     //                                after odone)
-  uint64_t* odone;  // [HEADS]                       a head's ob is stored
+  uint64_t* odone;  // [HEADS], replicated           a head's ob is stored
   uint32_t* guard;  // [G_WORDS]
 };
 constexpr size_t MAIL_WORDS[5] = {(size_t)MAX_PARTS * MAX_ROWS * N_A, (size_t)MAX_ROWS * Q_LORA / 2,

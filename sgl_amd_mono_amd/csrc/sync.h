@@ -77,6 +77,19 @@ MONO_DEV __amdgpu_buffer_rsrc_t coherent_rsrc(const void* p, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, bytes, BUF_DWORD3);
 }
 
+// A done word that many workgroups poll is put in DONE_REPLICAS copies 4 KB apart
+// (apart in the memory channels) and workgroup b polls copy b % DONE_REPLICAS, so no
+// single line takes every workgroup's polls. An array of n replicated done words takes
+// DONE_REPLICAS * 4 KB (n <= 512).
+constexpr int DONE_REPLICAS = 16;
+constexpr size_t DONE_STRIDE = 4096 / sizeof(uint64_t);
+constexpr size_t DONE_BYTES = DONE_REPLICAS * 4096;
+// thread k < DONE_REPLICAS of the calling workgroup puts copy k of done word i
+MONO_DEV void put_done(uint64_t* base, int i, uint32_t tag) {
+  if ((int)threadIdx.x < DONE_REPLICAS) mb_put(base + threadIdx.x * DONE_STRIDE + i, 0u, tag);
+}
+MONO_DEV const uint64_t* done_copy(const uint64_t* base) { return base + (blockIdx.x % DONE_REPLICAS) * DONE_STRIDE; }
+
 struct Guard {
   GuardArgs a;
   uint64_t deadline;  // absolute s_memrealtime tick
