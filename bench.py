@@ -5,8 +5,8 @@ JSON line. A step is one pass of the hot path over one batch of synthetic decode
 whose inputs and weights are already resident in HBM:
 
 * ``layer`` (default): 61 stacked, independently seeded decoder
-  layers at 8 rows over 32768-key contexts, each layer the four persistent launches
-  front -> sparse attention -> back -> FP8 MoE; one step runs every layer once and is
+  layers at 8 rows over 32768-key contexts, each layer three persistent launches
+  front -> sparse attention + back (one launch) -> FP8 MoE; one step runs every layer once and is
   replayed from a HIP graph. ``value`` is microseconds per layer.
 * ``moe_fp8`` (BASELINE config 2 at 8 rows): the FP8 routed + shared MoE half of the
   layer (RMSNorm, router, top-8, W8A8 experts, residual) through ``mono_moe_fp8_forward``.
@@ -441,14 +441,13 @@ def proj_bytes(w, names) -> int:
 FRONT_W = ("g_in", "w_qkv", "s_qkv", "w_ik", "s_ik", "w_iw", "g_q", "g_kv", "g_ik", "b_ik", "w_qb", "s_qb",
            "w_iq", "s_iq", "w_uk", "s_uk")
 BACK_W = ("w_uv", "s_uv", "w_o", "s_o")
-PHASES = ("front", "attn", "back", "moe")
 
 
 def bench_layer(args, dev):
     """``--layers`` (61) stacked, independently seeded decoder layers
     at ``--rows`` (8) rows, every row a ``--ctx``-key (32768) request whose new token is
-    its last. One step runs all layers once; it is captured in a HIP graph (244
-    persistent launches) and replayed, so host dispatch is off the timed path. The value
+    its last. One step runs all layers once; it is captured in a HIP graph (183
+    persistent launches: front, attention + back, MoE a layer) and replayed, so host dispatch is off the timed path. The value
     is microseconds per layer. A second timed region runs the same step eagerly with a
     HIP event between every two phases; its per-phase averages give the breakdown and
     the MoE kernel's launch duration for ``roofline``."""
@@ -472,7 +471,7 @@ def bench_layer(args, dev):
     cos, sin = workloads.rope_tables(ctx, dev)
     torch.cuda.synchronize()
     log(f"generated in {time.perf_counter() - t0:.1f} s; {torch.cuda.memory_allocated(dev) / 1e9:.1f} GB allocated")
-    rt = LayerRuntime(S, ctx, dev)
+    rt = LayerRuntime(S, ctx, dev, fused=not args.unfused)
     x_in = workloads.rows_bf16(S, 7168, dev, seed=5)
     xb = [torch.empty_like(x_in), torch.empty_like(x_in)]
 
@@ -526,7 +525,9 @@ def bench_layer(args, dev):
 
     # eager pass with phase events: the breakdown and the MoE launch durations
     n_eager = max(1, min(3, args.steps))
-    pev = [[[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(L)] for _ in range(n_eager)]
+    phases = rt.phases  # front, attention + back (one launch), MoE
+    pev = [[[torch.cuda.Event(enable_timing=True) for _ in range(len(phases) + 1)] for _ in range(L)]
+           for _ in range(n_eager)]
     torch.cuda.synchronize()
     for k in range(n_eager):
         x = x_in
@@ -536,10 +537,10 @@ def bench_layer(args, dev):
                            check_weights=False, on_phase=lambda i, l=l, k=k: pev[k][l][i + 1].record(stream))
     torch.cuda.synchronize()
     rt.check_errors()
-    ph = {p: [] for p in PHASES}
+    ph = {p: [] for p in phases}
     for k in range(n_eager):
         for l in range(L):
-            for i, p in enumerate(PHASES):
+            for i, p in enumerate(phases):
                 ph[p].append(pev[k][l][i].elapsed_time(pev[k][l][i + 1]) * 1e3)
     ph_us = {p: statistics.fmean(v) for p, v in ph.items()}
     eager_layer_us = sum(ph_us.values())
@@ -553,6 +554,8 @@ def bench_layer(args, dev):
         "back": proj_bytes(w0.proj, BACK_W) + S * (32 * 512 * 2 + 2 * 7168 * 2),
         "moe": statistics.fmean(moe_b),
     }
+    if "attn_back" in phases:
+        phase_bytes["attn_back"] = phase_bytes.pop("attn") + phase_bytes.pop("back")
     moe_durs = ph["moe"]
     traffic = read_traffic("k_moe_fp8")
     moe_achieved = statistics.fmean(
@@ -560,7 +563,7 @@ def bench_layer(args, dev):
     layer_bytes = sum(phase_bytes.values())
     log(f"{us:.2f} us/layer ({step_us / 1e3:.3f} ms a {L}-layer step, median {statistics.median(per) / L:.2f}), "
         f"{layer_bytes / (us * 1e-6) / 1e9:.0f} GB/s over the layer; eager phases "
-        + ", ".join(f"{p} {ph_us[p]:.1f}" for p in PHASES) + f" us; MoE {moe_achieved:.0f} GB/s; wall {wall:.2f} s")
+        + ", ".join(f"{p} {ph_us[p]:.1f}" for p in phases) + f" us; MoE {moe_achieved:.0f} GB/s; wall {wall:.2f} s")
 
     cpu = None
     if args.cpu_seconds > 0:
@@ -572,14 +575,14 @@ def bench_layer(args, dev):
         dtype="fp8_e4m3 weights (bf16 / fp8 MFMA, f32 accumulate), fp4 index, fp8 kv",
         config=dict(workload="BASELINE config 5: full fused decoder layer, one GPU's TP=4 share, 61 stacked layers",
                     rows=S, context=ctx, layers=L, hidden=7168, heads=32, experts=256, top_k=8, shared_experts=1,
-                    inter=512, launches_per_layer=4, graph=True),
+                    inter=512, launches_per_layer=len(phases), graph=True),
         extra=dict(
             us_per_layer_median=statistics.median(per) / L, us_per_layer_min=min(per) / L,
             us_per_layer_max=max(per) / L, rows_per_s=S / (us * 1e-6), step_wall_s=wall / args.steps,
             layer_algorithmic_bytes=layer_bytes, layer_achieved_gbs=layer_bytes / (us * 1e-6) / 1e9,
             phases_us_eager=ph_us, eager_layer_us=eager_layer_us,
             phases_algorithmic_bytes=phase_bytes,
-            phases_achieved_gbs={p: phase_bytes[p] / (ph_us[p] * 1e-6) / 1e9 for p in PHASES},
+            phases_achieved_gbs={p: phase_bytes[p] / (ph_us[p] * 1e-6) / 1e9 for p in phases},
             distinct_experts_mean=statistics.fmean(distinct),
         ),
         roofline=dict(
@@ -713,6 +716,8 @@ def main() -> int:
     ap.add_argument("--rows", type=int, default=8)
     ap.add_argument("--workload", choices=sorted(WORKLOADS), default="layer")
     ap.add_argument("--layers", type=int, default=61, help="stacked layers (layer workload)")
+    ap.add_argument("--unfused", action="store_true",
+                    help="layer workload: launch the attention and the back separately (four launches a layer)")
     ap.add_argument("--sets", type=int, default=2, help="weight sets rotated over the steps")
     ap.add_argument("--batches", type=int, default=16, help="activation batches rotated")
     ap.add_argument("--ctx", type=int, default=32768, help="keys a row (attn workload)")

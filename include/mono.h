@@ -285,8 +285,8 @@ typedef struct {
   int rows;
   int64_t* timeline;         /* optional i64 [tasks, 4] per task: start, inputs-ready, end
                                 ticks (s_memrealtime, 100 MHz), workgroup << 8 | stage
-                                (0 A, 1 B, 2 C, 3 D, 4 E); tasks = 140 (rows <= 8) or
-                                280, + 272 + 9 rows */
+                                (0 A, 1 B, 2 C, 3 D, 4 E, 5 N: the input RMSNorm of a
+                                row); tasks = 140 (rows <= 8) or 280, + 272 + 10 rows */
 } mono_front_args;
 
 typedef struct {
@@ -299,7 +299,7 @@ typedef struct {
 } mono_back_args;
 
 /* Wait sites of the projection launches: 0 stage-A partials, 1 q_an, 2 q_nope,
- * 3 raw index query, 4 W_UV output. */
+ * 3 raw index query, 4 W_UV output, 5 normed input rows. */
 int mono_proj_create(const mono_proj_config* cfg, mono_proj** out);
 int mono_proj_destroy(mono_proj* proj);
 int mono_front_forward(mono_proj* proj, const mono_proj_weights* w, const mono_front_args* args, void* stream);
@@ -308,6 +308,15 @@ int mono_proj_set_deadline(mono_proj* proj, double seconds);
 int mono_proj_read_errors(mono_proj* proj, int32_t* words);
 int mono_proj_clear_errors(mono_proj* proj);
 int mono_proj_set_fault(mono_proj* proj, int32_t site);
+
+/* mono_attn_back_forward: mono_attn_forward followed by mono_back_forward on its output
+ * (back->o_lat NULL or args->out), as ONE persistent launch of the attention runtime:
+ * the reference runs both in its single decoder-layer launch (kernel.py:2684-4197), so
+ * the back's weight loads start while the last splits and merges run. Results equal
+ * the two calls'. The launch uses the attention runtime's guard (its wait sites, 4 for
+ * the W_UV output and 5 for the merges' output). */
+int mono_attn_back_forward(mono_attn* attn, const mono_attn_args* args, const mono_proj_weights* w,
+                           const mono_back_args* back, void* stream);
 
 #ifdef __cplusplus
 }

@@ -106,6 +106,7 @@ SIGNATURES = {
     "mono_proj_destroy": (C.c_int, [_VP]),
     "mono_front_forward": (C.c_int, [_VP, C.POINTER(ProjWeights), C.POINTER(FrontArgs), _VP]),
     "mono_back_forward": (C.c_int, [_VP, C.POINTER(ProjWeights), C.POINTER(BackArgs), _VP]),
+    "mono_attn_back_forward": (C.c_int, [_VP, C.POINTER(AttnArgs), C.POINTER(ProjWeights), C.POINTER(BackArgs), _VP]),
     "mono_proj_set_deadline": (C.c_int, [_VP, C.c_double]),
     "mono_proj_read_errors": (C.c_int, [_VP, C.POINTER(C.c_int32)]),
     "mono_proj_clear_errors": (C.c_int, [_VP]),

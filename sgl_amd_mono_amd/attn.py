@@ -74,6 +74,14 @@ class AttnRuntime(Runtime):
         (int64 [n_tasks(rows), 4]) receives each task's start, inputs-ready and end
         s_memrealtime ticks (100 MHz) and workgroup << 8 | kind (0 score, 1 top-k,
         2 split, 3 merge)."""
+        args, out, dbg = self.args(step, caches, out, debug, timeline)
+        _lib.check(_lib.lib().mono_attn_forward(self._h, C.byref(args), self._stream()))
+        return (out, dbg) if debug else out
+
+    def args(self, step: AttnStep, caches: AttnCaches, out: torch.Tensor | None, debug: bool,
+             timeline: torch.Tensor | None):
+        """The checked launch arguments of ``forward`` (and of the fused attention + back
+        launch): (mono_attn_args, out, debug outputs)."""
         dev = self.device
         S = step.q.shape[0] if step.q.dim() == 3 else -1
         if not 1 <= S <= self.max_rows:
@@ -107,5 +115,5 @@ class AttnRuntime(Runtime):
         )  # fmt: skip
         if timeline is not None:
             need(timeline, "timeline", (self.n_tasks(S), 4), torch.int64, dev)
-        _lib.check(_lib.lib().mono_attn_forward(self._h, C.byref(args), self._stream()))
-        return (out, dbg) if debug else out
+        return args, out, dbg
+

@@ -13,6 +13,7 @@
 #include <cstring>
 #include <string>
 
+#include "attn_back_ops.h"
 #include "attn_ops.h"
 #include "mono.h"
 #include "moe_ops.h"
@@ -126,6 +127,7 @@ struct mono_moe : RuntimeBase {
 struct mono_attn : RuntimeBase {
   mono_attn_config cfg;
   mono::attn::Mail mail;
+  mono::proj::Mail back_mail;  // the fused attention + back launch's W_UV output and done words
 };
 
 struct mono_proj : RuntimeBase {
@@ -353,6 +355,9 @@ extern "C" int mono_attn_create(const mono_attn_config* cfg, mono_attn** out) {
   const size_t o_part = cv.take(R * SPLITS * NH * DV * 2);
   const size_t o_ml = cv.take(R * SPLITS * NH * 2 * 4);
   const size_t o_sdone = cv.take(R * SPLITS * 8);
+  const size_t o_mdone = cv.take(R * (NH / 2) * 8);
+  const size_t o_fob = cv.take((size_t)mono::proj::MAX_ROWS * mono::proj::HEADS * mono::proj::VDIM / 2 * 4);
+  const size_t o_fodone = cv.take(mono::DONE_BYTES);
   mono_attn* a = new mono_attn();
   a->magic = ATTN_MAGIC;
   a->cfg = c;
@@ -366,6 +371,11 @@ extern "C" int mono_attn_create(const mono_attn_config* cfg, mono_attn** out) {
     delete a;
     return fail(MONO_ESTATE, "the attention launch needs a CU count divisible by %d, got %d", TEAM, a->grid);
   }
+  a->mail.mdone = reinterpret_cast<uint64_t*>(a->at(o_mdone));
+  a->back_mail = mono::proj::Mail{};
+  a->back_mail.ob = reinterpret_cast<uint32_t*>(a->at(o_fob));
+  a->back_mail.odone = reinterpret_cast<uint64_t*>(a->at(o_fodone));
+  a->back_mail.guard = a->guard.words;
   a->mail.guard = a->guard.words;
   a->mail.score = reinterpret_cast<uint32_t*>(a->at(o_score));
   a->mail.sel = reinterpret_cast<uint64_t*>(a->at(o_sel));
@@ -416,6 +426,51 @@ extern "C" int mono_attn_forward(mono_attn* a, const mono_attn_args* args, void*
   AttnArgs g(*args, a->cfg.softmax_scale);
   hipError_t e = attn_forward(g, a->grid, a->mail, a->guard, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return fail(MONO_EHIP, "launching the sparse attention: %s", hipGetErrorString(e));
+  return ok();
+}
+
+extern "C" int mono_attn_back_forward(mono_attn* a, const mono_attn_args* args, const mono_proj_weights* w,
+                                      const mono_back_args* back, void* stream) {
+  using namespace mono::attn;
+  if (!args || !w || !back) return fail(MONO_EINVAL, "mono_attn_back_forward: args, w and back must be non-NULL");
+  if (!live(a, ATTN_MAGIC)) return fail(MONO_ESTATE, "not a live attention runtime");
+  if (args->rows < 1 || args->rows > a->cfg.max_rows || args->rows > mono::proj::MAX_ROWS)
+    return fail(MONO_EINVAL, "rows must be in [1, %d] (the runtime's max_rows), got %d",
+                std::min(a->cfg.max_rows, mono::proj::MAX_ROWS), args->rows);
+  if (back->rows != args->rows) return fail(MONO_EINVAL, "back->rows (%d) must equal args->rows (%d)", back->rows, args->rows);
+  if (back->o_lat && back->o_lat != args->out)
+    return fail(MONO_EINVAL, "back->o_lat must be NULL or args->out: the back reads the attention's output");
+  if (args->pt_stride < a->cfg.max_ctx / PAGE)
+    return fail(MONO_EINVAL, "pt_stride must cover max_ctx / 64 = %d pages, got %d", a->cfg.max_ctx / PAGE,
+                args->pt_stride);
+  if (args->n_pages < 1) return fail(MONO_EINVAL, "n_pages must be positive, got %d", args->n_pages);
+  if (int rc = check_device(a->device)) return rc;
+  REQUIRE_PTR(args->iq);
+  REQUIRE_PTR(args->iqs);
+  REQUIRE_PTR(args->iw);
+  REQUIRE_PTR(args->ikv);
+  REQUIRE_PTR(args->iks);
+  REQUIRE_PTR(args->q);
+  REQUIRE_PTR(args->kv);
+  REQUIRE_PTR(args->kv_scale);
+  REQUIRE_PTR(args->page_table);
+  REQUIRE_PTR(args->seq_lens);
+  REQUIRE_PTR(args->out);
+  REQUIRE_PTR(w->w_uv);
+  REQUIRE_PTR(w->s_uv);
+  REQUIRE_PTR(w->w_o);
+  REQUIRE_PTR(w->s_o);
+  REQUIRE_PTR(back->h);
+  REQUIRE_PTR(back->a);
+  int per_cu = 0;
+  HIP_TRY(mono::fused::attn_back_occupancy(&per_cu));
+  if (per_cu < 1) return fail(MONO_ESTATE, "the fused attention + back kernel does not fit on a CU");
+  mono_back_args b = *back;
+  b.o_lat = args->out;
+  AttnArgs g(*args, a->cfg.softmax_scale);
+  hipError_t e = mono::fused::attn_back_forward(g, a->mail, a->guard, *w, b, a->back_mail, a->grid,
+                                                static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(MONO_EHIP, "launching the fused attention + back: %s", hipGetErrorString(e));
   return ok();
 }
 

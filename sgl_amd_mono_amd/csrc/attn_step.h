@@ -1,0 +1,990 @@
+// Sparse-attention phase of one decode step on gfx950, as ONE persistent launch (one
+// 512-thread workgroup per CU). The reference runs it as stages of its decoder-layer
+// launch: FP4 index scores (deepseek_v4/gfx950/kernels/stages/indexer.py:460-602 and
+// the native-FP4 scorer deepseek_v41/gfx950/indexer/score_fp4.py:254-296), the exact
+// top-2048 (indexer.py:604-802, glm53/gfx950/kernel.py:3000-3636), the sparse MLA
+// split (kernel.py:3638-3973) and the split merge (kernel.py:3975-4123).
+//
+// Tasks, dealt round-robin over the workgroups in this order. A workgroup waits only on
+// tasks earlier in the list or on its own top-k team, whose members share one round
+// of the deal (teams never straddle a round), so the launch cannot deadlock while all
+// workgroups are resident; every wait is guarded (sync.h):
+//   score  (row, 1024 keys): 8 waves x 128 keys. The row's FP4 query (64 heads x 128
+//          dims, E2M1 + E8M0 per 32) is the A operand and 16 keys of SGLang's FP4 index
+//          plane the B operand of v_mfma_scale_f32_16x16x128_f8f6f4 with FP4 formats:
+//          the plane's E8M0 bytes are the MFMA's per-lane B scales as they lie (a
+//          lane's dword holds its key's scale for the page's four 16-key tiles).
+//          score = sum_h w_h relu(q_h . k) -> mailbox score, and the task's histogram
+//          of the keys' leading 8-bit digits -> mailbox hist1
+//   topk   (row, member of a team of 16): the row's scores as order-preserving u32
+//          keys, 2048 a member; an MSB-first 8-bit radix select of the 2048th largest
+//          key: digit 1 from the chunk histograms, digit 2 from the sum of the members'
+//          histograms (mailbox hist; a wave's most common digits go in as one atomic).
+//          The keys sharing both digits with the threshold (mailbox cand) are ranked by
+//          every member; a crowded bin (ties) takes digits 3 and 4 the same way as digit
+//          2 and a stable compaction from the members' counts (mailbox cnt). Every key
+//          above the threshold and the lowest positions equal to it, ascending -> cache
+//          slots (page_table[p / 64] * 64 + p % 64) -> mailbox sel (glm53/check.py:100-117)
+//   split  (row, 64 selected tokens): sub-tiles of 64 tokens gathered from the FP8
+//          cache and widened exactly to bf16 in LDS, bf16 MFMA 16x16x32 for q.k and
+//          p.v, the per-token scale folded into the logit and the probability, online
+//          softmax -> the split's partials (bf16, 32 KB in one contiguous run) and
+//          (m, l), then its done word (mailbox sdone)
+//   merge  (row, 2 heads): once every split of the row is done,
+//          out = sum_j e^(m_j - M) acc_j / sum_j e^(m_j - M) l_j, bf16
+#pragma once
+
+#include "attn_ops.h"
+#include "common.h"
+#include "sync.h"
+
+namespace mono {
+namespace attn {
+
+namespace {
+
+constexpr int AT = 512;
+constexpr int AW = AT / WAVE;
+constexpr int KPM = MAX_CTX / TEAM;          // keys a top-k team member owns
+constexpr int KPT = KPM / AT;                // keys a thread of a member holds
+constexpr int SUB = 64;                      // tokens a split sub-tile
+constexpr int Q_STRIDE = DQK + 8;            // bf16 a q row in LDS
+// dwords a cached row in LDS, as bf16 pairs: 16-byte aligned rows; the swizzle below
+// spreads a p.v column (8 rows, 8 apart for the 4 lane groups) over the banks
+constexpr int KVW = DQK / 2 + 4;
+constexpr int PB_STRIDE = SUB + 8;           // bf16 a probability row in LDS
+constexpr int KEYS_WAVE = CHUNK / AW;        // 128 keys a wave of a score task
+constexpr int KTILES = KEYS_WAVE / 16;
+constexpr float NEG_INF = -__builtin_huge_valf();
+static_assert(KPM % AT == 0 && PAGE % KPT == 0 && TEAM <= 16 && KEYS_WAVE % PAGE == 0 && SPLIT % SUB == 0, "tiling");
+static_assert(AT == NH * DV / 32, "a merge task covers 2 heads");
+
+enum { W_SCORE = 0, W_SEL = 1, W_PART = 2, W_TEAM = 3 };
+
+struct ScoreLds {
+  uint32_t hist[256];  // the task's leading-digit histogram
+};
+
+struct TopkLds {
+  int32_t pt[TOPK / PAGE];  // a short row's page table
+  uint32_t hist[256];       // this member's digit histogram
+  uint32_t tot[256];        // the team's
+  uint32_t pre[256];        // the members' before this one
+  uint32_t cu[CMAX];        // the team's threshold candidates, 0 past the last
+  int32_t xw[TEAM];         // the members' keys above the first digit
+  int32_t cnt[TEAM][2];     // the team's keys above / at the threshold
+  uint32_t digit, uT;
+  int32_t above, pre_above;
+};
+
+struct SplitLds {
+  uint16_t q[NH][Q_STRIDE];
+  uint32_t kvb[SUB * KVW];  // the sub-tile's rows widened to bf16, swizzled (kv_at)
+  float pf[NH][SUB];
+  uint16_t pb[NH][PB_STRIDE];
+  int32_t slot[SPLIT];
+  float kvs[SUB];
+  float alpha[NH];
+};
+
+struct MergeLds {
+  float w[2][SPLITS];  // each split's weight e^(m_j - M), 0 for an empty split
+  float den[2];        // sum_j w_j l_j
+};
+
+struct Lds {
+  union {
+    ScoreLds sc;
+    TopkLds t;
+    SplitLds sp;
+    MergeLds mg;
+  } u;
+  int32_t scan[AW];
+  uint32_t tag;
+  uint32_t err;
+};
+
+struct Args {
+  const uint8_t* iq;
+  const uint8_t* iqs;
+  const uint16_t* iw;
+  const uint8_t* ikv;
+  const uint8_t* iks;
+  const uint16_t* q;
+  const uint8_t* kv;
+  const float* kv_scale;
+  const int32_t* pt;
+  const int32_t* seq_lens;
+  int pt_stride;
+  int n_pages;
+  uint16_t* out;
+  int rows;
+  float* scores;
+  int32_t* topk;
+  int64_t* timeline;
+  float scale;
+  bool publish_out;  // a later stage of the launch reads `out`: each merge puts a done word
+  Mail mail;
+  GuardArgs guard;
+};
+
+MONO_DEV uint32_t radix_key(float f) {
+  const uint32_t b = __float_as_uint(f);
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+// FP4 x FP4 16x16x128 with per-lane E8M0 scales; the B scale byte is picked by OPB.
+template <int OPB>
+MONO_DEV f32x4 mfma_fp4_opb(const u32x4& a, const u32x4& b, int sa, int sb) {
+  const i32x8 A = {(int)a[0], (int)a[1], (int)a[2], (int)a[3], 0, 0, 0, 0};
+  const i32x8 B = {(int)b[0], (int)b[1], (int)b[2], (int)b[3], 0, 0, 0, 0};
+  const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A, B, z, 4, 4, 0, sa, OPB, sb);
+}
+
+// Dword of (token t, dims 2 w, 2 w + 1) in a sub-tile's bf16 rows: rows 8 apart XOR
+// their dword index by 8 so a p.v column's 4 lane groups hit different banks; 4-dword
+// groups stay contiguous and aligned for the q.k reads.
+MONO_DEV int kv_at(int t, int w) { return t * KVW + (w ^ (((t >> 3) & 3) << 3)); }
+
+// 4 E4M3 bytes -> 4 bf16 as 2 dwords (exact: every E4M3 value is a bf16 value)
+MONO_DEV u32x2 fp8x4_bf16(uint32_t w) {
+  const f32x2 lo = fp8x2_unpack<false>(w), hi = fp8x2_unpack<true>(w);
+  u32x2 o;
+  o[0] = (__float_as_uint(lo[0]) >> 16) | (__float_as_uint(lo[1]) & 0xffff0000u);
+  o[1] = (__float_as_uint(hi[0]) >> 16) | (__float_as_uint(hi[1]) & 0xffff0000u);
+  return o;
+}
+
+class Step {
+ public:
+  MONO_DEV Step(const Args& a, Lds& l) : A(a), L(l) {
+    tid = threadIdx.x;
+    lane = tid % WAVE;
+    wave = tid / WAVE;
+    g = lane / 16;
+    r = lane % 16;
+    G = gridDim.x;
+    CH = a.mail.max_ctx / CHUNK;
+  }
+
+  MONO_DEV void run() {
+    if (begin()) (void)tasks();
+  }
+
+  // The launch's tag and deadline (false: a failed launch stopped the runtime); clears
+  // the next launch's row histograms.
+  MONO_DEV bool begin() {
+    if (tid == 0) {
+      const uint32_t ticket = __hip_atomic_fetch_add(&A.guard.words[G_TICKET], 1u, __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT);
+      L.tag = ticket / (uint32_t)G + 1u;
+      L.err = ld_agent_u32(&A.guard.words[G_ERROR]);
+    }
+    __syncthreads();
+    if (L.err != 0) return false;
+    gd.a = A.guard;
+    gd.tag = L.tag;
+    gd.deadline = now_ticks() + A.guard.deadline_ticks;
+    for (int s = blockIdx.x; s < A.mail.max_rows; s += G) {  // the next launch's row histograms
+      uint32_t* nx = row_hist(gd.tag + 1u, s);
+      if (tid < ROWH) __hip_atomic_store(&nx[tid], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    return true;
+  }
+
+  MONO_DEV const Guard& guard() const { return gd; }
+
+  // tasks in the list: score tasks padded to a multiple of TEAM so no top-k team
+  // straddles a round, then top-k members, splits, merges
+  MONO_DEV int n_score() const { return (A.rows * CH + TEAM - 1) / TEAM * TEAM; }
+  MONO_DEV int n_tasks() const { return n_score() + A.rows * TEAM + A.rows * SPLITS + A.rows * (NH / 2); }
+
+  // This workgroup's tasks (false, workgroup-uniform: a wait failed).
+  MONO_DEV bool tasks() {
+    const int n_sc = n_score(), n_topk = A.rows * TEAM;
+    const int n_split = A.rows * SPLITS;
+    const int total = n_tasks();
+    score_stage(blockIdx.x, A.rows * CH);
+    // a workgroup's list is ordered by stage: one loop a stage keeps each loop body to
+    // one task kind (and its registers)
+    int T = first_at_or_after(n_sc);
+    for (; T < n_sc + n_topk; T += G) {
+      const uint64_t t0 = now_ticks();
+      const bool ok = topk_member((T - n_sc) / TEAM, (T - n_sc) % TEAM);
+      stamp(T, t0, 1);
+      if (!ok) return false;  // workgroup-uniform
+    }
+    for (T = first_at_or_after(n_sc + n_topk); T < n_sc + n_topk + n_split; T += G) {
+      const uint64_t t0 = now_ticks();
+      const int j = T - n_sc - n_topk;
+      const bool ok = split_task(j / SPLITS, j % SPLITS);
+      stamp(T, t0, 2);
+      if (!ok) return false;
+    }
+    for (T = first_at_or_after(n_sc + n_topk + n_split); T < total; T += G) {
+      const uint64_t t0 = now_ticks();
+      const int j = T - n_sc - n_topk - n_split;
+      const bool ok = merge_task(j / (NH / 2), j % (NH / 2));
+      stamp(T, t0, 3);
+      if (!ok) return false;
+    }
+    return true;
+  }
+
+ private:
+  const Args& A;
+  Lds& L;
+  Guard gd;
+  int tid, lane, wave, g, r, G, CH;
+  uint64_t waited = 0;
+
+  MONO_DEV int row_len(int s) const { return min(max(A.seq_lens[s], 0), A.mail.max_ctx); }
+  // row s's leading-digit histogram of the launch with this tag: launches alternate
+  // between two copies, and each launch clears the copy its successor uses
+  MONO_DEV uint32_t* row_hist(uint32_t tag, int s) const {
+    return A.mail.rowh + ((size_t)(tag & 1u) * A.mail.max_rows + s) * ROWH;
+  }
+  MONO_DEV int page_of(int s, int p) const {
+    const int pg = A.pt[(size_t)s * A.pt_stride + p / PAGE];
+    return min(max(pg, 0), A.n_pages - 1);
+  }
+  MONO_DEV int slot_of(int s, int p) const { return page_of(s, p) * PAGE + p % PAGE; }
+
+  // this workgroup's first task at or after list index `at` (tasks are dealt round-robin)
+  MONO_DEV int first_at_or_after(int at) const {
+    const int b = blockIdx.x;
+    return at <= b ? b : b + ((at - b + G - 1) / G) * G;
+  }
+
+  // timeline row of task T: start, inputs-ready and end ticks, workgroup << 8 | kind
+  // (kind 0 score .. 3 merge); `waited` is 0 for a task that waits on nothing
+  MONO_DEV void stamp(int T, uint64_t t0, int kind) const {
+    if (A.timeline && tid == 0) {
+      int64_t* tl = A.timeline + (size_t)T * 4;
+      tl[0] = (int64_t)t0;
+      tl[1] = (int64_t)waited;
+      tl[2] = (int64_t)now_ticks();
+      tl[3] = ((int64_t)blockIdx.x << 8) | kind;
+    }
+  }
+  MONO_DEV void mark_waited() { waited = now_ticks(); }
+
+  // ---------------------------------------------------------------- score
+  // A score task's operands for one wave: the row's FP4 query (head tile ht = heads
+  // 16 ht ..), its head weights, and 128 keys = 2 pages = 8 tiles of 16 keys (lane
+  // (g, r) holds chunk g of key 16 t + r) with their pages' E8M0 dwords.
+  struct ScoreOps {
+    int s, c, k0, n;
+    u32x4 qa[IH / 16];
+    int qsc[IH / 16];
+    uint32_t w2[IH / 16][2];
+    u32x4 kb[KTILES];
+    uint32_t ks[KEYS_WAVE / PAGE];
+  };
+
+  MONO_DEV void score_load(int T, ScoreOps& o) {
+    o.s = T / CH;
+    o.c = T % CH;
+    o.k0 = o.c * CHUNK + wave * KEYS_WAVE;
+    o.n = row_len(o.s);
+    if (o.k0 >= o.n) return;
+#pragma unroll
+    for (int ht = 0; ht < IH / 16; ++ht) {
+      const size_t row = (size_t)o.s * IH + 16 * ht + r;
+      o.qa[ht] = ld_u32x4(A.iq + row * (ID / 2) + g * 16);
+      o.qsc[ht] = A.iqs[row * (ID / 32) + g];
+      const u32x2 w4 = *reinterpret_cast<const u32x2*>(A.iw + (size_t)o.s * IH + 16 * ht + 4 * g);
+      o.w2[ht][0] = w4[0];
+      o.w2[ht][1] = w4[1];
+    }
+    int pg[KEYS_WAVE / PAGE];
+#pragma unroll
+    for (int i = 0; i < KEYS_WAVE / PAGE; ++i) pg[i] = page_of(o.s, o.k0 + i * PAGE);
+#pragma unroll
+    for (int kt = 0; kt < KTILES; ++kt)
+      o.kb[kt] = ld_nt_u32x4(A.ikv + ((size_t)(pg[kt / 4] * 4 + g) * PAGE + (kt % 4) * 16 + r) * 16);
+#pragma unroll
+    for (int i = 0; i < KEYS_WAVE / PAGE; ++i)
+      o.ks[i] = *reinterpret_cast<const uint32_t*>(A.iks + (size_t)(pg[i] * 4 + g) * PAGE + r * 4);
+  }
+
+  // The wave's 128 scores -> mailbox score (lane (g, r) ends with keys k0 + 16 g + r and
+  // k0 + 64 + 16 g + r, so each store covers 64 consecutive positions), then the task's
+  // histogram of their leading key digits, added into the row's histogram (the top-k's
+  // first radix pass) before the chunk is marked done (mailbox cdone). Every wave
+  // reaches the barriers; a wave past the row computes nothing.
+  MONO_DEV void score_compute(const ScoreOps& o) {
+    const bool live = o.k0 < o.n;  // wave-uniform
+    float sc[2] = {0.f, 0.f};
+    if (live) {
+      float wv[IH / 16][4];
+#pragma unroll
+      for (int ht = 0; ht < IH / 16; ++ht) {
+        wv[ht][0] = bf16_lo(o.w2[ht][0]);
+        wv[ht][1] = bf16_hi(o.w2[ht][0]);
+        wv[ht][2] = bf16_lo(o.w2[ht][1]);
+        wv[ht][3] = bf16_hi(o.w2[ht][1]);
+      }
+#pragma unroll
+      for (int kt = 0; kt < KTILES; ++kt) {
+        float part = 0.f;
+#pragma unroll
+        for (int ht = 0; ht < IH / 16; ++ht) {
+          f32x4 d;
+          switch (kt % 4) {
+            case 0: d = mfma_fp4_opb<0>(o.qa[ht], o.kb[kt], o.qsc[ht], (int)o.ks[kt / 4]); break;
+            case 1: d = mfma_fp4_opb<1>(o.qa[ht], o.kb[kt], o.qsc[ht], (int)o.ks[kt / 4]); break;
+            case 2: d = mfma_fp4_opb<2>(o.qa[ht], o.kb[kt], o.qsc[ht], (int)o.ks[kt / 4]); break;
+            default: d = mfma_fp4_opb<3>(o.qa[ht], o.kb[kt], o.qsc[ht], (int)o.ks[kt / 4]); break;
+          }
+#pragma unroll
+          for (int i = 0; i < 4; ++i) part += wv[ht][i] * fmaxf(d[i], 0.f);
+        }
+        part += __shfl_xor(part, 16, WAVE);  // every lane group now holds key 16 kt + r's sum
+        part += __shfl_xor(part, 32, WAVE);
+        if (kt % 4 == g) sc[kt / 4] = part;
+      }
+    }
+    bool kl[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int pos = o.k0 + 64 * i + 16 * g + r;
+      kl[i] = live && pos < o.n;
+      if (kl[i]) {
+        __hip_atomic_store(&A.mail.score[(size_t)o.s * A.mail.max_ctx + pos], __float_as_uint(sc[i]), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+        if (A.scores) A.scores[(size_t)o.s * A.mail.max_ctx + pos] = sc[i];
+      }
+    }
+    uint32_t* hist = L.u.sc.hist;
+    __syncthreads();  // the previous task's histogram is added and cleared
+#pragma unroll
+    for (int i = 0; i < 2; ++i) hist_add(hist, kl[i], radix_key(sc[i]) >> 24);
+    __syncthreads();
+    if (o.c * CHUNK < o.n) {  // workgroup-uniform
+      uint32_t* rh = row_hist(gd.tag, o.s);
+      if (tid < 256 && hist[tid] != 0u)
+        __hip_atomic_fetch_add(&rh[tid], hist[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __builtin_amdgcn_s_waitcnt(0);  // every add is performed before the chunk is marked done
+      __syncthreads();
+      if (tid == 0) mb_put(&A.mail.cdone[(size_t)o.s * CH + o.c], 0u, gd.tag);
+    }
+    if (tid < 256) hist[tid] = 0u;
+  }
+
+  // The workgroup's score tasks T0, T0 + G, ... < n_score, each task's loads issued
+  // before the previous task computes.
+  MONO_DEV void score_stage(int T0, int n_score) {
+    if (T0 >= n_score) return;
+    if (tid < 256) L.u.sc.hist[tid] = 0u;
+    ScoreOps cur, nxt;
+    score_load(T0, cur);
+    for (int T = T0; T < n_score; T += G) {
+      const uint64_t t0 = now_ticks();
+      const bool more = T + G < n_score;
+      if (more) score_load(T + G, nxt);
+      score_compute(cur);
+      stamp(T, t0, 0);
+      if (more) cur = nxt;
+    }
+    __syncthreads();  // the top-k tasks reuse the LDS
+  }
+
+  // ---------------------------------------------------------------- top-k
+  // exclusive prefix sum of v over the workgroup (a full barrier)
+  MONO_DEV int block_excl_scan(int v) {
+    const int incl = wave_incl_scan(v);
+    if (lane == WAVE - 1) L.scan[wave] = incl;
+    __syncthreads();
+    int before = 0;
+#pragma unroll
+    for (int w = 0; w < AW; ++w) before += w < wave ? L.scan[w] : 0;
+    __syncthreads();
+    return before + incl - v;
+  }
+
+  MONO_DEV void publish_sel(int s, int j, int slot) {
+    mb_put(&A.mail.sel[(size_t)s * TOPK + j], (uint32_t)slot, gd.tag);
+    if (A.topk) A.topk[(size_t)s * TOPK + j] = slot;
+  }
+
+  // Count a key digit into an LDS histogram: the lanes sharing the first live lane's
+  // digit (scores share sign and exponent bits, so leading digits pile onto few bins)
+  // as one atomic, every other live lane as a plain atomic (the LDS resolves spread
+  // addresses quickly; a wave of same-address atomics would serialize).
+  MONO_DEV void hist_add(uint32_t* hist, bool live, uint32_t d) {
+    const uint64_t act = __ballot(live);
+    if (act == 0) return;  // wave-uniform
+    const int first = __builtin_ctzll(act);
+    const uint32_t d0 = (uint32_t)__builtin_amdgcn_readlane((int)d, first);
+    const uint64_t same = __ballot(live && d == d0);
+    if (live && d != d0) atomicAdd(&hist[d], 1u);
+    if (lane == first) atomicAdd(&hist[d0], (uint32_t)__popcll(same));
+  }
+
+  // Pick the next digit from a 256-bin histogram (wave 0): the highest digit d with
+  // (keys above d) < need <= (keys above d) + hist[d] -> K.digit, K.above; with `pre`,
+  // also K.pre_above = the sum of pre over the bins above d.
+  MONO_DEV void pick_digit(TopkLds& K, const uint32_t* hist, int need, const uint32_t* pre) {
+    if (wave != 0) return;
+    int c[4], tot = 0;  // lane l holds bins 255 - 4l .. 252 - 4l, highest first
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      c[j] = (int)hist[255 - 4 * lane - j];
+      tot += c[j];
+    }
+    const int incl = wave_incl_scan(tot);
+    const int excl = incl - tot;
+    const bool mine = excl < need && need <= incl;
+    int dg = 0, ab = 0, run = excl;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (mine && dg == 0 && run + c[j] >= need) {
+        dg = 256 + 255 - 4 * lane - j;  // + 256: found
+        ab = run;
+      }
+      run += c[j];
+    }
+    const uint64_t who = __ballot(mine);
+    const int src = who ? __ffsll((long long)who) - 1 : 0;
+    dg = __builtin_amdgcn_readlane(dg, src) & 0xff;
+    ab = __builtin_amdgcn_readlane(ab, src);
+    if (pre) {
+      int x = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) x += 255 - 4 * lane - j > dg ? (int)pre[255 - 4 * lane - j] : 0;
+      x = wave_sum_i(x);
+      if (lane == 0) K.pre_above = x;
+    }
+    if (lane == 0) {
+      K.digit = (uint32_t)dg;
+      K.above = ab;
+    }
+  }
+
+  // One exchanged radix pass: member m's histogram of the digit at `shift` over its keys
+  // matching prefix under mask -> mailbox hist as 128 words of two 16-bit bins (a member
+  // holds at most KPM keys), plus `count` as word 128 when count >= 0; the team's sum
+  // -> K.tot, the sum over the members before m -> K.pre, the members' counts -> K.xw.
+  // Workgroup-uniform result.
+  MONO_DEV bool exchange_hist(int s, int m, int pass, const uint32_t (&key)[KPT], int cnt, uint32_t prefix,
+                              uint32_t mask, int shift, int count) {
+    static_assert(KPM < 65536, "16-bit bins");
+    TopkLds& K = L.u.t;
+    if (tid < 256) K.hist[tid] = 0u;
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < KPT; ++q) hist_add(K.hist, q < cnt && (key[q] & mask) == prefix, (key[q] >> shift) & 0xffu);
+    __syncthreads();
+    uint64_t* hb = &A.mail.hist[((size_t)s * PASSES + pass) * TEAM * HW];
+    bool ok = true;
+    if (tid < 128) {
+      mb_put(&hb[m * HW + tid], K.hist[2 * tid] | (K.hist[2 * tid + 1] << 16), gd.tag);
+      uint32_t v[TEAM];
+      const uint64_t* col = hb + tid;
+      const auto at = [col](int j) { return col + j * HW; };
+      ok = poll_words<TEAM, decltype(at), false, false>(at, v, (1u << TEAM) - 1u, W_TEAM, gd);
+      uint32_t t = 0, p = 0;  // two 16-bit sums side by side (at most TEAM KPM keys)
+#pragma unroll
+      for (int j = 0; j < TEAM; ++j) {
+        t += v[j];
+        p += j < m ? v[j] : 0u;
+      }
+      K.tot[2 * tid] = t & 0xffffu;
+      K.tot[2 * tid + 1] = t >> 16;
+      K.pre[2 * tid] = p & 0xffffu;
+      K.pre[2 * tid + 1] = p >> 16;
+    } else if (count >= 0 && tid < 128 + TEAM) {
+      const int j = tid - 128;
+      if (j == m) mb_put(&hb[m * HW + 128], (uint32_t)count, gd.tag);
+      uint32_t v = 0;
+      ok = poll_word(&hb[j * HW + 128], v, W_TEAM, gd);
+      K.xw[j] = (int)v;
+    }
+    return block_all(ok);
+  }
+
+  // a threshold candidate's rank word: larger first = score desc, position asc (the
+  // candidates share their keys' upper 16 bits)
+  MONO_DEV static uint32_t cand_word(uint32_t key, int pos) { return (key << 16) | (uint32_t)(0x7fff - pos); }
+
+  // Member m of row s's top-k team. The team selects the exact top-TOPK of the row
+  // (score desc, position asc) -> cache slots, ascending. Member m owns positions
+  // [m KPM, (m + 1) KPM), KPT of them in each thread's registers. An MSB-first 8-bit
+  // radix select of the threshold key: digit 1 from the score tasks' chunk histograms,
+  // digit 2 from the members' exchanged histograms. The keys left sharing both digits
+  // with the threshold (the candidates, few unless scores tie) are exchanged as (low
+  // key bits, position) and every member ranks them all; a crowded threshold bin
+  // instead takes digits 3 and 4 the same way as digit 2 and then the members' counts
+  // above / at the threshold (mailbox cnt). Each member writes its selected slots at
+  // its offset in position order.
+  MONO_DEV bool topk_member(int s, int m) {
+    TopkLds& K = L.u.t;
+    const int n = row_len(s);
+    if (n <= TOPK) {  // every key is selected; no score is needed
+      if (m == 0) {
+        for (int i = tid; i < TOPK / PAGE; i += AT) K.pt[i] = i * PAGE < n ? page_of(s, i * PAGE) : 0;
+        __syncthreads();
+        for (int j = tid; j < TOPK; j += AT) publish_sel(s, j, j < n ? K.pt[j / PAGE] * PAGE + j % PAGE : -1);
+        __syncthreads();  // the next task may rewrite the LDS page table
+      }
+      return true;
+    }
+    const int p0 = m * KPM + tid * KPT;
+    const int cnt = min(max(n - p0, 0), KPT);
+    const int page = cnt > 0 ? page_of(s, p0) : 0;  // a thread's keys share one page
+    bool ok = true;
+    // thread c < (scored chunks) waits for chunk c's scores and counts (done word)
+    if (tid < (n + CHUNK - 1) / CHUNK) {
+      uint32_t v;
+      ok = poll_word(&A.mail.cdone[(size_t)s * CH + tid], v, W_SCORE, gd);
+    }
+    if (!block_all(ok)) return false;
+    // then a thread's KPT consecutive scores: one 16-byte device-coherent load (the
+    // buffer reads zeros past the row), and the row histogram
+    uint32_t key[KPT];
+    {
+      static_assert(KPT == 4, "a thread's keys are one 16-byte load");
+      const __amdgpu_buffer_rsrc_t rs =
+          __builtin_amdgcn_make_buffer_rsrc(A.mail.score + (size_t)s * A.mail.max_ctx, 0, n * 4, BUF_DWORD3);
+      const u32x4 k4 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, p0 * 4, 0, SC1));
+#pragma unroll
+      for (int q = 0; q < KPT; ++q) key[q] = radix_key(__uint_as_float(k4[q]));
+    }
+    if (tid < 256) K.tot[tid] = ld_agent_u32(&row_hist(gd.tag, s)[tid]);
+    __syncthreads();
+    mark_waited();
+    pick_digit(K, K.tot, TOPK, nullptr);
+    __syncthreads();
+    int need = TOPK - K.above;
+    const uint32_t d1 = K.digit;
+    uint32_t prefix = d1 << 24, mask = 0xff000000u;
+    int above1 = 0;  // this member's keys above digit 1
+#pragma unroll
+    for (int q = 0; q < KPT; ++q) above1 += (q < cnt && (key[q] >> 24) > d1) ? 1 : 0;
+    above1 = wave_sum_i(above1);
+    if (lane == 0) L.scan[wave] = above1;
+    __syncthreads();
+    above1 = 0;
+#pragma unroll
+    for (int w = 0; w < AW; ++w) above1 += L.scan[w];
+    if (!exchange_hist(s, m, 1, key, cnt, prefix, mask, 16, above1)) return false;
+    pick_digit(K, K.tot, need, K.pre);
+    __syncthreads();
+    need -= K.above;
+    int above_before = K.pre_above;  // the earlier members' keys above the threshold's upper 16 bits
+    for (int j = 0; j < m; ++j) above_before += K.xw[j];
+    prefix |= K.digit << 16;
+    mask |= 0x00ff0000u;
+    const int n_cand = (int)K.tot[K.digit], cand_before = (int)K.pre[K.digit];
+    int sel_before;
+    uint32_t uT = 0;  // candidates: the lowest selected rank word
+    bool cand = n_cand <= CMAX;  // team-uniform
+    if (cand) {
+      const uint32_t P16 = prefix >> 16;
+      int c_my = 0;
+#pragma unroll
+      for (int q = 0; q < KPT; ++q) c_my += (q < cnt && (key[q] >> 16) == P16) ? 1 : 0;
+      int idx = cand_before + block_excl_scan(c_my);
+      uint64_t* cb = &A.mail.cand[(size_t)s * CMAX];
+#pragma unroll
+      for (int q = 0; q < KPT; ++q)
+        if (q < cnt && (key[q] >> 16) == P16) mb_put(&cb[idx++], cand_word(key[q], p0 + q), gd.tag);
+      static_assert(CMAX == AT, "a thread a candidate");
+      uint32_t u = 0;
+      ok = true;
+      if (tid < n_cand) ok = poll_word(&cb[tid], u, W_TEAM, gd);
+      K.cu[tid] = u;
+      if (!block_all(ok)) return false;
+      if (wave * WAVE < n_cand) {  // wave-uniform
+        int rank = 0;              // candidates ranked before this thread's
+        for (int j = 0; j < n_cand; j += 4) {
+          const u32x4 x = *reinterpret_cast<const u32x4*>(&K.cu[j]);
+          rank += (x[0] > u ? 1 : 0) + (x[1] > u ? 1 : 0) + (x[2] > u ? 1 : 0) + (x[3] > u ? 1 : 0);
+        }
+        if (tid < n_cand && rank == need - 1) K.uT = u;
+      }
+      __syncthreads();
+      uT = K.uT;
+      sel_before = above_before + __syncthreads_count(tid < cand_before && u >= uT);
+    } else {
+#pragma unroll 1
+      for (int pass = 2; pass < PASSES; ++pass) {
+        const int shift = 24 - 8 * pass;
+        __syncthreads();  // K.digit and K.tot are read
+        if (!exchange_hist(s, m, pass, key, cnt, prefix, mask, shift, -1)) return false;
+        pick_digit(K, K.tot, need, nullptr);
+        __syncthreads();
+        need -= K.above;
+        prefix |= K.digit << shift;
+        mask |= 0xffu << shift;
+      }
+      // the team's counts above / at T, then this member's offset
+      int c_gt = 0, c_eq = 0;
+#pragma unroll
+      for (int q = 0; q < KPT; ++q) {
+        c_gt += (q < cnt && key[q] > prefix) ? 1 : 0;
+        c_eq += (q < cnt && key[q] == prefix) ? 1 : 0;
+      }
+      const int gt_in = block_excl_scan(c_gt), eq_in = block_excl_scan(c_eq);
+      if (tid == AT - 1) {  // the last thread's inclusive sums are the member's totals
+        mb_put(&A.mail.cnt[((size_t)s * TEAM + m) * 2], (uint32_t)(gt_in + c_gt), gd.tag);
+        mb_put(&A.mail.cnt[((size_t)s * TEAM + m) * 2 + 1], (uint32_t)(eq_in + c_eq), gd.tag);
+      }
+      ok = true;
+      if (tid < 2 * TEAM) {
+        uint32_t v = 0;
+        ok = poll_word(&A.mail.cnt[(size_t)s * TEAM * 2 + tid], v, W_TEAM, gd);
+        K.cnt[tid / 2][tid % 2] = (int)v;
+      }
+      if (!block_all(ok)) return false;
+      int eq_before = 0;  // over the members before m, in position order
+      sel_before = 0;
+      for (int j = 0; j < m; ++j) {
+        const int take_j = min(max(need - eq_before, 0), K.cnt[j][1]);
+        sel_before += K.cnt[j][0] + take_j;
+        eq_before += K.cnt[j][1];
+      }
+      // this thread's share of the keys equal to T: the lowest positions first
+      uT = (uint32_t)min(max(need - (eq_before + eq_in), 0), c_eq);
+    }
+    // the selected keys in position order: above the threshold prefix, and the
+    // threshold's share (candidates ranked at or above uT / the first uT equal to T)
+    bool take[KPT];
+    int c_take = 0, te = 0;
+#pragma unroll
+    for (int q = 0; q < KPT; ++q) {
+      if (cand) {
+        const uint32_t hi = key[q] >> 16;
+        take[q] = q < cnt && (hi > (prefix >> 16) || (hi == (prefix >> 16) && cand_word(key[q], p0 + q) >= uT));
+      } else {
+        const bool eq = q < cnt && key[q] == prefix;
+        take[q] = (q < cnt && key[q] > prefix) || (eq && te < (int)uT);
+        te += eq ? 1 : 0;
+      }
+      c_take += take[q] ? 1 : 0;
+    }
+    int idx = sel_before + block_excl_scan(c_take);
+#pragma unroll
+    for (int q = 0; q < KPT; ++q)
+      if (take[q] && idx < TOPK) publish_sel(s, idx++, page * PAGE + (p0 + q) % PAGE);
+    return true;
+  }
+
+  // ---------------------------------------------------------------- split
+  static constexpr int GATHER = (SUB * (DQK / 16) + AT - 1) / AT;  // 16-byte loads a thread a sub-tile
+
+  // Issue sub-tile st's cache-row loads: consecutive lanes read consecutive 16-byte
+  // chunks of a row. Every load is unconditional (an empty slot or a surplus chunk
+  // reads row 0 and is masked later): a load under a condition is waited for at the
+  // join, which would serialize the gather's round trips.
+  MONO_DEV void gather_load(const SplitLds& P, int st, u32x4 (&gv)[GATHER], float& gs) {
+#pragma unroll
+    for (int i = 0; i < GATHER; ++i) {
+      const int f = min(tid + i * AT, SUB * (DQK / 16) - 1);
+      const int t = f / (DQK / 16), c = f % (DQK / 16);
+      const int slot = max(P.slot[st * SUB + t], 0);
+      gv[i] = ld_nt_u32x4(A.kv + (size_t)slot * DQK + c * 16);
+    }
+    gs = A.kv_scale[max(P.slot[st * SUB + tid % SUB], 0)];
+  }
+
+  // bf16 column d of 8 consecutive rows from t0: a p.v operand (8 tokens of one dim).
+  MONO_DEV static bf16x8 column8(const SplitLds& P, int t0, int d) {
+    const uint16_t* b = reinterpret_cast<const uint16_t*>(P.kvb);
+    u32x4 w;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t lo = b[2 * kv_at(t0 + 2 * j, d >> 1) + (d & 1)];
+      const uint32_t hi = b[2 * kv_at(t0 + 2 * j + 1, d >> 1) + (d & 1)];
+      w[j] = lo | (hi << 16);
+    }
+    return __builtin_bit_cast(bf16x8, w);
+  }
+
+  // Store the gathered rows of sub-tile st widened to bf16, row-major (swizzled); the
+  // rows of empty slots as zeros (their loads read row 0).
+  MONO_DEV void gather_store(SplitLds& P, int st, const u32x4 (&gv)[GATHER], float gs) {
+#pragma unroll
+    for (int i = 0; i < GATHER; ++i) {
+      const int f = tid + i * AT;
+      if (f < SUB * (DQK / 16)) {
+        const int t = f / (DQK / 16), c = f % (DQK / 16);
+        const bool live = P.slot[st * SUB + t] >= 0;
+        u32x4 lo = {0u, 0u, 0u, 0u}, hi = {0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          const u32x2 a = fp8x4_bf16(gv[i][q]), b = fp8x4_bf16(gv[i][q + 2]);
+          if (live) {
+            lo[2 * q] = a[0];
+            lo[2 * q + 1] = a[1];
+            hi[2 * q] = b[0];
+            hi[2 * q + 1] = b[1];
+          }
+        }
+        // dims 16c .. 16c + 15 are dwords 8c .. 8c + 7: one swizzled 8-dword block
+        *reinterpret_cast<u32x4*>(&P.kvb[kv_at(t, 8 * c)]) = lo;
+        *reinterpret_cast<u32x4*>(&P.kvb[kv_at(t, 8 * c) + 4]) = hi;
+      }
+    }
+    if (tid < SUB) P.kvs[tid] = P.slot[st * SUB + tid] >= 0 ? gs : 0.f;
+  }
+
+  MONO_DEV bool split_task(int s, int j) {
+    SplitLds& P = L.u.sp;
+    const int nsel = min(row_len(s), TOPK);
+    const int lo = j * SPLIT;
+    const int cnt = min(max(nsel - lo, 0), SPLIT);
+    const size_t mlb = ((size_t)s * SPLITS + j) * NH;
+    if (cnt == 0) {  // an empty split contributes nothing to the merge
+      if (tid < NH) {
+        st_agent_f32(&A.mail.ml[(mlb + tid) * 2], NEG_INF);
+        st_agent_f32(&A.mail.ml[(mlb + tid) * 2 + 1], 0.f);
+      }
+      split_done(s, j);
+      return true;
+    }
+    {
+      constexpr int QL = (NH * DQK / 8 + AT - 1) / AT;
+      u32x4 qv[QL];
+#pragma unroll
+      for (int i = 0; i < QL; ++i) {
+        const int f = min(tid + i * AT, NH * DQK / 8 - 1);  // unconditional (see gather_load)
+        qv[i] = ld_u32x4(A.q + (size_t)s * NH * DQK + (size_t)f * 8);
+      }
+#pragma unroll
+      for (int i = 0; i < QL; ++i) {
+        const int f = tid + i * AT;
+        if (f < NH * DQK / 8) *reinterpret_cast<u32x4*>(&P.q[f / (DQK / 8)][(f % (DQK / 8)) * 8]) = qv[i];
+      }
+    }
+    bool ok = true;
+    if (tid < SPLIT) {
+      int slot = -1;
+      if (tid < cnt) {
+        uint32_t v = 0;
+        ok = poll_word(&A.mail.sel[(size_t)s * TOPK + lo + tid], v, W_SEL, gd);
+        slot = (int)v;
+        if (slot < 0 || slot >= A.n_pages * PAGE) slot = -1;
+      }
+      P.slot[tid] = slot;
+    }
+    if (!block_all(ok)) return false;
+    mark_waited();
+
+    const int ht = wave / 4, tt = wave % 4;  // logit tile of this wave
+    f32x4 acc[2][4];
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int b = 0; b < 4; ++b) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m_run[4] = {NEG_INF, NEG_INF, NEG_INF, NEG_INF}, l_run[4] = {0.f, 0.f, 0.f, 0.f};
+    const int nsub = (cnt + SUB - 1) / SUB;
+    u32x4 gv[GATHER];
+    float gs;
+    gather_load(P, 0, gv, gs);
+
+#pragma unroll 1
+    for (int st = 0; st < nsub; ++st) {
+      gather_store(P, st, gv, gs);
+      __syncthreads();
+      if (st + 1 < nsub) gather_load(P, st + 1, gv, gs);  // in flight while this sub-tile computes
+      // logits of 16 heads x 16 tokens a wave: K = 576 in 18 bf16 steps
+      {
+        // two accumulators and operands read a step ahead: the LDS reads of step ks + 1
+        // overlap the MFMA of step ks
+        f32x4 d0 = {0.f, 0.f, 0.f, 0.f}, d1 = d0;
+        const uint16_t* qrow = &P.q[16 * ht + r][8 * g];
+        bf16x8 qa = *reinterpret_cast<const bf16x8*>(qrow);
+        bf16x8 kb = *reinterpret_cast<const bf16x8*>(&P.kvb[kv_at(16 * tt + r, 4 * g)]);
+#pragma unroll
+        for (int ks = 0; ks < DQK / 32; ++ks) {
+          bf16x8 qn = qa, kn = kb;
+          if (ks + 1 < DQK / 32) {
+            qn = *reinterpret_cast<const bf16x8*>(qrow + 32 * (ks + 1));
+            kn = *reinterpret_cast<const bf16x8*>(&P.kvb[kv_at(16 * tt + r, 16 * (ks + 1) + 4 * g)]);
+          }
+          if (ks % 2 == 0) d0 = mfma_bf16(qa, kb, d0);
+          else d1 = mfma_bf16(qa, kb, d1);
+          qa = qn;
+          kb = kn;
+        }
+        const f32x4 d = d0 + d1;
+        const int t = 16 * tt + r;
+        const bool valid = st * SUB + t < cnt && P.slot[st * SUB + t] >= 0;
+        const float sc = P.kvs[t] * A.scale;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) P.pf[16 * ht + 4 * g + i][t] = valid ? d[i] * sc : NEG_INF;
+      }
+      __syncthreads();
+      // online softmax of heads 4 wave .. 4 wave + 3; lane = token
+#pragma unroll
+      for (int hh = 0; hh < 4; ++hh) {
+        const int h = 4 * wave + hh;
+        const float x = P.pf[h][lane];
+        const float m_new = fmaxf(m_run[hh], wave_max(x));
+        const float p = (m_new == NEG_INF || x == NEG_INF) ? 0.f : hw_exp(x - m_new);
+        const float alpha = m_run[hh] == NEG_INF ? (m_new == NEG_INF ? 1.f : 0.f) : hw_exp(m_run[hh] - m_new);
+        l_run[hh] = l_run[hh] * alpha + wave_sum(p);
+        m_run[hh] = m_new;
+        P.pb[h][lane] = f32_to_bf16_bits(p * P.kvs[lane]);
+        if (lane == 0) P.alpha[h] = alpha;
+      }
+      __syncthreads();
+      // o[32 heads x 64 dims of this wave] = alpha o + p . v
+#pragma unroll
+      for (int a = 0; a < 2; ++a) {
+        float al[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) al[i] = P.alpha[16 * a + 4 * g + i];
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[a][b][i] *= al[i];
+      }
+#pragma unroll
+      for (int kt = 0; kt < SUB / 32; ++kt) {
+        bf16x8 pa[2], vb[4];  // every operand of the k step read before its MFMAs
+#pragma unroll
+        for (int a = 0; a < 2; ++a) pa[a] = *reinterpret_cast<const bf16x8*>(&P.pb[16 * a + r][32 * kt + 8 * g]);
+#pragma unroll
+        for (int b = 0; b < 4; ++b) vb[b] = column8(P, 32 * kt + 8 * g, 16 * (4 * wave + b) + r);
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+#pragma unroll
+          for (int a = 0; a < 2; ++a) acc[a][b] = mfma_bf16(pa[a], vb[b], acc[a][b]);
+      }
+      __syncthreads();
+    }
+    // the partials (bf16, the reference's split partials, kernel.py:4040-4066) staged as
+    // [head][dim] in LDS (lane r holds dim 16 n + r, its neighbour r ^ 1 the other half
+    // of a pair), then stored as the split's contiguous 32 KB by 16-byte
+    // device-coherent stores; then (m, l); then the split's done word
+    uint32_t* ot = P.kvb;  // free after the last P.V step's barrier
+    static_assert(sizeof(P.kvb) >= NH * DV * 2, "partial staging");
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int b = 0; b < 4; ++b)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float mine = acc[a][b][i], other = dpp_f<DPP_XOR1>(mine);
+          const int h = 16 * a + 4 * g + i, dim = 16 * (4 * wave + b) + r;
+          if ((r & 1) == 0) ot[(h * DV + dim) / 2] = pack_bf16x2(mine, other);
+        }
+    __syncthreads();
+    {
+      const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+          A.mail.part + ((size_t)s * SPLITS + j) * NH * DV, 0, NH * DV * 2, BUF_DWORD3);
+      constexpr int CH16 = NH * DV * 2 / 16;  // 16-byte chunks of the split's partials
+#pragma unroll
+      for (int q = 0; q < CH16 / AT; ++q) {
+        const int c = tid + AT * q;
+        __builtin_amdgcn_raw_buffer_store_b128(*reinterpret_cast<const u32x4*>(&ot[4 * c]), rs, 16 * c, 0, SC1);
+      }
+    }
+    if (lane < 4) {
+      const float m = lane == 0 ? m_run[0] : lane == 1 ? m_run[1] : lane == 2 ? m_run[2] : m_run[3];
+      const float l = lane == 0 ? l_run[0] : lane == 1 ? l_run[1] : lane == 2 ? l_run[2] : l_run[3];
+      const int h = 4 * wave + lane;
+      st_agent_f32(&A.mail.ml[(mlb + h) * 2], m);
+      st_agent_f32(&A.mail.ml[(mlb + h) * 2 + 1], l);
+    }
+    split_done(s, j);  // its barrier also frees the staging LDS for the next task
+    return true;
+  }
+
+  // every store of the split performed (each thread waits for its own), then its done word
+  MONO_DEV void split_done(int s, int j) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid == 0) mb_put(&A.mail.sdone[(size_t)s * SPLITS + j], 0u, gd.tag);
+  }
+
+  // ---------------------------------------------------------------- merge
+  MONO_DEV bool merge_task(int s, int hp) {
+    static_assert(SPLITS <= WAVE, "a lane a split");
+    MergeLds& Q = L.u.mg;
+    const int hh = tid / 256, h = 2 * hp + hh, d0 = (tid % 256) * 2;
+    const size_t rb = (size_t)s * SPLITS;
+    // every split of the row done: lane j of wave 0 polls split j's word
+    bool ok = true;
+    if (wave == 0 && lane < SPLITS) {
+      uint32_t v;
+      ok = poll_word(&A.mail.sdone[rb + lane], v, W_PART, gd);
+    }
+    if (!block_all(ok)) return false;
+    mark_waited();
+    // the split weights: lane j of waves 0 and 4 (heads 2 hp, 2 hp + 1) takes split j
+    if (wave % 4 == 0) {
+      const int jl = min(lane, SPLITS - 1);
+      const float m = ld_agent_f32(&A.mail.ml[((rb + jl) * NH + h) * 2]);
+      const float l = lane < SPLITS ? ld_agent_f32(&A.mail.ml[((rb + jl) * NH + h) * 2 + 1]) : 0.f;
+      const bool live = l > 0.f;
+      const float M = wave_max(live ? m : NEG_INF);
+      const float w = live ? hw_exp(m - M) : 0.f;
+      const float den = wave_sum(w * l);
+      if (lane < SPLITS) Q.w[hh][lane] = w;
+      if (lane == 0) Q.den[hh] = den;
+    }
+    // the channel pair of every split (unconditional loads; an empty split's words are
+    // read and ignored)
+    uint32_t av[SPLITS];
+#pragma unroll
+    for (int j = 0; j < SPLITS; ++j)
+      av[j] = ld_agent_u32(reinterpret_cast<const uint32_t*>(&A.mail.part[((rb + j) * NH + h) * DV + d0]));
+    __syncthreads();
+    float o[2] = {0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < SPLITS; ++j) {
+      const float w = Q.w[hh][j];
+      if (w > 0.f) {
+        o[0] += w * bf16_lo(av[j]);
+        o[1] += w * bf16_hi(av[j]);
+      }
+    }
+    const float den = Q.den[hh];
+    const float inv = den > 0.f ? 1.0f / den : 0.f;
+    uint32_t* po = reinterpret_cast<uint32_t*>(A.out + ((size_t)s * NH + h) * DV + d0);
+    const uint32_t ov = pack_bf16x2(o[0] * inv, o[1] * inv);
+    if (A.publish_out) {  // read in this launch: a device-coherent store, complete before the done word
+      __hip_atomic_store(po, ov, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __builtin_amdgcn_s_waitcnt(0);
+    } else {
+      *po = ov;
+    }
+    __syncthreads();  // (and the next task may rewrite the LDS weights)
+    if (A.publish_out && tid == 0) mb_put(&A.mail.mdone[(size_t)s * (NH / 2) + hp], 0u, gd.tag);
+    return true;
+  }
+};
+
+// The kernel arguments of a launch (shared by k_attn and the fused attention + back).
+void fill_args(Args& a, const AttnArgs& g, const Mail& mail, const GuardArgs& guard) {
+  a.iq = static_cast<const uint8_t*>(g.iq);
+  a.iqs = static_cast<const uint8_t*>(g.iqs);
+  a.iw = static_cast<const uint16_t*>(g.iw);
+  a.ikv = static_cast<const uint8_t*>(g.ikv);
+  a.iks = static_cast<const uint8_t*>(g.iks);
+  a.q = static_cast<const uint16_t*>(g.q);
+  a.kv = static_cast<const uint8_t*>(g.kv);
+  a.kv_scale = g.kv_scale;
+  a.pt = g.page_table;
+  a.seq_lens = g.seq_lens;
+  a.pt_stride = g.pt_stride;
+  a.n_pages = g.n_pages;
+  a.out = static_cast<uint16_t*>(g.out);
+  a.rows = g.rows;
+  a.scores = g.scores;
+  a.topk = g.topk;
+  a.timeline = g.timeline;
+  a.scale = g.softmax_scale;
+  a.publish_out = false;
+  a.mail = mail;
+  a.guard = guard;
+}
+
+}  // namespace
+}  // namespace attn
+}  // namespace mono

@@ -1,187 +1,10 @@
-// Back of the attention block on gfx950 as ONE persistent launch (one 512-thread
-// workgroup per CU, tasks dealt round-robin, tagged mailboxes between the stages):
-//   U  (head): o[:, h] = bf16(W_UV[h] o_lat[:, h]), 8 row groups of 16, one a wave,
-//      K = 512 in 4 steps -> ob (untagged bf16 pairs) and the head's done word
-//   O  (32-row tile) of W_o [7168, 4096]: 4 waves a row group, 8 128-k steps a wave,
-//      against o staged in LDS; a = bf16(h + W_o o)
-// (glm53/gfx950/kernel.py:3975-4197; the attention TP reduce there is the local
-// residual add here.)
-#include "common.h"
-#include "proj_common.h"
-#include "proj_ops.h"
-#include "sync.h"
+// The back launch (k_back) and its host side; the stages are in back_impl.h.
+#include "back_impl.h"
 
 namespace mono {
 namespace proj {
 
 namespace {
-
-constexpr int FT = 512;
-constexpr int FW = FT / WAVE;
-constexpr int O_K = HEADS * VDIM;         // 4096
-constexpr int NT_O = HIDDEN / 32;         // 224 tiles of 32 rows
-constexpr int XU = KV_LORA + 8;
-constexpr int XO = O_K + 8;
-constexpr int W_OB = 4;
-
-struct Lds {
-  union {
-    uint16_t xu[MAX_ROWS][XU];
-    uint16_t xo[MAX_ROWS][XO];
-  } u;
-  f32x4 red[FW][WAVE];
-  uint32_t tag;
-  uint32_t err;
-};
-
-struct Args {
-  mono_proj_weights w;
-  mono_back_args a;
-  Mail mail;
-  GuardArgs guard;
-};
-
-class Back {
- public:
-  MONO_DEV Back(const Args& args, Lds& l) : W(args.w), A(args.a), M(args.mail), L(l) {
-    tid = threadIdx.x;
-    lane = tid % WAVE;
-    wave = tid / WAVE;
-    g = lane / 16;
-    r = lane % 16;
-    G = gridDim.x;
-    S = A.rows;
-    guard_args = args.guard;
-  }
-
-  MONO_DEV void run() {
-    if (tid == 0) {
-      const uint32_t ticket = __hip_atomic_fetch_add(&guard_args.words[G_TICKET], 1u, __ATOMIC_RELAXED,
-                                                     __HIP_MEMORY_SCOPE_AGENT);
-      L.tag = ticket / (uint32_t)G + 1u;
-      L.err = ld_agent_u32(&guard_args.words[G_ERROR]);
-    }
-    __syncthreads();
-    if (L.err != 0) return;
-    gd.a = guard_args;
-    gd.tag = L.tag;
-    gd.deadline = now_ticks() + guard_args.deadline_ticks;
-    for (int T = blockIdx.x; T < HEADS + NT_O; T += G) {
-      const uint64_t t0 = now_ticks();
-      if (T < HEADS) {
-        stage_u(T);
-      } else if (!stage_o(T - HEADS)) {
-        return;
-      }
-      stamp(T, t0, T < HEADS ? 0 : 1);
-    }
-  }
-
- private:
-  const mono_proj_weights& W;
-  const mono_back_args& A;
-  const Mail& M;
-  Lds& L;
-  GuardArgs guard_args;
-  Guard gd;
-  int tid, lane, wave, g, r, G, S;
-  uint64_t waited = 0;
-
-  // timeline row of task T: start, inputs-ready and end ticks, workgroup << 8 | stage
-  MONO_DEV void stamp(int T, uint64_t t0, int kind) const {
-    if (A.timeline && tid == 0) {
-      int64_t* tl = A.timeline + (size_t)T * 4;
-      tl[0] = (int64_t)t0;
-      tl[1] = (int64_t)waited;
-      tl[2] = (int64_t)now_ticks();
-      tl[3] = ((int64_t)blockIdx.x << 8) | kind;
-    }
-  }
-
-  MONO_DEV void stage_u(int h) {
-    u32x4 WR[8];
-    float SC[4];
-    const int rg = (VDIM / 16) * h + wave;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      ld_fp8_tile(static_cast<const uint8_t*>(W.w_uv), KV_LORA / 32, rg, j, g, r, WR[2 * j], WR[2 * j + 1]);
-      SC[j] = W.s_uv[(rg * 16 / 128) * (KV_LORA / 128) + j];
-    }
-    const uint16_t* olat = static_cast<const uint16_t*>(A.o_lat);
-    for (int f = tid; f < S * (KV_LORA / 8); f += FT) {
-      const int s = f / (KV_LORA / 8), p = f % (KV_LORA / 8);
-      *reinterpret_cast<u32x4*>(&L.u.xu[s][8 * p]) = ld_u32x4(olat + ((size_t)s * HEADS + h) * KV_LORA + 8 * p);
-    }
-    __syncthreads();
-    waited = now_ticks();
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc += SC[j] * step_fp8(join(WR[2 * j], WR[2 * j + 1]), &L.u.xu[r][128 * j + 32 * g]);
-    if (r < S) {
-      const int v = h * VDIM + 16 * wave + 4 * g;  // output channel of o
-      u32x2 o;
-      o[0] = pack_bf16x2(acc[0], acc[1]);
-      o[1] = pack_bf16x2(acc[2], acc[3]);
-      __builtin_amdgcn_raw_buffer_store_b64(o, coherent_rsrc(M.ob, MAX_ROWS * (O_K / 2) * 4),
-                                            ((size_t)r * (O_K / 2) + v / 2) * 4, 0, SC1);
-      if (A.o) *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(A.o) + (size_t)r * O_K + v) = o;
-    }
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();  // the head's o is stored (and the next task rewrites the LDS)
-    put_done(M.odone, h, gd.tag);
-  }
-
-  MONO_DEV bool stage_o(int t) {
-    u32x4 WR[16];
-    float SC[8];
-    const int rg = 2 * t + wave / 4;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int ks = (wave % 4) * 8 + j;
-      ld_fp8_tile(static_cast<const uint8_t*>(W.w_o), O_K / 32, rg, ks, g, r, WR[2 * j], WR[2 * j + 1]);
-      SC[j] = W.s_o[(rg * 16 / 128) * (O_K / 128) + ks];
-    }
-    // every head's done word, then o of every row in one pass: thread t 16-byte units
-    // t + 512 q (row q; rows past S read as 0 and are not kept)
-    const uint64_t* od = done_copy(M.odone);
-    if (!hint_wait(HEADS, [od](int i) { return od + i; }, W_OB, gd)) return false;
-    {
-      const __amdgpu_buffer_rsrc_t rs = coherent_rsrc(M.ob, S * (O_K / 2) * 4);
-      static_assert(O_K / 8 == FT, "a row of o is one 16-byte unit a thread");
-      u32x4 v[MAX_ROWS];
-#pragma unroll
-      for (int q = 0; q < MAX_ROWS; ++q)
-        v[q] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, (q * FT + tid) * 16, 0, SC1));
-#pragma unroll
-      for (int q = 0; q < MAX_ROWS; ++q)
-        if (q < S) *reinterpret_cast<u32x4*>(&L.u.xo[q][8 * tid]) = v[q];
-    }
-    __syncthreads();
-    waited = now_ticks();
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int ks = (wave % 4) * 8 + j;
-      acc += SC[j] * step_fp8(join(WR[2 * j], WR[2 * j + 1]), &L.u.xo[r][128 * ks + 32 * g]);
-    }
-    L.red[wave][lane] = acc;
-    __syncthreads();
-    {
-      const int rgl = tid / 256, l = (tid / 4) % WAVE, i = tid % 4;
-      float y = 0.f;
-#pragma unroll
-      for (int k = 0; k < 4; ++k) y += L.red[4 * rgl + k][l][i];
-      const int s = l % 16, row = 32 * t + 16 * rgl + 4 * (l / 16) + i;
-      if (s < S) {
-        const size_t at = (size_t)s * HIDDEN + row;
-        const float hv = bf16_bits_to_f32(static_cast<const uint16_t*>(A.h)[at]);
-        static_cast<uint16_t*>(A.a)[at] = f32_to_bf16_bits(__fadd_rn(hv, y));
-      }
-    }
-    __syncthreads();
-    return true;
-  }
-};
 
 __global__ __launch_bounds__(FT, 1) void k_back(Args args) {
   __shared__ Lds lds;

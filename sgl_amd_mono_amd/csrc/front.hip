@@ -53,7 +53,7 @@ static_assert(ROW_PIECES % WAVE == 0 && KPW <= MAX_PARTS, "stage A split");
 MONO_DEV int kp_fp8(int S) { return S <= 8 ? 1 : 2; }
 MONO_DEV int nt_a(int S) { return A_TILES * kp_fp8(S) + W_TILES * KPW; }
 
-enum { W_PA = 0, W_QAN = 1, W_QNOPE = 2, W_IQRAW = 3, W_XN = 4 };
+enum { W_PA = 0, W_QAN = 1, W_QNOPE = 2, W_IQRAW = 3, W_XN = 5 };  // 4: the back's W_UV output
 
 struct Lds {
   union {

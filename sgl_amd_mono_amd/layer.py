@@ -209,6 +209,35 @@ class ProjRuntime(Runtime):
         return a
 
 
+def attn_back(attn, step, caches, w: ProjWeights, h: torch.Tensor, o_lat: torch.Tensor | None = None,
+              a: torch.Tensor | None = None, o: torch.Tensor | None = None, check_weights: bool = True,
+              debug: bool = False, timeline: torch.Tensor | None = None,
+              back_timeline: torch.Tensor | None = None):
+    """The sparse attention (``attn``, an AttnRuntime) and the back of the attention
+    block on its output as ONE launch (mono_attn_back_forward; the reference's layer
+    launch runs both, kernel.py:2684-4197): returns (o_lat, a) and, with ``debug``, the
+    attention's index scores and selected slots. Results equal AttnRuntime.forward
+    followed by ProjRuntime.back."""
+    dev = attn.device
+    args, o_lat, dbg = attn.args(step, caches, o_lat, debug, timeline)
+    S = args.rows
+    need(h, "h", (S, HIDDEN), torch.bfloat16, dev)
+    if check_weights:
+        w.check(dev)
+    a = torch.empty_like(h) if a is None else a
+    need(a, "a", (S, HIDDEN), torch.bfloat16, dev)
+    if o is not None:
+        need(o, "o", (S, HEADS * V_DIM), torch.bfloat16, dev)
+    if back_timeline is not None:
+        need(back_timeline, "back_timeline", (BACK_TASKS, 4), torch.int64, dev)
+    P = _lib.ptr
+    bargs = _lib.BackArgs(o_lat=P(o_lat), h=P(h), a=P(a), o=P(o), rows=S, timeline=P(back_timeline))
+    ws = w.c_struct()
+    _lib.check(_lib.lib().mono_attn_back_forward(attn._h, C.byref(args), C.byref(ws), C.byref(bargs),
+                                                 attn._stream()))
+    return (o_lat, a, dbg) if debug else (o_lat, a)
+
+
 @dataclass
 class LayerWeights:
     """One decoder layer: the attention block's projections and the FP8 MoE."""
@@ -219,18 +248,21 @@ class LayerWeights:
 
 class LayerRuntime:
     """One GPU's TP=4 share of a DeepSeek-V3.2-shaped decoder layer with an FP4 indexer
-    four persistent launches on the caller's stream, each phase's
+    three persistent launches on the caller's stream, each phase's
     outputs in scratch this runtime owns (the reference launches the same body as one
     grid, glm53/gfx950/kernel.py:6-45, with the TP all-reduces that are local residual
     adds here):
 
-        front (mono_front_forward) -> sparse attention (mono_attn_forward)
-          -> back (mono_back_forward) -> FP8 MoE + residual (mono_moe_fp8_forward)
+        front (mono_front_forward) -> sparse attention + back (mono_attn_back_forward)
+          -> FP8 MoE + residual (mono_moe_fp8_forward)
+
+    ``fused=False`` launches the attention (mono_attn_forward) and the back
+    (mono_back_forward) separately: four launches, the same results.
 
     No call synchronises with the host, so a caller may capture a step in a HIP graph.
     """
 
-    def __init__(self, max_rows: int = 8, max_ctx: int = 32768, device=None):
+    def __init__(self, max_rows: int = 8, max_ctx: int = 32768, device=None, fused: bool = True):
         from .attn import AttnRuntime
         from .moe import FP8_MOE, MoeRuntime
 
@@ -241,6 +273,9 @@ class LayerRuntime:
         self.attn = AttnRuntime(max_rows, max_ctx, device=self.device)
         self.moe = MoeRuntime(FP8_MOE, max_rows, self.device)
         self.max_rows, self.max_ctx = max_rows, max_ctx
+        self.fused = fused
+        # the launches of a layer, the names of forward's on_phase indices
+        self.phases = ("front", "attn_back", "moe") if fused else ("front", "attn", "back", "moe")
         self._front = FrontOut.empty(max_rows, self.device)
         self._o_lat = torch.empty(max_rows, HEADS, KV_LORA, dtype=torch.bfloat16, device=self.device)
         self._a = torch.empty(max_rows, HIDDEN, dtype=torch.bfloat16, device=self.device)
@@ -256,8 +291,8 @@ class LayerRuntime:
         at ``seq_lens - 1`` (this step's cache rows are written in place). ``keep``
         also returns the intermediates (front outputs, the index scores and selected
         slots, o_lat, a, the MoE routing and sum) as copies. ``on_phase(i)`` (if given)
-        is called after the launch of phase i is enqueued (0 front, 1 attention, 2 back,
-        3 MoE), e.g. to record timing events between the phases."""
+        is called after the launch of phase i (``self.phases[i]``) is enqueued, e.g. to
+        record timing events between the phases."""
         from .attn import AttnStep
 
         S = h.shape[0] if h.dim() == 2 else -1
@@ -269,16 +304,24 @@ class LayerRuntime:
                         check_weights=check_weights)
         mark(0)
         step = AttnStep(iq=fo.iq, iqs=fo.iqs, iw=fo.iw, q=fo.q, page_table=page_table, seq_lens=seq_lens)
-        if not keep:
-            o_lat = self.attn.forward(step, caches, out=self._o_lat[:S])
+        if self.fused:
+            res = attn_back(self.attn, step, caches, w.proj, h, o_lat=self._o_lat[:S], a=self._a[:S],
+                            check_weights=check_weights, debug=keep)
+            o_lat, a = res[0], res[1]
+            adbg = res[2] if keep else None
+            mark(1)
+        else:
+            if keep:
+                o_lat, adbg = self.attn.forward(step, caches, out=self._o_lat[:S], debug=True)
+            else:
+                o_lat = self.attn.forward(step, caches, out=self._o_lat[:S])
             mark(1)
             a = self.proj.back(o_lat, h, w.proj, a=self._a[:S], check_weights=check_weights)
             mark(2)
+        if not keep:
             x = self.moe.forward_fp8(a, w.moe, out=out)
-            mark(3)
+            mark(len(self.phases) - 1)
             return x
-        o_lat, adbg = self.attn.forward(step, caches, out=self._o_lat[:S], debug=True)
-        a = self.proj.back(o_lat, h, w.proj, a=self._a[:S], check_weights=check_weights)
         x, dbg = self.moe.forward_fp8(a, w.moe, out=out, debug=True)
         inter = dict(q=fo.q.clone(), iq=fo.iq.clone(), iqs=fo.iqs.clone(), iw=fo.iw.clone(), o_lat=o_lat.clone(),
                      a=a.clone(), index_scores=adbg["scores"], topk_slots=adbg["topk"], **dbg)

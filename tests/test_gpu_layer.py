@@ -109,3 +109,31 @@ def test_two_layers_phase_by_phase(gpu_device):
             del w, caches
     finally:
         rt.close()
+
+
+@pytest.mark.parametrize("rows", [1, 8])
+def test_fused_attention_back_equals_two_launches(gpu_device, rows):
+    """mono_attn_back_forward (one launch) gives bit for bit what mono_attn_forward then
+    mono_back_forward give, launch after launch (the launch-parity mailboxes alternate)."""
+    from sgl_amd_mono_amd.attn import AttnRuntime
+    from sgl_amd_mono_amd.layer import ProjRuntime, attn_back
+
+    lens = [CTX, 9000, 2049, 300, CTX - 5, 2048, 16000, 64][:rows]
+    ra, rp = AttnRuntime(8, CTX, device=gpu_device), ProjRuntime(8, gpu_device)
+    try:
+        w = workloads.proj_weights(gpu_device, seed=11)
+        for it in range(3):
+            print(f"[rows {rows}] launch pair {it}", flush=True)
+            step, caches = workloads.attn_case(lens, gpu_device, seed=12 + it, max_ctx=CTX)
+            h = workloads.rows_bf16(rows, ol.HIDDEN, gpu_device, seed=20 + it)
+            o1 = ra.forward(step, caches)
+            a1 = rp.back(o1, h, w)
+            o2, a2 = attn_back(ra, step, caches, w, h)
+            torch.cuda.synchronize()
+            ra.check_errors()
+            rp.check_errors()
+            assert torch.equal(o1, o2), "o_lat"
+            assert torch.equal(a1, a2), "a"
+    finally:
+        ra.close()
+        rp.close()
