@@ -188,7 +188,8 @@ typedef struct {
   const void* iks;           /* u8 [pages, 4, 64] E8M0; key t at byte (t % 16) * 4 + t / 16 */
   const void* q;             /* bf16 [rows, 32, 576] absorbed latent query then RoPE query */
   const void* kv;            /* u8 [pages * 64, 576] E4M3 latent then RoPE key */
-  const float* kv_scale;     /* f32 [pages * 64] per-token dequantisation scale */
+  const float* kv_scale;     /* f32 [pages * 64] per-token dequantisation scale, or NULL:
+                                the rows are raw E4M3 (scale 1), SGLang's HIP DSA MLA row */
   const int32_t* page_table; /* i32 [rows, pt_stride] logical page -> cache page */
   const int32_t* seq_lens;   /* i32 [rows] keys of each row (clamped to [0, max_ctx]) */
   int32_t pt_stride;
@@ -277,7 +278,8 @@ typedef struct {
   void* ikv;                 /* u8 [n_pages, 4, 64, 16] index plane, written in place */
   void* iks;                 /* u8 [n_pages, 4, 64] */
   void* kv;                  /* u8 [n_pages * 64, 576] MLA cache, written in place */
-  float* kv_scale;           /* f32 [n_pages * 64] */
+  float* kv_scale;           /* f32 [n_pages * 64], or NULL: rows written as raw E4M3
+                                (scale 1, values clamped to +-448) */
   void* q;                   /* out bf16 [rows, 32, 576] q_lat | q_pe */
   void* iq;                  /* out u8 [rows, 64, 64] E2M1 index query */
   void* iqs;                 /* out u8 [rows, 64, 4] E8M0 */

@@ -91,8 +91,10 @@ def select_topk(scores, seq_lens, page_table, k=TOPK):
 
 
 def kv_rows(kv, kv_scale, slots):
-    """Dequantised f32 [n, 576] cache rows at ``slots``."""
-    return codecs.e4m3_decode(kv[slots.long()]) * kv_scale[slots.long()].float()[:, None]
+    """Dequantised f32 [n, 576] cache rows at ``slots`` (``kv_scale`` None: raw E4M3
+    rows, scale 1)."""
+    rows = codecs.e4m3_decode(kv[slots.long()])
+    return rows if kv_scale is None else rows * kv_scale[slots.long()].float()[:, None]
 
 
 def sparse_mla(q, kv, kv_scale, sel, scale=SOFTMAX_SCALE):

@@ -102,11 +102,16 @@ def fwht(x: torch.Tensor) -> torch.Tensor:
     return y * (float(n) ** -0.5)
 
 
-def fp8_row_quant_pow2(row: torch.Tensor):
+def fp8_row_quant_pow2(row: torch.Tensor, scaled: bool = True):
     """Per-token E4M3 with a power-of-two scale: scale = 2^ceil(log2(max(amax, 1e-4)/448))
     (the index cache's UE8M0 rule, glm53/gfx950/kernel.py:2137-2151), codes =
     E4M3(v / scale) (exact division by a power of two). Returns (codes uint8 [..., n],
-    scale f32 [...])."""
+    scale f32 [...]). ``scaled=False``: SGLang's raw E4M3 row (the reference's
+    scale-less 576-B row, glm53/gfx950/runner.py:90-96): scale 1, values clamped to
+    [-448, 448]."""
+    if not scaled:
+        codes = codecs.e4m3_encode(row.float().clamp(-FP8_MAX, FP8_MAX))
+        return codes, torch.ones(row.shape[:-1], dtype=torch.float32)
     amax = row.float().abs().amax(-1)
     e = codecs.code_ceil(torch.clamp(amax, min=1e-4) / FP8_MAX)
     scale = torch.exp2(e.double() - 127).float()
@@ -130,7 +135,7 @@ def index_fp4(v: torch.Tensor):
     return codecs.fp4_block_quant(h)
 
 
-def front(h, pos, page_table, w, cos, sin):
+def front(h, pos, page_table, w, cos, sin, kv_scaled: bool = True):
     """The front of the layer for rows ``h`` [S, 7168] bf16 at positions ``pos`` [S]
     (each row's new token; its slot from ``page_table``). ``w``: dict of row-major
     weights (see ``sgl_amd_mono_amd.layer.LayerWeights``). Returns a dict:
@@ -138,7 +143,8 @@ def front(h, pos, page_table, w, cos, sin):
     q [S, 32, 576] bf16 (q_lat | q_pe), iq [S, 64, 64] uint8 (packed E2M1),
     iqs [S, 64, 4] uint8, iw [S, 64] bf16, and the cache rows this step writes:
     slot [S], kv [S, 576] uint8 E4M3 + kv_scale [S] f32, ikv [S, 4, 16] uint8 + iks
-    [S, 4] uint8; plus intermediates (x, q_a, kv_a, ik, q_an, q_nope, q_pe, q_lat)."""
+    [S, 4] uint8; plus intermediates (x, q_a, kv_a, ik, q_an, q_nope, q_pe, q_lat).
+    ``kv_scaled=False`` writes raw E4M3 MLA rows (scale 1)."""
     S = h.shape[0]
     pos = pos.long()
     c, s_ = cos[pos], sin[pos]  # [S, 32]
@@ -162,7 +168,7 @@ def front(h, pos, page_table, w, cos, sin):
     # then one power-of-two E4M3 scale a token
     kvn = codecs.bf16_round(rmsnorm(kv_a[:, :KV_LORA], w["g_kv"]))
     kpe = codecs.bf16_round(rope_pairs(kv_a[:, KV_LORA:], c, s_))
-    kv_codes, kv_scale = fp8_row_quant_pow2(torch.cat([kvn, kpe], -1))
+    kv_codes, kv_scale = fp8_row_quant_pow2(torch.cat([kvn, kpe], -1), scaled=kv_scaled)
 
     # index key: LayerNorm, RoPE on dims [0, 64), Hadamard, FP4 (kernel.py:2103-2131)
     kn = layernorm(ik, w["g_ik"], w["b_ik"])
@@ -193,7 +199,8 @@ def write_caches(f, caches_ikv, caches_iks, caches_kv, caches_kv_scale):
     for i, slot in enumerate(f["slot"].tolist()):
         page, t = slot // PAGE, slot % PAGE
         caches_kv[slot] = f["kv"][i]
-        caches_kv_scale[slot] = f["kv_scale"][i]
+        if caches_kv_scale is not None:
+            caches_kv_scale[slot] = f["kv_scale"][i]
         caches_ikv[page, :, t, :] = f["ikv"][i]
         caches_iks[page, :, scale_byte(t)] = f["iks"][i]
 

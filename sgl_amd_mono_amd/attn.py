@@ -32,7 +32,7 @@ class AttnCaches:
     ikv: torch.Tensor  # u8 [pages, 4, 64, 16] E2M1 index keys
     iks: torch.Tensor  # u8 [pages, 4, 64] E8M0
     kv: torch.Tensor  # u8 [pages * 64, 576] E4M3
-    kv_scale: torch.Tensor  # f32 [pages * 64]
+    kv_scale: torch.Tensor | None  # f32 [pages * 64]; None: raw E4M3 rows (scale 1)
 
 
 @dataclass
@@ -98,7 +98,8 @@ class AttnRuntime(Runtime):
         need(caches.ikv, "ikv", (pages, 4, PAGE, 16), torch.uint8, dev)
         need(caches.iks, "iks", (pages, 4, PAGE), torch.uint8, dev)
         need(caches.kv, "kv", (pages * PAGE, DQK), (torch.uint8, torch.float8_e4m3fn), dev)
-        need(caches.kv_scale, "kv_scale", (pages * PAGE,), torch.float32, dev)
+        if caches.kv_scale is not None:  # None: raw E4M3 rows (scale 1)
+            need(caches.kv_scale, "kv_scale", (pages * PAGE,), torch.float32, dev)
         if out is None:
             out = torch.empty(S, NH, DV, dtype=torch.bfloat16, device=dev)
         need(out, "out", (S, NH, DV), torch.bfloat16, dev)

@@ -81,6 +81,9 @@ struct RuntimeBase {
   void* blob = nullptr;
   size_t blob_bytes = 0;
   mono::GuardArgs guard{};
+  // one f32 1.0 after the mailboxes: the per-token scale of every row of an MLA cache
+  // passed without a scale plane (raw E4M3 rows), read and written at index 0
+  float* unit = nullptr;
 
   // Allocate and zero `bytes` of scratch with the guard words at `guard_off`. Tag 0
   // is never a launch's tag, so zeroed mailboxes read as empty.
@@ -92,13 +95,17 @@ struct RuntimeBase {
     if (int rc = occupancy(&per_cu)) return rc;
     if (per_cu < 1) return fail(MONO_ESTATE, "the persistent %s kernel does not fit on a CU (occupancy %d)", what, per_cu);
     grid = prop.multiProcessorCount;
-    hipError_t e = hipMalloc(&blob, bytes);
+    const size_t total = align256(bytes) + 256;
+    hipError_t e = hipMalloc(&blob, total);
     if (e != hipSuccess) {
       blob = nullptr;
-      return fail(MONO_ENOMEM, "hipMalloc(%zu) for the %s mailboxes: %s", bytes, what, hipGetErrorString(e));
+      return fail(MONO_ENOMEM, "hipMalloc(%zu) for the %s mailboxes: %s", total, what, hipGetErrorString(e));
     }
-    blob_bytes = bytes;
-    e = hipMemset(blob, 0, bytes);
+    blob_bytes = total;
+    unit = reinterpret_cast<float*>(at(align256(bytes)));
+    const float one = 1.0f;
+    e = hipMemset(blob, 0, total);
+    if (e == hipSuccess) e = hipMemcpy(unit, &one, sizeof(one), hipMemcpyHostToDevice);
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) return fail(MONO_EHIP, "clearing the %s mailboxes: %s", what, hipGetErrorString(e));
     guard.words = reinterpret_cast<uint32_t*>(at(guard_off));
@@ -401,6 +408,17 @@ extern "C" int mono_attn_destroy(mono_attn* a) {
   return rc ? rc : ok();
 }
 
+// The kernel arguments of an attention launch: a NULL kv_scale (raw E4M3 MLA rows)
+// reads the runtime's f32 1.0 for every row.
+static mono::attn::AttnArgs attn_args(const mono_attn* a, const mono_attn_args& args) {
+  mono::attn::AttnArgs g(args, a->cfg.softmax_scale);
+  if (!args.kv_scale) {
+    g.kv_scale = a->unit;
+    g.kv_mask = 0;
+  }
+  return g;
+}
+
 extern "C" int mono_attn_forward(mono_attn* a, const mono_attn_args* args, void* stream) {
   using namespace mono::attn;
   if (!args) return fail(MONO_EINVAL, "mono_attn_forward: args is NULL");
@@ -419,11 +437,10 @@ extern "C" int mono_attn_forward(mono_attn* a, const mono_attn_args* args, void*
   REQUIRE_PTR(args->iks);
   REQUIRE_PTR(args->q);
   REQUIRE_PTR(args->kv);
-  REQUIRE_PTR(args->kv_scale);
   REQUIRE_PTR(args->page_table);
   REQUIRE_PTR(args->seq_lens);
   REQUIRE_PTR(args->out);
-  AttnArgs g(*args, a->cfg.softmax_scale);
+  AttnArgs g = attn_args(a, *args);
   hipError_t e = attn_forward(g, a->grid, a->mail, a->guard, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return fail(MONO_EHIP, "launching the sparse attention: %s", hipGetErrorString(e));
   return ok();
@@ -452,7 +469,6 @@ extern "C" int mono_attn_back_forward(mono_attn* a, const mono_attn_args* args, 
   REQUIRE_PTR(args->iks);
   REQUIRE_PTR(args->q);
   REQUIRE_PTR(args->kv);
-  REQUIRE_PTR(args->kv_scale);
   REQUIRE_PTR(args->page_table);
   REQUIRE_PTR(args->seq_lens);
   REQUIRE_PTR(args->out);
@@ -467,7 +483,7 @@ extern "C" int mono_attn_back_forward(mono_attn* a, const mono_attn_args* args, 
   if (per_cu < 1) return fail(MONO_ESTATE, "the fused attention + back kernel does not fit on a CU");
   mono_back_args b = *back;
   b.o_lat = args->out;
-  AttnArgs g(*args, a->cfg.softmax_scale);
+  AttnArgs g = attn_args(a, *args);
   hipError_t e = mono::fused::attn_back_forward(g, a->mail, a->guard, *w, b, a->back_mail, a->grid,
                                                 static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return fail(MONO_EHIP, "launching the fused attention + back: %s", hipGetErrorString(e));
@@ -586,7 +602,6 @@ extern "C" int mono_front_forward(mono_proj* p, const mono_proj_weights* w, cons
   REQUIRE_PTR(args->ikv);
   REQUIRE_PTR(args->iks);
   REQUIRE_PTR(args->kv);
-  REQUIRE_PTR(args->kv_scale);
   REQUIRE_PTR(args->q);
   REQUIRE_PTR(args->iq);
   REQUIRE_PTR(args->iqs);
@@ -594,7 +609,14 @@ extern "C" int mono_front_forward(mono_proj* p, const mono_proj_weights* w, cons
   if (args->pt_stride < 1) return fail(MONO_EINVAL, "pt_stride must be positive, got %d", args->pt_stride);
   if (args->n_pages < 1) return fail(MONO_EINVAL, "n_pages must be positive, got %d", args->n_pages);
   if (args->max_pos < 1) return fail(MONO_EINVAL, "max_pos must be positive, got %d", args->max_pos);
-  hipError_t e = mono::proj::front_forward(*w, *args, p->grid, p->mail, p->guard, static_cast<hipStream_t>(stream));
+  // a NULL kv_scale writes raw E4M3 rows (scale 1) and stores its 1.0 in the runtime's word
+  mono_front_args fa = *args;
+  int kv_mask = -1;
+  if (!fa.kv_scale) {
+    fa.kv_scale = p->unit;
+    kv_mask = 0;
+  }
+  hipError_t e = mono::proj::front_forward(*w, fa, p->grid, p->mail, p->guard, kv_mask, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return fail(MONO_EHIP, "launching the front projections: %s", hipGetErrorString(e));
   return ok();
 }

@@ -51,6 +51,9 @@ struct Mail {
 
 struct AttnArgs : mono_attn_args {
   float softmax_scale;
+  // index mask of kv_scale: -1 with a per-token scale plane; 0 when the caller passed
+  // none and kv_scale points at one f32 1.0 (raw E4M3 rows)
+  int kv_mask = -1;
   AttnArgs(const mono_attn_args& a, float sc) : mono_attn_args(a), softmax_scale(sc) {}
 };
 

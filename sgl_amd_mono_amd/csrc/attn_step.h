@@ -113,6 +113,7 @@ struct Args {
   const uint16_t* q;
   const uint8_t* kv;
   const float* kv_scale;
+  int kv_mask;  // slot & kv_mask indexes kv_scale (0: one scale for every row)
   const int32_t* pt;
   const int32_t* seq_lens;
   int pt_stride;
@@ -687,7 +688,7 @@ class Step {
       const int slot = max(P.slot[st * SUB + t], 0);
       gv[i] = ld_nt_u32x4(A.kv + (size_t)slot * DQK + c * 16);
     }
-    gs = A.kv_scale[max(P.slot[st * SUB + tid % SUB], 0)];
+    gs = A.kv_scale[max(P.slot[st * SUB + tid % SUB], 0) & A.kv_mask];
   }
 
   // bf16 column d of 8 consecutive rows from t0: a p.v operand (8 tokens of one dim).
@@ -970,6 +971,7 @@ void fill_args(Args& a, const AttnArgs& g, const Mail& mail, const GuardArgs& gu
   a.q = static_cast<const uint16_t*>(g.q);
   a.kv = static_cast<const uint8_t*>(g.kv);
   a.kv_scale = g.kv_scale;
+  a.kv_mask = g.kv_mask;
   a.pt = g.page_table;
   a.seq_lens = g.seq_lens;
   a.pt_stride = g.pt_stride;

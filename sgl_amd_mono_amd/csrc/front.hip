@@ -74,11 +74,12 @@ struct Args {
   mono_front_args a;
   Mail mail;
   GuardArgs guard;
+  int kv_mask;  // -1: per-token power-of-two scales into a.kv_scale; 0: raw E4M3 rows
 };
 
 class Front {
  public:
-  MONO_DEV Front(const Args& args, Lds& l) : W(args.w), A(args.a), M(args.mail), L(l) {
+  MONO_DEV Front(const Args& args, Lds& l) : W(args.w), A(args.a), M(args.mail), L(l), kv_mask(args.kv_mask) {
     tid = threadIdx.x;
     lane = tid % WAVE;
     wave = tid / WAVE;
@@ -140,6 +141,7 @@ class Front {
   const mono_front_args& A;
   const Mail& M;
   Lds& L;
+  const int kv_mask;
   GuardArgs guard_args;
   Guard gd;
   int tid, lane, wave, g, r, G, S;
@@ -427,19 +429,22 @@ class Front {
 #pragma unroll
     for (int w = 0; w < FW; ++w) amax = fmaxf(amax, L.stat[w][0]);
     __syncthreads();
-    // scale = 2^ceil(log2(max(amax, 1e-4) / 448)) (kernel.py:2137-2151)
-    const uint32_t e = code_ceil(fmaxf(amax, 1e-4f) / FP8_MAX);
+    // scale = 2^ceil(log2(max(amax, 1e-4) / 448)) (kernel.py:2137-2151); a cache
+    // without a scale plane keeps raw E4M3 (scale 1, SGLang's HIP DSA row), values
+    // clamped to the E4M3 range (a no-op under the power-of-two scale)
+    const uint32_t e = kv_mask ? code_ceil(fmaxf(amax, 1e-4f) / FP8_MAX) : 127u;
     const float inv = pow2_of(254u - e);
     if (slot >= 0) {
       uint8_t* kvrow = static_cast<uint8_t*>(A.kv) + (size_t)slot * (KV_LORA + PE_DIM);
-      const float q0 = mul_rn(kvn, inv);
+      const float q0 = fminf(fmaxf(mul_rn(kvn, inv), -FP8_MAX), FP8_MAX);
       const float q1 = __shfl_down(q0, 1, WAVE), q2 = __shfl_down(q0, 2, WAVE), q3 = __shfl_down(q0, 3, WAVE);
       if (tid % 4 == 0) *reinterpret_cast<uint32_t*>(kvrow + tid) = fp8x4_pack(q0, q1, q2, q3);
-      const float e0 = mul_rn(p0, inv), e1 = mul_rn(p1, inv);
+      const float e0 = fminf(fmaxf(mul_rn(p0, inv), -FP8_MAX), FP8_MAX);
+      const float e1 = fminf(fmaxf(mul_rn(p1, inv), -FP8_MAX), FP8_MAX);
       const float e2 = __shfl_down(e0, 1, WAVE), e3 = __shfl_down(e1, 1, WAVE);
       if (tid < PE_DIM / 2 && tid % 2 == 0)
         *reinterpret_cast<uint32_t*>(kvrow + KV_LORA + 2 * tid) = fp8x4_pack(e0, e1, e2, e3);
-      if (tid == 0) A.kv_scale[slot] = pow2_of(e);
+      if (tid == 0) A.kv_scale[slot & kv_mask] = pow2_of(e);
     }
 
     // index key: LayerNorm, RoPE on dims [0, 64), Hadamard, FP4 (kernel.py:2103-2131)
@@ -618,13 +623,14 @@ hipError_t front_occupancy(int* blocks_per_cu) {
 }
 
 hipError_t front_forward(const mono_proj_weights& w, const mono_front_args& a, int grid, const Mail& mail,
-                         const GuardArgs& guard, hipStream_t st) {
+                         const GuardArgs& guard, int kv_mask, hipStream_t st) {
   if (a.rows < 1 || a.rows > MAX_ROWS || grid < 1) return hipErrorInvalidConfiguration;
   Args args;
   args.w = w;
   args.a = a;
   args.mail = mail;
   args.guard = guard;
+  args.kv_mask = kv_mask;
   k_front<<<grid, FT, 0, st>>>(args);
   return hipGetLastError();
 }

@@ -160,7 +160,8 @@ class ProjRuntime(Runtime):
         need(caches.ikv, "ikv", (pages, 4, 64, 16), torch.uint8, dev)
         need(caches.iks, "iks", (pages, 4, 64), torch.uint8, dev)
         need(caches.kv, "kv", (pages * 64, KV_LORA + PE_DIM), torch.uint8, dev)
-        need(caches.kv_scale, "kv_scale", (pages * 64,), torch.float32, dev)
+        if caches.kv_scale is not None:  # None: raw E4M3 rows (scale 1)
+            need(caches.kv_scale, "kv_scale", (pages * 64,), torch.float32, dev)
         if rope_cos.dim() != 2 or rope_cos.shape[1] != PE_DIM // 2:
             raise ValueError(f"rope_cos: expected [max_pos, {PE_DIM // 2}], got {tuple(rope_cos.shape)}")
         need(rope_cos, "rope_cos", tuple(rope_cos.shape), torch.float32, dev)

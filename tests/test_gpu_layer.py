@@ -137,3 +137,47 @@ def test_fused_attention_back_equals_two_launches(gpu_device, rows):
     finally:
         ra.close()
         rp.close()
+
+
+def test_layer_raw_e4m3_mla_rows(gpu_device):
+    """A layer over an MLA cache without a scale plane (``kv_scale=None``: raw E4M3
+    rows, SGLang's HIP DSA layout): the front writes each new row as E4M3 of the
+    values themselves (scale 1) and the attention reads every row unscaled."""
+    ctx, rows = 4096, 4
+    rt = LayerRuntime(rows, ctx, gpu_device)
+    cos, sin = workloads.rope_tables(ctx, gpu_device)
+    lens = [4096, 1500, 65, 2049]
+    print("[raw e4m3] weights", flush=True)
+    w = LayerWeights(proj=workloads.proj_weights(gpu_device, seed=21),
+                     moe=workloads.fp8_moe_weights(FP8_MOE, gpu_device, seed=22))
+    step, caches = workloads.attn_case(lens, gpu_device, seed=23, max_ctx=ctx)
+    caches.kv_scale = None
+    x = workloads.rows_bf16(rows, ol.HIDDEN, gpu_device, seed=24)
+    kv_before = caches.kv.cpu().clone()
+    try:
+        _, it = rt.forward(x, step.seq_lens, step.page_table, caches, w, cos, sin, keep=True)
+        torch.cuda.synchronize()
+        rt.check_errors()
+    finally:
+        rt.close()
+    pos = step.seq_lens.cpu().long() - 1
+    pt = step.page_table.cpu()
+    f = ol.front(x.cpu(), pos, pt, _cpu_proj(w.proj), cos.cpu(), sin.cpu(), kv_scaled=False)
+    _close(it["q"].cpu(), f["q"], "front q")
+    kv = caches.kv.cpu()
+    slots = f["slot"]
+    got, want = ocodecs.e4m3_decode(kv[slots]), ocodecs.e4m3_decode(f["kv"])
+    exact = float((kv[slots] == f["kv"]).float().mean())
+    step_ = torch.maximum(got.abs(), want.abs()) * 2.0**-3 + 2.0**-9
+    print(f"  raw rows: {exact:.4f} codes exact", flush=True)
+    assert exact >= 0.98 and bool(((got - want).abs() <= step_ * (1 + 1e-6)).all())
+    keep = torch.ones(kv.shape[0], dtype=torch.bool)
+    keep[slots] = False
+    assert torch.equal(kv[keep], kv_before[keep])
+    sel = it["topk_slots"].cpu()
+    c = {k: v.cpu() for k, v in vars(caches).items() if v is not None}
+    assert torch.equal(sel, oatt.select_topk(it["index_scores"].cpu(), step.seq_lens.cpu(), pt))
+    o_ref = oatt.sparse_mla(it["q"].cpu(), c["kv"], None, sel)
+    _close(it["o_lat"].cpu(), o_ref, "attention o_lat (unscaled rows)")
+    b = ol.back(it["o_lat"].cpu(), x.cpu(), _cpu_proj(w.proj))
+    _close(it["a"].cpu(), b["a"], "back a")

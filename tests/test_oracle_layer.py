@@ -235,3 +235,17 @@ def test_back_is_residual_plus_two_projections():
     # zero attention output leaves the residual stream unchanged
     z = ol.back(torch.zeros_like(o_lat), h, w)
     assert torch.equal(z["a"], h)
+
+
+def test_raw_e4m3_mla_row_is_unscaled_and_clamped():
+    """SGLang's scale-less MLA row: every E4M3 value codes itself (scale 1) and values
+    past the format's range clamp to +-448 (the largest finite E4M3)."""
+    from oracle import codecs
+
+    row = torch.tensor([[0.0, 1.0, -2.5, 448.0, 1000.0, -3000.0, 0.0625, 2.0**-9]])
+    codes, scale = ol.fp8_row_quant_pow2(row, scaled=False)
+    assert scale.tolist() == [1.0]
+    assert codecs.e4m3_decode(codes).tolist() == [[0.0, 1.0, -2.5, 448.0, 448.0, -448.0, 0.0625, 2.0**-9]]
+    # the scaled row of the same values is a power of two times codes within range
+    codes2, scale2 = ol.fp8_row_quant_pow2(row)
+    assert float(scale2) == 8.0 and bool((codecs.e4m3_decode(codes2).abs() <= 448).all())
