@@ -471,7 +471,7 @@ def bench_layer(args, dev):
     cos, sin = workloads.rope_tables(ctx, dev)
     torch.cuda.synchronize()
     log(f"generated in {time.perf_counter() - t0:.1f} s; {torch.cuda.memory_allocated(dev) / 1e9:.1f} GB allocated")
-    rt = LayerRuntime(S, ctx, dev, fused=not args.unfused)
+    rt = LayerRuntime(S, ctx, dev, mode=args.mode)
     x_in = workloads.rows_bf16(S, 7168, dev, seed=5)
     xb = [torch.empty_like(x_in), torch.empty_like(x_in)]
 
@@ -525,7 +525,7 @@ def bench_layer(args, dev):
 
     # eager pass with phase events: the breakdown and the MoE launch durations
     n_eager = max(1, min(3, args.steps))
-    phases = rt.phases  # front, attention + back (one launch), MoE
+    phases = rt.phases  # front, then attention + back + MoE (one launch) by default
     pev = [[[torch.cuda.Event(enable_timing=True) for _ in range(len(phases) + 1)] for _ in range(L)]
            for _ in range(n_eager)]
     torch.cuda.synchronize()
@@ -556,14 +556,22 @@ def bench_layer(args, dev):
     }
     if "attn_back" in phases:
         phase_bytes["attn_back"] = phase_bytes.pop("attn") + phase_bytes.pop("back")
-    moe_durs = ph["moe"]
-    traffic = read_traffic("k_moe_fp8")
+    if "attn_back_moe" in phases:
+        phase_bytes["attn_back_moe"] = phase_bytes.pop("attn") + phase_bytes.pop("back") + phase_bytes.pop("moe")
+    # the dominant launch: the MoE's own, or the fused attention + back + MoE launch
+    dom = "moe" if "moe" in phases else "attn_back_moe"
+    dom_kernel = {"moe": "k_moe_fp8", "attn_back_moe": "k_layer_tail"}[dom]
+    dom_fixed = phase_bytes[dom] - statistics.fmean(moe_b)  # its bytes besides the experts
+    dom_b = [b + dom_fixed for b in moe_b]  # per layer (each layer's own distinct experts)
+    moe_durs = ph[dom]
+    traffic = read_traffic(dom_kernel)
     moe_achieved = statistics.fmean(
-        b / (t * 1e-6) for b, t in zip([moe_b[l] for _ in range(n_eager) for l in range(L)], moe_durs)) / 1e9
+        b / (t * 1e-6) for b, t in zip([dom_b[l] for _ in range(n_eager) for l in range(L)], moe_durs)) / 1e9
     layer_bytes = sum(phase_bytes.values())
     log(f"{us:.2f} us/layer ({step_us / 1e3:.3f} ms a {L}-layer step, median {statistics.median(per) / L:.2f}), "
         f"{layer_bytes / (us * 1e-6) / 1e9:.0f} GB/s over the layer; eager phases "
-        + ", ".join(f"{p} {ph_us[p]:.1f}" for p in phases) + f" us; MoE {moe_achieved:.0f} GB/s; wall {wall:.2f} s")
+        + ", ".join(f"{p} {ph_us[p]:.1f}" for p in phases) + f" us; {dom_kernel} {moe_achieved:.0f} GB/s; "
+        f"wall {wall:.2f} s")
 
     cpu = None
     if args.cpu_seconds > 0:
@@ -587,8 +595,10 @@ def bench_layer(args, dev):
         ),
         roofline=dict(
             bound="hbm", achieved=moe_achieved, peak=HBM_PEAK_GBS, unit="GB/s", frac=moe_achieved / HBM_PEAK_GBS,
-            traffic=traffic, kernel="k_moe_fp8 (the MoE phase: 86% of the layer's bytes)",
-            bytes_per_launch=statistics.fmean(moe_b), avg_launch_us=statistics.fmean(moe_durs),
+            traffic=traffic,
+            kernel=(f"{dom_kernel} (the MoE phase: 86% of the layer's bytes)" if dom == "moe" else
+                    f"{dom_kernel} (sparse attention + W_UV / o_proj + FP8 MoE: 93% of the layer's bytes)"),
+            bytes_per_launch=statistics.fmean(dom_b), avg_launch_us=statistics.fmean(moe_durs),
         ),
         cpu_baseline=cpu,
     )
@@ -716,8 +726,9 @@ def main() -> int:
     ap.add_argument("--rows", type=int, default=8)
     ap.add_argument("--workload", choices=sorted(WORKLOADS), default="layer")
     ap.add_argument("--layers", type=int, default=61, help="stacked layers (layer workload)")
-    ap.add_argument("--unfused", action="store_true",
-                    help="layer workload: launch the attention and the back separately (four launches a layer)")
+    ap.add_argument("--mode", choices=("layer", "attn_back", "split"), default="layer",
+                    help="layer workload: the launch split (layer: front + one fused launch of attention, back "
+                         "and MoE; attn_back: three launches; split: four)")
     ap.add_argument("--sets", type=int, default=2, help="weight sets rotated over the steps")
     ap.add_argument("--batches", type=int, default=16, help="activation batches rotated")
     ap.add_argument("--ctx", type=int, default=32768, help="keys a row (attn workload)")

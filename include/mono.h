@@ -320,6 +320,54 @@ int mono_proj_set_fault(mono_proj* proj, int32_t site);
 int mono_attn_back_forward(mono_attn* attn, const mono_attn_args* args, const mono_proj_weights* w,
                            const mono_back_args* back, void* stream);
 
+/* --------------------------------------------------- the decoder layer */
+
+typedef struct mono_layer mono_layer;
+
+typedef struct {
+  int32_t device;
+  int32_t max_rows;     /* widest decode step, 1..16 */
+  int32_t max_ctx;      /* keys a row may hold, a multiple of 1024, <= 32768 */
+  float softmax_scale;  /* (qk_nope + qk_rope)^-1/2 = 192^-1/2 */
+  float route_scale;    /* routed_scaling_factor, 2.5 */
+  float eps;            /* post-attention RMSNorm epsilon, 1e-6 */
+} mono_layer_config;
+
+/* One step of one layer: the four parts' arguments as their own entry points take
+ * them. attn's q / iq / iqs / iw are the front's outputs and it reads the caches and
+ * step the front writes; back->o_lat is NULL or attn->out; moe->a is back->a. */
+typedef struct {
+  const mono_front_args* front;
+  const mono_attn_args* attn;
+  const mono_back_args* back;
+  const mono_moe_fp8_args* moe;
+} mono_layer_args;
+
+/* Replaces Glm53Runtime (runner.py:133-215) for a whole decoder layer: the mailboxes
+ * and guards of the front launch and of the fused attention + back + FP8 MoE launch. */
+int mono_layer_create(const mono_layer_config* cfg, mono_layer** out);
+int mono_layer_destroy(mono_layer* layer);
+/* Glm53LayerOp.launch (runner.py:240-321): the layer's front (as mono_front_forward),
+ * then the sparse attention, W_UV, o_proj + residual and the FP8 MoE + residual as ONE
+ * persistent launch (glm53/gfx950/kernel.py:2684-5187); results equal the four entry
+ * points'. Both launches are stream-ordered on `stream` and never synchronise. */
+int mono_layer_forward(mono_layer* layer, const mono_proj_weights* w, const mono_layer_args* args, void* stream);
+/* The two launches of mono_layer_forward on their own (same checks), for a caller that
+ * times or records between them: the front, then the fused rest. No counterpart in the
+ * reference, whose layer is one launch. */
+int mono_layer_front_forward(mono_layer* layer, const mono_proj_weights* w, const mono_layer_args* args,
+                             void* stream);
+int mono_layer_tail_forward(mono_layer* layer, const mono_proj_weights* w, const mono_layer_args* args,
+                            void* stream);
+int mono_layer_set_deadline(mono_layer* layer, double seconds);
+/* words: int32 [2 * MONO_GUARD_WORDS], the front launch's guard then the fused launch's
+ * (its wait sites: 0-3 the attention's, 4-5 the back's, 6 router logits, 7 route picks,
+ * 8 expert mid, 9 expert outputs, 10 the attention block's output rows). */
+int mono_layer_read_errors(mono_layer* layer, int32_t* words);
+int mono_layer_clear_errors(mono_layer* layer);
+/* launch 0: a front wait site (as mono_proj_set_fault); 1: a fused-launch site */
+int mono_layer_set_fault(mono_layer* layer, int32_t launch, int32_t site);
+
 #ifdef __cplusplus
 }
 #endif

@@ -83,6 +83,16 @@ class BackArgs(C.Structure):
     _fields_ = [("o_lat", _VP), ("h", _VP), ("a", _VP), ("o", _VP), ("rows", _I32), ("timeline", _VP)]
 
 
+class LayerConfig(C.Structure):
+    _fields_ = [("device", _I32), ("max_rows", _I32), ("max_ctx", _I32), ("softmax_scale", _F32),
+                ("route_scale", _F32), ("eps", _F32)]
+
+
+class LayerArgs(C.Structure):
+    _fields_ = [("front", C.POINTER(FrontArgs)), ("attn", C.POINTER(AttnArgs)), ("back", C.POINTER(BackArgs)),
+                ("moe", C.POINTER(MoeFp8Args))]
+
+
 # entry point -> (restype, argtypes); every name include/mono.h declares
 SIGNATURES = {
     "mono_abi_version": (C.c_int, []),
@@ -111,12 +121,24 @@ SIGNATURES = {
     "mono_proj_read_errors": (C.c_int, [_VP, C.POINTER(C.c_int32)]),
     "mono_proj_clear_errors": (C.c_int, [_VP]),
     "mono_proj_set_fault": (C.c_int, [_VP, C.c_int32]),
+    "mono_layer_create": (C.c_int, [C.POINTER(LayerConfig), C.POINTER(_VP)]),
+    "mono_layer_destroy": (C.c_int, [_VP]),
+    "mono_layer_forward": (C.c_int, [_VP, C.POINTER(ProjWeights), C.POINTER(LayerArgs), _VP]),
+    "mono_layer_front_forward": (C.c_int, [_VP, C.POINTER(ProjWeights), C.POINTER(LayerArgs), _VP]),
+    "mono_layer_tail_forward": (C.c_int, [_VP, C.POINTER(ProjWeights), C.POINTER(LayerArgs), _VP]),
+    "mono_layer_set_deadline": (C.c_int, [_VP, C.c_double]),
+    "mono_layer_read_errors": (C.c_int, [_VP, C.POINTER(C.c_int32)]),
+    "mono_layer_clear_errors": (C.c_int, [_VP]),
+    "mono_layer_set_fault": (C.c_int, [_VP, C.c_int32, C.c_int32]),
 }
 GUARD_WORDS = 4
 # wait sites of the launches (guard word 1 = site + 1)
 MOE_SITES = {0: "router logits", 1: "route picks", 2: "expert mid activations", 3: "expert outputs"}
 ATTN_SITES = {0: "index scores", 1: "selected slots", 2: "split partials", 3: "top-k team"}
 PROJ_SITES = {0: "stage-A partial sums", 1: "normed q_a", 2: "q_nope", 3: "raw index query", 4: "W_UV output"}
+# the fused attention + back + MoE launch of a layer runtime
+TAIL_SITES = {**ATTN_SITES, 4: "W_UV output", 5: "attention output", 6: "router logits", 7: "route picks",
+              8: "expert mid activations", 9: "expert outputs", 10: "attention block output rows"}
 
 _lock = threading.Lock()
 _lib = None

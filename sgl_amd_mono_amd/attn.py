@@ -82,39 +82,51 @@ class AttnRuntime(Runtime):
              timeline: torch.Tensor | None):
         """The checked launch arguments of ``forward`` (and of the fused attention + back
         launch): (mono_attn_args, out, debug outputs)."""
-        dev = self.device
-        S = step.q.shape[0] if step.q.dim() == 3 else -1
-        if not 1 <= S <= self.max_rows:
-            raise ValueError(f"q: expected [rows <= {self.max_rows}, {NH}, {DQK}], got {tuple(step.q.shape)}")
-        pages = caches.ikv.shape[0]
-        need(step.iq, "iq", (S, IH, ID // 2), torch.uint8, dev)
-        need(step.iqs, "iqs", (S, IH, ID // 32), torch.uint8, dev)
-        need(step.iw, "iw", (S, IH), torch.bfloat16, dev)
-        need(step.q, "q", (S, NH, DQK), torch.bfloat16, dev)
-        if step.page_table.dim() != 2 or step.page_table.shape[1] < self.max_ctx // PAGE:
-            raise ValueError(f"page_table: expected [rows, >= {self.max_ctx // PAGE}], got {tuple(step.page_table.shape)}")
-        need(step.page_table, "page_table", (S, step.page_table.shape[1]), torch.int32, dev)
-        need(step.seq_lens, "seq_lens", (S,), torch.int32, dev)
-        need(caches.ikv, "ikv", (pages, 4, PAGE, 16), torch.uint8, dev)
-        need(caches.iks, "iks", (pages, 4, PAGE), torch.uint8, dev)
-        need(caches.kv, "kv", (pages * PAGE, DQK), (torch.uint8, torch.float8_e4m3fn), dev)
-        if caches.kv_scale is not None:  # None: raw E4M3 rows (scale 1)
-            need(caches.kv_scale, "kv_scale", (pages * PAGE,), torch.float32, dev)
-        if out is None:
-            out = torch.empty(S, NH, DV, dtype=torch.bfloat16, device=dev)
-        need(out, "out", (S, NH, DV), torch.bfloat16, dev)
-        dbg = {}
-        if debug:
-            dbg = dict(scores=torch.zeros(S, self.max_ctx, dtype=torch.float32, device=dev),
-                       topk=torch.empty(S, TOPK, dtype=torch.int32, device=dev))
-        P = _lib.ptr
-        args = _lib.AttnArgs(
-            iq=P(step.iq), iqs=P(step.iqs), iw=P(step.iw), ikv=P(caches.ikv), iks=P(caches.iks),
-            q=P(step.q), kv=P(caches.kv), kv_scale=P(caches.kv_scale), page_table=P(step.page_table),
-            seq_lens=P(step.seq_lens), pt_stride=step.page_table.shape[1], n_pages=pages, out=P(out),
-            rows=S, scores=P(dbg.get("scores")), topk=P(dbg.get("topk")), timeline=P(timeline),
-        )  # fmt: skip
-        if timeline is not None:
-            need(timeline, "timeline", (self.n_tasks(S), 4), torch.int64, dev)
-        return args, out, dbg
+        return attn_args(self.device, self.max_rows, self.max_ctx, step, caches, out, debug, timeline)
+
+
+def n_tasks(max_ctx: int, rows: int) -> int:
+    """Tasks of one attention launch over ``rows`` rows (the timeline's length)."""
+    n_score = -(-rows * (max_ctx // 1024) // 16) * 16  # padded to whole top-k teams
+    return n_score + rows * 16 + rows * SPLITS + rows * (NH // 2)
+
+
+def attn_args(dev, max_rows: int, max_ctx: int, step: AttnStep, caches: AttnCaches, out: torch.Tensor | None,
+              debug: bool, timeline: torch.Tensor | None):
+    """Checked mono_attn_args for a runtime of ``max_rows`` x ``max_ctx`` on ``dev``:
+    (args, out, debug outputs)."""
+    S = step.q.shape[0] if step.q.dim() == 3 else -1
+    if not 1 <= S <= max_rows:
+        raise ValueError(f"q: expected [rows <= {max_rows}, {NH}, {DQK}], got {tuple(step.q.shape)}")
+    pages = caches.ikv.shape[0]
+    need(step.iq, "iq", (S, IH, ID // 2), torch.uint8, dev)
+    need(step.iqs, "iqs", (S, IH, ID // 32), torch.uint8, dev)
+    need(step.iw, "iw", (S, IH), torch.bfloat16, dev)
+    need(step.q, "q", (S, NH, DQK), torch.bfloat16, dev)
+    if step.page_table.dim() != 2 or step.page_table.shape[1] < max_ctx // PAGE:
+        raise ValueError(f"page_table: expected [rows, >= {max_ctx // PAGE}], got {tuple(step.page_table.shape)}")
+    need(step.page_table, "page_table", (S, step.page_table.shape[1]), torch.int32, dev)
+    need(step.seq_lens, "seq_lens", (S,), torch.int32, dev)
+    need(caches.ikv, "ikv", (pages, 4, PAGE, 16), torch.uint8, dev)
+    need(caches.iks, "iks", (pages, 4, PAGE), torch.uint8, dev)
+    need(caches.kv, "kv", (pages * PAGE, DQK), (torch.uint8, torch.float8_e4m3fn), dev)
+    if caches.kv_scale is not None:  # None: raw E4M3 rows (scale 1)
+        need(caches.kv_scale, "kv_scale", (pages * PAGE,), torch.float32, dev)
+    if out is None:
+        out = torch.empty(S, NH, DV, dtype=torch.bfloat16, device=dev)
+    need(out, "out", (S, NH, DV), torch.bfloat16, dev)
+    dbg = {}
+    if debug:
+        dbg = dict(scores=torch.zeros(S, max_ctx, dtype=torch.float32, device=dev),
+                   topk=torch.empty(S, TOPK, dtype=torch.int32, device=dev))
+    P = _lib.ptr
+    args = _lib.AttnArgs(
+        iq=P(step.iq), iqs=P(step.iqs), iw=P(step.iw), ikv=P(caches.ikv), iks=P(caches.iks),
+        q=P(step.q), kv=P(caches.kv), kv_scale=P(caches.kv_scale), page_table=P(step.page_table),
+        seq_lens=P(step.seq_lens), pt_stride=step.page_table.shape[1], n_pages=pages, out=P(out),
+        rows=S, scores=P(dbg.get("scores")), topk=P(dbg.get("topk")), timeline=P(timeline),
+    )  # fmt: skip
+    if timeline is not None:
+        need(timeline, "timeline", (n_tasks(max_ctx, S), 4), torch.int64, dev)
+    return args, out, dbg
 

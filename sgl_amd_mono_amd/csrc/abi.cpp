@@ -14,6 +14,7 @@
 #include <string>
 
 #include "attn_back_ops.h"
+#include "layer_ops.h"
 #include "attn_ops.h"
 #include "mono.h"
 #include "moe_ops.h"
@@ -277,8 +278,7 @@ static int check_moe(const mono_moe* m, int rows) {
   return check_device(m->device);
 }
 
-extern "C" int mono_moe_fp8_forward(mono_moe* m, const mono_moe_fp8_args* args, void* stream) {
-  using namespace mono::moe;
+static int check_moe_fp8(const mono_moe* m, const mono_moe_fp8_args* args) {
   if (!args) return fail(MONO_EINVAL, "mono_moe_fp8_forward: args is NULL");
   if (int rc = check_moe(m, args->rows)) return rc;
   if (m->cfg.weight_format != MONO_WEIGHT_FP8_BLOCK128 || m->cfg.router != MONO_ROUTER_SIGMOID_BIAS)
@@ -292,6 +292,12 @@ extern "C" int mono_moe_fp8_forward(mono_moe* m, const mono_moe_fp8_args* args, 
   REQUIRE_PTR(args->w2);
   REQUIRE_PTR(args->s2);
   REQUIRE_PTR(args->out);
+  return MONO_OK;
+}
+
+extern "C" int mono_moe_fp8_forward(mono_moe* m, const mono_moe_fp8_args* args, void* stream) {
+  using namespace mono::moe;
+  if (int rc = check_moe_fp8(m, args)) return rc;
   MoeFp8Args g(*args, m->cfg.route_scale, m->cfg.eps);
   hipError_t e = moe_fp8_forward(g, m->grid, m->mail, m->guard, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return fail(MONO_EHIP, "launching the FP8 MoE: %s", hipGetErrorString(e));
@@ -446,8 +452,8 @@ extern "C" int mono_attn_forward(mono_attn* a, const mono_attn_args* args, void*
   return ok();
 }
 
-extern "C" int mono_attn_back_forward(mono_attn* a, const mono_attn_args* args, const mono_proj_weights* w,
-                                      const mono_back_args* back, void* stream) {
+static int check_attn_back(const mono_attn* a, const mono_attn_args* args, const mono_proj_weights* w,
+                           const mono_back_args* back) {
   using namespace mono::attn;
   if (!args || !w || !back) return fail(MONO_EINVAL, "mono_attn_back_forward: args, w and back must be non-NULL");
   if (!live(a, ATTN_MAGIC)) return fail(MONO_ESTATE, "not a live attention runtime");
@@ -478,6 +484,13 @@ extern "C" int mono_attn_back_forward(mono_attn* a, const mono_attn_args* args, 
   REQUIRE_PTR(w->s_o);
   REQUIRE_PTR(back->h);
   REQUIRE_PTR(back->a);
+  return MONO_OK;
+}
+
+extern "C" int mono_attn_back_forward(mono_attn* a, const mono_attn_args* args, const mono_proj_weights* w,
+                                      const mono_back_args* back, void* stream) {
+  using namespace mono::attn;
+  if (int rc = check_attn_back(a, args, w, back)) return rc;
   int per_cu = 0;
   HIP_TRY(mono::fused::attn_back_occupancy(&per_cu));
   if (per_cu < 1) return fail(MONO_ESTATE, "the fused attention + back kernel does not fit on a CU");
@@ -654,4 +667,163 @@ extern "C" int mono_proj_read_errors(mono_proj* p, int32_t* words) {
 extern "C" int mono_proj_clear_errors(mono_proj* p) {
   if (!live(p, PROJ_MAGIC)) return fail(MONO_ESTATE, "not a live projection runtime");
   return guard_clear(p);
+}
+
+// ------------------------------------------------------------------ decoder layer
+
+// One decoder layer's runtimes: the projection, attention and FP8 MoE mailboxes and
+// guards, private to the layer (never handed out on their own), and the o_proj tiles'
+// done words of the fused launch. The front launch runs under the projection guard;
+// the fused launch (attention, back, MoE) under the attention guard, whose tickets tag
+// every mailbox word it writes (the MoE mailboxes included: no other launch writes
+// them, so their tags never collide).
+struct mono_layer {
+  uint32_t magic = 0;
+  mono_proj* p = nullptr;
+  mono_attn* a = nullptr;
+  mono_moe* m = nullptr;
+  uint64_t* a_done = nullptr;
+};
+static const uint32_t LAYER_MAGIC = 0x6c617972u;
+static bool layer_live(const mono_layer* L) { return L && L->magic == LAYER_MAGIC; }
+
+static int layer_release(mono_layer* L) {
+  int rc = MONO_OK;
+  if (L->a_done) {
+    hipError_t e = hipFree(L->a_done);
+    if (e != hipSuccess) rc = fail(MONO_EHIP, "hipFree: %s", hipGetErrorString(e));
+    L->a_done = nullptr;
+  }
+  if (L->m) rc = mono_moe_destroy(L->m) ? MONO_EHIP : rc;
+  if (L->a) rc = mono_attn_destroy(L->a) ? MONO_EHIP : rc;
+  if (L->p) rc = mono_proj_destroy(L->p) ? MONO_EHIP : rc;
+  L->m = nullptr;
+  L->a = nullptr;
+  L->p = nullptr;
+  L->magic = 0;
+  return rc;
+}
+
+extern "C" int mono_layer_create(const mono_layer_config* cfg, mono_layer** out) {
+  if (!cfg || !out) return fail(MONO_EINVAL, "mono_layer_create: cfg and out must be non-NULL");
+  *out = nullptr;
+  const mono_layer_config& c = *cfg;
+  if (c.max_rows < 1 || c.max_rows > mono::moe::MAX_ROWS)
+    return fail(MONO_EINVAL, "max_rows must be in [1, %d], got %d", mono::moe::MAX_ROWS, c.max_rows);
+  if (int rc = check_device(c.device)) return rc;
+  int per_cu = 0;
+  HIP_TRY(mono::layer::tail_occupancy(&per_cu));
+  if (per_cu < 1) return fail(MONO_ESTATE, "the fused layer kernel does not fit on a CU");
+  mono_layer* L = new mono_layer();
+  const mono_proj_config pc{c.device, c.max_rows};
+  const mono_attn_config ac{c.device, c.max_rows, c.max_ctx, c.softmax_scale};
+  const mono_moe_config mc{c.device, c.max_rows, 7168, 256, 8, 512, MONO_WEIGHT_FP8_BLOCK128,
+                           MONO_ROUTER_SIGMOID_BIAS, c.route_scale, c.eps};
+  int rc = mono_proj_create(&pc, &L->p);
+  if (!rc) rc = mono_attn_create(&ac, &L->a);
+  if (!rc) rc = mono_moe_create(&mc, &L->m);
+  if (!rc) {
+    hipError_t e = hipMalloc(&L->a_done, mono::DONE_BYTES);
+    if (e != hipSuccess) {
+      L->a_done = nullptr;
+      rc = fail(MONO_ENOMEM, "hipMalloc(%zu) for the layer's done words: %s", (size_t)mono::DONE_BYTES,
+                hipGetErrorString(e));
+    } else {
+      e = hipMemset(L->a_done, 0, mono::DONE_BYTES);
+      if (e == hipSuccess) e = hipDeviceSynchronize();
+      if (e != hipSuccess) rc = fail(MONO_EHIP, "clearing the layer's done words: %s", hipGetErrorString(e));
+    }
+  }
+  if (rc) {
+    const std::string why = g_error;
+    (void)layer_release(L);
+    delete L;
+    return fail(rc, "%s", why.c_str());
+  }
+  L->magic = LAYER_MAGIC;
+  *out = L;
+  return ok();
+}
+
+extern "C" int mono_layer_destroy(mono_layer* L) {
+  if (!L) return ok();
+  if (!layer_live(L)) return fail(MONO_ESTATE, "mono_layer_destroy: not a live layer runtime");
+  const int rc = layer_release(L);
+  delete L;
+  return rc ? rc : ok();
+}
+
+static int layer_launch(mono_layer* L, const mono_proj_weights* w, const mono_layer_args* args, void* stream,
+                        bool front, bool tail) {
+  if (!layer_live(L)) return fail(MONO_ESTATE, "not a live layer runtime");
+  if (!args || !w || !args->front || !args->attn || !args->back || !args->moe)
+    return fail(MONO_EINVAL, "mono_layer_forward: w, args and its four parts must be non-NULL");
+  const mono_front_args& f = *args->front;
+  const mono_attn_args& at = *args->attn;
+  const int rows = f.rows;
+  if (at.rows != rows || args->back->rows != rows || args->moe->rows != rows)
+    return fail(MONO_EINVAL, "front, attn, back and moe must have the same rows (%d, %d, %d, %d)", rows, at.rows,
+                args->back->rows, args->moe->rows);
+  if (at.q != f.q || at.iq != f.iq || at.iqs != f.iqs || at.iw != f.iw)
+    return fail(MONO_EINVAL, "attn's q, iq, iqs and iw must be the front's outputs");
+  if (at.ikv != f.ikv || at.iks != f.iks || at.kv != f.kv || at.kv_scale != f.kv_scale ||
+      at.page_table != f.page_table || at.seq_lens != f.seq_lens)
+    return fail(MONO_EINVAL, "attn must read the caches and step the front writes");
+  if (args->moe->a != args->back->a) return fail(MONO_EINVAL, "moe->a must be back->a: the MoE reads the back's output");
+  if (int rc = check_attn_back(L->a, args->attn, w, args->back)) return rc;
+  if (int rc = check_moe_fp8(L->m, args->moe)) return rc;
+  if (front) {
+    if (int rc = mono_front_forward(L->p, w, args->front, stream)) return rc;
+  }
+  if (!tail) return ok();
+  mono_back_args b = *args->back;
+  b.o_lat = at.out;
+  const mono::attn::AttnArgs g = attn_args(L->a, at);
+  const mono::moe::MoeFp8Args m(*args->moe, L->m->cfg.route_scale, L->m->cfg.eps);
+  hipError_t e = mono::layer::tail_forward(g, L->a->mail, L->a->guard, *w, b, L->a->back_mail, m, L->m->mail,
+                                           L->a_done, L->a->grid, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(MONO_EHIP, "launching the fused attention + back + MoE: %s", hipGetErrorString(e));
+  return ok();
+}
+
+extern "C" int mono_layer_forward(mono_layer* L, const mono_proj_weights* w, const mono_layer_args* args,
+                                  void* stream) {
+  return layer_launch(L, w, args, stream, true, true);
+}
+
+extern "C" int mono_layer_front_forward(mono_layer* L, const mono_proj_weights* w, const mono_layer_args* args,
+                                        void* stream) {
+  return layer_launch(L, w, args, stream, true, false);
+}
+
+extern "C" int mono_layer_tail_forward(mono_layer* L, const mono_proj_weights* w, const mono_layer_args* args,
+                                       void* stream) {
+  return layer_launch(L, w, args, stream, false, true);
+}
+
+extern "C" int mono_layer_set_deadline(mono_layer* L, double seconds) {
+  if (!layer_live(L)) return fail(MONO_ESTATE, "not a live layer runtime");
+  if (int rc = mono_proj_set_deadline(L->p, seconds)) return rc;
+  return mono_attn_set_deadline(L->a, seconds);
+}
+
+extern "C" int mono_layer_set_fault(mono_layer* L, int32_t launch, int32_t site) {
+  if (!layer_live(L)) return fail(MONO_ESTATE, "not a live layer runtime");
+  if (launch == 0) return mono_proj_set_fault(L->p, site);
+  if (launch == 1) return mono_attn_set_fault(L->a, site);
+  return fail(MONO_EINVAL, "launch must be 0 (front) or 1 (attention + back + MoE), got %d", launch);
+}
+
+extern "C" int mono_layer_read_errors(mono_layer* L, int32_t* words) {
+  if (!layer_live(L)) return fail(MONO_ESTATE, "not a live layer runtime");
+  if (!words) return fail(MONO_EINVAL, "words is NULL");
+  if (int rc = mono_proj_read_errors(L->p, words)) return rc;
+  return mono_attn_read_errors(L->a, words + MONO_GUARD_WORDS);
+}
+
+extern "C" int mono_layer_clear_errors(mono_layer* L) {
+  if (!layer_live(L)) return fail(MONO_ESTATE, "not a live layer runtime");
+  if (int rc = mono_proj_clear_errors(L->p)) return rc;
+  if (int rc = mono_attn_clear_errors(L->a)) return rc;
+  return mono_moe_clear_errors(L->m);
 }

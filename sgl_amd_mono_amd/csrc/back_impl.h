@@ -84,6 +84,10 @@ class Back {
     merged = merge_done;
   }
 
+  // A later phase of the launch reads `a`: each stage-O task stores its rows with
+  // device-coherent stores and then puts done word t (of NT_O, replicated) at a_done.
+  MONO_DEV void publish_a(uint64_t* done) { a_done = done; }
+
   static constexpr int N_TASKS = HEADS + NT_O;
 
   // This workgroup's tasks when the list's first task sits at index `base` of a longer
@@ -110,6 +114,7 @@ class Back {
   int tid, lane, wave, g, r, G, S;
   uint64_t waited = 0;
   const uint64_t* merged = nullptr;  // the attention merges' done words (fused launch)
+  uint64_t* a_done = nullptr;        // stage O's done words for a later phase (fused launch)
 
   // timeline row of task T: start, inputs-ready and end ticks, workgroup << 8 | stage
   MONO_DEV void stamp(int T, uint64_t t0, int kind) const {
@@ -205,8 +210,17 @@ class Back {
       if (s < S) {
         const size_t at = (size_t)s * HIDDEN + row;
         const float hv = bf16_bits_to_f32(static_cast<const uint16_t*>(A.h)[at]);
-        static_cast<uint16_t*>(A.a)[at] = f32_to_bf16_bits(__fadd_rn(hv, y));
+        const uint16_t av = f32_to_bf16_bits(__fadd_rn(hv, y));
+        if (a_done)  // read by another workgroup of this launch: write through to memory
+          __builtin_amdgcn_raw_buffer_store_b16(av, coherent_rsrc(A.a, S * HIDDEN * 2), at * 2, 0, SC1);
+        else
+          static_cast<uint16_t*>(A.a)[at] = av;
       }
+    }
+    if (a_done) {
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();  // every row of the tile is stored
+      put_done(a_done, t, gd.tag);
     }
     __syncthreads();
     return true;

@@ -125,6 +125,53 @@ class FrontOut:
         )
 
 
+def _rows(t: torch.Tensor, name: str, max_rows: int) -> int:
+    if t.dim() != 2 or not 1 <= t.shape[0] <= max_rows:
+        raise ValueError(f"{name}: expected [rows <= {max_rows}, {HIDDEN}], got {tuple(t.shape)}")
+    return t.shape[0]
+
+
+def front_args(dev, max_rows: int, h: torch.Tensor, seq_lens: torch.Tensor, page_table: torch.Tensor,
+               caches: AttnCaches, w: ProjWeights, rope_cos: torch.Tensor, rope_sin: torch.Tensor,
+               out: "FrontOut | None", check_weights: bool, timeline: torch.Tensor | None):
+    """Checked mono_front_args (and the weight table) for a runtime of ``max_rows`` on
+    ``dev``: (args, out, weights)."""
+    S = _rows(h, "h", max_rows)
+    need(h, "h", (S, HIDDEN), torch.bfloat16, dev)
+    need(seq_lens, "seq_lens", (S,), torch.int32, dev)
+    if page_table.dim() != 2 or page_table.shape[0] < S:
+        raise ValueError(f"page_table: expected [>= {S}, pages], got {tuple(page_table.shape)}")
+    need(page_table, "page_table", tuple(page_table.shape), torch.int32, dev)
+    pages = caches.ikv.shape[0]
+    need(caches.ikv, "ikv", (pages, 4, 64, 16), torch.uint8, dev)
+    need(caches.iks, "iks", (pages, 4, 64), torch.uint8, dev)
+    need(caches.kv, "kv", (pages * 64, KV_LORA + PE_DIM), torch.uint8, dev)
+    if caches.kv_scale is not None:  # None: raw E4M3 rows (scale 1)
+        need(caches.kv_scale, "kv_scale", (pages * 64,), torch.float32, dev)
+    if rope_cos.dim() != 2 or rope_cos.shape[1] != PE_DIM // 2:
+        raise ValueError(f"rope_cos: expected [max_pos, {PE_DIM // 2}], got {tuple(rope_cos.shape)}")
+    need(rope_cos, "rope_cos", tuple(rope_cos.shape), torch.float32, dev)
+    need(rope_sin, "rope_sin", tuple(rope_cos.shape), torch.float32, dev)
+    if check_weights:
+        w.check(dev)
+    out = FrontOut.empty(S, dev) if out is None else out
+    need(out.q, "q", (S, HEADS, KV_LORA + PE_DIM), torch.bfloat16, dev)
+    need(out.iq, "iq", (S, INDEX_HEADS, INDEX_DIM // 2), torch.uint8, dev)
+    need(out.iqs, "iqs", (S, INDEX_HEADS, INDEX_DIM // 32), torch.uint8, dev)
+    need(out.iw, "iw", (S, INDEX_HEADS), torch.bfloat16, dev)
+    P = _lib.ptr
+    args = _lib.FrontArgs(
+        h=P(h), seq_lens=P(seq_lens), page_table=P(page_table), pt_stride=page_table.shape[1],
+        n_pages=pages, rope_cos=P(rope_cos), rope_sin=P(rope_sin), max_pos=rope_cos.shape[0],
+        ikv=P(caches.ikv), iks=P(caches.iks), kv=P(caches.kv), kv_scale=P(caches.kv_scale),
+        q=P(out.q), iq=P(out.iq), iqs=P(out.iqs), iw=P(out.iw), rows=S, timeline=P(timeline),
+    )  # fmt: skip
+    if timeline is not None:
+        need(timeline, "timeline", (front_tasks(S), 4), torch.int64, dev)
+    ws = w.c_struct()
+    return args, out, ws
+
+
 class ProjRuntime(Runtime):
     """The C library's projection handle for a widest step ``max_rows`` (<= 16)."""
 
@@ -149,40 +196,8 @@ class ProjRuntime(Runtime):
         FrontOut; writes each row's MLA cache row and FP4 index key in place.
         ``timeline`` (int64 [front_tasks(rows), 4]) receives each task's start,
         inputs-ready and end ticks and workgroup << 8 | stage."""
-        dev = self.device
-        S = self._rows(h, "h")
-        need(h, "h", (S, HIDDEN), torch.bfloat16, dev)
-        need(seq_lens, "seq_lens", (S,), torch.int32, dev)
-        if page_table.dim() != 2 or page_table.shape[0] < S:
-            raise ValueError(f"page_table: expected [>= {S}, pages], got {tuple(page_table.shape)}")
-        need(page_table, "page_table", tuple(page_table.shape), torch.int32, dev)
-        pages = caches.ikv.shape[0]
-        need(caches.ikv, "ikv", (pages, 4, 64, 16), torch.uint8, dev)
-        need(caches.iks, "iks", (pages, 4, 64), torch.uint8, dev)
-        need(caches.kv, "kv", (pages * 64, KV_LORA + PE_DIM), torch.uint8, dev)
-        if caches.kv_scale is not None:  # None: raw E4M3 rows (scale 1)
-            need(caches.kv_scale, "kv_scale", (pages * 64,), torch.float32, dev)
-        if rope_cos.dim() != 2 or rope_cos.shape[1] != PE_DIM // 2:
-            raise ValueError(f"rope_cos: expected [max_pos, {PE_DIM // 2}], got {tuple(rope_cos.shape)}")
-        need(rope_cos, "rope_cos", tuple(rope_cos.shape), torch.float32, dev)
-        need(rope_sin, "rope_sin", tuple(rope_cos.shape), torch.float32, dev)
-        if check_weights:
-            w.check(dev)
-        out = FrontOut.empty(S, dev) if out is None else out
-        need(out.q, "q", (S, HEADS, KV_LORA + PE_DIM), torch.bfloat16, dev)
-        need(out.iq, "iq", (S, INDEX_HEADS, INDEX_DIM // 2), torch.uint8, dev)
-        need(out.iqs, "iqs", (S, INDEX_HEADS, INDEX_DIM // 32), torch.uint8, dev)
-        need(out.iw, "iw", (S, INDEX_HEADS), torch.bfloat16, dev)
-        P = _lib.ptr
-        args = _lib.FrontArgs(
-            h=P(h), seq_lens=P(seq_lens), page_table=P(page_table), pt_stride=page_table.shape[1],
-            n_pages=pages, rope_cos=P(rope_cos), rope_sin=P(rope_sin), max_pos=rope_cos.shape[0],
-            ikv=P(caches.ikv), iks=P(caches.iks), kv=P(caches.kv), kv_scale=P(caches.kv_scale),
-            q=P(out.q), iq=P(out.iq), iqs=P(out.iqs), iw=P(out.iw), rows=S, timeline=P(timeline),
-        )  # fmt: skip
-        if timeline is not None:
-            need(timeline, "timeline", (front_tasks(S), 4), torch.int64, dev)
-        ws = w.c_struct()
+        args, out, ws = front_args(self.device, self.max_rows, h, seq_lens, page_table, caches, w, rope_cos,
+                                   rope_sin, out, check_weights, timeline)
         _lib.check(_lib.lib().mono_front_forward(self._h, C.byref(ws), C.byref(args), self._stream()))
         return out
 
@@ -247,43 +262,107 @@ class LayerWeights:
     moe: Fp8MoeWeights
 
 
+class LayerHandle(Runtime):
+    """The C library's layer runtime (mono_layer): the front launch's and the fused
+    attention + back + MoE launch's mailboxes and guards in one handle."""
+
+    PREFIX = "mono_layer"
+    KIND = "layer"
+
+    def __init__(self, max_rows: int, max_ctx: int, device=None):
+        from .attn import SOFTMAX_SCALE
+        from .moe import FP8_MOE
+
+        super().__init__(device)
+        self._create(_lib.LayerConfig(device=self.device.index, max_rows=max_rows, max_ctx=max_ctx,
+                                      softmax_scale=SOFTMAX_SCALE, route_scale=FP8_MOE.route_scale,
+                                      eps=FP8_MOE.eps))
+
+    def set_fault(self, site: int, launch: int = 1) -> None:
+        """Tests of the fail-stop path: every wait at ``site`` of ``launch`` (0 front,
+        1 the fused rest) fails at once (-1: off)."""
+        _lib.check(self._fn("set_fault")(self._h, int(launch), int(site)))
+
+    def error_words(self) -> list[int]:
+        """The two launches' guard words (synchronises): front, then the fused rest."""
+        words = (C.c_int32 * (2 * _lib.GUARD_WORDS))()
+        with torch.cuda.device(self.device):
+            _lib.check(self._fn("read_errors")(self._h, words))
+        return list(words)
+
+    def check_errors(self) -> None:
+        w = self.error_words()
+        for k, (name, sites) in enumerate((("front", _lib.PROJ_SITES), ("attention + back + MoE", _lib.TAIL_SITES))):
+            e = w[4 * k:4 * k + 4]
+            if e[1]:
+                site = e[1] - 1
+                raise _lib.MonoError(
+                    _lib.MONO_ESTATE,
+                    f"layer {name} launch (tag {e[2]}) stopped: wait '{sites.get(site, site)}' passed its deadline "
+                    f"in workgroup {e[3]}; the runtime refuses launches until clear_errors()",
+                )
+
+
 class LayerRuntime:
     """One GPU's TP=4 share of a DeepSeek-V3.2-shaped decoder layer with an FP4 indexer
-    three persistent launches on the caller's stream, each phase's
-    outputs in scratch this runtime owns (the reference launches the same body as one
-    grid, glm53/gfx950/kernel.py:6-45, with the TP all-reduces that are local residual
-    adds here):
+    its launches on the caller's stream and each phase's outputs
+    in scratch this runtime owns. The reference launches the whole layer as one grid
+    (glm53/gfx950/kernel.py:6-45) with the TP all-reduces that are local residual adds
+    here. ``mode`` picks the launch split; every mode gives the same results:
 
-        front (mono_front_forward) -> sparse attention + back (mono_attn_back_forward)
-          -> FP8 MoE + residual (mono_moe_fp8_forward)
-
-    ``fused=False`` launches the attention (mono_attn_forward) and the back
-    (mono_back_forward) separately: four launches, the same results.
+    * ``"layer"`` (default, mono_layer_forward): the front, then the sparse attention,
+      the back and the FP8 MoE as ONE persistent launch;
+    * ``"attn_back"``: front; attention + back (mono_attn_back_forward); MoE;
+    * ``"split"``: front; attention; back; MoE (four launches).
 
     No call synchronises with the host, so a caller may capture a step in a HIP graph.
     """
 
-    def __init__(self, max_rows: int = 8, max_ctx: int = 32768, device=None, fused: bool = True):
+    # the launches of a layer, the names of forward's on_phase indices
+    MODES = {"layer": ("front", "attn_back_moe"), "attn_back": ("front", "attn_back", "moe"),
+             "split": ("front", "attn", "back", "moe")}
+
+    def __init__(self, max_rows: int = 8, max_ctx: int = 32768, device=None, mode: str = "layer",
+                 fused: bool | None = None):
         from .attn import AttnRuntime
         from .moe import FP8_MOE, MoeRuntime
 
+        if fused is not None:  # the older switch: fused=False is the four-launch split
+            mode = "attn_back" if fused else "split"
+        if mode not in self.MODES:
+            raise ValueError(f"mode must be one of {sorted(self.MODES)}, got {mode!r}")
         if not 1 <= max_rows <= MAX_ROWS:
             raise ValueError(f"max_rows must be in [1, {MAX_ROWS}], got {max_rows}")
-        self.proj = ProjRuntime(max_rows, device)
-        self.device = self.proj.device
-        self.attn = AttnRuntime(max_rows, max_ctx, device=self.device)
-        self.moe = MoeRuntime(FP8_MOE, max_rows, self.device)
+        self.mode = mode
         self.max_rows, self.max_ctx = max_rows, max_ctx
-        self.fused = fused
+        if mode == "layer":
+            self.handle = LayerHandle(max_rows, max_ctx, device)
+            self.device = self.handle.device
+            self.parts = (self.handle,)
+        else:
+            self.proj = ProjRuntime(max_rows, device)
+            self.device = self.proj.device
+            self.attn = AttnRuntime(max_rows, max_ctx, device=self.device)
+            self.moe = MoeRuntime(FP8_MOE, max_rows, self.device)
+            self.parts = (self.proj, self.attn, self.moe)
+        self.geo = FP8_MOE
         # the launches of a layer, the names of forward's on_phase indices
-        self.phases = ("front", "attn_back", "moe") if fused else ("front", "attn", "back", "moe")
+        self.phases = self.MODES[mode]
         self._front = FrontOut.empty(max_rows, self.device)
         self._o_lat = torch.empty(max_rows, HEADS, KV_LORA, dtype=torch.bfloat16, device=self.device)
         self._a = torch.empty(max_rows, HIDDEN, dtype=torch.bfloat16, device=self.device)
 
     def close(self) -> None:
-        for rt in (self.proj, self.attn, self.moe):
+        for rt in self.parts:
             rt.close()
+
+    def set_deadline(self, seconds: float) -> None:
+        for rt in self.parts:
+            rt.set_deadline(seconds)
+
+    def clear_errors(self) -> None:
+        for rt in self.parts:
+            rt.clear_errors()
 
     def forward(self, h: torch.Tensor, seq_lens: torch.Tensor, page_table: torch.Tensor, caches: AttnCaches,
                 w: LayerWeights, rope_cos: torch.Tensor, rope_sin: torch.Tensor, out: torch.Tensor | None = None,
@@ -294,40 +373,63 @@ class LayerRuntime:
         slots, o_lat, a, the MoE routing and sum) as copies. ``on_phase(i)`` (if given)
         is called after the launch of phase i (``self.phases[i]``) is enqueued, e.g. to
         record timing events between the phases."""
-        from .attn import AttnStep
+        from .attn import AttnStep, attn_args
+        from .moe import fp8_args
 
         S = h.shape[0] if h.dim() == 2 else -1
         if not 1 <= S <= self.max_rows:
             raise ValueError(f"h: expected [rows <= {self.max_rows}, {HIDDEN}], got {tuple(h.shape)}")
         fo = FrontOut(q=self._front.q[:S], iq=self._front.iq[:S], iqs=self._front.iqs[:S], iw=self._front.iw[:S])
         mark = on_phase if on_phase is not None else (lambda i: None)
-        self.proj.front(h, seq_lens, page_table, caches, w.proj, rope_cos, rope_sin, out=fo,
-                        check_weights=check_weights)
-        mark(0)
         step = AttnStep(iq=fo.iq, iqs=fo.iqs, iw=fo.iw, q=fo.q, page_table=page_table, seq_lens=seq_lens)
-        if self.fused:
-            res = attn_back(self.attn, step, caches, w.proj, h, o_lat=self._o_lat[:S], a=self._a[:S],
-                            check_weights=check_weights, debug=keep)
-            o_lat, a = res[0], res[1]
-            adbg = res[2] if keep else None
-            mark(1)
+        if self.mode == "layer":
+            dev = self.device
+            fargs, _, ws = front_args(dev, self.max_rows, h, seq_lens, page_table, caches, w.proj, rope_cos,
+                                      rope_sin, fo, check_weights, None)
+            aargs, o_lat, adbg = attn_args(dev, self.max_rows, self.max_ctx, step, caches, self._o_lat[:S], keep,
+                                           None)
+            a = self._a[:S]
+            need(h, "h", (S, HIDDEN), torch.bfloat16, dev)
+            bargs = _lib.BackArgs(o_lat=_lib.ptr(o_lat), h=_lib.ptr(h), a=_lib.ptr(a), o=None, rows=S, timeline=None)
+            margs, x, mdbg = fp8_args(dev, self.max_rows, self.geo, a, w.moe, out, keep)
+            largs = _lib.LayerArgs(C.pointer(fargs), C.pointer(aargs), C.pointer(bargs), C.pointer(margs))
+            lib, hd, st = _lib.lib(), self.handle._h, self.handle._stream()
+            if on_phase is None:
+                _lib.check(lib.mono_layer_forward(hd, C.byref(ws), C.byref(largs), st))
+            else:  # the two launches one by one, marked in between
+                _lib.check(lib.mono_layer_front_forward(hd, C.byref(ws), C.byref(largs), st))
+                mark(0)
+                _lib.check(lib.mono_layer_tail_forward(hd, C.byref(ws), C.byref(largs), st))
+                mark(1)
         else:
-            if keep:
-                o_lat, adbg = self.attn.forward(step, caches, out=self._o_lat[:S], debug=True)
+            self.proj.front(h, seq_lens, page_table, caches, w.proj, rope_cos, rope_sin, out=fo,
+                            check_weights=check_weights)
+            mark(0)
+            if self.mode == "attn_back":
+                res = attn_back(self.attn, step, caches, w.proj, h, o_lat=self._o_lat[:S], a=self._a[:S],
+                                check_weights=check_weights, debug=keep)
+                o_lat, a = res[0], res[1]
+                adbg = res[2] if keep else None
+                mark(1)
             else:
-                o_lat = self.attn.forward(step, caches, out=self._o_lat[:S])
-            mark(1)
-            a = self.proj.back(o_lat, h, w.proj, a=self._a[:S], check_weights=check_weights)
-            mark(2)
-        if not keep:
-            x = self.moe.forward_fp8(a, w.moe, out=out)
+                if keep:
+                    o_lat, adbg = self.attn.forward(step, caches, out=self._o_lat[:S], debug=True)
+                else:
+                    o_lat = self.attn.forward(step, caches, out=self._o_lat[:S])
+                mark(1)
+                a = self.proj.back(o_lat, h, w.proj, a=self._a[:S], check_weights=check_weights)
+                mark(2)
+            if keep:
+                x, mdbg = self.moe.forward_fp8(a, w.moe, out=out, debug=True)
+            else:
+                x = self.moe.forward_fp8(a, w.moe, out=out)
             mark(len(self.phases) - 1)
+        if not keep:
             return x
-        x, dbg = self.moe.forward_fp8(a, w.moe, out=out, debug=True)
         inter = dict(q=fo.q.clone(), iq=fo.iq.clone(), iqs=fo.iqs.clone(), iw=fo.iw.clone(), o_lat=o_lat.clone(),
-                     a=a.clone(), index_scores=adbg["scores"], topk_slots=adbg["topk"], **dbg)
+                     a=a.clone(), index_scores=adbg["scores"], topk_slots=adbg["topk"], **mdbg)
         return x, inter
 
     def check_errors(self) -> None:
-        for rt in (self.proj, self.attn, self.moe):
+        for rt in self.parts:
             rt.check_errors()

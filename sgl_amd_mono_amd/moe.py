@@ -86,37 +86,7 @@ class MoeRuntime(Runtime):
                     debug: bool = False):
         """``a + MoE(a)`` for one decode step. ``debug`` also
         returns the routing (scores, top-k ids / weights) and the f32 MoE sum."""
-        g, dev = self.geo, self.device
-        H, E, I, K = g.hidden, g.n_experts, g.inter, g.top_k
-        if a.dim() != 2 or not 1 <= a.shape[0] <= self.max_rows:
-            raise ValueError(f"a: expected [rows <= {self.max_rows}, {H}], got {tuple(a.shape)}")
-        S = a.shape[0]
-        need(a, "a", (S, H), torch.bfloat16, dev)
-        need(w.g_post, "g_post", (H,), torch.bfloat16, dev)
-        need(w.w_router, "w_router", (E, H), torch.bfloat16, dev)
-        need(w.bias, "bias", (E,), torch.float32, dev)
-        need(w.w13, "w13", (E + 1, 2 * I, H), FP8_TYPES, dev)
-        need(w.s13, "s13", (E + 1, 2 * I // 128, H // 128), torch.float32, dev)
-        need(w.w2, "w2", (E + 1, H, I), FP8_TYPES, dev)
-        need(w.s2, "s2", (E + 1, H // 128, I // 128), torch.float32, dev)
-        if out is None:
-            out = torch.empty_like(a)
-        need(out, "out", (S, H), torch.bfloat16, dev)
-        dbg = {}
-        if debug:
-            dbg = dict(
-                y=torch.empty(S, H, dtype=torch.float32, device=dev),
-                scores=torch.empty(S, E, dtype=torch.float32, device=dev),
-                topk_ids=torch.empty(S, K, dtype=torch.int32, device=dev),
-                topk_w=torch.empty(S, K, dtype=torch.float32, device=dev),
-            )
-        P = _lib.ptr
-        args = _lib.MoeFp8Args(
-            a=P(a), g_post=P(w.g_post), w_router=P(w.w_router), bias=P(w.bias),
-            w13=P(w.w13), s13=P(w.s13), w2=P(w.w2), s2=P(w.s2), out=P(out), rows=S,
-            y=P(dbg.get("y")), scores=P(dbg.get("scores")),
-            topk_ids=P(dbg.get("topk_ids")), topk_w=P(dbg.get("topk_w")),
-        )  # fmt: skip
+        args, out, dbg = fp8_args(self.device, self.max_rows, self.geo, a, w, out, debug)
         _lib.check(_lib.lib().mono_moe_fp8_forward(self._h, C.byref(args), self._stream()))
         return (out, dbg) if debug else out
 
@@ -152,3 +122,40 @@ class MoeRuntime(Runtime):
         )  # fmt: skip
         _lib.check(_lib.lib().mono_moe_mxfp4_forward(self._h, C.byref(args), self._stream()))
         return (out, dbg) if debug else out
+
+def fp8_args(dev, max_rows: int, geo: MoeGeometry, a: torch.Tensor, w: Fp8MoeWeights, out: torch.Tensor | None,
+             debug: bool):
+    """Checked mono_moe_fp8_args for a runtime of ``max_rows`` on ``dev``: (args, out,
+    debug outputs)."""
+    g = geo
+    H, E, I, K = g.hidden, g.n_experts, g.inter, g.top_k
+    if a.dim() != 2 or not 1 <= a.shape[0] <= max_rows:
+        raise ValueError(f"a: expected [rows <= {max_rows}, {H}], got {tuple(a.shape)}")
+    S = a.shape[0]
+    need(a, "a", (S, H), torch.bfloat16, dev)
+    need(w.g_post, "g_post", (H,), torch.bfloat16, dev)
+    need(w.w_router, "w_router", (E, H), torch.bfloat16, dev)
+    need(w.bias, "bias", (E,), torch.float32, dev)
+    need(w.w13, "w13", (E + 1, 2 * I, H), FP8_TYPES, dev)
+    need(w.s13, "s13", (E + 1, 2 * I // 128, H // 128), torch.float32, dev)
+    need(w.w2, "w2", (E + 1, H, I), FP8_TYPES, dev)
+    need(w.s2, "s2", (E + 1, H // 128, I // 128), torch.float32, dev)
+    if out is None:
+        out = torch.empty_like(a)
+    need(out, "out", (S, H), torch.bfloat16, dev)
+    dbg = {}
+    if debug:
+        dbg = dict(
+            y=torch.empty(S, H, dtype=torch.float32, device=dev),
+            scores=torch.empty(S, E, dtype=torch.float32, device=dev),
+            topk_ids=torch.empty(S, K, dtype=torch.int32, device=dev),
+            topk_w=torch.empty(S, K, dtype=torch.float32, device=dev),
+        )
+    P = _lib.ptr
+    args = _lib.MoeFp8Args(
+        a=P(a), g_post=P(w.g_post), w_router=P(w.w_router), bias=P(w.bias),
+        w13=P(w.w13), s13=P(w.s13), w2=P(w.w2), s2=P(w.s2), out=P(out), rows=S,
+        y=P(dbg.get("y")), scores=P(dbg.get("scores")),
+        topk_ids=P(dbg.get("topk_ids")), topk_w=P(dbg.get("topk_w")),
+    )  # fmt: skip
+    return args, out, dbg

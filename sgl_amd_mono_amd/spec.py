@@ -265,8 +265,7 @@ def _build(model, hf_config, ctx) -> _Built:
         raise ValueError(f"monokernel: the kernels run at most {MAX_ROWS} rows; this server routes {sorted(ctx.widths)}")
     device = cos.device
     rt = LayerRuntime(max(widths), max_context(context_len), device)
-    for part in (rt.proj, rt.attn, rt.moe):
-        part.set_deadline(getattr(ctx, "deadline_s", None) or DEADLINE_S)
+    rt.set_deadline(getattr(ctx, "deadline_s", None) or DEADLINE_S)
     return _Built(model, layers, rt, cos, sin, device, context_len)
 
 

@@ -181,3 +181,68 @@ def test_layer_raw_e4m3_mla_rows(gpu_device):
     _close(it["o_lat"].cpu(), o_ref, "attention o_lat (unscaled rows)")
     b = ol.back(it["o_lat"].cpu(), x.cpu(), _cpu_proj(w.proj))
     _close(it["a"].cpu(), b["a"], "back a")
+
+
+@pytest.mark.parametrize("rows", [1, 8, 16])
+def test_layer_launch_modes_agree_bitwise(gpu_device, rows):
+    """The fused layer launch (mono_layer_forward: front, then attention + back + MoE as
+    one launch) gives bit for bit what the three- and four-launch splits give, its
+    intermediates included, over two steps in a row (fresh tags on the second)."""
+    ctx = 8192
+    cos, sin = workloads.rope_tables(ctx, gpu_device)
+    lens = ([8192, 1500, 65, 2049, 4000, 64, 7000, 300] * 2)[:rows]
+    print(f"[modes] rows={rows}", flush=True)
+    w = LayerWeights(proj=workloads.proj_weights(gpu_device, seed=31),
+                     moe=workloads.fp8_moe_weights(FP8_MOE, gpu_device, seed=32))
+    x = workloads.rows_bf16(rows, ol.HIDDEN, gpu_device, seed=34)
+    got = {}
+    for mode in ("layer", "attn_back", "split"):
+        step, caches = workloads.attn_case(lens, gpu_device, seed=33, max_ctx=ctx)
+        rt = LayerRuntime(rows, ctx, gpu_device, mode=mode)
+        try:
+            outs = []
+            for _ in range(2):
+                outs.append(rt.forward(x, step.seq_lens, step.page_table, caches, w, cos, sin, keep=True))
+            torch.cuda.synchronize()
+            rt.check_errors()
+        finally:
+            rt.close()
+        got[mode] = (outs, caches.kv.clone(), caches.ikv.clone())
+    ref_outs, ref_kv, ref_ikv = got["split"]
+    for mode in ("layer", "attn_back"):
+        outs, kv, ikv = got[mode]
+        assert torch.equal(kv, ref_kv) and torch.equal(ikv, ref_ikv), mode
+        for (xo, it), (xr, ir) in zip(outs, ref_outs):
+            assert torch.equal(xo, xr), (mode, float((xo.float() - xr.float()).abs().max()))
+            for k in ("q", "o_lat", "a", "topk_slots", "topk_ids", "topk_w", "y"):
+                assert torch.equal(it[k], ir[k]), (mode, k)
+
+
+def test_layer_launch_fail_stop(gpu_device):
+    """A forced wait failure in the fused launch (the MoE's wait on the attention block's
+    output rows, site 10) stops it without a fault: the error names the site, later
+    launches are refused until the errors are cleared, then the layer runs again."""
+    ctx, rows = 4096, 2
+    cos, sin = workloads.rope_tables(ctx, gpu_device)
+    w = LayerWeights(proj=workloads.proj_weights(gpu_device, seed=41),
+                     moe=workloads.fp8_moe_weights(FP8_MOE, gpu_device, seed=42))
+    step, caches = workloads.attn_case([4096, 100], gpu_device, seed=43, max_ctx=ctx)
+    x = workloads.rows_bf16(rows, ol.HIDDEN, gpu_device, seed=44)
+    rt = LayerRuntime(rows, ctx, gpu_device)
+    try:
+        good = rt.forward(x, step.seq_lens, step.page_table, caches, w, cos, sin).clone()
+        torch.cuda.synchronize()
+        rt.check_errors()
+        rt.handle.set_fault(10, launch=1)
+        rt.forward(x, step.seq_lens, step.page_table, caches, w, cos, sin)
+        torch.cuda.synchronize()
+        with pytest.raises(Exception, match="attention block output rows"):
+            rt.check_errors()
+        rt.handle.set_fault(-1, launch=1)
+        rt.clear_errors()
+        again = rt.forward(x, step.seq_lens, step.page_table, caches, w, cos, sin)
+        torch.cuda.synchronize()
+        rt.check_errors()
+        assert torch.equal(again, good)
+    finally:
+        rt.close()
