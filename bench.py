@@ -544,6 +544,23 @@ def bench_layer(args, dev):
                 ph[p].append(pev[k][l][i].elapsed_time(pev[k][l][i + 1]) * 1e3)
     ph_us = {p: statistics.fmean(v) for p, v in ph.items()}
     eager_layer_us = sum(ph_us.values())
+    # one launch a layer: each layer's launch timed alone (an event pair around it, eager)
+    one = rt.launches == 1
+    layer_durs = []
+    if one:
+        lev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(L)]
+               for _ in range(n_eager)]
+        torch.cuda.synchronize()
+        for k in range(n_eager):
+            x = x_in
+            for l, (w, step, caches) in enumerate(layers):
+                lev[k][l][0].record(stream)
+                x = rt.forward(x, step.seq_lens, step.page_table, caches, w, cos, sin, out=xb[l % 2],
+                               check_weights=False)
+                lev[k][l][1].record(stream)
+        torch.cuda.synchronize()
+        rt.check_errors()
+        layer_durs = [lev[k][l][0].elapsed_time(lev[k][l][1]) * 1e3 for k in range(n_eager) for l in range(L)]
 
     w0 = layers[0][0]
     moe_fixed = 256 * 7168 * 2 + 256 * 4 + 7168 * 2 + 2 * S * 7168 * 2
@@ -558,12 +575,12 @@ def bench_layer(args, dev):
         phase_bytes["attn_back"] = phase_bytes.pop("attn") + phase_bytes.pop("back")
     if "attn_back_moe" in phases:
         phase_bytes["attn_back_moe"] = phase_bytes.pop("attn") + phase_bytes.pop("back") + phase_bytes.pop("moe")
-    # the dominant launch: the MoE's own, or the fused attention + back + MoE launch
-    dom = "moe" if "moe" in phases else "attn_back_moe"
-    dom_kernel = {"moe": "k_moe_fp8", "attn_back_moe": "k_layer_tail"}[dom]
-    dom_fixed = phase_bytes[dom] - statistics.fmean(moe_b)  # its bytes besides the experts
+    # the dominant launch: the whole layer's (one launch a layer), else the MoE's own
+    dom = "layer" if one else "moe"
+    dom_kernel = {"moe": "k_moe_fp8", "layer": "k_layer"}[dom]
+    dom_fixed = (sum(phase_bytes.values()) if one else phase_bytes["moe"]) - statistics.fmean(moe_b)
     dom_b = [b + dom_fixed for b in moe_b]  # per layer (each layer's own distinct experts)
-    moe_durs = ph[dom]
+    moe_durs = layer_durs if one else ph[dom]
     traffic = read_traffic(dom_kernel)
     moe_achieved = statistics.fmean(
         b / (t * 1e-6) for b, t in zip([dom_b[l] for _ in range(n_eager) for l in range(L)], moe_durs)) / 1e9
@@ -583,12 +600,13 @@ def bench_layer(args, dev):
         dtype="fp8_e4m3 weights (bf16 / fp8 MFMA, f32 accumulate), fp4 index, fp8 kv",
         config=dict(workload="BASELINE config 5: full fused decoder layer, one GPU's TP=4 share, 61 stacked layers",
                     rows=S, context=ctx, layers=L, hidden=7168, heads=32, experts=256, top_k=8, shared_experts=1,
-                    inter=512, launches_per_layer=len(phases), graph=True),
+                    inter=512, launches_per_layer=rt.launches, graph=True),
         extra=dict(
             us_per_layer_median=statistics.median(per) / L, us_per_layer_min=min(per) / L,
             us_per_layer_max=max(per) / L, rows_per_s=S / (us * 1e-6), step_wall_s=wall / args.steps,
             layer_algorithmic_bytes=layer_bytes, layer_achieved_gbs=layer_bytes / (us * 1e-6) / 1e9,
             phases_us_eager=ph_us, eager_layer_us=eager_layer_us,
+            layer_launch_us_eager=statistics.fmean(layer_durs) if one else None,
             phases_algorithmic_bytes=phase_bytes,
             phases_achieved_gbs={p: phase_bytes[p] / (ph_us[p] * 1e-6) / 1e9 for p in phases},
             distinct_experts_mean=statistics.fmean(distinct),
@@ -597,7 +615,7 @@ def bench_layer(args, dev):
             bound="hbm", achieved=moe_achieved, peak=HBM_PEAK_GBS, unit="GB/s", frac=moe_achieved / HBM_PEAK_GBS,
             traffic=traffic,
             kernel=(f"{dom_kernel} (the MoE phase: 86% of the layer's bytes)" if dom == "moe" else
-                    f"{dom_kernel} (sparse attention + W_UV / o_proj + FP8 MoE: 93% of the layer's bytes)"),
+                    f"{dom_kernel} (the whole decoder layer, one launch)"),
             bytes_per_launch=statistics.fmean(dom_b), avg_launch_us=statistics.fmean(moe_durs),
         ),
         cpu_baseline=cpu,

@@ -138,7 +138,9 @@ ATTN_SITES = {0: "index scores", 1: "selected slots", 2: "split partials", 3: "t
 PROJ_SITES = {0: "stage-A partial sums", 1: "normed q_a", 2: "q_nope", 3: "raw index query", 4: "W_UV output"}
 # the fused attention + back + MoE launch of a layer runtime
 TAIL_SITES = {**ATTN_SITES, 4: "W_UV output", 5: "attention output", 6: "router logits", 7: "route picks",
-              8: "expert mid activations", 9: "expert outputs", 10: "attention block output rows"}
+              8: "expert mid activations", 9: "expert outputs", 10: "attention block output rows",
+              **{11 + k: f"front: {v}" for k, v in {**PROJ_SITES, 5: "normed input rows"}.items()},
+              17: "front index query and keys", 18: "front q"}
 
 _lock = threading.Lock()
 _lib = None

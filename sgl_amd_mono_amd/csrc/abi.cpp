@@ -180,7 +180,7 @@ int guard_set_deadline(RuntimeBase* r, double seconds) {
 }
 
 int guard_set_fault(RuntimeBase* r, int32_t site) {
-  if (site < -1 || site > 15) return fail(MONO_EINVAL, "fault site must be -1 (none) or a wait site 0..15, got %d", site);
+  if (site < -1 || site > 31) return fail(MONO_EINVAL, "fault site must be -1 (none) or a wait site 0..31, got %d", site);
   r->guard.fault_site = site;
   return ok();
 }
@@ -547,6 +547,7 @@ extern "C" int mono_proj_create(const mono_proj_config* cfg, mono_proj** out) {
   const size_t o_adone = cv.take((size_t)mono::proj::MAX_A_TASKS * 8);
   const size_t o_qdone = cv.take(mono::DONE_BYTES);
   const size_t o_cdone = cv.take((size_t)mono::proj::C_TASKS * 8);
+  const size_t o_fdone = cv.take(mono::DONE_BYTES);
   mono_proj* p = new mono_proj();
   p->magic = PROJ_MAGIC;
   p->cfg = c;
@@ -567,6 +568,7 @@ extern "C" int mono_proj_create(const mono_proj_config* cfg, mono_proj** out) {
   p->mail.odone = reinterpret_cast<uint64_t*>(p->at(o_odone));
   p->mail.xn = reinterpret_cast<uint32_t*>(p->at(o_xn));
   p->mail.xdone = reinterpret_cast<uint64_t*>(p->at(o_xdone));
+  p->mail.fdone = reinterpret_cast<uint64_t*>(p->at(o_fdone));
   *out = p;
   return ok();
 }
@@ -587,8 +589,7 @@ static int check_proj(const mono_proj* p, const mono_proj_weights* w, int rows) 
   return check_device(p->device);
 }
 
-extern "C" int mono_front_forward(mono_proj* p, const mono_proj_weights* w, const mono_front_args* args,
-                                  void* stream) {
+static int check_front(const mono_proj* p, const mono_proj_weights* w, const mono_front_args* args) {
   if (!args) return fail(MONO_EINVAL, "mono_front_forward: args is NULL");
   if (int rc = check_proj(p, w, args->rows)) return rc;
   REQUIRE_PTR(w->g_in);
@@ -622,6 +623,12 @@ extern "C" int mono_front_forward(mono_proj* p, const mono_proj_weights* w, cons
   if (args->pt_stride < 1) return fail(MONO_EINVAL, "pt_stride must be positive, got %d", args->pt_stride);
   if (args->n_pages < 1) return fail(MONO_EINVAL, "n_pages must be positive, got %d", args->n_pages);
   if (args->max_pos < 1) return fail(MONO_EINVAL, "max_pos must be positive, got %d", args->max_pos);
+  return MONO_OK;
+}
+
+extern "C" int mono_front_forward(mono_proj* p, const mono_proj_weights* w, const mono_front_args* args,
+                                  void* stream) {
+  if (int rc = check_front(p, w, args)) return rc;
   // a NULL kv_scale writes raw E4M3 rows (scale 1) and stores its 1.0 in the runtime's word
   mono_front_args fa = *args;
   int kv_mask = -1;
@@ -772,16 +779,26 @@ static int layer_launch(mono_layer* L, const mono_proj_weights* w, const mono_la
   if (args->moe->a != args->back->a) return fail(MONO_EINVAL, "moe->a must be back->a: the MoE reads the back's output");
   if (int rc = check_attn_back(L->a, args->attn, w, args->back)) return rc;
   if (int rc = check_moe_fp8(L->m, args->moe)) return rc;
-  if (front) {
-    if (int rc = mono_front_forward(L->p, w, args->front, stream)) return rc;
-  }
-  if (!tail) return ok();
+  if (front && !tail) return mono_front_forward(L->p, w, args->front, stream);
   mono_back_args b = *args->back;
   b.o_lat = at.out;
   const mono::attn::AttnArgs g = attn_args(L->a, at);
   const mono::moe::MoeFp8Args m(*args->moe, L->m->cfg.route_scale, L->m->cfg.eps);
-  hipError_t e = mono::layer::tail_forward(g, L->a->mail, L->a->guard, *w, b, L->a->back_mail, m, L->m->mail,
-                                           L->a_done, L->a->grid, static_cast<hipStream_t>(stream));
+  hipError_t e;
+  if (front) {  // the whole layer as one launch (the front's checks are mono_front_forward's)
+    if (int rc = check_front(L->p, w, args->front)) return rc;
+    mono_front_args fa = *args->front;
+    int kv_mask = -1;
+    if (!fa.kv_scale) {
+      fa.kv_scale = L->p->unit;
+      kv_mask = 0;
+    }
+    e = mono::layer::layer_forward(*w, fa, L->p->mail, kv_mask, g, L->a->mail, L->a->guard, b, L->a->back_mail, m,
+                                   L->m->mail, L->a_done, L->a->grid, static_cast<hipStream_t>(stream));
+  } else {
+    e = mono::layer::tail_forward(g, L->a->mail, L->a->guard, *w, b, L->a->back_mail, m, L->m->mail, L->a_done,
+                                  L->a->grid, static_cast<hipStream_t>(stream));
+  }
   if (e != hipSuccess) return fail(MONO_EHIP, "launching the fused attention + back + MoE: %s", hipGetErrorString(e));
   return ok();
 }

@@ -36,6 +36,7 @@
 
 #include "attn_ops.h"
 #include "common.h"
+#include "proj_ops.h"
 #include "sync.h"
 
 namespace mono {
@@ -124,6 +125,11 @@ struct Args {
   int32_t* topk;
   int64_t* timeline;
   float scale;
+  // the front of the layer ran earlier in this launch: its replicated done words
+  // (proj::Mail::fdone: FD_B + s row s's index key and head weights, FD_E + 8 s + j its
+  // index query, FD_D + h head h of q), awaited at wait sites fsite and fsite + 1
+  const uint64_t* fdone;
+  int fsite;
   bool publish_out;  // a later stage of the launch reads `out`: each merge puts a done word
   Mail mail;
   GuardArgs guard;
@@ -206,7 +212,7 @@ class Step {
     const int n_sc = n_score(), n_topk = A.rows * TEAM;
     const int n_split = A.rows * SPLITS;
     const int total = n_tasks();
-    score_stage(blockIdx.x, A.rows * CH);
+    if (!score_stage(blockIdx.x, A.rows * CH)) return false;
     // a workgroup's list is ordered by stage: one loop a stage keeps each loop body to
     // one task kind (and its registers)
     int T = first_at_or_after(n_sc);
@@ -238,6 +244,7 @@ class Step {
   Lds& L;
   Guard gd;
   int tid, lane, wave, g, r, G, CH;
+  bool q_ready = false;  // the front's q has been awaited (a fused launch)
   uint64_t waited = 0;
 
   MONO_DEV int row_len(int s) const { return min(max(A.seq_lens[s], 0), A.mail.max_ctx); }
@@ -285,10 +292,20 @@ class Step {
   };
 
   MONO_DEV void score_load(int T, ScoreOps& o) {
+    score_where(T, o);
+    if (o.k0 >= o.n) return;
+    score_query(o);
+    score_keys(o);
+  }
+
+  MONO_DEV void score_where(int T, ScoreOps& o) const {
     o.s = T / CH;
     o.c = T % CH;
     o.k0 = o.c * CHUNK + wave * KEYS_WAVE;
     o.n = row_len(o.s);
+  }
+
+  MONO_DEV void score_query(ScoreOps& o) const {
     if (o.k0 >= o.n) return;
 #pragma unroll
     for (int ht = 0; ht < IH / 16; ++ht) {
@@ -299,6 +316,10 @@ class Step {
       o.w2[ht][0] = w4[0];
       o.w2[ht][1] = w4[1];
     }
+  }
+
+  MONO_DEV void score_keys(ScoreOps& o) const {
+    if (o.k0 >= o.n) return;
     int pg[KEYS_WAVE / PAGE];
 #pragma unroll
     for (int i = 0; i < KEYS_WAVE / PAGE; ++i) pg[i] = page_of(o.s, o.k0 + i * PAGE);
@@ -376,11 +397,27 @@ class Step {
 
   // The workgroup's score tasks T0, T0 + G, ... < n_score, each task's loads issued
   // before the previous task computes.
-  MONO_DEV void score_stage(int T0, int n_score) {
-    if (T0 >= n_score) return;
+  MONO_DEV bool score_stage(int T0, int n_score) {
+    if (T0 >= n_score) return true;
     if (tid < 256) L.u.sc.hist[tid] = 0u;
     ScoreOps cur, nxt;
-    score_load(T0, cur);
+    if (A.fdone) {
+      // the front of this launch writes each row's index query, head weights and new
+      // key: the first task's keys stream before the wait unless its chunk holds its
+      // row's new key (position n - 1), then every row's front outputs are awaited
+      score_where(T0, cur);
+      const bool fresh = cur.n > 0 && cur.c == (cur.n - 1) / CHUNK;
+      if (!fresh) score_keys(cur);
+      const uint64_t* fd = done_copy(A.fdone);
+      const int nr = A.rows;
+      if (!hint_wait(nr * (1 + IH / 8), [fd, nr](int i) { return fd + (i < nr ? proj::FD_B + i : proj::FD_E + i - nr); },
+                     A.fsite, gd))
+        return false;
+      if (fresh) score_keys(cur);
+      score_query(cur);
+    } else {
+      score_load(T0, cur);
+    }
     for (int T = T0; T < n_score; T += G) {
       const uint64_t t0 = now_ticks();
       const bool more = T + G < n_score;
@@ -390,6 +427,7 @@ class Step {
       if (more) cur = nxt;
     }
     __syncthreads();  // the top-k tasks reuse the LDS
+    return true;
   }
 
   // ---------------------------------------------------------------- top-k
@@ -746,6 +784,11 @@ class Step {
       split_done(s, j);
       return true;
     }
+    if (A.fdone && !q_ready) {  // every head of q from the front of this launch
+      const uint64_t* fd = done_copy(A.fdone) + proj::FD_D;
+      if (!hint_wait(NH, [fd](int i) { return fd + i; }, A.fsite + 1, gd)) return false;
+      q_ready = true;
+    }
     {
       constexpr int QL = (NH * DQK / 8 + AT - 1) / AT;
       u32x4 qv[QL];
@@ -983,6 +1026,8 @@ void fill_args(Args& a, const AttnArgs& g, const Mail& mail, const GuardArgs& gu
   a.timeline = g.timeline;
   a.scale = g.softmax_scale;
   a.publish_out = false;
+  a.fdone = nullptr;
+  a.fsite = 0;
   a.mail = mail;
   a.guard = guard;
 }

@@ -13,6 +13,7 @@
 // and tag; the back's sites are 4 and 5, the MoE's are MOE_SITE0 + 0..4.
 #include "attn_step.h"
 #include "back_impl.h"
+#include "front_impl.h"
 #include "layer_ops.h"
 #include "moe_fp8_step.h"
 
@@ -34,12 +35,18 @@ union Lds {
   moe::Lds mo;
 };
 
-__global__ __launch_bounds__(512, 1) void k_layer_tail(Args args) {
-  __shared__ Lds lds;
-  attn::Step st(args.at, lds.at);
-  if (!st.begin()) return;
-  const Guard g = st.guard();
-  if (!st.tasks()) return;
+struct LayerArgs {
+  proj::fr::Args fr;
+  Args tail;
+};
+
+union LayerLds {
+  Lds tail;
+  proj::fr::Lds fr;
+};
+
+// The back and the MoE after the attention, on the attention's guard.
+MONO_DEV void back_moe(const Args& args, Lds& lds, const attn::Step& st, const Guard& g) {
   __syncthreads();  // the LDS passes from the attention's layout to the back's
   {
     proj::Back bk(args.bk, lds.bk);
@@ -53,10 +60,40 @@ __global__ __launch_bounds__(512, 1) void k_layer_tail(Args args) {
   ms.run();
 }
 
+__global__ __launch_bounds__(512, 1) void k_layer_tail(Args args) {
+  __shared__ Lds lds;
+  attn::Step st(args.at, lds.at);
+  if (!st.begin()) return;
+  const Guard g = st.guard();
+  if (!st.tasks()) return;
+  back_moe(args, lds, st, g);
+}
+
+// The whole decoder layer: the front's tasks first (under the attention's tag), then
+// the attention, whose score tasks and splits wait on the front's done words.
+__global__ __launch_bounds__(512, 1) void k_layer(LayerArgs args) {
+  __shared__ LayerLds lds;
+  attn::Step st(args.tail.at, lds.tail.at);
+  if (!st.begin()) return;  // the tag lives in registers from here on
+  const Guard g = st.guard();
+  {
+    proj::fr::Front f(args.fr, lds.fr);
+    f.adopt(g, FRONT_SITE0);
+    if (!f.tasks()) return;
+  }
+  __syncthreads();  // the LDS passes from the front's layout to the attention's
+  if (!st.tasks()) return;
+  back_moe(args.tail, lds.tail, st, g);
+}
+
 }  // namespace
 
 hipError_t tail_occupancy(int* blocks_per_cu) {
-  return hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, k_layer_tail, 512, 0);
+  int a = 0, b = 0;
+  hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&a, k_layer_tail, 512, 0);
+  if (e == hipSuccess) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, k_layer, 512, 0);
+  *blocks_per_cu = a < b ? a : b;
+  return e;
 }
 
 hipError_t tail_forward(const attn::AttnArgs& g, const attn::Mail& amail, const GuardArgs& guard,
@@ -75,6 +112,33 @@ hipError_t tail_forward(const attn::AttnArgs& g, const attn::Mail& amail, const 
   moe::fill_args(a.mo, m, mmail, guard);
   a.a_done = a_done;
   k_layer_tail<<<grid, 512, 0, st>>>(a);
+  return hipGetLastError();
+}
+
+hipError_t layer_forward(const mono_proj_weights& w, const mono_front_args& f, const proj::Mail& fmail,
+                         int kv_mask, const attn::AttnArgs& g, const attn::Mail& amail, const GuardArgs& guard,
+                         const mono_back_args& b, const proj::Mail& bmail, const moe::MoeFp8Args& m,
+                         const moe::Mail& mmail, uint64_t* a_done, int grid, hipStream_t st) {
+  if (f.rows != g.rows || f.rows < 1 || f.rows > proj::MAX_ROWS || g.rows > attn::MAX_ROWS || g.rows > moe::MAX_ROWS ||
+      b.rows != g.rows || m.rows != g.rows || grid < 1 || amail.max_ctx % attn::CHUNK || amail.max_ctx > attn::MAX_CTX)
+    return hipErrorInvalidConfiguration;
+  LayerArgs a;
+  a.fr.w = w;
+  a.fr.a = f;
+  a.fr.mail = fmail;
+  a.fr.guard = guard;
+  a.fr.kv_mask = kv_mask;
+  attn::fill_args(a.tail.at, g, amail, guard);
+  a.tail.at.publish_out = true;
+  a.tail.at.fdone = fmail.fdone;
+  a.tail.at.fsite = ATTN_FRONT_SITE;
+  a.tail.bk.w = w;
+  a.tail.bk.a = b;
+  a.tail.bk.mail = bmail;
+  a.tail.bk.guard = guard;
+  moe::fill_args(a.tail.mo, m, mmail, guard);
+  a.tail.a_done = a_done;
+  k_layer<<<grid, 512, 0, st>>>(a);
   return hipGetLastError();
 }
 

@@ -35,8 +35,14 @@ struct Mail {
   uint32_t* ob;     // [MAX_ROWS][HEADS * VDIM / 2]  W_UV o_lat, bf16 pairs (untagged; read
                     //                                after odone)
   uint64_t* odone;  // [HEADS], replicated           a head's ob is stored
+  uint64_t* fdone;  // [FD_WORDS], replicated         the front's outputs are stored, for a
+                    //                                later phase of the launch: FD_B + s (row
+                    //                                s's KV row, index key and head weights),
+                    //                                FD_E + e (index-query task e), FD_D + h
+                    //                                (head h of q: q_lat and q_pe)
   uint32_t* guard;  // [G_WORDS]
 };
+constexpr int FD_B = 0, FD_E = MAX_ROWS, FD_D = MAX_ROWS + MAX_ROWS * 8, FD_WORDS = FD_D + 32;
 constexpr size_t MAIL_WORDS[5] = {(size_t)MAX_PARTS * MAX_ROWS * N_A, (size_t)MAX_ROWS * Q_LORA / 2,
                                   (size_t)MAX_ROWS * HEADS * NOPE / 2, (size_t)MAX_ROWS * IH * ID / 2,
                                   (size_t)MAX_ROWS * HEADS * VDIM / 2};

@@ -67,6 +67,13 @@ MONO_DEV void st_agent_f32(float* p, float v) {
   __hip_atomic_store(reinterpret_cast<uint32_t*>(p), __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// A device-coherent (write-through) store of 1, 2, 4 or 8 bytes: data another
+// workgroup of the launch reads after a done word.
+template <class T>
+MONO_DEV void st_dev(T* p, T v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Untagged data behind a tagged done word: the producer stores it with device-coherent
 // buffer stores, waits for them (s_waitcnt 0) and a barrier, then puts the done word;
 // the consumer polls the done word, then reads the data with device-coherent loads.

@@ -310,8 +310,9 @@ class LayerRuntime:
     (glm53/gfx950/kernel.py:6-45) with the TP all-reduces that are local residual adds
     here. ``mode`` picks the launch split; every mode gives the same results:
 
-    * ``"layer"`` (default, mono_layer_forward): the front, then the sparse attention,
-      the back and the FP8 MoE as ONE persistent launch;
+    * ``"layer"`` (default, mono_layer_forward): the whole layer as ONE persistent
+      launch (front, sparse attention, back, FP8 MoE); with ``on_phase`` the front and
+      the rest run as two launches so a caller can time them apart;
     * ``"attn_back"``: front; attention + back (mono_attn_back_forward); MoE;
     * ``"split"``: front; attention; back; MoE (four launches).
 
@@ -348,6 +349,8 @@ class LayerRuntime:
         self.geo = FP8_MOE
         # the launches of a layer, the names of forward's on_phase indices
         self.phases = self.MODES[mode]
+        # launches a step of one layer takes without on_phase
+        self.launches = 1 if mode == "layer" else len(self.phases)
         self._front = FrontOut.empty(max_rows, self.device)
         self._o_lat = torch.empty(max_rows, HEADS, KV_LORA, dtype=torch.bfloat16, device=self.device)
         self._a = torch.empty(max_rows, HIDDEN, dtype=torch.bfloat16, device=self.device)

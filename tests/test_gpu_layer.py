@@ -218,10 +218,13 @@ def test_layer_launch_modes_agree_bitwise(gpu_device, rows):
                 assert torch.equal(it[k], ir[k]), (mode, k)
 
 
-def test_layer_launch_fail_stop(gpu_device):
-    """A forced wait failure in the fused launch (the MoE's wait on the attention block's
-    output rows, site 10) stops it without a fault: the error names the site, later
-    launches are refused until the errors are cleared, then the layer runs again."""
+@pytest.mark.parametrize("site,what", [(10, "attention block output rows"), (11, "front: stage-A partial sums"),
+                                       (17, "front index query and keys"), (18, "front q")])
+def test_layer_launch_fail_stop(gpu_device, site, what):
+    """A forced wait failure in the one-launch layer (the MoE's wait on the attention
+    block's output rows, the front's stage-A wait, the attention's waits on the front)
+    stops it without a fault: the error names the site, later launches are refused
+    until the errors are cleared, then the layer runs again."""
     ctx, rows = 4096, 2
     cos, sin = workloads.rope_tables(ctx, gpu_device)
     w = LayerWeights(proj=workloads.proj_weights(gpu_device, seed=41),
@@ -233,10 +236,10 @@ def test_layer_launch_fail_stop(gpu_device):
         good = rt.forward(x, step.seq_lens, step.page_table, caches, w, cos, sin).clone()
         torch.cuda.synchronize()
         rt.check_errors()
-        rt.handle.set_fault(10, launch=1)
+        rt.handle.set_fault(site, launch=1)
         rt.forward(x, step.seq_lens, step.page_table, caches, w, cos, sin)
         torch.cuda.synchronize()
-        with pytest.raises(Exception, match="attention block output rows"):
+        with pytest.raises(Exception, match=what):
             rt.check_errors()
         rt.handle.set_fault(-1, launch=1)
         rt.clear_errors()
