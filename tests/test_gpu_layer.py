@@ -249,3 +249,38 @@ def test_layer_launch_fail_stop(gpu_device, site, what):
         assert torch.equal(again, good)
     finally:
         rt.close()
+
+
+def test_layer_verify_chain_sees_its_own_draft_keys(gpu_device):
+    """MTP verify rows: four rows of one request at consecutive positions (sharing its
+    page table) in one step, the chain crossing a 1024-key chunk boundary. Each row
+    must score the keys the earlier rows write in the same step: the one-launch layer
+    gives bit for bit what the split launches give (where the front's launch ends
+    before the attention's starts), and every row selects the chain's earlier keys."""
+    ctx = 4096
+    cos, sin = workloads.rope_tables(ctx, gpu_device)
+    w = LayerWeights(proj=workloads.proj_weights(gpu_device, seed=51),
+                     moe=workloads.fp8_moe_weights(FP8_MOE, gpu_device, seed=52))
+    x = workloads.rows_bf16(4, ol.HIDDEN, gpu_device, seed=54)
+    lens = [1023, 1024, 1025, 1026]  # new keys at 1022 .. 1025
+    got = {}
+    for mode in ("layer", "split"):
+        step, caches = workloads.attn_case([ctx], gpu_device, seed=53, max_ctx=ctx)
+        pt = step.page_table[:1].repeat(4, 1).contiguous()
+        seq = torch.tensor(lens, dtype=torch.int32, device=gpu_device)
+        rt = LayerRuntime(4, ctx, gpu_device, mode=mode)
+        try:
+            got[mode] = rt.forward(x, seq, pt, caches, w, cos, sin, keep=True)
+            torch.cuda.synchronize()
+            rt.check_errors()
+        finally:
+            rt.close()
+    (xl, il), (xs, is_) = got["layer"], got["split"]
+    assert torch.equal(il["index_scores"], is_["index_scores"])
+    assert torch.equal(il["topk_slots"], is_["topk_slots"])
+    assert torch.equal(xl, xs)
+    # rows of at most 2048 keys select all of them, the chain's earlier keys included
+    pt0 = step.page_table[0].cpu().long()
+    for j, n in enumerate(lens):
+        want = (pt0[torch.arange(n) // 64] * 64 + torch.arange(n) % 64).to(torch.int32)
+        assert torch.equal(il["topk_slots"][j, :n].cpu(), want), j
