@@ -14,19 +14,25 @@
  *
  * Reference interfaces replaced (yuychang/sgl-amd-mono):
  *   - Glm53Runtime(key, rank, group, device)            glm53/gfx950/runner.py:133-215
- *       -> mono_moe_create / mono_attn_create (scratch, counters, guard words)
- *   - Glm53Runtime.set_deadline / advance_step          glm53/gfx950/runner.py:197-210
- *       -> mono_set_deadline / mono_advance_step
+ *       -> mono_layer_create (and mono_moe_create / mono_attn_create / mono_proj_create
+ *          for one phase): scratch, launch counters, guard words
+ *   - Glm53Runtime.set_deadline                          glm53/gfx950/runner.py:197-204
+ *       -> mono_layer_set_deadline (mono_*_set_deadline)
+ *   - Glm53Runtime.advance_step (the step epoch)        glm53/gfx950/runner.py:205-210
+ *       -> no call: every launch takes its tag from the guard's own ticket counter
  *   - Glm53LayerOp.launch(h, caches, cos, sin, step)    glm53/gfx950/runner.py:240-321
  *       (rt.dispatch of 42 raw data_ptr() ints + stream)
- *       -> mono_moe_fp8_forward  (its MoE half, stages 8-10, kernel.py:4199-5187)
+ *       -> mono_layer_forward    (the whole decoder layer, kernel.py:6-45)
  *       -> mono_front_forward    (its projections up to the index query, kernel.py:1367-2443)
-       -> mono_attn_forward     (its sparse-attention half, kernel.py:2684-4123)
-       -> mono_back_forward     (W_UV, o_proj and the residual, kernel.py:3975-4197)
+ *       -> mono_attn_forward     (its sparse-attention half, kernel.py:2684-4123)
+ *       -> mono_back_forward     (W_UV, o_proj and the residual, kernel.py:3975-4197)
+ *       -> mono_moe_fp8_forward  (its MoE half, stages 8-10, kernel.py:4199-5187)
  *   - minimax_m31 FFN launch, A16W4 experts              minimax_m31/ffn.py:1182-1378
  *       -> mono_moe_mxfp4_forward
  *   - guard error words read back by tests              common/guard.py:16-30,100-241
- *       -> mono_read_error_words
+ *       -> mono_layer_read_errors (mono_*_read_errors), mono_layer_pending_error
+ *   - test fault injection (SGLANG_AMD_MONO_FAULT_INJECT) common/guard.py:79-88
+ *       -> mono_layer_set_fault (mono_*_set_fault)
  */
 #ifndef MONO_GFX950_H
 #define MONO_GFX950_H
@@ -38,7 +44,7 @@
 extern "C" {
 #endif
 
-#define MONO_ABI_VERSION 1
+#define MONO_ABI_VERSION 2
 
 enum {
   MONO_OK = 0,
@@ -52,15 +58,22 @@ enum { MONO_ROUTER_SIGMOID_BIAS = 0, MONO_ROUTER_SOFTMAX = 1 };
 
 /* Guard words a runtime exposes (mono_*_read_errors), after the reference's guard
  * block (sgl_amd_mono/common/guard.py:16-30):
- *   [0] launch tickets (workgroups x launches so far)
- *   [1] 0, or 1 + the id of the first inter-workgroup wait that passed its deadline;
- *       sticky: every later launch of the runtime exits at once (fail-stop) until
+ *   [0] tag epochs completed (tags repeat every 2^32 - 2 launches; the first launch of
+ *       each later epoch zeroes the guard's mailboxes before anything runs)
+ *   [1] 0, or 1 + the id of the first inter-workgroup wait that passed its deadline
+ *       (31: the epoch scrub's barrier); sticky: every later launch under the guard
+ *       exits at once (fail-stop), writing NaN over its output, until
  *       mono_*_clear_errors
  *   [2] tag of the launch that failed
  *   [3] the workgroup that failed first
+ *   [4..5] launch tickets, u64 (workgroups x launches so far)
+ *   [6] scrub barrier arrivals
+ *   [7] 0
+ * Every launch that fails a wait, or that the sticky error refuses, also writes the
+ * error to a pinned host word (mono_layer_pending_error) and NaN over its output.
  * Wait sites of the MoE launch: 0 router logits, 1 route picks, 2 expert mid
  * activations, 3 expert outputs. */
-#define MONO_GUARD_WORDS 4
+#define MONO_GUARD_WORDS 8
 enum { MONO_WEIGHT_FP8_BLOCK128 = 0, MONO_WEIGHT_MXFP4 = 1 };
 
 /* Version of this ABI (MONO_ABI_VERSION of the library). */
@@ -344,7 +357,9 @@ typedef struct {
 } mono_layer_args;
 
 /* Replaces Glm53Runtime (runner.py:133-215) for a whole decoder layer: the mailboxes
- * and guards of the front launch and of the fused attention + back + FP8 MoE launch. */
+ * of the front, the attention, the back and the FP8 MoE, and ONE guard (one ticket
+ * counter, one set of error words) for every launch of the layer, whichever of
+ * mono_layer_forward / _front_forward / _tail_forward the caller mixes. */
 int mono_layer_create(const mono_layer_config* cfg, mono_layer** out);
 int mono_layer_destroy(mono_layer* layer);
 /* Glm53LayerOp.launch (runner.py:240-321): the layer's front (as mono_front_forward),
@@ -359,14 +374,31 @@ int mono_layer_front_forward(mono_layer* layer, const mono_proj_weights* w, cons
                              void* stream);
 int mono_layer_tail_forward(mono_layer* layer, const mono_proj_weights* w, const mono_layer_args* args,
                             void* stream);
+/* Deadline of every wait of the layer's launches (Glm53Runtime.set_deadline,
+ * runner.py:197-204; a serving caller passes half its watchdog, at most 60 s). */
 int mono_layer_set_deadline(mono_layer* layer, double seconds);
-/* words: int32 [2 * MONO_GUARD_WORDS], the front launch's guard then the fused launch's
- * (its wait sites: 0-3 the attention's, 4-5 the back's, 6 router logits, 7 route picks,
- * 8 expert mid, 9 expert outputs, 10 the attention block's output rows). */
+/* words: int32 [MONO_GUARD_WORDS], the layer's guard (synchronises). Wait sites: 0-3
+ * the attention's (index scores, selected slots, split partials, top-k team), 4 W_UV
+ * output, 5 attention output, 6 router logits, 7 route picks, 8 expert mid, 9 expert
+ * outputs, 10 the attention block's output rows, 11-16 the front's (stage-A partials,
+ * q_an, q_nope, raw index query, -, normed input rows), 17 the front's index outputs,
+ * 18 the front's q, 31 the tag-epoch scrub. */
 int mono_layer_read_errors(mono_layer* layer, int32_t* words);
+/* The layer's pinned host error word, without synchronising: 0, or 1 + the wait site
+ * of a launch that failed or was refused since the last clear (-1: not a live layer).
+ * No counterpart in the reference, which stops a failed launch by a GPU fault
+ * (common/guard.py:91-97); a serving caller checks it once a step. */
+int32_t mono_layer_pending_error(mono_layer* layer);
+/* Synchronise, clear the sticky error and the host word so the layer launches again. */
 int mono_layer_clear_errors(mono_layer* layer);
-/* launch 0: a front wait site (as mono_proj_set_fault); 1: a fused-launch site */
-int mono_layer_set_fault(mono_layer* layer, int32_t launch, int32_t site);
+/* Tests of the fail-stop path (the reference's SGLANG_AMD_MONO_FAULT_INJECT
+ * rank:site:after, common/guard.py:79-88): every wait at `site` of every launch from
+ * the `after`-th next launch on fails at once, as if its deadline had passed (after 0:
+ * the next launch; synchronises when after > 0); site -1 turns it off. */
+int mono_layer_set_fault(mono_layer* layer, int32_t site, int64_t after);
+/* Tests of the tag epochs (synchronises): the next launch takes launch ordinal
+ * `ordinal`, i.e. tag ordinal % (2^32 - 2) + 1. No counterpart in the reference. */
+int mono_layer_set_launch_ordinal(mono_layer* layer, uint64_t ordinal);
 
 #ifdef __cplusplus
 }

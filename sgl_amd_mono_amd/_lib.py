@@ -11,7 +11,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libmono_gfx950.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 MONO_OK, MONO_EINVAL, MONO_EHIP, MONO_ESTATE, MONO_ENOMEM = 0, 1, 2, 3, 4
 ROUTER_SIGMOID_BIAS, ROUTER_SOFTMAX = 0, 1
@@ -128,19 +128,28 @@ SIGNATURES = {
     "mono_layer_tail_forward": (C.c_int, [_VP, C.POINTER(ProjWeights), C.POINTER(LayerArgs), _VP]),
     "mono_layer_set_deadline": (C.c_int, [_VP, C.c_double]),
     "mono_layer_read_errors": (C.c_int, [_VP, C.POINTER(C.c_int32)]),
+    "mono_layer_pending_error": (C.c_int32, [_VP]),
     "mono_layer_clear_errors": (C.c_int, [_VP]),
-    "mono_layer_set_fault": (C.c_int, [_VP, C.c_int32, C.c_int32]),
+    "mono_layer_set_fault": (C.c_int, [_VP, C.c_int32, C.c_int64]),
+    "mono_layer_set_launch_ordinal": (C.c_int, [_VP, C.c_uint64]),
 }
-GUARD_WORDS = 4
+GUARD_WORDS = 8
+# guard words: tag epochs, error (1 + site), failing tag, failing workgroup, u64 tickets
+G_EPOCH, G_ERROR, G_FAIL_TAG, G_FAIL_BLOCK, G_TICKET = 0, 1, 2, 3, 4
+# tags repeat every TAG_PERIOD launches (a launch's tag is ordinal % TAG_PERIOD + 1)
+TAG_PERIOD = 2**32 - 2
+SCRUB_SITE = 31
 # wait sites of the launches (guard word 1 = site + 1)
 MOE_SITES = {0: "router logits", 1: "route picks", 2: "expert mid activations", 3: "expert outputs"}
 ATTN_SITES = {0: "index scores", 1: "selected slots", 2: "split partials", 3: "top-k team"}
 PROJ_SITES = {0: "stage-A partial sums", 1: "normed q_a", 2: "q_nope", 3: "raw index query", 4: "W_UV output"}
-# the fused attention + back + MoE launch of a layer runtime
-TAIL_SITES = {**ATTN_SITES, 4: "W_UV output", 5: "attention output", 6: "router logits", 7: "route picks",
-              8: "expert mid activations", 9: "expert outputs", 10: "attention block output rows",
-              **{11 + k: f"front: {v}" for k, v in {**PROJ_SITES, 5: "normed input rows"}.items()},
-              17: "front index query and keys", 18: "front q"}
+# every launch of a layer runtime (one guard)
+LAYER_SITES = {**ATTN_SITES, 4: "W_UV output", 5: "attention output", 6: "router logits", 7: "route picks",
+               8: "expert mid activations", 9: "expert outputs", 10: "attention block output rows",
+               **{11 + k: f"front: {v}" for k, v in {**PROJ_SITES, 5: "normed input rows"}.items()},
+               17: "front index query and keys", 18: "front q", SCRUB_SITE: "tag-epoch scrub"}
+# the front's own sites in a layer runtime's numbering
+LAYER_FRONT_SITE0 = 11
 
 _lock = threading.Lock()
 _lib = None

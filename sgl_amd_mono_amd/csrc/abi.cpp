@@ -61,9 +61,13 @@ const double TICKS_PER_S = 100e6;  // s_memrealtime runs at 100 MHz
 const double DEFAULT_DEADLINE_S = 2.0;
 const double MAX_DEADLINE_S = 3600.0;
 
-// Carves one device allocation into 256-byte aligned pieces.
+// Carves one device allocation into 256-byte aligned pieces after the runtime's header
+// (its first 256 bytes: the guard words, the scrub table and the unit scale).
+constexpr size_t HEADER = 256;
+constexpr size_t SCRUB_OFF = 64;  // the guard's scrub table in the header
+constexpr size_t UNIT_OFF = 192;  // the f32 1.0 in the header
 struct Carve {
-  size_t off = 0;
+  size_t off = HEADER;
   size_t take(size_t bytes) {
     const size_t at = off;
     off += align256(bytes);
@@ -72,6 +76,35 @@ struct Carve {
 };
 
 }  // namespace
+
+// A pinned host word the launches' guard copies its errors to (system scope), so the
+// host sees a stopped launch without synchronising.
+struct HostErr {
+  uint32_t* host = nullptr;  // host address
+  uint32_t* dev = nullptr;   // the device's address of it
+  int alloc(const char* what) {
+    void* p = nullptr;
+    hipError_t e = hipHostMalloc(&p, 64, hipHostMallocCoherent | hipHostMallocMapped);
+    if (e != hipSuccess) return fail(MONO_ENOMEM, "hipHostMalloc for the %s error word: %s", what, hipGetErrorString(e));
+    host = static_cast<uint32_t*>(p);
+    *host = 0;
+    void* d = nullptr;
+    e = hipHostGetDevicePointer(&d, p, 0);
+    if (e != hipSuccess) return fail(MONO_EHIP, "hipHostGetDevicePointer: %s", hipGetErrorString(e));
+    dev = static_cast<uint32_t*>(d);
+    return MONO_OK;
+  }
+  uint32_t read() const { return host ? __atomic_load_n(host, __ATOMIC_ACQUIRE) : 0u; }
+  void clear() {
+    if (host) __atomic_store_n(host, 0u, __ATOMIC_RELEASE);
+  }
+  int release() {
+    if (!host) return MONO_OK;
+    hipError_t e = hipHostFree(host);
+    host = dev = nullptr;
+    return e == hipSuccess ? MONO_OK : fail(MONO_EHIP, "hipHostFree: %s", hipGetErrorString(e));
+  }
+};
 
 // What every runtime handle has: its device, the persistent grid, the scratch blob
 // and the guard (common/guard.py:100-241 in the reference).
@@ -82,13 +115,15 @@ struct RuntimeBase {
   void* blob = nullptr;
   size_t blob_bytes = 0;
   mono::GuardArgs guard{};
-  // one f32 1.0 after the mailboxes: the per-token scale of every row of an MLA cache
-  // passed without a scale plane (raw E4M3 rows), read and written at index 0
+  HostErr herr;
+  // one f32 1.0 in the header: the per-token scale of every row of an MLA cache passed
+  // without a scale plane (raw E4M3 rows), read and written at index 0
   float* unit = nullptr;
 
-  // Allocate and zero `bytes` of scratch with the guard words at `guard_off`. Tag 0
-  // is never a launch's tag, so zeroed mailboxes read as empty.
-  int init(int dev, size_t bytes, size_t guard_off, int (*occupancy)(int*), const char* what) {
+  // Allocate and zero the header and `bytes` of mailboxes (a Carve's `off`), and write
+  // the scrub table: every mailbox after the header. Tag 0 is never a launch's tag, so
+  // zeroed mailboxes read as empty.
+  int init(int dev, size_t bytes, int (*occupancy)(int*), const char* what) {
     device = dev;
     hipDeviceProp_t prop;
     HIP_TRY(hipGetDeviceProperties(&prop, dev));
@@ -96,34 +131,46 @@ struct RuntimeBase {
     if (int rc = occupancy(&per_cu)) return rc;
     if (per_cu < 1) return fail(MONO_ESTATE, "the persistent %s kernel does not fit on a CU (occupancy %d)", what, per_cu);
     grid = prop.multiProcessorCount;
-    const size_t total = align256(bytes) + 256;
+    const size_t total = align256(bytes);
     hipError_t e = hipMalloc(&blob, total);
     if (e != hipSuccess) {
       blob = nullptr;
       return fail(MONO_ENOMEM, "hipMalloc(%zu) for the %s mailboxes: %s", total, what, hipGetErrorString(e));
     }
     blob_bytes = total;
-    unit = reinterpret_cast<float*>(at(align256(bytes)));
+    if (int rc = herr.alloc(what)) return rc;
+    unit = reinterpret_cast<float*>(at(UNIT_OFF));
+    mono::ScrubRegion table[mono::SCRUB_MAX] = {};
+    table[0] = mono::ScrubRegion{reinterpret_cast<uint32_t*>(at(HEADER)), (total - HEADER) / 16};
     const float one = 1.0f;
     e = hipMemset(blob, 0, total);
     if (e == hipSuccess) e = hipMemcpy(unit, &one, sizeof(one), hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(at(SCRUB_OFF), table, sizeof(table), hipMemcpyHostToDevice);
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) return fail(MONO_EHIP, "clearing the %s mailboxes: %s", what, hipGetErrorString(e));
-    guard.words = reinterpret_cast<uint32_t*>(at(guard_off));
+    guard.words = reinterpret_cast<uint32_t*>(at(0));
+    guard.scrub = reinterpret_cast<const mono::ScrubRegion*>(at(SCRUB_OFF));
+    guard.host_err = herr.dev;
     guard.deadline_ticks = (uint64_t)(DEFAULT_DEADLINE_S * TICKS_PER_S);
     guard.fault_site = -1;
+    guard.fault_from = 0;
     return MONO_OK;
   }
   char* at(size_t off) const { return static_cast<char*>(blob) + off; }
+  // the mailboxes after the header, as a scrub region
+  mono::ScrubRegion mailboxes() const {
+    return mono::ScrubRegion{reinterpret_cast<uint32_t*>(at(HEADER)), (blob_bytes - HEADER) / 16};
+  }
   // Free the scratch; the handle is dead afterwards (idempotent like PeerBuffer.close,
   // common/peer.py:157-165).
   int release() {
     magic = 0;
-    if (!blob) return MONO_OK;
+    int rc = herr.release();
+    if (!blob) return rc;
     hipError_t e = hipFree(blob);
     blob = nullptr;
     if (e != hipSuccess) return fail(MONO_EHIP, "hipFree: %s", hipGetErrorString(e));
-    return MONO_OK;
+    return rc;
   }
 };
 
@@ -171,32 +218,73 @@ int occ_attn(int* n) {
 
 bool live(const RuntimeBase* r, uint32_t magic) { return r && r->magic == magic; }
 
-int guard_set_deadline(RuntimeBase* r, double seconds) {
+// The guard controls, on a guard's kernel arguments, its device, grid and host word.
+struct GuardRef {
+  mono::GuardArgs* g;
+  int device;
+  int grid;
+  HostErr* herr;
+};
+GuardRef ref(RuntimeBase* r) { return GuardRef{&r->guard, r->device, r->grid, &r->herr}; }
+
+int guard_set_deadline(GuardRef r, double seconds) {
   if (!(seconds > 0.0) || seconds > MAX_DEADLINE_S)
     return fail(MONO_EINVAL, "deadline must be in (0, %.0f] seconds, got %g", MAX_DEADLINE_S, seconds);
   const double ticks = seconds * TICKS_PER_S;
-  r->guard.deadline_ticks = ticks < 1.0 ? 1u : (uint64_t)ticks;
+  r.g->deadline_ticks = ticks < 1.0 ? 1u : (uint64_t)ticks;
   return ok();
 }
 
-int guard_set_fault(RuntimeBase* r, int32_t site) {
+// The launches' ordinal so far (synchronises): launch tickets / grid.
+int guard_ordinal(GuardRef r, uint64_t* ord) {
+  if (int rc = check_device(r.device)) return rc;
+  HIP_TRY(hipDeviceSynchronize());
+  uint64_t tickets = 0;
+  HIP_TRY(hipMemcpy(&tickets, r.g->words + mono::G_TICKET, sizeof(tickets), hipMemcpyDeviceToHost));
+  *ord = tickets / (uint64_t)r.grid;
+  return MONO_OK;
+}
+
+// The host-forced fault at `site` for every launch from `after` launches on (-1: off).
+int guard_set_fault(GuardRef r, int32_t site, int64_t after) {
   if (site < -1 || site > 31) return fail(MONO_EINVAL, "fault site must be -1 (none) or a wait site 0..31, got %d", site);
-  r->guard.fault_site = site;
+  if (after < 0) return fail(MONO_EINVAL, "after must be >= 0 launches, got %lld", (long long)after);
+  uint64_t from = 0;
+  if (site >= 0 && after > 0) {
+    if (int rc = guard_ordinal(r, &from)) return rc;
+    from += (uint64_t)after;
+  }
+  r.g->fault_site = site;
+  r.g->fault_from = from;
   return ok();
 }
 
-int guard_read(RuntimeBase* r, int32_t* words) {
+int guard_read(GuardRef r, int32_t* words) {
   if (!words) return fail(MONO_EINVAL, "read_errors: words is NULL");
-  if (int rc = check_device(r->device)) return rc;
+  if (int rc = check_device(r.device)) return rc;
   HIP_TRY(hipDeviceSynchronize());
-  HIP_TRY(hipMemcpy(words, r->guard.words, MONO_GUARD_WORDS * sizeof(int32_t), hipMemcpyDeviceToHost));
+  HIP_TRY(hipMemcpy(words, r.g->words, MONO_GUARD_WORDS * sizeof(int32_t), hipMemcpyDeviceToHost));
   return ok();
 }
 
-int guard_clear(RuntimeBase* r) {
-  if (int rc = check_device(r->device)) return rc;
+// Clear the sticky error (words 1-3, the tickets stay) and the host word.
+int guard_clear(GuardRef r) {
+  if (int rc = check_device(r.device)) return rc;
   HIP_TRY(hipDeviceSynchronize());
-  HIP_TRY(hipMemset(r->guard.words + mono::G_ERROR, 0, (MONO_GUARD_WORDS - 1) * sizeof(int32_t)));
+  HIP_TRY(hipMemset(r.g->words + mono::G_ERROR, 0, 3 * sizeof(int32_t)));
+  HIP_TRY(hipDeviceSynchronize());
+  r.herr->clear();
+  return ok();
+}
+
+// Move the launch ordinal to `ordinal` (synchronises; tests of the tag epochs): the next
+// launch takes tag ordinal % TAG_PERIOD + 1.
+int guard_set_ordinal(GuardRef r, uint64_t ordinal) {
+  if (ordinal > UINT64_MAX / (uint64_t)r.grid) return fail(MONO_EINVAL, "ordinal %llu is out of range", (unsigned long long)ordinal);
+  if (int rc = check_device(r.device)) return rc;
+  HIP_TRY(hipDeviceSynchronize());
+  const uint64_t tickets = ordinal * (uint64_t)r.grid;
+  HIP_TRY(hipMemcpy(r.g->words + mono::G_TICKET, &tickets, sizeof(tickets), hipMemcpyHostToDevice));
   HIP_TRY(hipDeviceSynchronize());
   return ok();
 }
@@ -241,7 +329,6 @@ extern "C" int mono_moe_create(const mono_moe_config* cfg, mono_moe** out) {
   const size_t H = c.hidden, E = c.n_experts, I = c.inter;
   const size_t max_act = (size_t)std::min(c.max_rows * c.top_k, c.n_experts) + 1;
   Carve cv;
-  const size_t o_guard = cv.take(mono::G_WORDS * 4);
   const size_t o_rlog = cv.take((size_t)moe_fp8_router_slices() * MAX_ROWS * E * 8);
   const size_t o_rsel = cv.take((size_t)MAX_ROWS * 2 * MAX_TOPK * 8);
   const size_t o_mid = cv.take(max_act * MAX_ROWS * I * 8);
@@ -249,7 +336,7 @@ extern "C" int mono_moe_create(const mono_moe_config* cfg, mono_moe** out) {
   mono_moe* m = new mono_moe();
   m->magic = MOE_MAGIC;
   m->cfg = c;
-  if (int rc = m->init(c.device, cv.off, o_guard, fp8 ? occ_moe_fp8 : occ_moe_mxfp4, "MoE")) {
+  if (int rc = m->init(c.device, cv.off, fp8 ? occ_moe_fp8 : occ_moe_mxfp4, "MoE")) {
     (void)m->release();
     delete m;
     return rc;
@@ -324,22 +411,22 @@ extern "C" int mono_moe_mxfp4_forward(mono_moe* m, const mono_moe_mxfp4_args* ar
 
 extern "C" int mono_moe_set_deadline(mono_moe* m, double seconds) {
   if (!live(m, MOE_MAGIC)) return fail(MONO_ESTATE, "not a live MoE runtime");
-  return guard_set_deadline(m, seconds);
+  return guard_set_deadline(ref(m), seconds);
 }
 
 extern "C" int mono_moe_set_fault(mono_moe* m, int32_t site) {
   if (!live(m, MOE_MAGIC)) return fail(MONO_ESTATE, "not a live MoE runtime");
-  return guard_set_fault(m, site);
+  return guard_set_fault(ref(m), site, 0);
 }
 
 extern "C" int mono_moe_read_errors(mono_moe* m, int32_t* words) {
   if (!live(m, MOE_MAGIC)) return fail(MONO_ESTATE, "not a live MoE runtime");
-  return guard_read(m, words);
+  return guard_read(ref(m), words);
 }
 
 extern "C" int mono_moe_clear_errors(mono_moe* m) {
   if (!live(m, MOE_MAGIC)) return fail(MONO_ESTATE, "not a live MoE runtime");
-  return guard_clear(m);
+  return guard_clear(ref(m));
 }
 
 // ------------------------------------------------------------------ attention runtime
@@ -357,7 +444,6 @@ extern "C" int mono_attn_create(const mono_attn_config* cfg, mono_attn** out) {
   if (int rc = check_device(c.device)) return rc;
   const size_t R = c.max_rows;
   Carve cv;
-  const size_t o_guard = cv.take(mono::G_WORDS * 4);
   const size_t o_score = cv.take(R * c.max_ctx * 4);
   const size_t o_sel = cv.take(R * TOPK * 8);
   const size_t o_rowh = cv.take(2 * R * ROWH * 4);
@@ -374,7 +460,7 @@ extern "C" int mono_attn_create(const mono_attn_config* cfg, mono_attn** out) {
   mono_attn* a = new mono_attn();
   a->magic = ATTN_MAGIC;
   a->cfg = c;
-  if (int rc = a->init(c.device, cv.off, o_guard, occ_attn, "attention")) {
+  if (int rc = a->init(c.device, cv.off, occ_attn, "attention")) {
     (void)a->release();
     delete a;
     return rc;
@@ -393,6 +479,9 @@ extern "C" int mono_attn_create(const mono_attn_config* cfg, mono_attn** out) {
   a->mail.score = reinterpret_cast<uint32_t*>(a->at(o_score));
   a->mail.sel = reinterpret_cast<uint64_t*>(a->at(o_sel));
   a->mail.rowh = reinterpret_cast<uint32_t*>(a->at(o_rowh));
+  // the row histograms are atomic accumulators by launch parity: the guard's flip words
+  a->guard.flip = a->mail.rowh;
+  a->guard.flip_words = (int32_t)(R * ROWH);
   a->mail.cdone = reinterpret_cast<uint64_t*>(a->at(o_cdone));
   a->mail.hist = reinterpret_cast<uint64_t*>(a->at(o_hist));
   a->mail.cand = reinterpret_cast<uint64_t*>(a->at(o_cand));
@@ -505,22 +594,22 @@ extern "C" int mono_attn_back_forward(mono_attn* a, const mono_attn_args* args, 
 
 extern "C" int mono_attn_set_deadline(mono_attn* a, double seconds) {
   if (!live(a, ATTN_MAGIC)) return fail(MONO_ESTATE, "not a live attention runtime");
-  return guard_set_deadline(a, seconds);
+  return guard_set_deadline(ref(a), seconds);
 }
 
 extern "C" int mono_attn_set_fault(mono_attn* a, int32_t site) {
   if (!live(a, ATTN_MAGIC)) return fail(MONO_ESTATE, "not a live attention runtime");
-  return guard_set_fault(a, site);
+  return guard_set_fault(ref(a), site, 0);
 }
 
 extern "C" int mono_attn_read_errors(mono_attn* a, int32_t* words) {
   if (!live(a, ATTN_MAGIC)) return fail(MONO_ESTATE, "not a live attention runtime");
-  return guard_read(a, words);
+  return guard_read(ref(a), words);
 }
 
 extern "C" int mono_attn_clear_errors(mono_attn* a) {
   if (!live(a, ATTN_MAGIC)) return fail(MONO_ESTATE, "not a live attention runtime");
-  if (int rc = guard_clear(a)) return rc;
+  if (int rc = guard_clear(ref(a))) return rc;
   // a failed launch may have left row histograms uncleared for its successor
   HIP_TRY(hipMemset(a->mail.rowh, 0, 2 * (size_t)a->cfg.max_rows * mono::attn::ROWH * sizeof(uint32_t)));
   HIP_TRY(hipDeviceSynchronize());
@@ -538,7 +627,6 @@ extern "C" int mono_proj_create(const mono_proj_config* cfg, mono_proj** out) {
     return fail(MONO_EINVAL, "max_rows must be in [1, %d], got %d", MAX_ROWS, c.max_rows);
   if (int rc = check_device(c.device)) return rc;
   Carve cv;
-  const size_t o_guard = cv.take(mono::G_WORDS * 4);
   size_t o_mb[5];
   for (int i = 0; i < 5; ++i) o_mb[i] = cv.take(MAIL_WORDS[i] * 4);
   const size_t o_odone = cv.take(mono::DONE_BYTES);
@@ -551,7 +639,7 @@ extern "C" int mono_proj_create(const mono_proj_config* cfg, mono_proj** out) {
   mono_proj* p = new mono_proj();
   p->magic = PROJ_MAGIC;
   p->cfg = c;
-  if (int rc = p->init(c.device, cv.off, o_guard, occ_proj, "projection")) {
+  if (int rc = p->init(c.device, cv.off, occ_proj, "projection")) {
     (void)p->release();
     delete p;
     return rc;
@@ -636,7 +724,8 @@ extern "C" int mono_front_forward(mono_proj* p, const mono_proj_weights* w, cons
     fa.kv_scale = p->unit;
     kv_mask = 0;
   }
-  hipError_t e = mono::proj::front_forward(*w, fa, p->grid, p->mail, p->guard, kv_mask, static_cast<hipStream_t>(stream));
+  hipError_t e =
+      mono::proj::front_forward(*w, fa, p->grid, p->mail, p->guard, kv_mask, 0, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return fail(MONO_EHIP, "launching the front projections: %s", hipGetErrorString(e));
   return ok();
 }
@@ -658,47 +747,52 @@ extern "C" int mono_back_forward(mono_proj* p, const mono_proj_weights* w, const
 
 extern "C" int mono_proj_set_deadline(mono_proj* p, double seconds) {
   if (!live(p, PROJ_MAGIC)) return fail(MONO_ESTATE, "not a live projection runtime");
-  return guard_set_deadline(p, seconds);
+  return guard_set_deadline(ref(p), seconds);
 }
 
 extern "C" int mono_proj_set_fault(mono_proj* p, int32_t site) {
   if (!live(p, PROJ_MAGIC)) return fail(MONO_ESTATE, "not a live projection runtime");
-  return guard_set_fault(p, site);
+  return guard_set_fault(ref(p), site, 0);
 }
 
 extern "C" int mono_proj_read_errors(mono_proj* p, int32_t* words) {
   if (!live(p, PROJ_MAGIC)) return fail(MONO_ESTATE, "not a live projection runtime");
-  return guard_read(p, words);
+  return guard_read(ref(p), words);
 }
 
 extern "C" int mono_proj_clear_errors(mono_proj* p) {
   if (!live(p, PROJ_MAGIC)) return fail(MONO_ESTATE, "not a live projection runtime");
-  return guard_clear(p);
+  return guard_clear(ref(p));
 }
 
 // ------------------------------------------------------------------ decoder layer
 
-// One decoder layer's runtimes: the projection, attention and FP8 MoE mailboxes and
-// guards, private to the layer (never handed out on their own), and the o_proj tiles'
-// done words of the fused launch. The front launch runs under the projection guard;
-// the fused launch (attention, back, MoE) under the attention guard, whose tickets tag
-// every mailbox word it writes (the MoE mailboxes included: no other launch writes
-// them, so their tags never collide).
+// One decoder layer's runtimes: the projection, attention and FP8 MoE mailboxes,
+// private to the layer (never handed out on their own), the o_proj tiles' done words of
+// the fused launch, and the layer's guard. Every launch of the layer (the whole layer,
+// or its front and the fused rest apart) runs under that one guard: the attention
+// runtime's guard words (one ticket counter, so tags never collide between the
+// launches, whichever the caller mixes) and host word, its row histograms as the flip
+// words, and a scrub table of all four mailbox regions.
 struct mono_layer {
   uint32_t magic = 0;
   mono_proj* p = nullptr;
   mono_attn* a = nullptr;
   mono_moe* m = nullptr;
+  void* extra = nullptr;  // a_done, then the scrub table
   uint64_t* a_done = nullptr;
+  mono::GuardArgs guard{};
 };
 static const uint32_t LAYER_MAGIC = 0x6c617972u;
 static bool layer_live(const mono_layer* L) { return L && L->magic == LAYER_MAGIC; }
+static GuardRef layer_ref(mono_layer* L) { return GuardRef{&L->guard, L->a->device, L->a->grid, &L->a->herr}; }
 
 static int layer_release(mono_layer* L) {
   int rc = MONO_OK;
-  if (L->a_done) {
-    hipError_t e = hipFree(L->a_done);
+  if (L->extra) {
+    hipError_t e = hipFree(L->extra);
     if (e != hipSuccess) rc = fail(MONO_EHIP, "hipFree: %s", hipGetErrorString(e));
+    L->extra = nullptr;
     L->a_done = nullptr;
   }
   if (L->m) rc = mono_moe_destroy(L->m) ? MONO_EHIP : rc;
@@ -729,16 +823,25 @@ extern "C" int mono_layer_create(const mono_layer_config* cfg, mono_layer** out)
   int rc = mono_proj_create(&pc, &L->p);
   if (!rc) rc = mono_attn_create(&ac, &L->a);
   if (!rc) rc = mono_moe_create(&mc, &L->m);
+  const size_t table_off = mono::DONE_BYTES;
   if (!rc) {
-    hipError_t e = hipMalloc(&L->a_done, mono::DONE_BYTES);
+    hipError_t e = hipMalloc(&L->extra, table_off + 256);
     if (e != hipSuccess) {
-      L->a_done = nullptr;
-      rc = fail(MONO_ENOMEM, "hipMalloc(%zu) for the layer's done words: %s", (size_t)mono::DONE_BYTES,
+      L->extra = nullptr;
+      rc = fail(MONO_ENOMEM, "hipMalloc(%zu) for the layer's done words: %s", (size_t)(table_off + 256),
                 hipGetErrorString(e));
     } else {
-      e = hipMemset(L->a_done, 0, mono::DONE_BYTES);
+      L->a_done = static_cast<uint64_t*>(L->extra);
+      mono::ScrubRegion table[mono::SCRUB_MAX] = {L->a->mailboxes(), L->p->mailboxes(), L->m->mailboxes(),
+                                                  mono::ScrubRegion{reinterpret_cast<uint32_t*>(L->a_done),
+                                                                    mono::DONE_BYTES / 16}};
+      char* tb = static_cast<char*>(L->extra) + table_off;
+      e = hipMemset(L->extra, 0, table_off + 256);
+      if (e == hipSuccess) e = hipMemcpy(tb, table, sizeof(table), hipMemcpyHostToDevice);
       if (e == hipSuccess) e = hipDeviceSynchronize();
       if (e != hipSuccess) rc = fail(MONO_EHIP, "clearing the layer's done words: %s", hipGetErrorString(e));
+      L->guard = L->a->guard;
+      L->guard.scrub = reinterpret_cast<const mono::ScrubRegion*>(tb);
     }
   }
   if (rc) {
@@ -779,27 +882,30 @@ static int layer_launch(mono_layer* L, const mono_proj_weights* w, const mono_la
   if (args->moe->a != args->back->a) return fail(MONO_EINVAL, "moe->a must be back->a: the MoE reads the back's output");
   if (int rc = check_attn_back(L->a, args->attn, w, args->back)) return rc;
   if (int rc = check_moe_fp8(L->m, args->moe)) return rc;
-  if (front && !tail) return mono_front_forward(L->p, w, args->front, stream);
   mono_back_args b = *args->back;
   b.o_lat = at.out;
   const mono::attn::AttnArgs g = attn_args(L->a, at);
   const mono::moe::MoeFp8Args m(*args->moe, L->m->cfg.route_scale, L->m->cfg.eps);
+  const hipStream_t st = static_cast<hipStream_t>(stream);
   hipError_t e;
-  if (front) {  // the whole layer as one launch (the front's checks are mono_front_forward's)
+  if (front) {
     if (int rc = check_front(L->p, w, args->front)) return rc;
     mono_front_args fa = *args->front;
     int kv_mask = -1;
-    if (!fa.kv_scale) {
-      fa.kv_scale = L->p->unit;
+    if (!fa.kv_scale) {  // raw E4M3 rows: the 1.0 the attention reads too
+      fa.kv_scale = L->a->unit;
       kv_mask = 0;
     }
-    e = mono::layer::layer_forward(*w, fa, L->p->mail, kv_mask, g, L->a->mail, L->a->guard, b, L->a->back_mail, m,
-                                   L->m->mail, L->a_done, L->a->grid, static_cast<hipStream_t>(stream));
+    if (tail)  // the whole layer as one launch
+      e = mono::layer::layer_forward(*w, fa, L->p->mail, kv_mask, g, L->a->mail, L->guard, b, L->a->back_mail, m,
+                                     L->m->mail, L->a_done, L->a->grid, st);
+    else  // the front alone, under the layer's guard (its sites numbered as in the one launch)
+      e = mono::proj::front_forward(*w, fa, L->a->grid, L->p->mail, L->guard, kv_mask, mono::layer::FRONT_SITE0, st);
   } else {
-    e = mono::layer::tail_forward(g, L->a->mail, L->a->guard, *w, b, L->a->back_mail, m, L->m->mail, L->a_done,
-                                  L->a->grid, static_cast<hipStream_t>(stream));
+    e = mono::layer::tail_forward(g, L->a->mail, L->guard, *w, b, L->a->back_mail, m, L->m->mail, L->a_done,
+                                  L->a->grid, st);
   }
-  if (e != hipSuccess) return fail(MONO_EHIP, "launching the fused attention + back + MoE: %s", hipGetErrorString(e));
+  if (e != hipSuccess) return fail(MONO_EHIP, "launching the layer: %s", hipGetErrorString(e));
   return ok();
 }
 
@@ -820,27 +926,34 @@ extern "C" int mono_layer_tail_forward(mono_layer* L, const mono_proj_weights* w
 
 extern "C" int mono_layer_set_deadline(mono_layer* L, double seconds) {
   if (!layer_live(L)) return fail(MONO_ESTATE, "not a live layer runtime");
-  if (int rc = mono_proj_set_deadline(L->p, seconds)) return rc;
-  return mono_attn_set_deadline(L->a, seconds);
+  return guard_set_deadline(layer_ref(L), seconds);
 }
 
-extern "C" int mono_layer_set_fault(mono_layer* L, int32_t launch, int32_t site) {
+extern "C" int mono_layer_set_fault(mono_layer* L, int32_t site, int64_t after) {
   if (!layer_live(L)) return fail(MONO_ESTATE, "not a live layer runtime");
-  if (launch == 0) return mono_proj_set_fault(L->p, site);
-  if (launch == 1) return mono_attn_set_fault(L->a, site);
-  return fail(MONO_EINVAL, "launch must be 0 (front) or 1 (attention + back + MoE), got %d", launch);
+  return guard_set_fault(layer_ref(L), site, after);
 }
 
 extern "C" int mono_layer_read_errors(mono_layer* L, int32_t* words) {
   if (!layer_live(L)) return fail(MONO_ESTATE, "not a live layer runtime");
-  if (!words) return fail(MONO_EINVAL, "words is NULL");
-  if (int rc = mono_proj_read_errors(L->p, words)) return rc;
-  return mono_attn_read_errors(L->a, words + MONO_GUARD_WORDS);
+  return guard_read(layer_ref(L), words);
+}
+
+extern "C" int32_t mono_layer_pending_error(mono_layer* L) {
+  if (!layer_live(L)) return -1;
+  return (int32_t)L->a->herr.read();
 }
 
 extern "C" int mono_layer_clear_errors(mono_layer* L) {
   if (!layer_live(L)) return fail(MONO_ESTATE, "not a live layer runtime");
-  if (int rc = mono_proj_clear_errors(L->p)) return rc;
-  if (int rc = mono_attn_clear_errors(L->a)) return rc;
-  return mono_moe_clear_errors(L->m);
+  if (int rc = guard_clear(layer_ref(L))) return rc;
+  // a refused launch skipped clearing its successor's row histograms
+  HIP_TRY(hipMemset(L->a->mail.rowh, 0, 2 * (size_t)L->a->cfg.max_rows * mono::attn::ROWH * sizeof(uint32_t)));
+  HIP_TRY(hipDeviceSynchronize());
+  return ok();
+}
+
+extern "C" int mono_layer_set_launch_ordinal(mono_layer* L, uint64_t ordinal) {
+  if (!layer_live(L)) return fail(MONO_ESTATE, "not a live layer runtime");
+  return guard_set_ordinal(layer_ref(L), ordinal);
 }

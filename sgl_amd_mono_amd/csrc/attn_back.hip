@@ -28,13 +28,15 @@ union Lds {
 __global__ __launch_bounds__(512, 1) void k_attn_back(Args args) {
   __shared__ Lds lds;
   attn::Step st(args.at, lds.at);
-  if (!st.begin()) return;
+  // a failed or refused launch writes NaN over its output `a`
+  const auto poison = [&](bool share) { poison_bf16(args.bk.a.a, (size_t)args.bk.a.rows * proj::HIDDEN, share); };
+  if (!st.begin()) return poison(true);
   const Guard g = st.guard();
-  if (!st.tasks()) return;
+  if (!st.tasks()) return poison(false);
   __syncthreads();  // the LDS passes from the attention's layout to the back's
   proj::Back bk(args.bk, lds.bk);
   bk.adopt(g, args.at.mail.mdone);
-  (void)bk.tasks(st.n_tasks());
+  if (!bk.tasks(st.n_tasks())) poison(false);
 }
 
 }  // namespace

@@ -101,8 +101,6 @@ struct Lds {
     MergeLds mg;
   } u;
   int32_t scan[AW];
-  uint32_t tag;
-  uint32_t err;
 };
 
 struct Args {
@@ -176,29 +174,17 @@ class Step {
   }
 
   MONO_DEV void run() {
-    if (begin()) (void)tasks();
+    if (!begin()) return poison(true);
+    if (!tasks()) poison(false);
   }
 
-  // The launch's tag and deadline (false: a failed launch stopped the runtime); clears
-  // the next launch's row histograms.
-  MONO_DEV bool begin() {
-    if (tid == 0) {
-      const uint32_t ticket = __hip_atomic_fetch_add(&A.guard.words[G_TICKET], 1u, __ATOMIC_RELAXED,
-                                                     __HIP_MEMORY_SCOPE_AGENT);
-      L.tag = ticket / (uint32_t)G + 1u;
-      L.err = ld_agent_u32(&A.guard.words[G_ERROR]);
-    }
-    __syncthreads();
-    if (L.err != 0) return false;
-    gd.a = A.guard;
-    gd.tag = L.tag;
-    gd.deadline = now_ticks() + A.guard.deadline_ticks;
-    for (int s = blockIdx.x; s < A.mail.max_rows; s += G) {  // the next launch's row histograms
-      uint32_t* nx = row_hist(gd.tag + 1u, s);
-      if (tid < ROWH) __hip_atomic_store(&nx[tid], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    return true;
-  }
+  // NaN over the launch's output (sync.h poison_bf16)
+  MONO_DEV void poison(bool share) const { poison_bf16(A.out, (size_t)A.rows * NH * DV, share); }
+
+  // The launch's tag and deadline (false: the guard refused the launch or its epoch
+  // scrub failed). The row histograms are the guard's flip accumulators: the launch
+  // start clears the copy the next launch adds into.
+  MONO_DEV bool begin() { return guard_begin(A.guard, gd); }
 
   MONO_DEV const Guard& guard() const { return gd; }
 

@@ -33,8 +33,6 @@ struct Lds {
     uint16_t xo[MAX_ROWS][XO];
   } u;
   f32x4 red[FW][WAVE];
-  uint32_t tag;
-  uint32_t err;
 };
 
 struct Args {
@@ -58,24 +56,15 @@ class Back {
   }
 
   MONO_DEV void run() {
-    if (begin()) (void)tasks(0);
+    if (!begin()) return poison(true);
+    if (!tasks(0)) poison(false);
   }
 
-  // The launch's tag and deadline (false: a failed launch stopped the runtime).
-  MONO_DEV bool begin() {
-    if (tid == 0) {
-      const uint32_t ticket = __hip_atomic_fetch_add(&guard_args.words[G_TICKET], 1u, __ATOMIC_RELAXED,
-                                                     __HIP_MEMORY_SCOPE_AGENT);
-      L.tag = ticket / (uint32_t)G + 1u;
-      L.err = ld_agent_u32(&guard_args.words[G_ERROR]);
-    }
-    __syncthreads();
-    if (L.err != 0) return false;
-    gd.a = guard_args;
-    gd.tag = L.tag;
-    gd.deadline = now_ticks() + guard_args.deadline_ticks;
-    return true;
-  }
+  // The launch's tag and deadline (false: the guard refused the launch).
+  MONO_DEV bool begin() { return guard_begin(guard_args, gd); }
+
+  // NaN over the launch's output `a` (sync.h poison_bf16)
+  MONO_DEV void poison(bool share) const { poison_bf16(A.a, (size_t)S * HIDDEN, share); }
 
   // Run under another launch's guard (a fused launch: its tag, deadline and fail word),
   // after that launch's attention merges: their done words [rows][HEADS / 2].

@@ -22,7 +22,7 @@ hipError_t front_occupancy(int* blocks_per_cu) {
 }
 
 hipError_t front_forward(const mono_proj_weights& w, const mono_front_args& a, int grid, const Mail& mail,
-                         const GuardArgs& guard, int kv_mask, hipStream_t st) {
+                         const GuardArgs& guard, int kv_mask, int site0, hipStream_t st) {
   if (a.rows < 1 || a.rows > MAX_ROWS || grid < 1) return hipErrorInvalidConfiguration;
   Args args;
   args.w = w;
@@ -30,6 +30,7 @@ hipError_t front_forward(const mono_proj_weights& w, const mono_front_args& a, i
   args.mail = mail;
   args.guard = guard;
   args.kv_mask = kv_mask;
+  args.site0 = site0;
   k_front<<<grid, FT, 0, st>>>(args);
   return hipGetLastError();
 }

@@ -72,8 +72,6 @@ struct Lds {
   f32x4 red[FW][WAVE];
   float stat[FW][2];
   uint16_t gin[HIDDEN];  // the input RMSNorm weight, loaded once a launch
-  uint32_t tag;
-  uint32_t err;
 };
 
 struct Args {
@@ -82,6 +80,7 @@ struct Args {
   Mail mail;
   GuardArgs guard;
   int kv_mask;  // -1: per-token power-of-two scales into a.kv_scale; 0: raw E4M3 rows
+  int site0;    // the launch's first wait site (a layer's guard numbers the front's after its own)
 };
 
 class Front {
@@ -95,22 +94,16 @@ class Front {
     G = gridDim.x;
     S = A.rows;
     guard_args = args.guard;
+    site0 = args.site0;
   }
 
   MONO_DEV void run() {
-    if (tid == 0) {
-      const uint32_t ticket = __hip_atomic_fetch_add(&guard_args.words[G_TICKET], 1u, __ATOMIC_RELAXED,
-                                                     __HIP_MEMORY_SCOPE_AGENT);
-      L.tag = ticket / (uint32_t)G + 1u;
-      L.err = ld_agent_u32(&guard_args.words[G_ERROR]);
-    }
-    __syncthreads();
-    if (L.err != 0) return;
-    gd.a = guard_args;
-    gd.tag = L.tag;
-    gd.deadline = now_ticks() + guard_args.deadline_ticks;
-    (void)tasks();
+    if (!guard_begin(guard_args, gd)) return poison(true);
+    if (!tasks()) poison(false);
   }
+
+  // NaN over the launch's output q (sync.h poison_bf16)
+  MONO_DEV void poison(bool share) const { poison_bf16(A.q, (size_t)S * HEADS * (KV_LORA + PE_DIM), share); }
 
   // Run under another phase's guard in the same launch (its tag, deadline and fail
   // word; wait sites offset by site_base).
@@ -162,7 +155,7 @@ class Front {
   const Mail& M;
   Lds& L;
   const int kv_mask;
-  int site0 = 0;
+  int site0;
   GuardArgs guard_args;
   Guard gd;
   int tid, lane, wave, g, r, G, S;

@@ -45,28 +45,34 @@ union LayerLds {
   proj::fr::Lds fr;
 };
 
-// The back and the MoE after the attention, on the attention's guard.
-MONO_DEV void back_moe(const Args& args, Lds& lds, const attn::Step& st, const Guard& g) {
+// A failed or refused launch writes NaN over the layer's output x_out (sync.h).
+MONO_DEV void poison(const Args& args, bool share) {
+  poison_bf16(args.mo.out, (size_t)args.mo.rows * moe::H, share);
+}
+
+// The back and the MoE after the attention, on the attention's guard (false: a wait
+// failed).
+MONO_DEV bool back_moe(const Args& args, Lds& lds, const attn::Step& st, const Guard& g) {
   __syncthreads();  // the LDS passes from the attention's layout to the back's
   {
     proj::Back bk(args.bk, lds.bk);
     bk.adopt(g, args.at.mail.mdone);
     bk.publish_a(args.a_done);
-    if (!bk.tasks(st.n_tasks())) return;
+    if (!bk.tasks(st.n_tasks())) return false;
   }
   __syncthreads();  // and to the MoE's
   moe::Step ms(args.mo, lds.mo);
   ms.adopt(g, args.a_done, proj::NT_O, MOE_SITE0);
-  ms.run();
+  bool refused;
+  return ms.run(refused);
 }
 
 __global__ __launch_bounds__(512, 1) void k_layer_tail(Args args) {
   __shared__ Lds lds;
   attn::Step st(args.at, lds.at);
-  if (!st.begin()) return;
+  if (!st.begin()) return poison(args, true);
   const Guard g = st.guard();
-  if (!st.tasks()) return;
-  back_moe(args, lds, st, g);
+  if (!st.tasks() || !back_moe(args, lds, st, g)) poison(args, false);
 }
 
 // The whole decoder layer: the front's tasks first (under the attention's tag), then
@@ -74,16 +80,15 @@ __global__ __launch_bounds__(512, 1) void k_layer_tail(Args args) {
 __global__ __launch_bounds__(512, 1) void k_layer(LayerArgs args) {
   __shared__ LayerLds lds;
   attn::Step st(args.tail.at, lds.tail.at);
-  if (!st.begin()) return;  // the tag lives in registers from here on
+  if (!st.begin()) return poison(args.tail, true);  // the tag lives in registers from here on
   const Guard g = st.guard();
   {
     proj::fr::Front f(args.fr, lds.fr);
     f.adopt(g, FRONT_SITE0);
-    if (!f.tasks()) return;
+    if (!f.tasks()) return poison(args.tail, false);
   }
   __syncthreads();  // the LDS passes from the front's layout to the attention's
-  if (!st.tasks()) return;
-  back_moe(args.tail, lds.tail, st, g);
+  if (!st.tasks() || !back_moe(args.tail, lds.tail, st, g)) poison(args.tail, false);
 }
 
 }  // namespace
@@ -128,6 +133,7 @@ hipError_t layer_forward(const mono_proj_weights& w, const mono_front_args& f, c
   a.fr.mail = fmail;
   a.fr.guard = guard;
   a.fr.kv_mask = kv_mask;
+  a.fr.site0 = FRONT_SITE0;
   attn::fill_args(a.tail.at, g, amail, guard);
   a.tail.at.publish_out = true;
   a.tail.at.fdone = fmail.fdone;

@@ -11,7 +11,8 @@ namespace {
 __global__ __launch_bounds__(FT, 1) void k_moe_fp8(Args args) {
   __shared__ Lds lds;
   Step st(args, lds);
-  st.run();
+  bool refused;
+  if (!st.run(refused)) st.poison(refused);
 }
 
 }  // namespace

@@ -92,8 +92,6 @@ struct Lds {
   PlanLds<E, TOPK> plan;
   uint32_t rkey[E];
   float rraw[E];
-  uint32_t tag;
-  uint32_t err;
 };
 
 struct Args {
@@ -153,12 +151,13 @@ class Step {
     site0 = site_base;
   }
 
-  MONO_DEV void run() {
-    if (!a_done && tid == 0) {
-      const uint32_t ticket = __hip_atomic_fetch_add(&A.guard.words[G_TICKET], 1u, __ATOMIC_RELAXED,
-                                                     __HIP_MEMORY_SCOPE_AGENT);
-      L.tag = ticket / (uint32_t)G + 1u;
-      L.err = ld_agent_u32(&A.guard.words[G_ERROR]);
+  // The MoE of the step (false, workgroup-uniform: a wait failed; `refused`: the guard
+  // refused the launch before anything ran).
+  MONO_DEV bool run(bool& refused) {
+    refused = false;
+    if (!a_done && !guard_begin(A.guard, gd)) {  // a failed launch stops the guard until the host clears it
+      refused = true;
+      return false;
     }
     // the router task's weights go out before anything waits
     const int rt = blockIdx.x;
@@ -169,13 +168,7 @@ class Step {
       // read with plain loads after that (no workgroup reads it earlier in the launch,
       // so no cache holds an older copy of its lines)
       const uint64_t* ad = done_copy(a_done);
-      if (!hint_wait(n_a_done, [ad](int i) { return ad + i; }, site0 + W_A, gd)) return;
-    } else {
-      __syncthreads();
-      if (L.err != 0) return;  // a failed launch stops the runtime until the host clears it
-      gd.a = A.guard;
-      gd.tag = L.tag;
-      gd.deadline = now_ticks() + A.guard.deadline_ticks;
+      if (!hint_wait(n_a_done, [ad](int i) { return ad + i; }, site0 + W_A, gd)) return false;
     }
 
     u32x4 ar[PER_ROW];  // wave w's row w, kept for the quantisation
@@ -183,12 +176,15 @@ class Step {
     __syncthreads();
     if (rt < ROUTER_TASKS) router(rt, wr);
     if ((int)blockIdx.x >= G - S) {
-      if (!route(G - 1 - (int)blockIdx.x)) return;
+      if (!route(G - 1 - (int)blockIdx.x)) return false;
     }
     quant_rows(ar);
     __syncthreads();
-    tasks();
+    return tasks();
   }
+
+  // NaN over the launch's output (sync.h poison_bf16)
+  MONO_DEV void poison(bool share) const { poison_bf16(A.out, (size_t)S * H, share); }
 
  private:
   const Args& A;
@@ -392,11 +388,11 @@ class Step {
 
   // Each turn: consume the task's weights (waiting on its inputs), issue the next
   // task's weight loads, then publish the task's results while those loads fly.
-  MONO_DEV void tasks() {
+  MONO_DEV bool tasks() {
     int T = blockIdx.x;
     // a shared-expert tile needs no plan: its loads go out before the plan is read
     if (T < NT) load_task(K_UP, T);
-    if (!load_plan()) return;
+    if (!load_plan()) return false;
     int kind = classify(T);
     if (T >= NT) load_task(kind, T);
     // consecutive up tiles, half by half: the next tile's first half goes out once this
@@ -425,7 +421,7 @@ class Step {
     while (kind != K_NONE) {
       f32x4 acc[4];
       if (kind == K_DOWN) {
-        if (!down_compute(T, acc)) return;
+        if (!down_compute(T, acc)) return false;
       } else if (kind == K_UP) {
         acc[0] = f32x4{0.f, 0.f, 0.f, 0.f};
         acc[1] = acc[0];
@@ -440,11 +436,12 @@ class Step {
       } else if (kind == K_DOWN) {
         down_publish(T, acc);
       } else {
-        if (!final_task(T)) return;
+        if (!final_task(T)) return false;
       }
       T = T2;
       kind = kind2;
     }
+    return true;
   }
 
   // ---------------------------------------------------------------- up
@@ -621,8 +618,12 @@ class Step {
   MONO_DEV bool final_task(int T) {
     const int f = T - L.plan.n_act * (NT + DN_GROUPS);
     bool ok = true;
-    if (tid < S * FIN_ROWS) {
-      const int s = tid / FIN_ROWS, h = f * FIN_ROWS + tid % FIN_ROWS;
+    // the thread's row and column re-derived from an opaque copy of its index: hoisted
+    // out of the task loop, the row's offset would be held (and spilled) across tasks
+    int t = (int)threadIdx.x;
+    asm volatile("" : "+v"(t));
+    if (t < S * FIN_ROWS) {
+      const int s = t / FIN_ROWS, h = f * FIN_ROWS + t % FIN_ROWS;
       const uint64_t* base = &A.mail.ypart[(size_t)s * H + h];
       const int32_t* slots = L.plan.rowslot[s];
       uint32_t v[NSLOT];

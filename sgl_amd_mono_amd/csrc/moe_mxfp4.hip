@@ -56,8 +56,6 @@ struct Lds {
   PlanLds<E, TOPK> plan;
   uint32_t rkey[E];
   float rraw[E];
-  uint32_t tag;
-  uint32_t err;
 };
 
 struct Args {
@@ -111,22 +109,15 @@ class Step {
   }
 
   MONO_DEV void run() {
-    if (tid == 0) {
-      const uint32_t ticket = __hip_atomic_fetch_add(&A.guard.words[G_TICKET], 1u, __ATOMIC_RELAXED,
-                                                     __HIP_MEMORY_SCOPE_AGENT);
-      L.tag = ticket / (uint32_t)G + 1u;
-      L.err = ld_agent_u32(&A.guard.words[G_ERROR]);
-    }
-    __syncthreads();
-    if (L.err != 0) return;
-    gd.a = A.guard;
-    gd.tag = L.tag;
-    gd.deadline = now_ticks() + A.guard.deadline_ticks;
+    if (!guard_begin(A.guard, gd)) return poison(true);
     if ((int)blockIdx.x >= G - S) route(G - 1 - (int)blockIdx.x);
     load_rows();
     __syncthreads();
-    tasks();
+    if (!tasks()) poison(false);
   }
+
+  // NaN over the launch's output (sync.h poison_bf16)
+  MONO_DEV void poison(bool share) const { poison_bf16(A.out, (size_t)S * H, share); }
 
  private:
   const Args& A;
@@ -256,33 +247,34 @@ class Step {
     }
   }
 
-  MONO_DEV void tasks() {
+  MONO_DEV bool tasks() {
     int T = blockIdx.x;
     bool ok;
     int kind = classify(T, ok);
-    if (!ok) return;
+    if (!ok) return false;
     load_task(kind, T);
     while (kind != K_NONE) {
       f32x4 acc[2];
       if (kind == K_UP) {
         up_compute(acc[0], acc[1]);
       } else if (kind == K_DOWN) {
-        if (!down_compute(T, acc)) return;
+        if (!down_compute(T, acc)) return false;
       }
       const int T2 = T + G;
       const int kind2 = classify(T2, ok);
-      if (!ok) return;
+      if (!ok) return false;
       load_task(kind2, T2);
       if (kind == K_UP) {
         up_publish(T, acc[0], acc[1]);
       } else if (kind == K_DOWN) {
         down_publish(T, acc);
       } else {
-        if (!final_task(T)) return;
+        if (!final_task(T)) return false;
       }
       T = T2;
       kind = kind2;
     }
+    return true;
   }
 
   // ---------------------------------------------------------------- up

@@ -50,9 +50,10 @@ constexpr size_t MAIL_WORDS[5] = {(size_t)MAX_PARTS * MAX_ROWS * N_A, (size_t)MA
 hipError_t front_occupancy(int* blocks_per_cu);
 hipError_t back_occupancy(int* blocks_per_cu);
 // kv_mask: -1 writes per-token scales into a.kv_scale; 0 writes raw E4M3 rows (scale 1)
-// and a.kv_scale points at one f32 word
+// and a.kv_scale points at one f32 word; site0: the number of the launch's first wait
+// site under `guard`
 hipError_t front_forward(const mono_proj_weights& w, const mono_front_args& a, int grid, const Mail& mail,
-                         const GuardArgs& guard, int kv_mask, hipStream_t st);
+                         const GuardArgs& guard, int kv_mask, int site0, hipStream_t st);
 hipError_t back_forward(const mono_proj_weights& w, const mono_back_args& a, int grid, const Mail& mail,
                         const GuardArgs& guard, hipStream_t st);
 

@@ -10,39 +10,82 @@
 // the reference's tagged (value, tag) pair (sgl_amd_mono/common/sync.py:30-207,
 // glm53/gfx950/kernel.py:29-35,636-647), restated for HIP.
 //
-// Tags: every workgroup of a launch takes a ticket from guard word 0 with one atomic
-// add; ticket / gridDim.x is the launch's ordinal (launches of one runtime are
-// stream-ordered, so their tickets never interleave) and the tag is ordinal + 1. A
-// HIP-graph replay takes fresh tickets, so it never sees a stale word as ready.
+// Tags: every workgroup of a launch takes a ticket from the 64-bit counter at guard
+// words 4-5 with one atomic add; ticket / gridDim.x is the launch's ordinal (launches
+// sharing a guard are stream-ordered, so their tickets never interleave) and the tag is
+// ordinal % TAG_PERIOD + 1. A HIP-graph replay takes fresh tickets, so it never sees a
+// stale word as ready.
+//
+// Tag epochs: tags repeat every TAG_PERIOD launches, and a word left unwritten for
+// exactly that long would read as fresh (the reference scrubs its mailboxes for the
+// same reason, deepseek_v4/gfx950/kernels/layer.py:837-849). The first launch of every
+// epoch after the first (tag 1, ordinal > 0) therefore zeroes every mailbox the guard's
+// launches write (the guard's scrub table) and meets the whole grid at a barrier
+// (guard word 6) before any workgroup goes on, so within an epoch a word either holds a
+// tag of that epoch or 0. TAG_PERIOD is even, so a tag's parity alternates through the
+// wrap as well (the flip accumulators below rely on it).
 //
 // Guard words (int32 [8] in device memory, common/guard.py:16-30 in the reference):
-//   0  launch tickets
+//   0  tag epochs completed (scrubs run)
 //   1  error: 1 + the id of the first wait site that ran out of time (sticky: every
-//      later launch of the runtime exits at once until the host clears it)
+//      later launch of the guard exits at once until the host clears it)
 //   2  tag of the failing launch (waits of that launch give up when they see it)
 //   3  workgroup that failed first
+//   4-5 launch tickets, u64
+//   6  scrub barrier arrivals (u32, G more a scrub)
 // Every wait polls its words until their tags match, checking the deadline
 // (s_memrealtime, 100 MHz) after its first poll and then every POLL_CHECK polls, and
-// the launch's fail tag every POLL_CHECK polls. On expiry it records the error,
-// raises word 2 and returns false; the caller makes the failure workgroup-uniform and
-// the workgroup exits. No wait ever blocks past the deadline and nothing faults: the
-// launch drains and the host reads the error words (fail-stop without a GPU fault).
+// the launch's fail tag every POLL_CHECK polls. On expiry it records the error (and
+// copies it to the host's pinned error word), raises word 2 and returns false; the
+// caller makes the failure workgroup-uniform and the workgroup exits after writing NaN
+// over the launch's output. No wait ever blocks past the deadline and nothing faults:
+// the launch drains, the host sees the error without synchronising, and a caller that
+// reads the output anyway reads NaN (fail-stop without a GPU fault).
 #pragma once
 
 #include "common.h"
 
 namespace mono {
 
-enum GuardWord { G_TICKET = 0, G_ERROR = 1, G_FAIL_TAG = 2, G_FAIL_BLOCK = 3, G_WORDS = 8 };
+enum GuardWord {
+  G_EPOCH = 0,
+  G_ERROR = 1,
+  G_FAIL_TAG = 2,
+  G_FAIL_BLOCK = 3,
+  G_TICKET = 4,  // u64 at words 4-5
+  G_BARRIER = 6,
+  G_WORDS = 8
+};
 constexpr int POLL_CHECK = 32;
+// tags 1 .. TAG_PERIOD; 0 marks an empty mailbox word
+constexpr uint64_t TAG_PERIOD = 0xFFFFFFFEull;
+// the wait site of the scrub barrier
+constexpr int SCRUB_SITE = 31;
+constexpr int SCRUB_MAX = 4;
 
-// Kernel-argument part of the guard: the words, the deadline and the host-forced
-// fault (a wait site whose waits the host makes fail at once, for tests of the error
-// path; -1 = none).
+// A device region of mailboxes the scrub zeroes: n16 16-byte units at p.
+struct ScrubRegion {
+  uint32_t* p;
+  uint64_t n16;
+};
+
+// Kernel-argument part of the guard.
 struct GuardArgs {
   uint32_t* words;
+  // [SCRUB_MAX] in device memory: the guard's mailboxes (p = NULL past the last region)
+  const ScrubRegion* scrub;
+  // atomic accumulators used by launch parity: [2][flip_words]; every launch zeroes
+  // the copy of its successor's parity, (tag + 1) & 1 (NULL: none)
+  uint32_t* flip;
+  // a pinned host word (device-visible): 1 + the failed wait site of the first failure
+  // or refused launch, so the host sees a stop without synchronising (NULL: none)
+  uint32_t* host_err;
   uint64_t deadline_ticks;
+  // the host-forced fault (tests of the error path): every wait at fault_site of a
+  // launch whose ordinal is at least fault_from fails at once (-1: none)
+  uint64_t fault_from;
   int32_t fault_site;
+  int32_t flip_words;
 };
 
 MONO_DEV uint64_t now_ticks() { return __builtin_amdgcn_s_memrealtime(); }
@@ -97,18 +140,31 @@ MONO_DEV void put_done(uint64_t* base, int i, uint32_t tag) {
 }
 MONO_DEV const uint64_t* done_copy(const uint64_t* base) { return base + (blockIdx.x % DONE_REPLICAS) * DONE_STRIDE; }
 
+// Copy an error code to the host's pinned error word: a plain system-scope store (no
+// atomic read-modify-write over the bus; the device's sticky error word keeps the
+// first failure, this word any failure's code), which the host reads without
+// synchronising.
+MONO_DEV void report_host(uint32_t* host_err, uint32_t code) {
+  if (host_err) __hip_atomic_store(host_err, code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+// A launch's guard once it has begun (guard_begin): what its waits need.
 struct Guard {
-  GuardArgs a;
+  uint32_t* words;
+  uint32_t* host_err;
   uint64_t deadline;  // absolute s_memrealtime tick
   uint32_t tag;
+  int fault;  // this launch's host-forced fault site (-1: none)
 
   // Record a failure at `site` (first one wins) and raise the launch's fail tag.
   MONO_DEV void fail(int site) const {
     uint32_t expect = 0;
-    if (__hip_atomic_compare_exchange_strong(&a.words[G_ERROR], &expect, (uint32_t)site + 1u, __ATOMIC_RELAXED,
-                                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
-      __hip_atomic_store(&a.words[G_FAIL_BLOCK], (uint32_t)blockIdx.x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(&a.words[G_FAIL_TAG], tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (__hip_atomic_compare_exchange_strong(&words[G_ERROR], &expect, (uint32_t)site + 1u, __ATOMIC_RELAXED,
+                                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
+      __hip_atomic_store(&words[G_FAIL_BLOCK], (uint32_t)blockIdx.x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      report_host(host_err, (uint32_t)site + 1u);
+    }
+    __hip_atomic_store(&words[G_FAIL_TAG], tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   // True (and the failure recorded) once the deadline has passed; with `peers`, also
   // once another workgroup of this launch has failed (one more memory round trip).
@@ -117,7 +173,7 @@ struct Guard {
       fail(site);
       return true;
     }
-    return peers && ld_agent_u32(&a.words[G_FAIL_TAG]) == tag;
+    return peers && ld_agent_u32(&words[G_FAIL_TAG]) == tag;
   }
 };
 
@@ -137,7 +193,7 @@ struct Guard {
 // workgroups, where a probe's extra round trip is the cost that matters).
 template <int N, class At, bool CACHED_FIRST = false, bool PROBE = true>
 MONO_DEV bool poll_words(At at, uint32_t (&v)[N], uint32_t pending, int site, const Guard& g) {
-  if (pending && site == g.a.fault_site) {  // host-forced fault: the wait fails at once
+  if (pending && site == g.fault) {  // host-forced fault: the wait fails at once
     g.fail(site);
     return false;
   }
@@ -218,5 +274,98 @@ MONO_DEV bool hint_wait(int n, At at, int site, const Guard& g) {
 
 // Workgroup-uniform AND of a per-thread flag (a full barrier).
 MONO_DEV bool block_all(bool ok) { return __syncthreads_and(ok ? 1 : 0) != 0; }
+
+// Zero the guard's mailboxes (the first launch of a tag epoch), then meet every
+// workgroup of the grid: each adds one to guard word 6 once its zeros are stored and
+// waits until the launch's G arrivals are in (every scrub adds exactly G, so the count
+// is a multiple of G between scrubs). Workgroup-uniform result.
+MONO_DEV bool scrub_mailboxes(const GuardArgs& a, const Guard& gd) {
+  const uint32_t n_threads = gridDim.x * blockDim.x;
+  const uint32_t me = blockIdx.x * blockDim.x + threadIdx.x;
+  const u32x4 zero = {0u, 0u, 0u, 0u};
+  for (int k = 0; k < SCRUB_MAX; ++k) {
+    const ScrubRegion rg = a.scrub[k];
+    if (!rg.p) break;  // uniform
+    // device-coherent 16-byte stores (regions are far below 4 GB)
+    const __amdgpu_buffer_rsrc_t rs = coherent_rsrc(rg.p, (uint32_t)(rg.n16 * 16));
+    for (uint64_t i = me; i < rg.n16; i += n_threads)
+      __builtin_amdgcn_raw_buffer_store_b128(zero, rs, (int)(i * 16), 0, SC1);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  __shared__ uint32_t target;
+  if (threadIdx.x == 0) {
+    uint32_t* bar = &gd.words[G_BARRIER];
+    const uint32_t before = __hip_atomic_fetch_add(bar, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    target = before - before % gridDim.x + gridDim.x;
+    if (blockIdx.x == 0)
+      (void)__hip_atomic_fetch_add(&gd.words[G_EPOCH], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  bool ok = true;
+  if (threadIdx.x == 0) {
+    const uint32_t want = target;
+    for (uint32_t spin = 0;; ++spin) {
+      if ((int32_t)(ld_agent_u32(&gd.words[G_BARRIER]) - want) >= 0) break;
+      if (spin % POLL_CHECK == 0 && gd.expired(SCRUB_SITE, spin > 0)) {
+        ok = false;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+  }
+  return block_all(ok);
+}
+
+// The start of every launch, called by every thread of the workgroup: take the
+// workgroup's ticket, set up the guard (tag, deadline, this launch's forced fault),
+// scrub the mailboxes at the start of a tag epoch and clear the successor's copy of the
+// flip accumulators. False (workgroup-uniform) if the guard's sticky error refuses the
+// launch (a refused launch reports the error to the host word) or the scrub failed.
+MONO_DEV bool guard_begin(const GuardArgs& a, Guard& gd) {
+  __shared__ uint32_t sh[4];
+  if (threadIdx.x == 0) {
+    uint64_t* tickets = reinterpret_cast<uint64_t*>(&a.words[G_TICKET]);
+    const uint64_t ticket = __hip_atomic_fetch_add(tickets, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint64_t ord = ticket / gridDim.x;
+    const uint64_t in_epoch = ord % TAG_PERIOD;
+    sh[0] = (uint32_t)in_epoch + 1u;
+    sh[1] = ld_agent_u32(&a.words[G_ERROR]);
+    sh[2] = ord >= a.fault_from ? 1u : 0u;
+    sh[3] = (in_epoch == 0 && ord != 0) ? 1u : 0u;
+  }
+  __syncthreads();
+  gd.words = a.words;
+  gd.host_err = a.host_err;
+  gd.tag = sh[0];
+  gd.deadline = now_ticks() + a.deadline_ticks;
+  gd.fault = sh[2] ? a.fault_site : -1;
+  const uint32_t err = sh[1];
+  const bool scrub = sh[3] != 0;
+  __syncthreads();  // sh is read before any later launch's use of it
+  if (err != 0) {
+    if (threadIdx.x == 0) report_host(a.host_err, err);
+    return false;
+  }
+  if (scrub && !scrub_mailboxes(a, gd)) return false;
+  if (a.flip) {
+    uint32_t* nx = a.flip + (size_t)((gd.tag + 1u) & 1u) * a.flip_words;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < a.flip_words; i += gridDim.x * blockDim.x)
+      __hip_atomic_store(&nx[i], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  return true;
+}
+
+// A launch that failed or was refused writes NaN over its bf16 output (n elements at p)
+// so a caller that reads it anyway gets no plausible numbers: `share` writes the
+// workgroup's grid-strided share (every workgroup refuses together), otherwise the
+// whole output (the workgroups that saw a failure; others may have finished).
+MONO_DEV void poison_bf16(void* p, size_t n, bool share) {
+  if (!p) return;
+  uint32_t* w = static_cast<uint32_t*>(p);
+  const size_t words = n / 2;
+  const size_t step = share ? (size_t)gridDim.x * blockDim.x : blockDim.x;
+  for (size_t i = (share ? blockIdx.x * blockDim.x : 0) + threadIdx.x; i < words; i += step) w[i] = 0x7fc07fc0u;
+}
 
 }  // namespace mono

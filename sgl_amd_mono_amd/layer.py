@@ -278,29 +278,24 @@ class LayerHandle(Runtime):
                                       softmax_scale=SOFTMAX_SCALE, route_scale=FP8_MOE.route_scale,
                                       eps=FP8_MOE.eps))
 
-    def set_fault(self, site: int, launch: int = 1) -> None:
-        """Tests of the fail-stop path: every wait at ``site`` of ``launch`` (0 front,
-        1 the fused rest) fails at once (-1: off)."""
-        _lib.check(self._fn("set_fault")(self._h, int(launch), int(site)))
+    SITES = _lib.LAYER_SITES
 
-    def error_words(self) -> list[int]:
-        """The two launches' guard words (synchronises): front, then the fused rest."""
-        words = (C.c_int32 * (2 * _lib.GUARD_WORDS))()
+    def set_fault(self, site: int, after: int = 0) -> None:
+        """Tests of the fail-stop path (the reference's fault injection): every wait at
+        ``site`` (layer numbering, ``_lib.LAYER_SITES``) of every launch from the
+        ``after``-th next one on fails at once (-1: off)."""
+        _lib.check(self._fn("set_fault")(self._h, int(site), int(after)))
+
+    def pending_error(self) -> int:
+        """The pinned host error word, read without synchronising: 0, or 1 + the wait
+        site of a launch that failed or was refused since the last clear."""
+        return int(self._fn("pending_error")(self._h))
+
+    def set_launch_ordinal(self, ordinal: int) -> None:
+        """Tests of the tag epochs (synchronises): the next launch takes tag
+        ``ordinal % TAG_PERIOD + 1``."""
         with torch.cuda.device(self.device):
-            _lib.check(self._fn("read_errors")(self._h, words))
-        return list(words)
-
-    def check_errors(self) -> None:
-        w = self.error_words()
-        for k, (name, sites) in enumerate((("front", _lib.PROJ_SITES), ("attention + back + MoE", _lib.TAIL_SITES))):
-            e = w[4 * k:4 * k + 4]
-            if e[1]:
-                site = e[1] - 1
-                raise _lib.MonoError(
-                    _lib.MONO_ESTATE,
-                    f"layer {name} launch (tag {e[2]}) stopped: wait '{sites.get(site, site)}' passed its deadline "
-                    f"in workgroup {e[3]}; the runtime refuses launches until clear_errors()",
-                )
+            _lib.check(self._fn("set_launch_ordinal")(self._h, int(ordinal)))
 
 
 class LayerRuntime:
@@ -436,3 +431,18 @@ class LayerRuntime:
     def check_errors(self) -> None:
         for rt in self.parts:
             rt.check_errors()
+
+    def raise_pending(self) -> None:
+        """Raise MonoError if a launch failed or was refused since the last clear, read
+        from the pinned host word without synchronising (a serving loop calls it once a
+        step; the launch that failed wrote NaN over its output)."""
+        if self.mode != "layer":
+            return
+        code = self.handle.pending_error()
+        if code:
+            site = code - 1
+            raise _lib.MonoError(
+                _lib.MONO_ESTATE,
+                f"a layer launch stopped at wait '{_lib.LAYER_SITES.get(site, site)}' (deadline passed or refused "
+                "after an earlier failure); its output is NaN and the runtime refuses launches until clear_errors()",
+            )

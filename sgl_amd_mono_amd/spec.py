@@ -62,7 +62,11 @@ TP_SIZES = (4,)
 # one persistent workgroup per CU of an MI355X
 BLOCKS = 256
 LOCAL_SHARE_ENV = "SGL_AMD_MONO_AMD_LOCAL_SHARE"
-DEADLINE_S = 2.0
+# the reference's test fault injection, rank:site[:after] (common/guard.py:79-88); site in
+# the layer runtime's numbering (_lib.LAYER_SITES)
+FAULT_INJECT_ENV = "SGLANG_AMD_MONO_FAULT_INJECT"
+# a wait's deadline: below the server's watchdog, at most this long (common/guard.py:4-6)
+MAX_DEADLINE_S = 60.0
 
 # Each covered layer against SGLang's layer on the same input (check mode): the stream
 # it writes, the KV row, the index key; the top-k of its own scores exactly
@@ -98,7 +102,8 @@ def config_disable_reasons(cfg, hf_config) -> list[str]:
         if getattr(hf_config, key, None) != want
     ]
     if getattr(hf_config, "moe_layer_freq", 1) != 1:
-        reasons.append("needs every layer after the dense ones to be MoE")
+        reasons.append(f"moe_layer_freq {hf_config.moe_layer_freq}: a launch carries a routed MoE, so every "
+                       "layer from first_k_dense_replace on must have one")
     quant = getattr(hf_config, "quantization_config", None) or {}
     if quant.get("quant_method") != "fp8" or list(quant.get("weight_block_size") or ()) != [128, 128]:
         reasons.append(f"needs the FP8 block-128 checkpoint, got {quant.get('quant_method')!r} "
@@ -113,7 +118,8 @@ def config_disable_reasons(cfg, hf_config) -> list[str]:
         getattr(cfg, "speculative_eagle_topk", 1) != 1
         or cfg.speculative_num_draft_tokens != cfg.speculative_num_steps + 1
     ):
-        reasons.append("MTP verifies one draft chain: topk 1, draft tokens = steps + 1")
+        reasons.append("speculative decoding: the launch's rows of a request must form one causal chain "
+                       "(speculative_eagle_topk 1 and speculative_num_draft_tokens = speculative_num_steps + 1)")
     context_len = getattr(cfg, "context_length", None)
     if context_len is not None and max_context(context_len) > 32768:
         reasons.append(f"context {context_len}: a row holds at most 32768 keys on the kernels")
@@ -140,8 +146,8 @@ def model_disable_reasons(model, hf_config, copies: dict) -> list[str]:
             row_major.setdefault(name, []).append(i)
     for name, ids in row_major.items():
         where = f"layer {ids[0]}" if len(ids) == 1 else f"{len(ids)} layers from {ids[0]}"
-        reasons.append(f"{name} of {where}: needs AITER's (16, 16) FP8 layout, which SGLang applies for its "
-                       "AITER block-FP8 GEMM")
+        reasons.append(f"{name} of {where} is row-major: the launches read FP8 weights in place in the "
+                       "16 x 16 shuffled layout of SGLang's AITER block-FP8 path")
     return reasons
 
 
@@ -180,6 +186,8 @@ class _Built:
         """``DeepseekV2ForCausalLM.forward`` for a decode or verify step; a step wider
         than the runtime runs the model's own forward."""
         lm = self.lm
+        if self.runtime is not None:  # a launch that stopped earlier: raise, never serve its NaN
+            self.runtime.raise_pending()
         if plan.key.rows > self.max_rows:
             return type(lm).forward(lm, input_ids, positions, forward_batch, input_embeds, pp_proxy_tensors)
         hidden = self._backbone(plan, input_ids, positions, forward_batch, input_embeds)
@@ -265,8 +273,38 @@ def _build(model, hf_config, ctx) -> _Built:
         raise ValueError(f"monokernel: the kernels run at most {MAX_ROWS} rows; this server routes {sorted(ctx.widths)}")
     device = cos.device
     rt = LayerRuntime(max(widths), max_context(context_len), device)
-    rt.set_deadline(getattr(ctx, "deadline_s", None) or DEADLINE_S)
+    rt.set_deadline(deadline_seconds(ctx))
+    fault = fault_injection(p.tp_rank)
+    if fault is not None:
+        rt.handle.set_fault(*fault)
     return _Built(model, layers, rt, cos, sin, device, context_len)
+
+
+def deadline_seconds(ctx) -> float:
+    """Every wait's deadline: the framework's own (``ctx.deadline_s``, half its watchdog
+    at most 60 s, as the reference's build takes it, glm53/spec.py:569), else half of
+    ``ctx.watchdog_timeout`` at most 60 s, else 60 s."""
+    given = getattr(ctx, "deadline_s", None)
+    if given:
+        return float(given)
+    watchdog = getattr(ctx, "watchdog_timeout", None)
+    return min(0.5 * float(watchdog), MAX_DEADLINE_S) if watchdog else MAX_DEADLINE_S
+
+
+def fault_injection(rank: int):
+    """This rank's test fault from ``SGLANG_AMD_MONO_FAULT_INJECT=rank:site[:after]``:
+    (site, after) for ``LayerHandle.set_fault``, or None (the reference's
+    common/guard.py:79-88: once ``after`` launches have run, the wait at ``site``
+    fails)."""
+    spec = os.environ.get(FAULT_INJECT_ENV, "")
+    if not spec:
+        return None
+    parts = (spec.split(":") + ["0", "0"])[:3]
+    try:
+        r, site, after = (int(x or 0) for x in parts)
+    except ValueError:
+        raise ValueError(f"{FAULT_INJECT_ENV}={spec!r}: expected rank:site[:after] integers") from None
+    return (site, after) if r == rank else None
 
 
 SPEC = MonoSpec(

@@ -223,8 +223,10 @@ def test_layer_launch_modes_agree_bitwise(gpu_device, rows):
 def test_layer_launch_fail_stop(gpu_device, site, what):
     """A forced wait failure in the one-launch layer (the MoE's wait on the attention
     block's output rows, the front's stage-A wait, the attention's waits on the front)
-    stops it without a fault: the error names the site, later launches are refused
-    until the errors are cleared, then the layer runs again."""
+    stops it without a fault: the error names the site, the host word reports it
+    without a synchronisation, the failed launch's output is NaN, later launches are
+    refused (their output NaN too) until the errors are cleared, then the layer runs
+    again."""
     ctx, rows = 4096, 2
     cos, sin = workloads.rope_tables(ctx, gpu_device)
     w = LayerWeights(proj=workloads.proj_weights(gpu_device, seed=41),
@@ -236,16 +238,26 @@ def test_layer_launch_fail_stop(gpu_device, site, what):
         good = rt.forward(x, step.seq_lens, step.page_table, caches, w, cos, sin).clone()
         torch.cuda.synchronize()
         rt.check_errors()
-        rt.handle.set_fault(site, launch=1)
-        rt.forward(x, step.seq_lens, step.page_table, caches, w, cos, sin)
+        assert rt.handle.pending_error() == 0
+        rt.handle.set_fault(site)
+        bad = rt.forward(x, step.seq_lens, step.page_table, caches, w, cos, sin).clone()
         torch.cuda.synchronize()
+        assert rt.handle.pending_error() == site + 1
+        with pytest.raises(Exception, match=what):
+            rt.raise_pending()
         with pytest.raises(Exception, match=what):
             rt.check_errors()
-        rt.handle.set_fault(-1, launch=1)
+        assert bool(bad.isnan().all()), "a failed launch's output is NaN"
+        rt.handle.set_fault(-1)
+        refused = rt.forward(x, step.seq_lens, step.page_table, caches, w, cos, sin).clone()
+        torch.cuda.synchronize()
+        assert bool(refused.isnan().all()), "a refused launch's output is NaN"
         rt.clear_errors()
+        assert rt.handle.pending_error() == 0
         again = rt.forward(x, step.seq_lens, step.page_table, caches, w, cos, sin)
         torch.cuda.synchronize()
         rt.check_errors()
+        rt.raise_pending()
         assert torch.equal(again, good)
     finally:
         rt.close()

@@ -72,7 +72,7 @@ def test_config_refusals(local_share):
     assert any("--page-size 32" in r for r in mono.config_disable_reasons(pages, DSV32))
     mtp = SimpleNamespace(**{**vars(CFG), "speculative_algorithm": "EAGLE", "speculative_eagle_topk": 2,
                              "speculative_num_steps": 3, "speculative_num_draft_tokens": 4})
-    assert any("one draft chain" in r for r in mono.config_disable_reasons(mtp, DSV32))
+    assert any("one causal chain" in r for r in mono.config_disable_reasons(mtp, DSV32))
     chain = SimpleNamespace(**{**vars(mtp), "speculative_eagle_topk": 1})
     assert mono.config_disable_reasons(chain, DSV32) == []
     long = SimpleNamespace(**{**vars(CFG), "context_length": 163840})
@@ -122,12 +122,19 @@ def test_step_table_rows_keys_and_pad_rows():
 
 
 class _Runtime:
-    """Records each covered layer's launch; returns h + 1 as the layer's output."""
+    """Records each covered layer's launch; returns h + 1 as the layer's output.
+    ``pending`` stands for the pinned host word a stopped launch sets."""
 
     max_rows = 16
 
-    def __init__(self):
-        self.calls = []
+    def __init__(self, pending: int = 0):
+        self.calls, self.pending = [], pending
+
+    def raise_pending(self):
+        if self.pending:
+            from sgl_amd_mono_amd import _lib
+
+            raise _lib.MonoError(_lib.MONO_ESTATE, f"a layer launch stopped at wait {self.pending - 1}")
 
     def forward(self, h, seq_lens, page_table, caches, w, cos, sin, check_weights=True):
         self.calls.append((h.clone(), seq_lens.clone(), caches, w))
@@ -172,6 +179,48 @@ def test_backbone_runs_dense_layers_then_launches():
     assert out[0] == "logits" and float(out[1][0, 0]) == 170.0
     # each layer bound its caches once, scale-less E4M3 rows
     assert covered[3].caches.kv_scale is None and covered[3].caches.kv.shape == (64, 576)
+
+
+def test_a_stopped_launch_raises_instead_of_serving():
+    """A launch that failed a wait (or was refused after one) sets the runtime's pinned
+    host word; the next forward raises before anything runs, so SGLang never samples
+    tokens from the NaN the stopped launch left in its output."""
+    from sgl_amd_mono_amd import _lib
+
+    lm = _Lm(SimpleNamespace(embed_tokens=lambda ids: torch.ones(1, 7168), layers=[], norm=lambda h: h))
+    rt = _Runtime(pending=9)  # expert outputs
+    built = mono._Built(lm, {3: None}, rt, None, None, "cpu", context_len=4096)
+    key = registry.ShapeKey(forward_mode="decode", batch_size=1, tokens_per_request=1)
+    with pytest.raises(_lib.MonoError, match="stopped at wait 8"):
+        built.forward(registry.Plan(key=key), "ids", torch.tensor([3]), SimpleNamespace())
+    assert rt.calls == [] and lm.ran == []
+    # a step wider than the runtime raises as well: the model's forward would run the
+    # dense layers on the same GPU whose launch stopped
+    key = registry.ShapeKey(forward_mode="decode", batch_size=17, tokens_per_request=1)
+    with pytest.raises(_lib.MonoError):
+        built.forward(registry.Plan(key=key), "ids", "positions", "batch")
+
+
+def test_deadline_follows_the_watchdog():
+    """The framework's deadline when it gives one, else half the watchdog at most 60 s
+    (common/guard.py:4-6), else 60 s."""
+    assert mono.deadline_seconds(SimpleNamespace(deadline_s=12.5)) == 12.5
+    assert mono.deadline_seconds(SimpleNamespace(watchdog_timeout=30)) == 15.0
+    assert mono.deadline_seconds(SimpleNamespace(watchdog_timeout=300)) == 60.0
+    assert mono.deadline_seconds(SimpleNamespace()) == 60.0
+
+
+def test_fault_injection_env(monkeypatch):
+    """SGLANG_AMD_MONO_FAULT_INJECT=rank:site[:after], the reference's format."""
+    monkeypatch.delenv(mono.FAULT_INJECT_ENV, raising=False)
+    assert mono.fault_injection(0) is None
+    monkeypatch.setenv(mono.FAULT_INJECT_ENV, "1:8:40")
+    assert mono.fault_injection(1) == (8, 40) and mono.fault_injection(0) is None
+    monkeypatch.setenv(mono.FAULT_INJECT_ENV, "0:17")
+    assert mono.fault_injection(0) == (17, 0)
+    monkeypatch.setenv(mono.FAULT_INJECT_ENV, "0:x")
+    with pytest.raises(ValueError, match="rank:site"):
+        mono.fault_injection(0)
 
 
 # ---- binding SGLang-shaped tensors in place ----
