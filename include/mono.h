@@ -219,6 +219,21 @@ typedef struct {
 
 int mono_attn_forward(mono_attn* attn, const mono_attn_args* args, void* stream);
 
+/* mono_attn_forward without a runtime and without any allocation. No counterpart in the
+ * reference: it is for callers that cannot allocate (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc). The launch's mailboxes and
+ * guard words live in the library's static device scratch, about 10 MiB that each GPU
+ * the library runs on holds until the process ends, sized for at most 8 rows of at
+ * most 32768 keys (rows beyond 8, or a page table narrower than 512 pages, are
+ * refused with MONO_EINVAL). The first call on a device clears that scratch with a
+ * fill kernel on `stream` and must not run under stream capture; no call allocates or
+ * synchronises. Every call on one GPU shares its scratch: calls must be stream-ordered,
+ * and calls that overlap on one GPU race. Results equal mono_attn_forward's on a
+ * runtime of max_rows 8, max_ctx 32768 and the same softmax_scale. Errors are not
+ * sticky (no handle exists to clear them): a launch whose wait passes its 2 s deadline
+ * writes NaN over `out`, and the next call runs normally. */
+int mono_attn_forward_noalloc(const mono_attn_args* args, float softmax_scale, void* stream);
+
 /* Guard controls of an attention runtime (as the MoE runtime's). Wait sites: 0 index
  * scores (a row's score chunks), 1 selected slots, 2 split partials, 3 top-k team
  * histograms and candidates. */

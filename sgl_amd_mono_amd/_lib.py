@@ -108,6 +108,7 @@ SIGNATURES = {
     "mono_attn_create": (C.c_int, [C.POINTER(AttnConfig), C.POINTER(_VP)]),
     "mono_attn_destroy": (C.c_int, [_VP]),
     "mono_attn_forward": (C.c_int, [_VP, C.POINTER(AttnArgs), _VP]),
+    "mono_attn_forward_noalloc": (C.c_int, [C.POINTER(AttnArgs), C.c_float, _VP]),
     "mono_attn_set_deadline": (C.c_int, [_VP, C.c_double]),
     "mono_attn_read_errors": (C.c_int, [_VP, C.POINTER(C.c_int32)]),
     "mono_attn_clear_errors": (C.c_int, [_VP]),

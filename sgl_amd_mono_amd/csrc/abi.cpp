@@ -13,6 +13,7 @@
 #include <cstring>
 #include <string>
 
+#include "abi_errors.h"
 #include "attn_back_ops.h"
 #include "layer_ops.h"
 #include "attn_ops.h"
@@ -76,6 +77,12 @@ struct Carve {
 };
 
 }  // namespace
+
+namespace mono {
+// the library's error string for entry points in other sources (abi_errors.h)
+int abi_fail(int code, const char* msg) { return fail(code, "%s", msg); }
+int abi_ok() { return ok(); }
+}  // namespace mono
 
 // A pinned host word the launches' guard copies its errors to (system scope), so the
 // host sees a stopped launch without synchronising.
@@ -154,6 +161,7 @@ struct RuntimeBase {
     guard.deadline_ticks = (uint64_t)(DEFAULT_DEADLINE_S * TICKS_PER_S);
     guard.fault_site = -1;
     guard.fault_from = 0;
+    guard.sticky = 1;
     return MONO_OK;
   }
   char* at(size_t off) const { return static_cast<char*>(blob) + off; }

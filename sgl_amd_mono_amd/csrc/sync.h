@@ -86,6 +86,9 @@ struct GuardArgs {
   uint64_t fault_from;
   int32_t fault_site;
   int32_t flip_words;
+  // 1: a failure refuses every later launch until the host clears it (a runtime
+  // handle's guard); 0: later launches run (a guard no host call can clear)
+  int32_t sticky;
 };
 
 MONO_DEV uint64_t now_ticks() { return __builtin_amdgcn_s_memrealtime(); }
@@ -295,11 +298,16 @@ MONO_DEV bool scrub_mailboxes(const GuardArgs& a, const Guard& gd) {
   __syncthreads();
   __shared__ uint32_t target;
   if (threadIdx.x == 0) {
+    if (blockIdx.x == 0) {
+      (void)__hip_atomic_fetch_add(&gd.words[G_EPOCH], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      // a failure's tag of the old epoch must not read as this epoch's (a guard that
+      // runs on after a failure reaches the wrap); stored before this workgroup arrives
+      __hip_atomic_store(&gd.words[G_FAIL_TAG], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __builtin_amdgcn_s_waitcnt(0);
+    }
     uint32_t* bar = &gd.words[G_BARRIER];
     const uint32_t before = __hip_atomic_fetch_add(bar, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     target = before - before % gridDim.x + gridDim.x;
-    if (blockIdx.x == 0)
-      (void)__hip_atomic_fetch_add(&gd.words[G_EPOCH], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   __syncthreads();
   bool ok = true;
@@ -330,7 +338,7 @@ MONO_DEV bool guard_begin(const GuardArgs& a, Guard& gd) {
     const uint64_t ord = ticket / gridDim.x;
     const uint64_t in_epoch = ord % TAG_PERIOD;
     sh[0] = (uint32_t)in_epoch + 1u;
-    sh[1] = ld_agent_u32(&a.words[G_ERROR]);
+    sh[1] = a.sticky ? ld_agent_u32(&a.words[G_ERROR]) : 0u;
     sh[2] = ord >= a.fault_from ? 1u : 0u;
     sh[3] = (in_epoch == 0 && ord != 0) ? 1u : 0u;
   }
