@@ -18,13 +18,8 @@ import torch
 import torch.nn.functional as F
 
 from . import codecs, topk
-
-
-def rmsnorm(x: torch.Tensor, gamma: torch.Tensor, eps: float) -> torch.Tensor:
-    """f32 x * rsqrt(mean(x^2) + eps) * gamma (glm53/gfx950/kernel.py:1367-1415)."""
-    x = x.float()
-    rstd = torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps)
-    return x * rstd * gamma.float()
+# one RMSNorm for every phase (glm53/gfx950/kernel.py:1367-1415): the projections'
+from .layer import rmsnorm  # noqa: F401
 
 
 # ---------------------------------------------------------------- config 1
