@@ -562,6 +562,22 @@ def bench_layer(args, dev):
         rt.check_errors()
         layer_durs = [lev[k][l][0].elapsed_time(lev[k][l][1]) * 1e3 for k in range(n_eager) for l in range(L)]
 
+    # eager pass with in-kernel phase ticks (one launch a layer): the critical path and
+    # each phase's span inside the launch
+    stamped = None
+    if one:
+        grid = torch.cuda.get_device_properties(dev).multi_processor_count
+        ticks = torch.zeros(n_eager, L, grid, 16, dtype=torch.int64, device=dev)
+        torch.cuda.synchronize()
+        for k in range(n_eager):
+            x = x_in
+            for l, (w, step, caches) in enumerate(layers):
+                x = rt.forward(x, step.seq_lens, step.page_table, caches, w, cos, sin, out=xb[l % 2],
+                               check_weights=False, ticks=ticks[k, l])
+        torch.cuda.synchronize()
+        rt.check_errors()
+        stamped = ticks.cpu()
+
     w0 = layers[0][0]
     moe_fixed = 256 * 7168 * 2 + 256 * 4 + 7168 * 2 + 2 * S * 7168 * 2
     moe_b = [d * fp8_expert_bytes(FP8_MOE) + moe_fixed for d in distinct]
@@ -585,6 +601,14 @@ def bench_layer(args, dev):
     moe_achieved = statistics.fmean(
         b / (t * 1e-6) for b, t in zip([dom_b[l] for _ in range(n_eager) for l in range(L)], moe_durs)) / 1e9
     layer_bytes = sum(phase_bytes.values())
+    phase_ticks = None
+    if stamped is not None:
+        pb = {"front": proj_bytes(w0.proj, FRONT_W) + S * 7168 * 2 + S * (576 + 4 + 68)
+                       + S * (32 * 576 * 2 + 64 * 68 + 128),
+              "attn": attn_step_bytes(lens), "back": proj_bytes(w0.proj, BACK_W) + S * (32 * 512 * 2 + 2 * 7168 * 2)}
+        phase_ticks = layer_phase_breakdown(stamped, pb, [moe_b[l] for l in range(L)])
+        log("phases (in-kernel ticks, us): " + ", ".join(f"{k} {v:.2f}" for k, v in phase_ticks.items()
+                                                         if k.endswith("_us")))
     log(f"{us:.2f} us/layer ({step_us / 1e3:.3f} ms a {L}-layer step, median {statistics.median(per) / L:.2f}), "
         f"{layer_bytes / (us * 1e-6) / 1e9:.0f} GB/s over the layer; eager phases "
         + ", ".join(f"{p} {ph_us[p]:.1f}" for p in phases) + f" us; {dom_kernel} {moe_achieved:.0f} GB/s; "
@@ -611,6 +635,7 @@ def bench_layer(args, dev):
             phases_achieved_gbs={p: phase_bytes[p] / (ph_us[p] * 1e-6) / 1e9 for p in phases},
             distinct_experts_mean=statistics.fmean(distinct),
         ),
+        phases=phase_ticks,
         roofline=dict(
             bound="hbm", achieved=moe_achieved, peak=HBM_PEAK_GBS, unit="GB/s", frac=moe_achieved / HBM_PEAK_GBS,
             traffic=traffic,
@@ -620,6 +645,43 @@ def bench_layer(args, dev):
         ),
         cpu_baseline=cpu,
     )
+
+
+def layer_phase_breakdown(ticks, fixed_bytes: dict, moe_bytes: list) -> dict:
+    """Phases of one-launch layers from their per-workgroup ticks ([steps, layers, grid, 8]:
+    begin, front done, attention done, back done, MoE plan ready, end; 100 MHz).
+
+    The critical path: the launch's begin (first workgroup), then the moment the last
+    workgroup finished each phase (front, attention, back, MoE plan, end); the five
+    differences add up to the launch. A phase's span runs from the first workgroup
+    entering it (its previous phase done) to the last leaving it; its achieved GB/s is
+    its algorithmic bytes over that span. Means over every stamped launch."""
+    t = ticks.double() * 10e-3  # us
+    begin = t[..., 0].min(-1).values
+    last = [t[..., i].max(-1).values for i in range(1, 6)]  # front, attn, back, plan, end
+    first = [t[..., i].min(-1).values for i in range(0, 4)]  # entering front, attn, back, MoE
+    crit = {"front_us": last[0] - begin, "attn_us": last[1] - last[0], "back_us": last[2] - last[1],
+            "moe_prologue_us": last[3] - last[2], "moe_stream_us": last[4] - last[3]}
+    span = {"front_span_us": last[0] - first[0], "attn_span_us": last[1] - first[1],
+            "back_span_us": last[2] - first[2], "moe_span_us": last[4] - first[3]}
+    out = {k: float(v.mean()) for k, v in {**crit, **span}.items()}
+    out["launch_us"] = float((last[4] - begin).mean())
+    moe_b = torch_tensor(moe_bytes)[None, :].expand_as(span["moe_span_us"]).double()
+    out["front_gbs"] = fixed_bytes["front"] / out["front_span_us"] / 1e3
+    out["attn_gbs"] = fixed_bytes["attn"] / out["attn_span_us"] / 1e3
+    out["back_gbs"] = fixed_bytes["back"] / out["back_span_us"] / 1e3
+    out["moe_gbs"] = float((moe_b / span["moe_span_us"]).mean()) / 1e3
+    out["attn_frac"] = out["attn_gbs"] / HBM_PEAK_GBS
+    out["moe_frac"] = out["moe_gbs"] / HBM_PEAK_GBS
+    out["note"] = ("critical path *_us add up to launch_us; *_span_us from the first workgroup entering a phase "
+                   "to the last leaving it (phases overlap); *_gbs = algorithmic bytes / span")
+    return out
+
+
+def torch_tensor(v):
+    import torch
+
+    return torch.tensor(v, dtype=torch.float64)
 
 
 CALIB_BYTES = 1 << 30  # the calibration copy of a PMC pass: 1 GiB read, 1 GiB written
@@ -793,6 +855,7 @@ def main() -> int:
         "config": r["config"],
         "roofline": r["roofline"],
         "cpu_baseline": r["cpu_baseline"],
+        "phases": r.get("phases"),
         **r["extra"],
     }
     print(json.dumps(line), flush=True)

@@ -369,6 +369,14 @@ typedef struct {
   const mono_attn_args* attn;
   const mono_back_args* back;
   const mono_moe_fp8_args* moe;
+  /* optional i64 [grid, 16] (the layer's launches; NULL skips): per workgroup, the
+   * s_memrealtime tick (100 MHz) at which it [0] began, finished its [1] front tasks,
+   * [2] attention tasks, [3] back tasks, [4] had the MoE's expert plan, [5] finished;
+   * and the MoE prologue's moments: [6] the attention block's output seen, [7] its
+   * norm statistics, [8] its router task done, [9] its route done (the last `rows`
+   * workgroups only), [10] the rows quantised; the rest 0. The reference's per-CTA
+   * stamps (common/stamps.py:24-33). */
+  int64_t* ticks;
 } mono_layer_args;
 
 /* Replaces Glm53Runtime (runner.py:133-215) for a whole decoder layer: the mailboxes

@@ -90,7 +90,12 @@ class LayerConfig(C.Structure):
 
 class LayerArgs(C.Structure):
     _fields_ = [("front", C.POINTER(FrontArgs)), ("attn", C.POINTER(AttnArgs)), ("back", C.POINTER(BackArgs)),
-                ("moe", C.POINTER(MoeFp8Args))]
+                ("moe", C.POINTER(MoeFp8Args)), ("ticks", _VP)]
+
+
+# the phase boundaries a one-launch layer stamps per workgroup (mono_layer_args.ticks)
+LAYER_TICKS = ("begin", "front", "attn", "back", "plan", "end", "a_seen", "norm", "router", "route", "quant")
+LAYER_TICK_WORDS = 16
 
 
 # entry point -> (restype, argtypes); every name include/mono.h declares

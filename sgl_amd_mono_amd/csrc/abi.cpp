@@ -906,12 +906,12 @@ static int layer_launch(mono_layer* L, const mono_proj_weights* w, const mono_la
     }
     if (tail)  // the whole layer as one launch
       e = mono::layer::layer_forward(*w, fa, L->p->mail, kv_mask, g, L->a->mail, L->guard, b, L->a->back_mail, m,
-                                     L->m->mail, L->a_done, L->a->grid, st);
+                                     L->m->mail, L->a_done, args->ticks, L->a->grid, st);
     else  // the front alone, under the layer's guard (its sites numbered as in the one launch)
       e = mono::proj::front_forward(*w, fa, L->a->grid, L->p->mail, L->guard, kv_mask, mono::layer::FRONT_SITE0, st);
   } else {
     e = mono::layer::tail_forward(g, L->a->mail, L->guard, *w, b, L->a->back_mail, m, L->m->mail, L->a_done,
-                                  L->a->grid, st);
+                                  args->ticks, L->a->grid, st);
   }
   if (e != hipSuccess) return fail(MONO_EHIP, "launching the layer: %s", hipGetErrorString(e));
   return ok();

@@ -27,7 +27,15 @@ struct Args {
   proj::Args bk;
   moe::Args mo;
   uint64_t* a_done;
+  int64_t* ticks;  // [grid][16] phase ticks (NULL: none)
 };
+
+// the layer's moments in a workgroup's tick row (4 and 6-10: the MoE's, moe_fp8_step.h)
+enum { T_BEGIN = 0, T_FRONT = 1, T_ATTN = 2, T_BACK = 3, T_END = 5, T_WORDS = 16 };
+
+MONO_DEV void stamp(int64_t* ticks, int k) {
+  if (ticks && threadIdx.x == 0) ticks[blockIdx.x * T_WORDS + k] = (int64_t)now_ticks();
+}
 
 union Lds {
   attn::Lds at;
@@ -60,19 +68,25 @@ MONO_DEV bool back_moe(const Args& args, Lds& lds, const attn::Step& st, const G
     bk.publish_a(args.a_done);
     if (!bk.tasks(st.n_tasks())) return false;
   }
+  stamp(args.ticks, T_BACK);
   __syncthreads();  // and to the MoE's
   moe::Step ms(args.mo, lds.mo);
   ms.adopt(g, args.a_done, proj::NT_O, MOE_SITE0);
   bool refused;
-  return ms.run(refused);
+  if (!ms.run(refused)) return false;
+  stamp(args.ticks, T_END);
+  return true;
 }
 
 __global__ __launch_bounds__(512, 1) void k_layer_tail(Args args) {
   __shared__ Lds lds;
   attn::Step st(args.at, lds.at);
   if (!st.begin()) return poison(args, true);
+  stamp(args.ticks, T_BEGIN);
   const Guard g = st.guard();
-  if (!st.tasks() || !back_moe(args, lds, st, g)) poison(args, false);
+  if (!st.tasks()) return poison(args, false);
+  stamp(args.ticks, T_ATTN);
+  if (!back_moe(args, lds, st, g)) poison(args, false);
 }
 
 // The whole decoder layer: the front's tasks first (under the attention's tag), then
@@ -81,14 +95,18 @@ __global__ __launch_bounds__(512, 1) void k_layer(LayerArgs args) {
   __shared__ LayerLds lds;
   attn::Step st(args.tail.at, lds.tail.at);
   if (!st.begin()) return poison(args.tail, true);  // the tag lives in registers from here on
+  stamp(args.tail.ticks, T_BEGIN);
   const Guard g = st.guard();
   {
     proj::fr::Front f(args.fr, lds.fr);
     f.adopt(g, FRONT_SITE0);
     if (!f.tasks()) return poison(args.tail, false);
   }
+  stamp(args.tail.ticks, T_FRONT);
   __syncthreads();  // the LDS passes from the front's layout to the attention's
-  if (!st.tasks() || !back_moe(args.tail, lds.tail, st, g)) poison(args.tail, false);
+  if (!st.tasks()) return poison(args.tail, false);
+  stamp(args.tail.ticks, T_ATTN);
+  if (!back_moe(args.tail, lds.tail, st, g)) poison(args.tail, false);
 }
 
 }  // namespace
@@ -103,7 +121,8 @@ hipError_t tail_occupancy(int* blocks_per_cu) {
 
 hipError_t tail_forward(const attn::AttnArgs& g, const attn::Mail& amail, const GuardArgs& guard,
                         const mono_proj_weights& w, const mono_back_args& b, const proj::Mail& bmail,
-                        const moe::MoeFp8Args& m, const moe::Mail& mmail, uint64_t* a_done, int grid, hipStream_t st) {
+                        const moe::MoeFp8Args& m, const moe::Mail& mmail, uint64_t* a_done, int64_t* ticks, int grid,
+                        hipStream_t st) {
   if (g.rows < 1 || g.rows > attn::MAX_ROWS || g.rows > proj::MAX_ROWS || g.rows > moe::MAX_ROWS || b.rows != g.rows ||
       m.rows != g.rows || grid < 1 || amail.max_ctx % attn::CHUNK || amail.max_ctx > attn::MAX_CTX)
     return hipErrorInvalidConfiguration;
@@ -116,6 +135,8 @@ hipError_t tail_forward(const attn::AttnArgs& g, const attn::Mail& amail, const 
   a.bk.guard = guard;
   moe::fill_args(a.mo, m, mmail, guard);
   a.a_done = a_done;
+  a.ticks = ticks;
+  a.mo.ticks = ticks;
   k_layer_tail<<<grid, 512, 0, st>>>(a);
   return hipGetLastError();
 }
@@ -123,7 +144,7 @@ hipError_t tail_forward(const attn::AttnArgs& g, const attn::Mail& amail, const 
 hipError_t layer_forward(const mono_proj_weights& w, const mono_front_args& f, const proj::Mail& fmail,
                          int kv_mask, const attn::AttnArgs& g, const attn::Mail& amail, const GuardArgs& guard,
                          const mono_back_args& b, const proj::Mail& bmail, const moe::MoeFp8Args& m,
-                         const moe::Mail& mmail, uint64_t* a_done, int grid, hipStream_t st) {
+                         const moe::Mail& mmail, uint64_t* a_done, int64_t* ticks, int grid, hipStream_t st) {
   if (f.rows != g.rows || f.rows < 1 || f.rows > proj::MAX_ROWS || g.rows > attn::MAX_ROWS || g.rows > moe::MAX_ROWS ||
       b.rows != g.rows || m.rows != g.rows || grid < 1 || amail.max_ctx % attn::CHUNK || amail.max_ctx > attn::MAX_CTX)
     return hipErrorInvalidConfiguration;
@@ -144,6 +165,8 @@ hipError_t layer_forward(const mono_proj_weights& w, const mono_front_args& f, c
   a.tail.bk.guard = guard;
   moe::fill_args(a.tail.mo, m, mmail, guard);
   a.tail.a_done = a_done;
+  a.tail.ticks = ticks;
+  a.tail.mo.ticks = ticks;
   k_layer<<<grid, 512, 0, st>>>(a);
   return hipGetLastError();
 }

@@ -23,13 +23,14 @@ hipError_t tail_occupancy(int* blocks_per_cu);
 // the o_proj tiles' replicated done words (DONE_BYTES)
 hipError_t tail_forward(const attn::AttnArgs& g, const attn::Mail& amail, const GuardArgs& guard,
                         const mono_proj_weights& w, const mono_back_args& b, const proj::Mail& bmail,
-                        const moe::MoeFp8Args& m, const moe::Mail& mmail, uint64_t* a_done, int grid, hipStream_t st);
+                        const moe::MoeFp8Args& m, const moe::Mail& mmail, uint64_t* a_done, int64_t* ticks, int grid,
+                        hipStream_t st);
 // the whole layer as one launch: the front (its mailboxes fmail, kv_mask as front_forward)
 // and then tail_forward's phases, all under `guard`
 hipError_t layer_forward(const mono_proj_weights& w, const mono_front_args& f, const proj::Mail& fmail,
                          int kv_mask, const attn::AttnArgs& g, const attn::Mail& amail, const GuardArgs& guard,
                          const mono_back_args& b, const proj::Mail& bmail, const moe::MoeFp8Args& m,
-                         const moe::Mail& mmail, uint64_t* a_done, int grid, hipStream_t st);
+                         const moe::Mail& mmail, uint64_t* a_done, int64_t* ticks, int grid, hipStream_t st);
 
 }  // namespace layer
 }  // namespace mono

@@ -111,6 +111,9 @@ struct Args {
   int rows;
   float route_scale;
   float eps;
+  // the fused layer's phase ticks ([grid][16], NULL: none): workgroup b stamps word
+  // 16 b + k at MoE moment k (T_* below)
+  int64_t* ticks;
   Mail mail;
   GuardArgs guard;
 };
@@ -128,6 +131,9 @@ MONO_DEV bf16x8 normed8(const uint16_t* a, const uint16_t* g, float rstd) {
 
 // Task kinds of the round-robin list
 enum { K_NONE = 0, K_UP = 1, K_DOWN = 2, K_FINAL = 3 };
+
+// the MoE's moments in a fused layer's tick row (its other words are the layer's)
+enum { T_PLAN = 4, T_A = 6, T_NORM = 7, T_ROUTER = 8, T_ROUTE = 9, T_QUANT = 10, T_ROW = 16 };
 
 class Step {
  public:
@@ -169,22 +175,32 @@ class Step {
       // so no cache holds an older copy of its lines)
       const uint64_t* ad = done_copy(a_done);
       if (!hint_wait(n_a_done, [ad](int i) { return ad + i; }, site0 + W_A, gd)) return false;
+      stamp(T_A);
     }
 
     u32x4 ar[PER_ROW];  // wave w's row w, kept for the quantisation
     norm_stats(ar);
     __syncthreads();
+    stamp(T_NORM);
     if (rt < ROUTER_TASKS) router(rt, wr);
+    stamp(T_ROUTER);
     if ((int)blockIdx.x >= G - S) {
       if (!route(G - 1 - (int)blockIdx.x)) return false;
+      stamp(T_ROUTE);
     }
     quant_rows(ar);
     __syncthreads();
+    stamp(T_QUANT);
     return tasks();
   }
 
   // NaN over the launch's output (sync.h poison_bf16)
   MONO_DEV void poison(bool share) const { poison_bf16(A.out, (size_t)S * H, share); }
+
+  // this workgroup's tick at MoE moment k (a fused layer with ticks only)
+  MONO_DEV void stamp(int k) const {
+    if (A.ticks && tid == 0) A.ticks[blockIdx.x * T_ROW + k] = (int64_t)now_ticks();
+  }
 
  private:
   const Args& A;
@@ -393,6 +409,7 @@ class Step {
     // a shared-expert tile needs no plan: its loads go out before the plan is read
     if (T < NT) load_task(K_UP, T);
     if (!load_plan()) return false;
+    stamp(T_PLAN);
     int kind = classify(T);
     if (T >= NT) load_task(kind, T);
     // consecutive up tiles, half by half: the next tile's first half goes out once this
@@ -660,6 +677,7 @@ void fill_args(Args& a, const MoeFp8Args& g, const Mail& mail, const GuardArgs& 
   a.rows = g.rows;
   a.route_scale = g.route_scale;
   a.eps = g.eps;
+  a.ticks = nullptr;
   a.mail = mail;
   a.guard = guard;
 }

@@ -364,13 +364,14 @@ class LayerRuntime:
 
     def forward(self, h: torch.Tensor, seq_lens: torch.Tensor, page_table: torch.Tensor, caches: AttnCaches,
                 w: LayerWeights, rope_cos: torch.Tensor, rope_sin: torch.Tensor, out: torch.Tensor | None = None,
-                check_weights: bool = True, keep: bool = False, on_phase=None):
+                check_weights: bool = True, keep: bool = False, on_phase=None, ticks: torch.Tensor | None = None):
         """x_out [rows, 7168] bf16 = the layer applied to rows ``h`` whose new tokens sit
         at ``seq_lens - 1`` (this step's cache rows are written in place). ``keep``
         also returns the intermediates (front outputs, the index scores and selected
         slots, o_lat, a, the MoE routing and sum) as copies. ``on_phase(i)`` (if given)
         is called after the launch of phase i (``self.phases[i]``) is enqueued, e.g. to
-        record timing events between the phases."""
+        record timing events between the phases. ``ticks`` (int64 [grid, 16], one-launch
+        mode) receives each workgroup's phase ticks (``_lib.LAYER_TICKS``, 100 MHz)."""
         from .attn import AttnStep, attn_args
         from .moe import fp8_args
 
@@ -390,7 +391,11 @@ class LayerRuntime:
             need(h, "h", (S, HIDDEN), torch.bfloat16, dev)
             bargs = _lib.BackArgs(o_lat=_lib.ptr(o_lat), h=_lib.ptr(h), a=_lib.ptr(a), o=None, rows=S, timeline=None)
             margs, x, mdbg = fp8_args(dev, self.max_rows, self.geo, a, w.moe, out, keep)
-            largs = _lib.LayerArgs(C.pointer(fargs), C.pointer(aargs), C.pointer(bargs), C.pointer(margs))
+            if ticks is not None:
+                grid = torch.cuda.get_device_properties(dev).multi_processor_count
+                need(ticks, "ticks", (grid, _lib.LAYER_TICK_WORDS), torch.int64, dev)
+            largs = _lib.LayerArgs(C.pointer(fargs), C.pointer(aargs), C.pointer(bargs), C.pointer(margs),
+                                   _lib.ptr(ticks))
             lib, hd, st = _lib.lib(), self.handle._h, self.handle._stream()
             if on_phase is None:
                 _lib.check(lib.mono_layer_forward(hd, C.byref(ws), C.byref(largs), st))
