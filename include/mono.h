@@ -328,7 +328,7 @@ typedef struct {
   int64_t* timeline; /* optional i64 [256, 4] as in mono_front_args (stage 0 U, 1 O) */
 } mono_back_args;
 
-/* Wait sites of the projection launches: 0 stage-A partials, 1 q_an, 2 q_nope,
+/* Wait sites of the projection launches: 0 stage-A partials, 1 stage-A q_a tiles, 2 q_nope,
  * 3 raw index query, 4 W_UV output, 5 normed input rows. */
 int mono_proj_create(const mono_proj_config* cfg, mono_proj** out);
 int mono_proj_destroy(mono_proj* proj);

@@ -148,7 +148,7 @@ SCRUB_SITE = 31
 # wait sites of the launches (guard word 1 = site + 1)
 MOE_SITES = {0: "router logits", 1: "route picks", 2: "expert mid activations", 3: "expert outputs"}
 ATTN_SITES = {0: "index scores", 1: "selected slots", 2: "split partials", 3: "top-k team"}
-PROJ_SITES = {0: "stage-A partial sums", 1: "normed q_a", 2: "q_nope", 3: "raw index query", 4: "W_UV output"}
+PROJ_SITES = {0: "stage-A partial sums", 1: "stage-A q_a tiles", 2: "q_nope", 3: "raw index query", 4: "W_UV output"}
 # every launch of a layer runtime (one guard)
 LAYER_SITES = {**ATTN_SITES, 4: "W_UV output", 5: "attention output", 6: "router logits", 7: "route picks",
                8: "expert mid activations", 9: "expert outputs", 10: "attention block output rows",

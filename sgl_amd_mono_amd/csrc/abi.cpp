@@ -635,13 +635,12 @@ extern "C" int mono_proj_create(const mono_proj_config* cfg, mono_proj** out) {
     return fail(MONO_EINVAL, "max_rows must be in [1, %d], got %d", MAX_ROWS, c.max_rows);
   if (int rc = check_device(c.device)) return rc;
   Carve cv;
-  size_t o_mb[5];
-  for (int i = 0; i < 5; ++i) o_mb[i] = cv.take(MAIL_WORDS[i] * 4);
+  size_t o_mb[4];
+  for (int i = 0; i < 4; ++i) o_mb[i] = cv.take(MAIL_WORDS[i] * 4);
   const size_t o_odone = cv.take(mono::DONE_BYTES);
   const size_t o_xn = cv.take((size_t)mono::proj::MAX_ROWS * mono::proj::HIDDEN * 2);
   const size_t o_xdone = cv.take(mono::DONE_BYTES);
-  const size_t o_adone = cv.take((size_t)mono::proj::MAX_A_TASKS * 8);
-  const size_t o_qdone = cv.take(mono::DONE_BYTES);
+  const size_t o_adone = cv.take(mono::DONE_BYTES);
   const size_t o_cdone = cv.take((size_t)mono::proj::C_TASKS * 8);
   const size_t o_fdone = cv.take(mono::DONE_BYTES);
   mono_proj* p = new mono_proj();
@@ -654,13 +653,11 @@ extern "C" int mono_proj_create(const mono_proj_config* cfg, mono_proj** out) {
   }
   p->mail.guard = p->guard.words;
   p->mail.pa = reinterpret_cast<uint32_t*>(p->at(o_mb[0]));
-  p->mail.qan = reinterpret_cast<uint32_t*>(p->at(o_mb[1]));
-  p->mail.qnope = reinterpret_cast<uint32_t*>(p->at(o_mb[2]));
-  p->mail.iqraw = reinterpret_cast<uint32_t*>(p->at(o_mb[3]));
+  p->mail.qnope = reinterpret_cast<uint32_t*>(p->at(o_mb[1]));
+  p->mail.iqraw = reinterpret_cast<uint32_t*>(p->at(o_mb[2]));
   p->mail.adone = reinterpret_cast<uint64_t*>(p->at(o_adone));
-  p->mail.qdone = reinterpret_cast<uint64_t*>(p->at(o_qdone));
   p->mail.cdone = reinterpret_cast<uint64_t*>(p->at(o_cdone));
-  p->mail.ob = reinterpret_cast<uint32_t*>(p->at(o_mb[4]));
+  p->mail.ob = reinterpret_cast<uint32_t*>(p->at(o_mb[3]));
   p->mail.odone = reinterpret_cast<uint64_t*>(p->at(o_odone));
   p->mail.xn = reinterpret_cast<uint32_t*>(p->at(o_xn));
   p->mail.xdone = reinterpret_cast<uint64_t*>(p->at(o_xdone));

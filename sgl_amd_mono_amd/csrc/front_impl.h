@@ -13,11 +13,13 @@
 //      the weight burst goes out first, then the rows' done words are awaited and the
 //      task's K part of every row arrives by DMA into LDS; its 128-k steps -> partial
 //      sums (mailbox pa)
-//   B  (row): the K parts summed in order; q_a RMSNorm -> q_an (bf16 pairs); KV RMSNorm +
-//      k_pe RoPE -> one power-of-two-scaled E4M3 row into the MLA cache; index key
-//      LayerNorm + RoPE + Hadamard + FP4 into the index plane; head weights
-//   C  (64-row tile) of W_qb (6144) and W_iq (8192) against q_an: q_nope (bf16 pairs),
-//      q_pe (RoPE, straight to q), raw index query (bf16 pairs)
+//   B  (row): the K parts summed in order; KV RMSNorm + k_pe RoPE -> one
+//      power-of-two-scaled E4M3 row into the MLA cache; index key LayerNorm + RoPE +
+//      Hadamard + FP4 into the index plane; head weights
+//   C  (64-row tile) of W_qb (6144) and W_iq (8192) against q_an, the q_a RMSNorm that
+//      every C task forms itself from stage A's q_a outputs (waiting on the q_a tiles,
+//      not on a hand-off through B): q_nope (bf16 pairs), q_pe (RoPE, straight to q),
+//      raw index query (bf16 pairs)
 //   D  (head): q_lat = W_UK^T q_nope -> q[:, h, :512]
 //   E  (row, 8 heads): index query RoPE + Hadamard + FP4 -> iq, iqs
 // A workgroup waits only on tasks of earlier stages, and every workgroup is resident,
@@ -60,7 +62,7 @@ static_assert(ROW_PIECES % WAVE == 0 && KPW <= MAX_PARTS, "stage A split");
 MONO_DEV int kp_fp8(int S) { return S <= 8 ? 1 : 2; }
 MONO_DEV int nt_a(int S) { return A_TILES * kp_fp8(S) + W_TILES * KPW; }
 
-enum { W_PA = 0, W_QAN = 1, W_QNOPE = 2, W_IQRAW = 3, W_XN = 5 };  // 4: the back's W_UV output
+enum { W_PA = 0, W_QA = 1, W_QNOPE = 2, W_IQRAW = 3, W_XN = 5 };  // 4: the back's W_UV output
 
 struct Lds {
   union {
@@ -296,7 +298,7 @@ class Front {
     }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();  // the partials are stored (and the next task rewrites the LDS)
-    if (tid == 0) mb_put(&M.adone[t], 0u, gd.tag);
+    put_done(M.adone, t, gd.tag);
     return true;
   }
 
@@ -365,15 +367,12 @@ class Front {
     const int slot = slot_of(s), pr = rope_row(s);
     const float cl = A.rope_cos[(size_t)pr * (PE_DIM / 2) + tid % (PE_DIM / 2)];
     const float sl = A.rope_sin[(size_t)pr * (PE_DIM / 2) + tid % (PE_DIM / 2)];
-    const uint16_t* gq = static_cast<const uint16_t*>(W.g_q);
-    const uint32_t gq0 = *reinterpret_cast<const uint32_t*>(gq + 2 * tid);
-    const uint32_t gq1 = *reinterpret_cast<const uint32_t*>(gq + 2 * min(tid + FT, Q_LORA / 2 - 1));
     const float gkv = bf16_bits_to_f32(static_cast<const uint16_t*>(W.g_kv)[tid]);
     const float gik0 = W.g_ik[2 * lane], gik1 = W.g_ik[2 * lane + 1];
     const float bik0 = W.b_ik[2 * lane], bik1 = W.b_ik[2 * lane + 1];
     {
       // every stage-A task's done word, then row s's partials in one pass
-      const uint64_t* ad = M.adone;
+      const uint64_t* ad = done_copy(M.adone);
       if (!hint_wait(nt_a(S), [ad](int i) { return ad + i; }, site0 + W_PA, gd)) return false;
       mark_waited();
 #pragma unroll
@@ -401,29 +400,9 @@ class Front {
     __syncthreads();
     const float* row = L.u.row[0];
 
-    // q_a and KV latent sums of squares (kernel.py:1978-2003, 2005-2050)
-    float sq = 0.f;
-    for (int c = tid; c < Q_LORA; c += FT) sq += row[c] * row[c];
+    // the KV latent's sum of squares (kernel.py:2005-2050); the q_a RMSNorm is stage C's
     const float kv = row[Q_LORA + tid];
-    const f32x2 ss = block_sum2(sq, kv * kv);
-    const float rq = 1.0f / sqrtf(ss[0] / (float)Q_LORA + EPS);
-    const float rk = 1.0f / sqrtf(ss[1] / (float)KV_LORA + EPS);
-
-    // q_an, published as bf16 pairs
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int j = tid + FT * h;
-      if (j < Q_LORA / 2) {
-        const uint32_t gw = h == 0 ? gq0 : gq1;
-        const float y0 = mul_rn(mul_rn(row[2 * j], rq), bf16_lo(gw));
-        const float y1 = mul_rn(mul_rn(row[2 * j + 1], rq), bf16_hi(gw));
-        __hip_atomic_store(&M.qan[(size_t)s * (Q_LORA / 2) + j], pack_bf16x2(y0, y1), __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-      }
-    }
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();  // row s of q_an is stored
-    put_done(M.qdone, s, gd.tag);
+    const float rk = 1.0f / sqrtf(block_sum2(0.f, kv * kv)[1] / (float)KV_LORA + EPS);
 
     // KV row: bf16 latent and RoPE'd k_pe, one power-of-two E4M3 scale
     const float kvn = bf16_round(mul_rn(mul_rn(kv, rk), gkv));
@@ -494,6 +473,48 @@ class Front {
   }
 
   // ------------------------------------------------------------ stage C
+  static constexpr int QA_VL = Q_LORA / 4 / WAVE;  // 16-byte q_a pieces a lane holds of a row
+  static_assert(Q_LORA % (4 * WAVE) == 0, "q_a rows split evenly over a wave's lanes");
+
+  // q_an = bf16(q_a * rstd * g_q) of every row into L.u.xc (kernel.py:1978-2003), from
+  // stage A's raw q_a (its K parts summed in part order): wave w normalises rows w, w + 8,
+  // a lane 6 pieces of 4 consecutive columns, the row's sum of squares a wave sum. One
+  // round of unconditional 16-byte loads: the second part's reads fall past the buffer
+  // (zeros, no traffic) unless the step splits K.
+  MONO_DEV void qa_norm(const u32x2 (&gq)[QA_VL]) {
+    const bool two = kp_fp8(S) == 2;
+    const __amdgpu_buffer_rsrc_t rs = coherent_rsrc(M.pa, (uint32_t)((two ? 2 : 1) * MAX_ROWS * N_A * 4));
+    for (int s = wave; s < S; s += FW) {  // wave-uniform
+      u32x4 p0[QA_VL], p1[QA_VL];
+#pragma unroll
+      for (int j = 0; j < QA_VL; ++j) {
+        const int c = 4 * (lane + WAVE * j);
+        p0[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, (s * N_A + c) * 4, 0, SC1));
+        p1[j] = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, ((MAX_ROWS + s) * N_A + c) * 4, 0, SC1));
+      }
+      float x[QA_VL][4];
+      float sq = 0.f;
+#pragma unroll
+      for (int j = 0; j < QA_VL; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float a = __uint_as_float(p0[j][q]), b = __uint_as_float(p1[j][q]);
+          x[j][q] = two ? a + b : a;
+          sq += x[j][q] * x[j][q];
+        }
+      const float rq = 1.0f / sqrtf(wave_sum(sq) / (float)Q_LORA + EPS);
+#pragma unroll
+      for (int j = 0; j < QA_VL; ++j) {
+        const int c = 4 * (lane + WAVE * j);
+        u32x2 o;
+        o[0] = pack_bf16x2(mul_rn(mul_rn(x[j][0], rq), bf16_lo(gq[j][0])), mul_rn(mul_rn(x[j][1], rq), bf16_hi(gq[j][0])));
+        o[1] = pack_bf16x2(mul_rn(mul_rn(x[j][2], rq), bf16_lo(gq[j][1])), mul_rn(mul_rn(x[j][3], rq), bf16_hi(gq[j][1])));
+        *reinterpret_cast<u32x2*>(&L.u.xc[s][c]) = o;
+      }
+    }
+  }
+
   MONO_DEV bool stage_c(int c) {
     const bool qb = c < QB_TILES;
     const uint8_t* wb = static_cast<const uint8_t*>(qb ? W.w_qb : W.w_iq);
@@ -515,21 +536,15 @@ class Front {
     const int prc = rope_row(min(so, S - 1)), ic = max(qd - NOPE, 0) / 2;
     const float rc = A.rope_cos[(size_t)prc * (PE_DIM / 2) + ic];
     const float rs = A.rope_sin[(size_t)prc * (PE_DIM / 2) + ic];
-    const uint64_t* qdn = done_copy(M.qdone);
-    if (!hint_wait(S, [qdn](int i) { return qdn + i; }, site0 + W_QAN, gd)) return false;
-    {  // q_an of every row in one pass of 16-byte device-coherent loads (192 a row)
-      constexpr int UR = Q_LORA / 8, NU = (MAX_ROWS * UR + FT - 1) / FT;
-      const __amdgpu_buffer_rsrc_t rsq = coherent_rsrc(M.qan, S * (Q_LORA / 2) * 4);
-      u32x4 v[NU];
+    // the q_a RMSNorm weight of this lane's columns, before the wait
+    u32x2 gq[QA_VL];
 #pragma unroll
-      for (int q = 0; q < NU; ++q)
-        v[q] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsq, (tid + FT * q) * 16, 0, SC1));
-#pragma unroll
-      for (int q = 0; q < NU; ++q) {
-        const int u = tid + FT * q;
-        if (u < S * UR) *reinterpret_cast<u32x4*>(&L.u.xc[u / UR][8 * (u % UR)]) = v[q];
-      }
-    }
+    for (int j = 0; j < QA_VL; ++j)
+      gq[j] = *reinterpret_cast<const u32x2*>(static_cast<const uint16_t*>(W.g_q) + 4 * (lane + WAVE * j));
+    // the q_a tiles of stage A (task t holds tile t / kp), then q_an of every row
+    const uint64_t* ad = done_copy(M.adone);
+    if (!hint_wait((Q_LORA / 16) * kp_fp8(S), [ad](int i) { return ad + i; }, site0 + W_QA, gd)) return false;
+    qa_norm(gq);
     __syncthreads();
     mark_waited();
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};

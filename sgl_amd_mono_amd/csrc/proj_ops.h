@@ -23,9 +23,7 @@ constexpr int C_TASKS = HEADS * QK / 64 + IH * ID / 64;                   // sta
 // tagged done words (see sync.h).
 struct Mail {
   uint32_t* pa;     // [MAX_PARTS][MAX_ROWS][N_A]    stage-A partial sums, f32
-  uint64_t* adone;  // [MAX_A_TASKS]                 a stage-A task's partials are stored
-  uint32_t* qan;    // [MAX_ROWS][Q_LORA / 2]        normed q_a, bf16 pairs
-  uint64_t* qdone;  // [MAX_ROWS], replicated        row s of qan is stored
+  uint64_t* adone;  // [MAX_A_TASKS], replicated     a stage-A task's partials are stored
   uint32_t* qnope;  // [MAX_ROWS][HEADS][NOPE / 2]   q_nope, bf16 pairs
   uint32_t* iqraw;  // [MAX_ROWS][IH][ID / 2]        raw index query, bf16 pairs
   uint64_t* cdone;  // [C_TASKS]                     a stage-C tile's outputs are stored
@@ -43,9 +41,10 @@ struct Mail {
   uint32_t* guard;  // [G_WORDS]
 };
 constexpr int FD_B = 0, FD_E = MAX_ROWS, FD_D = MAX_ROWS + MAX_ROWS * 8, FD_WORDS = FD_D + 32;
-constexpr size_t MAIL_WORDS[5] = {(size_t)MAX_PARTS * MAX_ROWS * N_A, (size_t)MAX_ROWS * Q_LORA / 2,
-                                  (size_t)MAX_ROWS * HEADS * NOPE / 2, (size_t)MAX_ROWS * IH * ID / 2,
-                                  (size_t)MAX_ROWS * HEADS * VDIM / 2};
+// words of the untagged mailboxes pa, qnope, iqraw, ob
+constexpr size_t MAIL_WORDS[4] = {(size_t)MAX_PARTS * MAX_ROWS * N_A, (size_t)MAX_ROWS * HEADS * NOPE / 2,
+                                  (size_t)MAX_ROWS * IH * ID / 2, (size_t)MAX_ROWS * HEADS * VDIM / 2};
+static_assert(MAX_A_TASKS <= 512, "stage-A done words fit one replicated array");
 
 hipError_t front_occupancy(int* blocks_per_cu);
 hipError_t back_occupancy(int* blocks_per_cu);

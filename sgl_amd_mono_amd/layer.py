@@ -364,14 +364,18 @@ class LayerRuntime:
 
     def forward(self, h: torch.Tensor, seq_lens: torch.Tensor, page_table: torch.Tensor, caches: AttnCaches,
                 w: LayerWeights, rope_cos: torch.Tensor, rope_sin: torch.Tensor, out: torch.Tensor | None = None,
-                check_weights: bool = True, keep: bool = False, on_phase=None, ticks: torch.Tensor | None = None):
+                check_weights: bool = True, keep: bool = False, on_phase=None, ticks: torch.Tensor | None = None,
+                timelines: dict | None = None):
         """x_out [rows, 7168] bf16 = the layer applied to rows ``h`` whose new tokens sit
         at ``seq_lens - 1`` (this step's cache rows are written in place). ``keep``
         also returns the intermediates (front outputs, the index scores and selected
         slots, o_lat, a, the MoE routing and sum) as copies. ``on_phase(i)`` (if given)
         is called after the launch of phase i (``self.phases[i]``) is enqueued, e.g. to
         record timing events between the phases. ``ticks`` (int64 [grid, 16], one-launch
-        mode) receives each workgroup's phase ticks (``_lib.LAYER_TICKS``, 100 MHz)."""
+        mode) receives each workgroup's phase ticks (``_lib.LAYER_TICKS``, 100 MHz);
+        ``timelines`` (one-launch mode) maps "front" / "attn" / "back" to int64 per-task
+        timelines of those phases (front_tasks(rows), attn.n_tasks(max_ctx, rows),
+        BACK_TASKS rows of start, inputs-ready and end ticks, workgroup << 8 | stage)."""
         from .attn import AttnStep, attn_args
         from .moe import fp8_args
 
@@ -383,13 +387,17 @@ class LayerRuntime:
         step = AttnStep(iq=fo.iq, iqs=fo.iqs, iw=fo.iw, q=fo.q, page_table=page_table, seq_lens=seq_lens)
         if self.mode == "layer":
             dev = self.device
+            tl = timelines or {}
             fargs, _, ws = front_args(dev, self.max_rows, h, seq_lens, page_table, caches, w.proj, rope_cos,
-                                      rope_sin, fo, check_weights, None)
+                                      rope_sin, fo, check_weights, tl.get("front"))
             aargs, o_lat, adbg = attn_args(dev, self.max_rows, self.max_ctx, step, caches, self._o_lat[:S], keep,
-                                           None)
+                                           tl.get("attn"))
             a = self._a[:S]
             need(h, "h", (S, HIDDEN), torch.bfloat16, dev)
-            bargs = _lib.BackArgs(o_lat=_lib.ptr(o_lat), h=_lib.ptr(h), a=_lib.ptr(a), o=None, rows=S, timeline=None)
+            if tl.get("back") is not None:
+                need(tl["back"], "timelines['back']", (BACK_TASKS, 4), torch.int64, dev)
+            bargs = _lib.BackArgs(o_lat=_lib.ptr(o_lat), h=_lib.ptr(h), a=_lib.ptr(a), o=None, rows=S,
+                                  timeline=_lib.ptr(tl.get("back")))
             margs, x, mdbg = fp8_args(dev, self.max_rows, self.geo, a, w.moe, out, keep)
             if ticks is not None:
                 grid = torch.cuda.get_device_properties(dev).multi_processor_count
