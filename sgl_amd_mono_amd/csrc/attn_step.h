@@ -389,12 +389,12 @@ class Step {
     ScoreOps cur, nxt;
     if (A.fdone) {
       // the front of this launch writes each row's index query, head weights and new
-      // key: the first task's keys stream before the wait unless its chunk may hold a
-      // key written in this launch (the row's last `rows` positions: its own new key
-      // and, for the rows of a verify chain, those of the chain's earlier rows), then
-      // every row's front outputs are awaited
+      // key: the first task's keys stream before the wait, except a wave's whose 128
+      // keys may hold a key written in this launch (the row's last `rows` positions: its
+      // own new key and, for the rows of a verify chain, those of the chain's earlier
+      // rows), then every row's front outputs are awaited
       score_where(T0, cur);
-      const bool fresh = cur.n > 0 && (cur.c + 1) * CHUNK > cur.n - A.rows;
+      const bool fresh = cur.k0 < cur.n && cur.k0 + KEYS_WAVE > cur.n - A.rows;  // wave-uniform
       if (!fresh) score_keys(cur);
       const uint64_t* fd = done_copy(A.fdone);
       const int nr = A.rows;
