@@ -96,6 +96,12 @@ def test_attn_48_rows_mixed_contexts(rt, gpu_device):
     _check(rt, ctx, 2, gpu_device)
 
 
+def test_attn_48_rows_full_contexts(rt, gpu_device):
+    """BASELINE config 3 at its largest size: 48 rows of (nearly) 32768 keys each."""
+    ctx = [32768] * 44 + [32767, 32704, 30001, 16385]
+    _check(rt, ctx, 7, gpu_device)
+
+
 @pytest.mark.parametrize("period", [1, 6])
 def test_attn_repeated_scores(rt, gpu_device, period):
     """Index planes whose pages repeat every `period` pages: each score recurs about

@@ -296,3 +296,86 @@ def test_layer_verify_chain_sees_its_own_draft_keys(gpu_device):
     for j, n in enumerate(lens):
         want = (pt0[torch.arange(n) // 64] * 64 + torch.arange(n) % 64).to(torch.int32)
         assert torch.equal(il["topk_slots"][j, :n].cpu(), want), j
+
+
+def test_layer_verify_chain_matches_oracle(gpu_device):
+    """MTP verify rows past 2048 keys against the oracle (glm53/check.py:100-146):
+    four rows of one request at positions 5118 .. 5121 (the chain crosses the 5120-key
+    chunk boundary), one launch. The oracle runs each row's front and writes its cache
+    rows in order into CPU copies of the caches; then, per row over those caches:
+
+    * the device's chain rows match the oracle's cache rows code by code;
+    * index scores over the device's caches within 1e-4 of the row's largest score,
+      the chain keys included (a stale read of a draft key would miss by far more);
+    * the selection bit-exact against the exact top-2048 of the row's own scores, and
+      it holds every chain key that the oracle's own scores select (``topk_own``);
+    * o_lat against sparse MLA over the oracle-written caches, then ``a`` and x_out
+      on the device's intermediates as in the phase-by-phase test."""
+    ctx, rows = 8192, 4
+    lens = [5119, 5120, 5121, 5122]  # new keys at 5118 .. 5121
+    cos, sin = workloads.rope_tables(ctx, gpu_device)
+    print("[verify chain] weights", flush=True)
+    w = LayerWeights(proj=workloads.proj_weights(gpu_device, seed=61),
+                     moe=workloads.fp8_moe_weights(FP8_MOE, gpu_device, seed=62))
+    step, caches = workloads.attn_case([ctx], gpu_device, seed=63, max_ctx=ctx)
+    pt_dev = step.page_table[:1].repeat(rows, 1).contiguous()
+    seq = torch.tensor(lens, dtype=torch.int32, device=gpu_device)
+    x = workloads.rows_bf16(rows, ol.HIDDEN, gpu_device, seed=64)
+    before = {k: getattr(caches, k).cpu().clone() for k in ("ikv", "iks", "kv", "kv_scale")}
+    rt = LayerRuntime(rows, ctx, gpu_device)
+    try:
+        x_out, it = rt.forward(x, seq, pt_dev, caches, w, cos, sin, keep=True)
+        torch.cuda.synchronize()
+        rt.check_errors()
+    finally:
+        rt.close()
+    h, pt, pos = x.cpu(), pt_dev.cpu(), seq.cpu().long() - 1
+    proj = _cpu_proj(w.proj)
+    exp = {k: v.clone() for k, v in before.items()}
+    fronts = []
+    for j in range(rows):  # each draft's front, its cache rows written before the next row's
+        f = ol.front(h[j:j + 1], pos[j:j + 1], pt[j:j + 1], proj, cos.cpu(), sin.cpu())
+        ol.write_caches(f, exp["ikv"], exp["iks"], exp["kv"], exp["kv_scale"])
+        fronts.append(f)
+    _close(it["q"].cpu(), torch.cat([f["q"] for f in fronts]), "front q")
+    got = {k: getattr(caches, k).cpu() for k in exp}
+    slots = torch.cat([f["slot"] for f in fronts])
+    assert len(set(slots.tolist())) == rows
+    exact = float((got["kv"][slots] == exp["kv"][slots]).float().mean())
+    pages, offs = slots // 64, slots % 64
+    ik_exact = float((got["ikv"][pages, :, offs] == exp["ikv"][pages, :, offs]).float().mean())
+    print(f"  chain rows: MLA codes {exact:.4f} exact, index-key bytes {ik_exact:.4f} exact", flush=True)
+    assert exact >= 0.98 and ik_exact >= 0.9
+
+    scores, sel = it["index_scores"].cpu(), it["topk_slots"].cpu()
+    ref_dev = oatt.index_scores(it["iq"].cpu(), it["iqs"].cpu(), it["iw"].cpu(), got["ikv"], got["iks"], pt,
+                                seq.cpu(), ctx)
+    ref_own = oatt.index_scores(it["iq"].cpu(), it["iqs"].cpu(), it["iw"].cpu(), exp["ikv"], exp["iks"], pt,
+                                seq.cpu(), ctx)
+    want_sel = oatt.select_topk(scores, seq.cpu(), pt)
+    own_sel = oatt.select_topk(ref_own, seq.cpu(), pt)
+    chain_total = 0
+    for j, n in enumerate(lens):
+        tol = 1e-4 * float(ref_dev[j, :n].abs().max()) + 1e-6
+        assert float((scores[j, :n] - ref_dev[j, :n]).abs().max()) <= tol, j
+        assert float((scores[j, n - j - 1:n] - ref_dev[j, n - j - 1:n]).abs().max()) <= tol, j  # chain keys
+        chain = set(slots[:j + 1].tolist())
+        picked, oracle_picked = set(sel[j, :2048].tolist()), set(own_sel[j, :2048].tolist())
+        assert (oracle_picked & chain) <= picked, (j, oracle_picked & chain, picked & chain)
+        chain_total += len(picked & chain)
+    print(f"  chain keys selected over the four rows: {chain_total}", flush=True)
+    assert torch.equal(sel, want_sel)
+    assert chain_total > 0  # the seeds put draft keys in the selections
+    o_ref = oatt.sparse_mla(it["q"].cpu(), exp["kv"], exp["kv_scale"], sel)
+    _close(it["o_lat"].cpu(), o_ref, "attention o_lat")
+    b = ol.back(it["o_lat"].cpu(), h, proj)
+    _close(it["a"].cpu(), b["a"], "back a")
+    m = w.moe
+    ids_ref, w_ref = otopk.router_top8(it["scores"].cpu(), m.bias.cpu(), FP8_MOE.top_k, FP8_MOE.route_scale)
+    assert torch.equal(it["topk_ids"].cpu().long(), ids_ref)
+    ref = omoe.fp8_moe_block(
+        it["a"].cpu(), m.g_post.cpu(), m.w_router.cpu(), m.bias.cpu(), CpuExperts(m.w13, True),
+        CpuExperts(m.s13), CpuExperts(m.w2, True), CpuExperts(m.s2), eps=FP8_MOE.eps, top_k=FP8_MOE.top_k,
+        inter=FP8_MOE.inter, ids=ids_ref, weights=w_ref,
+    )  # fmt: skip
+    _close(x_out.cpu(), ref["out"], "moe x_out")

@@ -37,8 +37,11 @@ def _linear(w, s):
 def _sglang_layer(seed, dev, rot):
     """Synthetic weights of one layer in SGLang's module names (FP8 linears already in
     the (16, 16) layout, the shared expert fused as expert 256)."""
-    p = workloads.proj_weights(dev, seed=seed)
-    m = workloads.fp8_moe_weights(FP8_MOE, dev, seed=seed + 1)
+    return _sglang_layer_of(workloads.proj_weights(dev, seed=seed), workloads.fp8_moe_weights(FP8_MOE, dev, seed=seed + 1),
+                            dev, rot)
+
+
+def _sglang_layer_of(p, m, dev, rot):
     uk = ocodecs.aiter_unshuffle(p.w_uk.cpu()).reshape(32, 512, 128)
     uv = ocodecs.aiter_unshuffle(p.w_uv.cpu()).reshape(32, 128, 512)
     iw = ocodecs.aiter_unshuffle(p.w_iw.cpu().view(torch.uint8)).view(torch.bfloat16)
@@ -130,3 +133,120 @@ def test_spec_forward_runs_the_launches(gpu_device, monkeypatch):
         assert built.forward(registry.Plan(key=wide), None, pos, batch) == "own" and len(ran) == 1
     finally:
         built.runtime.close()
+
+
+class _OracleIndexer(torch.nn.Module):
+    """The stand-in indexer: its forward hands on the selection (KV slots, -1 past a
+    row's keys), where check mode's hook reads SGLang's selection."""
+
+    def __init__(self, ns):
+        super().__init__()
+        for k, v in vars(ns).items():
+            setattr(self, k, v)
+
+    def forward(self, selection):
+        return selection
+
+
+class _OracleLayer:
+    """SGLang's layer module stood in by the CPU oracle chain (front, cache write,
+    index scores, exact top-2048, sparse MLA, back, FP8 MoE) on the same weights:
+    ``(positions, hidden, batch, residual) -> (hidden, None)``, writing its cache rows
+    into the layer's pools like SGLang's layer."""
+
+    def __init__(self, i, seed, dev, rot, cos, sin):
+        from test_gpu_layer import CpuExperts, _cpu_proj
+
+        from sgl_amd_mono_amd import sglang_bind
+
+        ns, p, m = _sglang_parts(seed, dev, rot)
+        vars(self).update(vars(ns))
+        self.self_attn.indexer = _OracleIndexer(self.self_attn.indexer)
+        self.i, self.cos, self.sin = i, cos.cpu(), sin.cpu()
+        # the projections as the spec binds them (W_UK / W_UV with SGLang's per-tensor scale)
+        self.proj = _cpu_proj(sglang_bind.layer_weights(self, i, {}).proj)
+        self.m = m
+        self.experts = (CpuExperts(m.w13, True), CpuExperts(m.s13), CpuExperts(m.w2, True), CpuExperts(m.s2))
+
+    def __call__(self, positions, hidden, batch, residual):
+        from oracle import attention as oatt
+        from oracle import layer as ol
+        from oracle import moe as omoe
+        from sgl_amd_mono_amd import sglang_bind
+        from sgl_amd_mono_amd.moe import FP8_MOE
+
+        dev = hidden.device
+        h, pos = hidden.cpu(), positions.cpu().long()
+        pt = forward_context.ATTN_BACKEND.forward_metadata.real_page_table.cpu()[:h.shape[0]]
+        f = ol.front(h, pos, pt, self.proj, self.cos, self.sin, kv_scaled=False)
+        c = sglang_bind.caches(forward_context.POOL, self.i)
+        cpu = {k: getattr(c, k).cpu() for k in ("ikv", "iks", "kv")}
+        ol.write_caches(f, cpu["ikv"], cpu["iks"], cpu["kv"], None)
+        for k in cpu:
+            getattr(c, k).copy_(cpu[k])
+        lens = pos.to(torch.int32) + 1
+        scores = oatt.index_scores(f["iq"], f["iqs"], f["iw"], cpu["ikv"], cpu["iks"], pt, lens, CTX)
+        sel = self.self_attn.indexer(oatt.select_topk(scores, lens, pt))
+        o = oatt.sparse_mla(f["q"].to(torch.bfloat16), cpu["kv"], None, sel)
+        a = ol.back(o.to(torch.bfloat16), h, self.proj)["a"]
+        m = self.m
+        out = omoe.fp8_moe_block(a, m.g_post.cpu(), m.w_router.cpu(), m.bias.cpu(), *self.experts, eps=FP8_MOE.eps,
+                                 top_k=FP8_MOE.top_k, inter=FP8_MOE.inter)["out"]
+        return out.to(dev), None
+
+
+def _sglang_parts(seed, dev, rot):
+    p = workloads.proj_weights(dev, seed=seed)
+    m = workloads.fp8_moe_weights(FP8_MOE, dev, seed=seed + 1)
+    return _sglang_layer_of(p, m, dev, rot), p, m
+
+
+def test_check_mode_against_the_oracle_layer(gpu_device, monkeypatch, caplog):
+    """SGLANG_AMD_MONO_CHECK=1 with the CPU oracle chain standing in for SGLang's layer
+    module: every covered layer's stream, MLA rows, index keys and selection are
+    measured against it, and none violates the spec's NUMERICS bounds."""
+    from sgl_amd_mono_amd import check
+    from sgl_amd_mono_amd import spec as mono
+
+    dev = gpu_device
+    monkeypatch.setenv(mono.LOCAL_SHARE_ENV, "1")
+    monkeypatch.setenv(check.CHECK_ENV, "1")
+    caplog.set_level("INFO", logger="sgl_amd_mono_amd.check")
+    cos, sin = workloads.rope_tables(CTX, dev)
+    rot = SimpleNamespace(cos_sin_cache=torch.cat([cos, sin], -1))
+    print("[check mode] building a 2-layer model with oracle stand-in layers", flush=True)
+    layers = [_OracleLayer(0, 21, dev, rot, cos, sin), _OracleLayer(1, 22, dev, rot, cos, sin)]
+    model = SimpleNamespace(embed_tokens=lambda ids: workloads.rows_bf16(ROWS, 7168, dev, seed=23), layers=layers,
+                            norm=lambda h, r=None: h)
+    lm = SimpleNamespace(model=model, lm_head=None, logits_processor=lambda ids, h, head, batch: h)
+    hf = SimpleNamespace(first_k_dense_replace=0, num_hidden_layers=2)
+    lens = [4096, 1500, 65, 3000]
+    step, c0 = workloads.attn_case(lens, dev, seed=24, max_ctx=CTX)
+    _, c1 = workloads.attn_case(lens, dev, seed=25, max_ctx=CTX)
+    c0.kv_scale = c1.kv_scale = None
+    pools = {i: (c.kv.view(-1, 1, 576), c.ikv.view(-1, 1, 4, 64, 16), c.iks.view(-1, 1, 4, 64))
+             for i, c in ((0, c0), (1, c1))}
+    forward_context.POOL = SimpleNamespace(get_key_buffer=lambda i: pools[i][0],
+                                           get_index_k_fp4_payload_buffer=lambda i: pools[i][1],
+                                           get_index_k_fp4_scale_buffer=lambda i: pools[i][2])
+    forward_context.ATTN_BACKEND = SimpleNamespace(forward_metadata=SimpleNamespace(real_page_table=step.page_table))
+    runtime_context.PARALLEL = SimpleNamespace(tp_size=4, tp_rank=0, tp_group=None)
+    runtime_context.MODEL_CONFIG = SimpleNamespace(context_len=CTX)
+    built = mono.SPEC.build(lm, hf, SimpleNamespace(widths=[4], copies={}, deadline_s=2.0))
+    try:
+        assert built.check_layers
+        pos = step.seq_lens.long() - 1
+        slots = step.page_table.gather(1, (pos // 64)[:, None]).squeeze(1).long() * 64 + pos % 64
+        key = registry.ShapeKey(forward_mode="decode", batch_size=ROWS, tokens_per_request=1)
+        print("[check mode] forward", flush=True)
+        built.forward(registry.Plan(key=key), None, pos, SimpleNamespace(out_cache_loc=slots))
+        torch.cuda.synchronize()
+        built.runtime.check_errors()
+    finally:
+        built.runtime.close()
+    info = [r.getMessage() for r in caplog.records if r.levelname == "INFO"]
+    for line in info:
+        print("  " + line, flush=True)
+    assert len(info) == 2 and all("layer.topk_own.max_abs" in line for line in info)
+    errors = [r.getMessage() for r in caplog.records if r.levelname == "ERROR"]
+    assert not errors, errors

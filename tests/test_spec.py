@@ -326,3 +326,116 @@ def test_rope_tables_from_the_rotary_cache():
     bad = SimpleNamespace(self_attn=SimpleNamespace(rotary_emb=rot, indexer=SimpleNamespace(rotary_emb=other)))
     with pytest.raises(sglang_bind.BindError, match="rotary"):
         sglang_bind.rope_tables([layer, bad], {})
+
+
+# ---- check mode (SGLANG_AMD_MONO_CHECK=1) ----
+
+class _CheckModule:
+    """SGLang's layer as check mode calls it: ``(positions, hidden, batch, residual)``
+    -> ``(hidden, residual)``; it writes ``rows`` into the caches at the step's slots
+    and records the cache rows it saw."""
+
+    def __init__(self, caches_of, rows):
+        self.caches_of, self.rows, self.saw = caches_of, rows, []
+
+    def __call__(self, positions, hidden, batch, residual):
+        c, slots = self.caches_of(), batch.out_cache_loc.long()
+        self.saw.append(c.kv[slots].clone())
+        c.kv[slots] = self.rows["kv"]
+        c.ikv[slots // 64, :, slots % 64] = self.rows["ikv"]
+        return hidden * 2, hidden
+
+
+class _CheckRuntime(_Runtime):
+    """A launch that writes ``rows`` and returns 3 h (+ ``bump``) with the given
+    index scores and selection as its kept intermediates."""
+
+    def __init__(self, caches_of, rows, scores, selection, bump=0.0):
+        super().__init__()
+        self.caches_of, self.rows, self.scores, self.sel, self.bump = caches_of, rows, scores, selection, bump
+        self.saw = []
+
+    def forward(self, h, seq_lens, page_table, caches, w, cos, sin, check_weights=True, keep=False):
+        assert keep
+        self.saw.append(caches.kv[self.rows["slots"]].clone())
+        caches.kv[self.rows["slots"]] = self.rows["kv"]
+        caches.ikv[self.rows["slots"] // 64, :, self.rows["slots"] % 64] = self.rows["ikv"]
+        return h * 3 + self.bump, dict(index_scores=self.scores, topk_slots=self.sel)
+
+
+def _check_case(monkeypatch, bump=0.0, kv_delta=0, swap_selected=False):
+    """Two rows at positions 2999 and 99 of two requests over 50 pages each; scores
+    fall with position, so a row's exact top-2048 is its first 2048 positions."""
+    from sgl_amd_mono_amd import check
+
+    monkeypatch.setenv(check.CHECK_ENV, "1")
+    S, pages, ctx = 2, 100, 3200
+    g = torch.Generator().manual_seed(3)
+    kv = torch.randint(0, 120, (pages * 64, 1, 576), generator=g, dtype=torch.uint8)
+    pay = torch.randint(0, 256, (pages, 1, 4, 64, 16), generator=g, dtype=torch.uint8)
+    sc = torch.randint(120, 130, (pages, 1, 4, 64), generator=g, dtype=torch.uint8)
+    pool = SimpleNamespace(get_key_buffer=lambda i: kv, get_index_k_fp4_payload_buffer=lambda i: pay,
+                           get_index_k_fp4_scale_buffer=lambda i: sc)
+    forward_context.POOL = pool
+    table = torch.cat([torch.arange(50, 100), torch.arange(0, 50)]).to(torch.int32).reshape(2, 50)
+    forward_context.ATTN_BACKEND = SimpleNamespace(forward_metadata=SimpleNamespace(real_page_table=table))
+    pos = torch.tensor([2999, 99])
+    slots = table[torch.arange(2), pos // 64].long() * 64 + pos % 64
+    rows = dict(slots=slots, kv=torch.randint(0, 120, (2, 576), generator=g, dtype=torch.uint8),
+                ikv=torch.randint(0, 256, (2, 4, 16), generator=g, dtype=torch.uint8))
+    launch_rows = dict(rows, kv=rows["kv"] + kv_delta)
+    scores = -torch.arange(ctx, dtype=torch.float32).repeat(S, 1)
+    first = torch.arange(2048)
+    sel = torch.full((S, 2048), -1, dtype=torch.int32)
+    sel[0] = (table[0, first // 64].long() * 64 + first % 64).to(torch.int32)
+    sel[1, :100] = (table[1, first[:100] // 64].long() * 64 + first[:100] % 64).to(torch.int32)
+    if swap_selected:
+        sel[0, 5] = int(table[0, 2100 // 64]) * 64 + 2100 % 64
+    layer = mono._Layer(0, None, "w0")  # one covered layer, no dense ones
+    bound = lambda: layer.caches  # noqa: E731
+    layer.module = _CheckModule(bound, rows)
+    rt = _CheckRuntime(bound, launch_rows, scores, sel, bump)
+    model = SimpleNamespace(embed_tokens=lambda ids: torch.ones(S, 7168), layers=["L0"], norm=lambda h: h)
+    lm = _Lm(model)
+    lm.logits_processor = lambda ids, hidden, head, batch: hidden
+    lm.lm_head = None
+    built = mono._Built(lm, {0: layer}, rt, None, None, "cpu", context_len=ctx)
+    before = kv.view(-1, 576)[slots].clone()
+    key = registry.ShapeKey(forward_mode="decode", batch_size=S, tokens_per_request=1)
+    out = built.forward(registry.Plan(key=key), "ids", pos, SimpleNamespace(out_cache_loc=slots))
+    return out, before, layer.module, rt, kv.view(-1, 576)[slots].clone(), launch_rows
+
+
+def test_check_mode_measures_the_launch_against_sglangs_layer(monkeypatch, caplog):
+    """SGLang's module runs first on the caches as they were, its rows are restored, the
+    launch writes its own; every metric is logged and none is violated."""
+    caplog.set_level("INFO", logger="sgl_amd_mono_amd.check")
+    out, before, module, rt, after, launch_rows = _check_case(monkeypatch)
+    assert torch.equal(module.saw[0], before) and torch.equal(rt.saw[0], before)
+    assert torch.equal(after, launch_rows["kv"]) and float(out[0, 0]) == 3.0
+    info = [r.getMessage() for r in caplog.records if r.levelname == "INFO"]
+    assert len(info) == 1 and "layer.streams.cosine=1" in info[0] and "layer.topk_exact.max_abs=0" in info[0]
+    assert "layer.kv.cosine=1" in info[0] and "layer.index.cosine=1" in info[0]
+    assert not [r for r in caplog.records if r.levelname == "ERROR"]
+
+
+@pytest.mark.parametrize("plant, metric", [
+    (dict(bump=0.5), "layer.streams.rel"),
+    (dict(kv_delta=9), "layer.kv.cosine"),
+    (dict(swap_selected=True), "layer.topk_exact.max_abs"),
+])
+def test_check_mode_reports_violations(monkeypatch, caplog, plant, metric):
+    """A planted difference (the stream shifted, other MLA rows written, one key of the
+    exact top-2048 swapped for a lower one) is logged as that metric's violation."""
+    caplog.set_level("INFO", logger="sgl_amd_mono_amd.check")
+    _check_case(monkeypatch, **plant)
+    errors = [r.getMessage() for r in caplog.records if r.levelname == "ERROR"]
+    assert any(metric in e for e in errors), errors
+
+
+def test_check_mode_is_off_by_default(monkeypatch):
+    from sgl_amd_mono_amd import check
+
+    monkeypatch.delenv(check.CHECK_ENV, raising=False)
+    built = mono._Built(_Lm(), {3: None}, None, None, None, "cpu", context_len=4096)
+    assert built.check_layers is False
