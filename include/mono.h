@@ -19,7 +19,7 @@
  *   - Glm53Runtime.set_deadline                          glm53/gfx950/runner.py:197-204
  *       -> mono_layer_set_deadline (mono_*_set_deadline)
  *   - Glm53Runtime.advance_step (the step epoch)        glm53/gfx950/runner.py:205-210
- *       -> no call: every launch takes its tag from the guard's own ticket counter
+ *       -> no call: every launch takes its tag from the guard's own launch counters
  *   - Glm53LayerOp.launch(h, caches, cos, sin, step)    glm53/gfx950/runner.py:240-321
  *       (rt.dispatch of 42 raw data_ptr() ints + stream)
  *       -> mono_layer_forward    (the whole decoder layer, kernel.py:6-45)
@@ -44,7 +44,7 @@
 extern "C" {
 #endif
 
-#define MONO_ABI_VERSION 2
+#define MONO_ABI_VERSION 3
 
 enum {
   MONO_OK = 0,
@@ -66,7 +66,7 @@ enum { MONO_ROUTER_SIGMOID_BIAS = 0, MONO_ROUTER_SOFTMAX = 1 };
  *       mono_*_clear_errors
  *   [2] tag of the launch that failed
  *   [3] the workgroup that failed first
- *   [4..5] launch tickets, u64 (workgroups x launches so far)
+ *   [4..5] launches begun, u64 (each workgroup also counts them in its own counter)
  *   [6] scrub barrier arrivals
  *   [7] 0
  * Every launch that fails a wait, or that the sticky error refuses, also writes the
@@ -166,6 +166,10 @@ typedef struct {
   float* y;             /* optional f32 [rows, H] */
   int32_t* topk_ids;    /* optional i32 [rows, top_k] */
   float* topk_w;        /* optional f32 [rows, top_k] */
+  int64_t* timeline;    /* optional i64 [max_act * 36 + 96, 4], max_act = min(8 max_rows, 256) + 1:
+                           per task of the list (up tiles, down groups, finals) start,
+                           inputs-ready (0: no wait) and end ticks (100 MHz) and
+                           workgroup << 8 | kind (1 up, 2 down, 3 final) */
 } mono_moe_mxfp4_args;
 
 int mono_moe_mxfp4_forward(mono_moe* moe, const mono_moe_mxfp4_args* args, void* stream);
@@ -380,8 +384,8 @@ typedef struct {
 } mono_layer_args;
 
 /* Replaces Glm53Runtime (runner.py:133-215) for a whole decoder layer: the mailboxes
- * of the front, the attention, the back and the FP8 MoE, and ONE guard (one ticket
- * counter, one set of error words) for every launch of the layer, whichever of
+ * of the front, the attention, the back and the FP8 MoE, and ONE guard (one count of
+ * launches, one set of error words) for every launch of the layer, whichever of
  * mono_layer_forward / _front_forward / _tail_forward the caller mixes. */
 int mono_layer_create(const mono_layer_config* cfg, mono_layer** out);
 int mono_layer_destroy(mono_layer* layer);

@@ -11,7 +11,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libmono_gfx950.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 MONO_OK, MONO_EINVAL, MONO_EHIP, MONO_ESTATE, MONO_ENOMEM = 0, 1, 2, 3, 4
 ROUTER_SIGMOID_BIAS, ROUTER_SOFTMAX = 0, 1
@@ -39,7 +39,7 @@ class MoeFp8Args(C.Structure):
 class MoeMxfp4Args(C.Structure):
     _fields_ = [
         ("x", _VP), ("logits", _VP), ("w13", _VP), ("s13", _VP), ("w2", _VP), ("s2", _VP),
-        ("out", _VP), ("rows", _I32), ("y", _VP), ("topk_ids", _VP), ("topk_w", _VP),
+        ("out", _VP), ("rows", _I32), ("y", _VP), ("topk_ids", _VP), ("topk_w", _VP), ("timeline", _VP),
     ]
 
 
@@ -140,7 +140,7 @@ SIGNATURES = {
     "mono_layer_set_launch_ordinal": (C.c_int, [_VP, C.c_uint64]),
 }
 GUARD_WORDS = 8
-# guard words: tag epochs, error (1 + site), failing tag, failing workgroup, u64 tickets
+# guard words: tag epochs, error (1 + site), failing tag, failing workgroup, u64 launches begun
 G_EPOCH, G_ERROR, G_FAIL_TAG, G_FAIL_BLOCK, G_TICKET = 0, 1, 2, 3, 4
 # tags repeat every TAG_PERIOD launches (a launch's tag is ordinal % TAG_PERIOD + 1)
 TAG_PERIOD = 2**32 - 2

@@ -12,6 +12,7 @@
 #include <cstdio>
 #include <cstring>
 #include <string>
+#include <vector>
 
 #include "abi_errors.h"
 #include "attn_back_ops.h"
@@ -63,10 +64,13 @@ const double DEFAULT_DEADLINE_S = 2.0;
 const double MAX_DEADLINE_S = 3600.0;
 
 // Carves one device allocation into 256-byte aligned pieces after the runtime's header
-// (its first 256 bytes: the guard words, the scrub table and the unit scale).
-constexpr size_t HEADER = 256;
-constexpr size_t SCRUB_OFF = 64;  // the guard's scrub table in the header
-constexpr size_t UNIT_OFF = 192;  // the f32 1.0 in the header
+// (the guard words, the scrub table and the unit scale in its first 256 bytes, then the
+// per-workgroup launch counters).
+constexpr size_t SCRUB_OFF = 64;    // the guard's scrub table in the header
+constexpr size_t UNIT_OFF = 192;    // the f32 1.0 in the header
+constexpr size_t TICKETS_OFF = 256;  // u64 [MAX_GRID] launch counters, one a workgroup
+constexpr int MAX_GRID = 1024;
+constexpr size_t HEADER = TICKETS_OFF + MAX_GRID * sizeof(uint64_t);
 struct Carve {
   size_t off = HEADER;
   size_t take(size_t bytes) {
@@ -138,6 +142,7 @@ struct RuntimeBase {
     if (int rc = occupancy(&per_cu)) return rc;
     if (per_cu < 1) return fail(MONO_ESTATE, "the persistent %s kernel does not fit on a CU (occupancy %d)", what, per_cu);
     grid = prop.multiProcessorCount;
+    if (grid > MAX_GRID) return fail(MONO_ESTATE, "%d CUs: the launch counters hold at most %d workgroups", grid, MAX_GRID);
     const size_t total = align256(bytes);
     hipError_t e = hipMalloc(&blob, total);
     if (e != hipSuccess) {
@@ -156,6 +161,7 @@ struct RuntimeBase {
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) return fail(MONO_EHIP, "clearing the %s mailboxes: %s", what, hipGetErrorString(e));
     guard.words = reinterpret_cast<uint32_t*>(at(0));
+    guard.tickets = reinterpret_cast<uint64_t*>(at(TICKETS_OFF));
     guard.scrub = reinterpret_cast<const mono::ScrubRegion*>(at(SCRUB_OFF));
     guard.host_err = herr.dev;
     guard.deadline_ticks = (uint64_t)(DEFAULT_DEADLINE_S * TICKS_PER_S);
@@ -243,13 +249,11 @@ int guard_set_deadline(GuardRef r, double seconds) {
   return ok();
 }
 
-// The launches' ordinal so far (synchronises): launch tickets / grid.
+// The launches' ordinal so far (synchronises): workgroup 0's launch counter.
 int guard_ordinal(GuardRef r, uint64_t* ord) {
   if (int rc = check_device(r.device)) return rc;
   HIP_TRY(hipDeviceSynchronize());
-  uint64_t tickets = 0;
-  HIP_TRY(hipMemcpy(&tickets, r.g->words + mono::G_TICKET, sizeof(tickets), hipMemcpyDeviceToHost));
-  *ord = tickets / (uint64_t)r.grid;
+  HIP_TRY(hipMemcpy(ord, r.g->tickets, sizeof(*ord), hipMemcpyDeviceToHost));
   return MONO_OK;
 }
 
@@ -288,11 +292,12 @@ int guard_clear(GuardRef r) {
 // Move the launch ordinal to `ordinal` (synchronises; tests of the tag epochs): the next
 // launch takes tag ordinal % TAG_PERIOD + 1.
 int guard_set_ordinal(GuardRef r, uint64_t ordinal) {
-  if (ordinal > UINT64_MAX / (uint64_t)r.grid) return fail(MONO_EINVAL, "ordinal %llu is out of range", (unsigned long long)ordinal);
+  if (ordinal == UINT64_MAX) return fail(MONO_EINVAL, "ordinal %llu is out of range", (unsigned long long)ordinal);
   if (int rc = check_device(r.device)) return rc;
   HIP_TRY(hipDeviceSynchronize());
-  const uint64_t tickets = ordinal * (uint64_t)r.grid;
-  HIP_TRY(hipMemcpy(r.g->words + mono::G_TICKET, &tickets, sizeof(tickets), hipMemcpyHostToDevice));
+  std::vector<uint64_t> counters((size_t)r.grid, ordinal);
+  HIP_TRY(hipMemcpy(r.g->tickets, counters.data(), counters.size() * sizeof(uint64_t), hipMemcpyHostToDevice));
+  HIP_TRY(hipMemcpy(r.g->words + mono::G_TICKET, &ordinal, sizeof(ordinal), hipMemcpyHostToDevice));
   HIP_TRY(hipDeviceSynchronize());
   return ok();
 }
@@ -776,7 +781,7 @@ extern "C" int mono_proj_clear_errors(mono_proj* p) {
 // private to the layer (never handed out on their own), the o_proj tiles' done words of
 // the fused launch, and the layer's guard. Every launch of the layer (the whole layer,
 // or its front and the fused rest apart) runs under that one guard: the attention
-// runtime's guard words (one ticket counter, so tags never collide between the
+// runtime's guard words and launch counters (one count of launches, so tags never collide between the
 // launches, whichever the caller mixes) and host word, its row histograms as the flip
 // words, and a scrub table of all four mailbox regions.
 struct mono_layer {

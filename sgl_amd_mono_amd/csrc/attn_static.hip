@@ -35,9 +35,11 @@ constexpr int MAX_DEVICES = 64;
 constexpr size_t al256(size_t n) { return (n + 255) & ~size_t(255); }
 
 // the carve of the array: a 256-byte header (guard words, scrub table, the f32 1.0 of
-// raw E4M3 rows), then the mailboxes of a runtime with max_rows NA_ROWS, max_ctx NA_CTX
-constexpr size_t O_SCRUB = 64, O_UNIT = 192;
-constexpr size_t O_SCORE = 256;
+// raw E4M3 rows), the per-workgroup launch counters, then the mailboxes of a runtime
+// with max_rows NA_ROWS, max_ctx NA_CTX
+constexpr size_t O_SCRUB = 64, O_UNIT = 192, O_TICKETS = 256;
+constexpr int MAX_GRID = 1024;
+constexpr size_t O_SCORE = O_TICKETS + MAX_GRID * sizeof(uint64_t);
 constexpr size_t O_SEL = O_SCORE + al256((size_t)NA_ROWS * NA_CTX * 4);
 constexpr size_t O_ROWH = O_SEL + al256((size_t)NA_ROWS * TOPK * 8);
 constexpr size_t O_CDONE = O_ROWH + al256((size_t)2 * NA_ROWS * ROWH * 4);
@@ -67,7 +69,7 @@ __global__ __launch_bounds__(256) void k_scratch_init(uint8_t* base) {
        i += (size_t)gridDim.x * blockDim.x)
     p[i] = zero;
   if (blockIdx.x == 0) {
-    if (threadIdx.x < O_SCORE / 16) p[threadIdx.x] = zero;
+    for (size_t i = threadIdx.x; i < O_SCORE / 16; i += blockDim.x) p[i] = zero;
     __syncthreads();
     if (threadIdx.x == 0) {
       ScrubRegion* t = reinterpret_cast<ScrubRegion*>(base + O_SCRUB);
@@ -121,6 +123,7 @@ int device_scratch(hipStream_t st, DeviceScratch* out) {
     if (e != hipSuccess) return failf(MONO_EHIP, "querying device %d: %s", dev, hipGetErrorString(e));
     if (per_cu < 1) return failf(MONO_ESTATE, "the persistent attention kernel does not fit on a CU");
     if (cus % TEAM) return failf(MONO_ESTATE, "the attention launch needs a CU count divisible by %d, got %d", TEAM, cus);
+    if (cus > MAX_GRID) return failf(MONO_ESTATE, "%d CUs: the launch counters hold at most %d workgroups", cus, MAX_GRID);
     k_scratch_init<<<cus, 256, 0, st>>>(static_cast<uint8_t*>(p));
     e = hipGetLastError();
     if (e != hipSuccess) return failf(MONO_EHIP, "clearing the static scratch: %s", hipGetErrorString(e));
@@ -173,6 +176,7 @@ extern "C" int mono_attn_forward_noalloc(const mono_attn_args* args, float softm
   mail.max_rows = NA_ROWS;
   mono::GuardArgs guard{};
   guard.words = mail.guard;
+  guard.tickets = reinterpret_cast<uint64_t*>(base + O_TICKETS);
   guard.scrub = reinterpret_cast<const mono::ScrubRegion*>(base + O_SCRUB);
   guard.flip = mail.rowh;
   guard.flip_words = NA_ROWS * ROWH;

@@ -76,14 +76,15 @@ struct PlanLds {
   int32_t n_act;
 };
 
+template <int E, int TOPK, int THREADS>
+MONO_DEV void plan_from_picks(PlanLds<E, TOPK>& P, int S);
+
 // Build the plan from every row's picks (mailbox rsel: ids, then weights). All
 // threads of the workgroup call it; false (workgroup-uniform) if a wait failed.
 template <int E, int TOPK, int THREADS>
 MONO_DEV bool build_plan(PlanLds<E, TOPK>& P, const uint64_t* rsel, int S, int site, const Guard& gd) {
-  static_assert(THREADS >= E && THREADS / WAVE <= 16, "one thread an expert");
-  const int tid = threadIdx.x, lane = tid % WAVE, wave = tid / WAVE;
+  const int tid = threadIdx.x;
   bool ok = true;
-  for (int e = tid; e < E; e += THREADS) P.used[e] = 0u;
   if (tid < S * 2 * MAX_TOPK) {
     const int s = tid / (2 * MAX_TOPK), k = tid % (2 * MAX_TOPK);
     if (k % MAX_TOPK < TOPK) {
@@ -94,6 +95,18 @@ MONO_DEV bool build_plan(PlanLds<E, TOPK>& P, const uint64_t* rsel, int S, int s
     }
   }
   if (!block_all(ok)) return false;
+  plan_from_picks<E, TOPK, THREADS>(P, S);
+  return true;
+}
+
+// The plan from the picks already in P.pick_id / P.pick_w (ids in [0, E)); all threads
+// of the workgroup call it, after a barrier that orders the picks' writes.
+template <int E, int TOPK, int THREADS>
+MONO_DEV void plan_from_picks(PlanLds<E, TOPK>& P, int S) {
+  static_assert(THREADS >= E && THREADS / WAVE <= 16, "one thread an expert");
+  const int tid = threadIdx.x, lane = tid % WAVE, wave = tid / WAVE;
+  for (int e = tid; e < E; e += THREADS) P.used[e] = 0u;
+  __syncthreads();
   if (tid < S * TOPK) {
     const int s = tid / TOPK, k = tid % TOPK;
     atomicOr(&P.used[P.pick_id[s][k]], 1u << s);
@@ -136,7 +149,6 @@ MONO_DEV bool build_plan(PlanLds<E, TOPK>& P, const uint64_t* rsel, int S, int s
     if (k == 0) P.rowslot[s][0] = 0;
   }
   __syncthreads();
-  return true;
 }
 
 // Route weight of slot d for row s (0 if the slot does not serve the row).

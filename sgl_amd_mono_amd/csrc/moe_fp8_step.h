@@ -8,7 +8,7 @@
 // barrier and every wait is bounded by the guard's deadline.
 //
 // Work, in the order each workgroup walks it:
-//   ticket   one atomic add a workgroup -> the launch's tag (sync.h)
+//   ticket   one atomic add on the workgroup's own launch counter -> the launch's tag (sync.h)
 //   norm     every workgroup: the RMSNorm statistics of all rows (kernel.py:1367-1415);
 //            wave w keeps row w in registers for xq
 //   router   task t < 16 * RK on workgroup t: 16 experts x a 512-wide K slice of the

@@ -30,6 +30,8 @@ hipError_t moe_fp8_occupancy(int* blocks_per_cu);
 hipError_t moe_fp8_forward(const MoeFp8Args& g, int grid, const Mail& mail, const GuardArgs& guard, hipStream_t st);
 
 bool moe_mxfp4_supported(const MoeGeom& geo);
+// Tasks in the MXFP4 launch's list at most, for max_act expert slots (timeline rows).
+int moe_mxfp4_tasks(int max_act);
 hipError_t moe_mxfp4_occupancy(int* blocks_per_cu);
 hipError_t moe_mxfp4_forward(const mono_moe_mxfp4_args& g, int grid, const Mail& mail, const GuardArgs& guard,
                              hipStream_t st);

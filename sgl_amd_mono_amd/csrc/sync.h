@@ -10,11 +10,13 @@
 // the reference's tagged (value, tag) pair (sgl_amd_mono/common/sync.py:30-207,
 // glm53/gfx950/kernel.py:29-35,636-647), restated for HIP.
 //
-// Tags: every workgroup of a launch takes a ticket from the 64-bit counter at guard
-// words 4-5 with one atomic add; ticket / gridDim.x is the launch's ordinal (launches
-// sharing a guard are stream-ordered, so their tickets never interleave) and the tag is
-// ordinal % TAG_PERIOD + 1. A HIP-graph replay takes fresh tickets, so it never sees a
-// stale word as ready.
+// Tags: every workgroup of a launch counts the guard's launches itself: workgroup b
+// adds one to its own 64-bit counter (tickets[b], one atomic add on a word no other
+// workgroup touches, so the grid's adds never serialise on one address) and the value
+// before the add is the launch's ordinal (launches sharing a guard are stream-ordered
+// and each runs every workgroup of the same grid, so all counters stay equal); the tag
+// is ordinal % TAG_PERIOD + 1. Workgroup 0 also stores ordinal + 1 at guard words 4-5
+// for the host. A HIP-graph replay counts on, so it never sees a stale word as ready.
 //
 // Tag epochs: tags repeat every TAG_PERIOD launches, and a word left unwritten for
 // exactly that long would read as fresh (the reference scrubs its mailboxes for the
@@ -31,7 +33,7 @@
 //      later launch of the guard exits at once until the host clears it)
 //   2  tag of the failing launch (waits of that launch give up when they see it)
 //   3  workgroup that failed first
-//   4-5 launch tickets, u64
+//   4-5 launches begun, u64 (workgroup 0's count)
 //   6  scrub barrier arrivals (u32, G more a scrub)
 // Every wait polls its words until their tags match, checking the deadline
 // (s_memrealtime, 100 MHz) after its first poll and then every POLL_CHECK polls, and
@@ -52,7 +54,7 @@ enum GuardWord {
   G_ERROR = 1,
   G_FAIL_TAG = 2,
   G_FAIL_BLOCK = 3,
-  G_TICKET = 4,  // u64 at words 4-5
+  G_TICKET = 4,  // u64 at words 4-5: launches begun
   G_BARRIER = 6,
   G_WORDS = 8
 };
@@ -72,6 +74,8 @@ struct ScrubRegion {
 // Kernel-argument part of the guard.
 struct GuardArgs {
   uint32_t* words;
+  // [grid] per-workgroup launch counters (u64), outside every scrub region
+  uint64_t* tickets;
   // [SCRUB_MAX] in device memory: the guard's mailboxes (p = NULL past the last region)
   const ScrubRegion* scrub;
   // atomic accumulators used by launch parity: [2][flip_words]; every launch zeroes
@@ -325,20 +329,39 @@ MONO_DEV bool scrub_mailboxes(const GuardArgs& a, const Guard& gd) {
   return block_all(ok);
 }
 
-// The start of every launch, called by every thread of the workgroup: take the
-// workgroup's ticket, set up the guard (tag, deadline, this launch's forced fault),
+// The guard's two reads at a launch's start (thread 0's values; 0 elsewhere): the
+// workgroup's launch ordinal (its counter's value before this launch's add) and the
+// sticky error word. guard_fetch issues them; their first use in guard_begin waits, so
+// a kernel that calls guard_fetch first and loads its own inputs before guard_begin
+// overlaps the two round trips with those loads (vector memory returns in order).
+struct GuardFetch {
+  uint64_t ord;
+  uint32_t err;
+};
+MONO_DEV GuardFetch guard_fetch(const GuardArgs& a) {
+  GuardFetch f{0, 0u};
+  if (threadIdx.x == 0) {
+    f.ord = __hip_atomic_fetch_add(a.tickets + blockIdx.x, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    f.err = a.sticky ? ld_agent_u32(&a.words[G_ERROR]) : 0u;
+  }
+  return f;
+}
+
+// The start of every launch, called by every thread of the workgroup with what
+// guard_fetch returned: set up the guard (tag, deadline, this launch's forced fault),
 // scrub the mailboxes at the start of a tag epoch and clear the successor's copy of the
 // flip accumulators. False (workgroup-uniform) if the guard's sticky error refuses the
 // launch (a refused launch reports the error to the host word) or the scrub failed.
-MONO_DEV bool guard_begin(const GuardArgs& a, Guard& gd) {
+MONO_DEV bool guard_begin(const GuardArgs& a, Guard& gd, const GuardFetch& f) {
   __shared__ uint32_t sh[4];
   if (threadIdx.x == 0) {
-    uint64_t* tickets = reinterpret_cast<uint64_t*>(&a.words[G_TICKET]);
-    const uint64_t ticket = __hip_atomic_fetch_add(tickets, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const uint64_t ord = ticket / gridDim.x;
+    const uint64_t ord = f.ord;
+    if (blockIdx.x == 0)
+      __hip_atomic_store(reinterpret_cast<uint64_t*>(&a.words[G_TICKET]), ord + 1, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
     const uint64_t in_epoch = ord % TAG_PERIOD;
     sh[0] = (uint32_t)in_epoch + 1u;
-    sh[1] = a.sticky ? ld_agent_u32(&a.words[G_ERROR]) : 0u;
+    sh[1] = f.err;
     sh[2] = ord >= a.fault_from ? 1u : 0u;
     sh[3] = (in_epoch == 0 && ord != 0) ? 1u : 0u;
   }
@@ -363,6 +386,7 @@ MONO_DEV bool guard_begin(const GuardArgs& a, Guard& gd) {
   }
   return true;
 }
+MONO_DEV bool guard_begin(const GuardArgs& a, Guard& gd) { return guard_begin(a, gd, guard_fetch(a)); }
 
 // A launch that failed or was refused writes NaN over its bf16 output (n elements at p)
 // so a caller that reads it anyway gets no plausible numbers: `share` writes the

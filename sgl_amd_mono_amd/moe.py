@@ -90,9 +90,17 @@ class MoeRuntime(Runtime):
         _lib.check(_lib.lib().mono_moe_fp8_forward(self._h, C.byref(args), self._stream()))
         return (out, dbg) if debug else out
 
+    def mxfp4_tasks(self) -> int:
+        """Rows of an MXFP4 launch's timeline: the task list at most (every expert slot's
+        24 up tiles and 12 down groups, then 96 final tasks)."""
+        max_act = min(self.max_rows * self.geo.top_k, self.geo.n_experts) + 1
+        return max_act * (self.geo.inter // 16 + self.geo.hidden // 256) + self.geo.hidden // 32
+
     def forward_mxfp4(self, x: torch.Tensor, logits: torch.Tensor, w: Mxfp4MoeWeights,
-                      out: torch.Tensor | None = None, debug: bool = False):
-        """``MoE(x)`` with MXFP4 experts behind a softmax router."""
+                      out: torch.Tensor | None = None, debug: bool = False, timeline: torch.Tensor | None = None):
+        """``MoE(x)`` with MXFP4 experts behind a softmax router.
+        ``timeline`` (int64 [mxfp4_tasks(), 4]) receives each task's start,
+        inputs-ready and end ticks and workgroup << 8 | kind (1 up, 2 down, 3 final)."""
         g, dev = self.geo, self.device
         H, E, I, K = g.hidden, g.n_experts, g.inter, g.top_k
         if x.dim() != 2 or not 1 <= x.shape[0] <= self.max_rows:
@@ -107,6 +115,8 @@ class MoeRuntime(Runtime):
         if out is None:
             out = torch.empty_like(x)
         need(out, "out", (S, H), torch.bfloat16, dev)
+        if timeline is not None:
+            need(timeline, "timeline", (self.mxfp4_tasks(), 4), torch.int64, dev)
         dbg = {}
         if debug:
             dbg = dict(
@@ -118,7 +128,7 @@ class MoeRuntime(Runtime):
         args = _lib.MoeMxfp4Args(
             x=P(x), logits=P(logits), w13=P(w.w13), s13=P(w.s13), w2=P(w.w2), s2=P(w.s2),
             out=P(out), rows=S, y=P(dbg.get("y")), topk_ids=P(dbg.get("topk_ids")),
-            topk_w=P(dbg.get("topk_w")),
+            topk_w=P(dbg.get("topk_w")), timeline=P(timeline),
         )  # fmt: skip
         _lib.check(_lib.lib().mono_moe_mxfp4_forward(self._h, C.byref(args), self._stream()))
         return (out, dbg) if debug else out

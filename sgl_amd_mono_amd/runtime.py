@@ -61,8 +61,9 @@ class Runtime:
         _lib.check(self._fn("set_fault")(self._h, int(site)))
 
     def error_words(self) -> list[int]:
-        """The guard words (synchronises): [tickets, 1 + failed wait site or 0, failing
-        launch tag, failing workgroup]."""
+        """The guard words (synchronises): [tag epochs, 1 + failed wait site or 0, failing
+        launch tag, failing workgroup, launches begun (u64, two words), scrub barrier,
+        reserved]."""
         words = (C.c_int32 * _lib.GUARD_WORDS)()
         with torch.cuda.device(self.device):
             _lib.check(self._fn("read_errors")(self._h, words))

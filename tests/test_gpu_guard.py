@@ -1,4 +1,4 @@
-"""The layer runtime's guard on the GPU: one ticket counter for every launch of a layer
+"""The layer runtime's guard on the GPU: one count of launches for every launch of a layer
 (whichever launches a caller mixes), tag epochs (tags repeat every 2^32 - 2 launches,
 and the first launch of an epoch scrubs every mailbox, the reference's reason for its
 own scrub: deepseek_v4/gfx950/kernels/layer.py:837-849), and the host-forced fault
@@ -85,12 +85,11 @@ def test_layer_tag_epoch_wrap(gpu_device):
         rt.check_errors()
         rt.handle.set_launch_ordinal(_lib.TAG_PERIOD - 3)
         crossing = [(8, 201), (16, 203), (3, 205), (16, 207), (8, 209), (3, 211)]
-        grid = torch.cuda.get_device_properties(gpu_device).multi_processor_count
         fresh_runs = []
         for i, (rows, seed) in enumerate(crossing):
             words = rt.handle.error_words()
-            tickets = (words[_lib.G_TICKET] & 0xFFFFFFFF) | (words[_lib.G_TICKET + 1] & 0xFFFFFFFF) << 32
-            ordinal = tickets // grid
+            # guard words 4-5: the launches begun (the ordinal of the next launch)
+            ordinal = (words[_lib.G_TICKET] & 0xFFFFFFFF) | (words[_lib.G_TICKET + 1] & 0xFFFFFFFF) << 32
             assert ordinal == _lib.TAG_PERIOD - 3 + i, (i, ordinal)
             print(f"[wrap] launch {i}: ordinal {ordinal}, tag {ordinal % _lib.TAG_PERIOD + 1}, rows {rows}", flush=True)
             got = _step(rt, rows, seed, gpu_device, cos, sin, w)
