@@ -71,8 +71,8 @@ enum { MONO_ROUTER_SIGMOID_BIAS = 0, MONO_ROUTER_SOFTMAX = 1 };
  *   [7] 0
  * Every launch that fails a wait, or that the sticky error refuses, also writes the
  * error to a pinned host word (mono_layer_pending_error) and NaN over its output.
- * Wait sites of the MoE launch: 0 router logits, 1 route picks, 2 expert mid
- * activations, 3 expert outputs. */
+ * Wait sites of the MoE launch: 0 router tasks (their done words), 2 expert mid
+ * activations, 3 expert outputs (1 is not used). */
 #define MONO_GUARD_WORDS 8
 enum { MONO_WEIGHT_FP8_BLOCK128 = 0, MONO_WEIGHT_MXFP4 = 1 };
 
@@ -406,7 +406,7 @@ int mono_layer_tail_forward(mono_layer* layer, const mono_proj_weights* w, const
 int mono_layer_set_deadline(mono_layer* layer, double seconds);
 /* words: int32 [MONO_GUARD_WORDS], the layer's guard (synchronises). Wait sites: 0-3
  * the attention's (index scores, selected slots, split partials, top-k team), 4 W_UV
- * output, 5 attention output, 6 router logits, 7 route picks, 8 expert mid, 9 expert
+ * output, 5 attention output, 6 router tasks, 7 (not used), 8 expert mid, 9 expert
  * outputs, 10 the attention block's output rows, 11-16 the front's (stage-A partials,
  * q_an, q_nope, raw index query, -, normed input rows), 17 the front's index outputs,
  * 18 the front's q, 31 the tag-epoch scrub. */

@@ -146,11 +146,11 @@ G_EPOCH, G_ERROR, G_FAIL_TAG, G_FAIL_BLOCK, G_TICKET = 0, 1, 2, 3, 4
 TAG_PERIOD = 2**32 - 2
 SCRUB_SITE = 31
 # wait sites of the launches (guard word 1 = site + 1)
-MOE_SITES = {0: "router logits", 1: "route picks", 2: "expert mid activations", 3: "expert outputs"}
+MOE_SITES = {0: "router tasks", 1: "(not used)", 2: "expert mid activations", 3: "expert outputs"}
 ATTN_SITES = {0: "index scores", 1: "selected slots", 2: "split partials", 3: "top-k team"}
 PROJ_SITES = {0: "stage-A partial sums", 1: "stage-A q_a tiles", 2: "q_nope", 3: "raw index query", 4: "W_UV output"}
 # every launch of a layer runtime (one guard)
-LAYER_SITES = {**ATTN_SITES, 4: "W_UV output", 5: "attention output", 6: "router logits", 7: "route picks",
+LAYER_SITES = {**ATTN_SITES, 4: "W_UV output", 5: "attention output", 6: "router tasks", 7: "(not used)",
                8: "expert mid activations", 9: "expert outputs", 10: "attention block output rows",
                **{11 + k: f"front: {v}" for k, v in {**PROJ_SITES, 5: "normed input rows"}.items()},
                17: "front index query and keys", 18: "front q", SCRUB_SITE: "tag-epoch scrub"}

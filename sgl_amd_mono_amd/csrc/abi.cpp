@@ -342,8 +342,10 @@ extern "C" int mono_moe_create(const mono_moe_config* cfg, mono_moe** out) {
   const size_t H = c.hidden, E = c.n_experts, I = c.inter;
   const size_t max_act = (size_t)std::min(c.max_rows * c.top_k, c.n_experts) + 1;
   Carve cv;
-  const size_t o_rlog = cv.take((size_t)moe_fp8_router_slices() * MAX_ROWS * E * 8);
-  const size_t o_rsel = cv.take((size_t)MAX_ROWS * 2 * MAX_TOPK * 8);
+  const size_t o_xq = cv.take((size_t)MAX_ROWS * H);
+  const size_t o_xs = cv.take((size_t)MAX_ROWS * (H / 128) * 4);
+  const size_t o_score = cv.take((size_t)MAX_ROWS * E * 4);
+  const size_t o_rdone = cv.take(mono::DONE_BYTES);
   const size_t o_mid = cv.take(max_act * MAX_ROWS * I * 8);
   const size_t o_ypart = cv.take(max_act * MAX_ROWS * H * 8);
   mono_moe* m = new mono_moe();
@@ -355,8 +357,10 @@ extern "C" int mono_moe_create(const mono_moe_config* cfg, mono_moe** out) {
     return rc;
   }
   m->mail.guard = m->guard.words;
-  m->mail.rlog = reinterpret_cast<uint64_t*>(m->at(o_rlog));
-  m->mail.rsel = reinterpret_cast<uint64_t*>(m->at(o_rsel));
+  m->mail.xq = reinterpret_cast<uint8_t*>(m->at(o_xq));
+  m->mail.xs = reinterpret_cast<float*>(m->at(o_xs));
+  m->mail.score = reinterpret_cast<float*>(m->at(o_score));
+  m->mail.rdone = reinterpret_cast<uint64_t*>(m->at(o_rdone));
   m->mail.mid = reinterpret_cast<uint64_t*>(m->at(o_mid));
   m->mail.ypart = reinterpret_cast<uint64_t*>(m->at(o_ypart));
   *out = m;

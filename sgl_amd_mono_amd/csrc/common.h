@@ -128,6 +128,9 @@ MONO_DEV uint32_t pack_bf16x2(float lo, float hi) {
   return (uint32_t)f32_to_bf16_bits(lo) | ((uint32_t)f32_to_bf16_bits(hi) << 16);
 }
 MONO_DEV float bf16_round(float f) { return (float)(__bf16)f; }
+// a dword as two bf16 (low half first), taken by value: __builtin_bit_cast of an
+// ext_vector element (v[i]) reads element 0 whatever i is (hipcc of ROCm 7.2)
+MONO_DEV bf16x2 as_bf16x2(uint32_t u) { return __builtin_bit_cast(bf16x2, u); }
 
 // ------------------------------------------------------------------ FP8 (OCP E4M3)
 // two f32 (already clamped to +-448) -> two E4M3 bytes in the low 16 bits, RNE

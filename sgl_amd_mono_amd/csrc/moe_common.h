@@ -43,11 +43,15 @@ MONO_DEV void wave_topk(uint32_t (&key)[4], int (&id)[4], float (&raw)[4], int n
   my_id = 0;
   for (int k = 0; k < TOPK; ++k) {
     const uint32_t m = wave_umax(key[0]);
-    const uint32_t cand = key[0] == m ? 0xffffu - (uint32_t)id[0] : 0u;
-    const int pick = min((int)(0xffffu - wave_umax(cand)), n_ids - 1);
-    const bool hit = key[0] == m && id[0] == pick;
-    const uint64_t bal = __ballot(hit);
+    uint64_t bal = __ballot(key[0] == m);
+    if (__popcll(bal) > 1) {  // wave-uniform: an exact tie of keys, the lowest id wins
+      const uint32_t cand = key[0] == m ? 0xffffu - (uint32_t)id[0] : 0u;
+      const int low = (int)(0xffffu - wave_umax(cand));
+      bal = __ballot(key[0] == m && id[0] == low);
+    }
     const int src = __ffsll((long long)bal) - 1;
+    const bool hit = lane == src;
+    const int pick = min(__builtin_amdgcn_readlane(id[0], src), n_ids - 1);
     const float rv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, raw[0]), src));
     if (lane == k) {
       my_raw = rv;
@@ -78,26 +82,6 @@ struct PlanLds {
 
 template <int E, int TOPK, int THREADS>
 MONO_DEV void plan_from_picks(PlanLds<E, TOPK>& P, int S);
-
-// Build the plan from every row's picks (mailbox rsel: ids, then weights). All
-// threads of the workgroup call it; false (workgroup-uniform) if a wait failed.
-template <int E, int TOPK, int THREADS>
-MONO_DEV bool build_plan(PlanLds<E, TOPK>& P, const uint64_t* rsel, int S, int site, const Guard& gd) {
-  const int tid = threadIdx.x;
-  bool ok = true;
-  if (tid < S * 2 * MAX_TOPK) {
-    const int s = tid / (2 * MAX_TOPK), k = tid % (2 * MAX_TOPK);
-    if (k % MAX_TOPK < TOPK) {
-      uint32_t v = 0;
-      ok = poll_word(&rsel[s * 2 * MAX_TOPK + k], v, site, gd);
-      if (k < MAX_TOPK) P.pick_id[s][k] = min(max((int)v, 0), E - 1);
-      else P.pick_w[s][k - MAX_TOPK] = __uint_as_float(v);
-    }
-  }
-  if (!block_all(ok)) return false;
-  plan_from_picks<E, TOPK, THREADS>(P, S);
-  return true;
-}
 
 // The plan from the picks already in P.pick_id / P.pick_w (ids in [0, E)); all threads
 // of the workgroup call it, after a barrier that orders the picks' writes.

@@ -21,14 +21,12 @@ bool moe_fp8_supported(const MoeGeom& geo) {
   return geo.hidden == H && geo.n_experts == E && geo.inter == I && geo.top_k == TOPK;
 }
 
-int moe_fp8_router_slices() { return RK; }
-
 hipError_t moe_fp8_occupancy(int* blocks_per_cu) {
   return hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, k_moe_fp8, FT, 0);
 }
 
 hipError_t moe_fp8_forward(const MoeFp8Args& g, int grid, const Mail& mail, const GuardArgs& guard, hipStream_t st) {
-  if (grid < ROUTER_TASKS || grid < MAX_ROWS || g.rows < 1 || g.rows > MAX_ROWS) return hipErrorInvalidConfiguration;
+  if (grid < 1 || g.rows < 1 || g.rows > MAX_ROWS) return hipErrorInvalidConfiguration;
   Args a;
   fill_args(a, g, mail, guard);
   k_moe_fp8<<<grid, FT, 0, st>>>(a);

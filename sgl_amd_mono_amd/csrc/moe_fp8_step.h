@@ -9,25 +9,27 @@
 //
 // Work, in the order each workgroup walks it:
 //   ticket   one atomic add on the workgroup's own launch counter -> the launch's tag (sync.h)
-//   norm     every workgroup: the RMSNorm statistics of all rows (kernel.py:1367-1415);
-//            wave w keeps row w in registers for xq
-//   router   task t < 16 * RK on workgroup t: 16 experts x a 512-wide K slice of the
-//            bf16 router GEMV on the bf16-rounded normed rows (MFMA 16x16x32 bf16)
-//            -> partial logits (mailbox rlog)
-//   route    row s on workgroup G-1-s: the K slices summed in order, sigmoid, top-8 by
-//            the f32 bits of (score + bias) with lowest-id ties, weights = score / sum
-//            x route_scale (kernel.py:1575-1629) -> the row's picks (mailbox rsel)
-//   xq       every workgroup: per-128 FP8 quantisation of the normed rows into LDS
-//            (amax / 448 with a hardware reciprocal, kernel.py:1440-1450), after the
-//            router and route so that neither waits for it
-//   plan     every workgroup, before its first routed tile: the distinct experts of
-//            the step; slot 0 is the shared expert (weight 1), slots 1.. the picked
-//            experts by ascending id
+//   router   task t < 64 ceil(S / 2), on workgroups t, t + G, ...: experts 4 (t % 64) .. + 3
+//            over rows 2 (t / 64) and 2 (t / 64) + 1, all of H in the task (the reference
+//            gives a router task one row, kernel.py:4199-4330). The rows' RMSNorm
+//            statistics (kernel.py:1367-1415), the bf16-rounded normed rows against the bf16
+//            router rows (v_dot2 with f32 accumulation) -> sigmoid scores; and one 512-k
+//            chunk of one of the rows quantised per 128 to FP8 (amax / 448 with a hardware
+//            reciprocal, kernel.py:1440-1450) while it is in registers. Both go out
+//            with device-coherent stores, then the task's done word (rdone)
+//   gather   every workgroup, once every router task is done: the step's FP8 rows
+//            straight into LDS (global_load_lds), their block scales, and each wave's
+//            rows' scores into registers
+//   route    every workgroup, wave w routing row w (and w + 8): top-8 by the f32 bits of
+//            (score + bias) with lowest-id ties, weights = score / sum x route_scale
+//            (kernel.py:1575-1629)
+//   plan     the distinct experts of the step; slot 0 is the shared expert (weight 1),
+//            slots 1.. the picked experts by ascending id
 //   tasks    one round-robin list over the workgroups:
 //            up     (slot, 16-channel tile): FP8 x FP8 MFMA 16x16x128 with the 128x128
 //                   weight block scale x the activation block scale per 128-k, the 8
 //                   waves splitting K, SiLU(gate) * up -> mailbox mid
-//            down   (slot, 256 output rows): the slot's mid quantised per 128 to FP8 in
+//            down   (slot, 448 output rows): the slot's mid quantised per 128 to FP8 in
 //                   LDS (kernel.py:5118-5125), FP8 MFMA, x weight block scale x mid
 //                   block scale x route weight -> mailbox ypart
 //            final  (32 output rows): the row's slots summed in plan order + the
@@ -61,18 +63,18 @@ constexpr int IB = I / 128;          // 128-k blocks of a mid row
 constexpr int NT = I / 16;           // up tiles a slot
 constexpr int UP_KBW = KB / FW;      // k blocks a wave of an up tile
 constexpr int UP_H0 = 4;             // of them in an up tile's first half (W[0..7]); the rest W[8..13]
-constexpr int RK = 14;               // router K slices
-constexpr int RKW = H / RK / FW;     // k a wave of a router task
-constexpr int RSTEP = RKW / 32;      // bf16 MFMA steps a wave of a router task
-constexpr int ROUTER_TASKS = (E / 16) * RK;
+constexpr int RT_E = 4;              // experts a router task
+constexpr int RT_S = 2;              // rows a router task
+constexpr int RT_EG = E / RT_E;      // router tasks a row pair
+constexpr int RCH = H / 512;         // 512-k chunks of a row: wave w holds chunks w and w + 8
 constexpr int DN_ROWS = 448;         // output rows of a down task: 28 16-row tiles x 4 k blocks
 constexpr int DN_GROUPS = H / DN_ROWS;
 constexpr int DN_PAIR = DN_ROWS / 16 / (FW / 2);  // row tiles of a wave pair
 constexpr int FIN_ROWS = 32;
 constexpr int FIN_TASKS = H / FIN_ROWS;
 constexpr int NSLOT = TOPK + 1;      // slots a row uses: the shared expert and its picks
-constexpr int PER_ROW = H / (8 * WAVE);  // 16-byte loads a lane makes of a hidden row
-static_assert(KB % FW == 0 && RKW % 32 == 0 && H % (RK * FW) == 0, "tiling");
+static_assert(KB % FW == 0 && RCH > FW && RCH <= 2 * FW && E % RT_E == 0 && RT_EG >= RT_S * RCH, "tiling");
+static_assert(H % (16 * WAVE) == 0 && E == 4 * WAVE && MAX_ROWS * KB <= 2 * FT, "the gather's copies");
 static_assert(UP_KBW * 2 == 14 && DN_PAIR * IB == 2 * 14 && H % DN_ROWS == 0, "14 weight tiles a wave");
 static_assert(IB == 4 && DN_PAIR == 7, "a wave pair's row tiles: 3 whole and half of one each");
 static_assert(I == 8 * WAVE && MAX_ROWS <= 2 * FW, "a down task's wave reads one or two mid rows, 8 channels a lane");
@@ -80,18 +82,22 @@ static_assert(MAX_ROWS * FIN_ROWS <= FT, "a final task's thread owns one (row, o
 
 // wait sites (guard error word = site + 1), offset by the Step's site0 in a fused
 // launch; W_A: the attention block's output rows (fused launch only)
-enum { W_LOGITS = 0, W_PICKS = 1, W_MID = 2, W_YPART = 3, W_A = 4 };
+enum { W_ROUTER = 0, W_MID = 2, W_YPART = 3, W_A = 4 };
 
 struct Lds {
   uint8_t xq[MAX_ROWS][H];          // FP8 normed rows
-  float xs[MAX_ROWS][KB];           // their block scales
-  float rstd[MAX_ROWS];
-  f32x4 red[2][FW][WAVE];           // cross-wave sums
+  float xs[MAX_ROWS][FW][8];        // their block scales: an up tile wave's UP_KBW, padded to 8
+  union {
+    f32x4 red[2][FW][WAVE];         // cross-wave sums of the expert tasks
+    struct {
+      float rss[FW][RT_S];            // a router task's sums of squares, a wave each
+      float rlg[FW][4][RT_E * RT_S];  // its logits, a 16-lane row of a wave each (apart
+                                      // from rss: fast waves write rlg while others read rss)
+    } rt;
+  };
   uint8_t bq[MAX_ROWS][I];          // a down task's FP8 mid
   float coef[MAX_ROWS][IB];         // its block scale x route weight
   PlanLds<E, TOPK> plan;
-  uint32_t rkey[E];
-  float rraw[E];
 };
 
 struct Args {
@@ -118,29 +124,20 @@ struct Args {
   GuardArgs guard;
 };
 
-// bf16(a * rstd * gamma) of 8 consecutive k as one bf16 MFMA operand
-// (stage_x_rmsnorm, kernel.py:1367-1400)
-MONO_DEV bf16x8 normed8(const uint16_t* a, const uint16_t* g, float rstd) {
-  const u32x4 av = ld_u32x4(a), gv = ld_u32x4(g);
-  u32x4 o;
-#pragma unroll
-  for (int q = 0; q < 4; ++q)
-    o[q] = pack_bf16x2(bf16_lo(av[q]) * rstd * bf16_lo(gv[q]), bf16_hi(av[q]) * rstd * bf16_hi(gv[q]));
-  return __builtin_bit_cast(bf16x8, o);
-}
-
 // Task kinds of the round-robin list
 enum { K_NONE = 0, K_UP = 1, K_DOWN = 2, K_FINAL = 3 };
 
-// the MoE's moments in a fused layer's tick row (its other words are the layer's)
-enum { T_PLAN = 4, T_A = 6, T_NORM = 7, T_ROUTER = 8, T_ROUTE = 9, T_QUANT = 10, T_ROW = 16 };
+// the MoE's moments in a fused layer's tick row (its other words are the layer's): the
+// attention block's rows seen, the first router task's statistics, the router tasks
+// done, the gather done, the rows routed, the plan built
+enum { T_PLAN = 4, T_A = 6, T_NORM = 7, T_ROUTER = 8, T_GATHER = 9, T_ROUTE = 10, T_ROW = 16 };
 
 class Step {
  public:
   MONO_DEV Step(const Args& a, Lds& l) : A(a), L(l) {
     tid = threadIdx.x;
     lane = tid % WAVE;
-    wave = tid / WAVE;
+    wave = __builtin_amdgcn_readfirstlane(tid / WAVE);  // uniform: wave arithmetic stays scalar
     g = lane / 16;
     r = lane % 16;
     G = gridDim.x;
@@ -165,10 +162,13 @@ class Step {
       refused = true;
       return false;
     }
-    // the router task's weights go out before anything waits
-    const int rt = blockIdx.x;
-    u32x4 wr[RSTEP];
-    if (rt < ROUTER_TASKS) router_load(rt, wr);
+    // the first router task's weights and the route's biases go out before anything waits
+    const int n_rt = RT_EG * ((S + RT_S - 1) / RT_S);
+    int t = blockIdx.x;
+    u32x4 wr[RT_E][2], gr[2];
+    if (t < n_rt) router_load(t, wr, gr);
+    const f32x4 bias4 = *reinterpret_cast<const f32x4*>(A.bias + 4 * lane);
+    const float bias[4] = {bias4[0], bias4[1], bias4[2], bias4[3]};
     if (a_done) {
       // every row of `a` is stored once its producers' done words carry the tag; `a` is
       // read with plain loads after that (no workgroup reads it earlier in the launch,
@@ -177,20 +177,22 @@ class Step {
       if (!hint_wait(n_a_done, [ad](int i) { return ad + i; }, site0 + W_A, gd)) return false;
       stamp(T_A);
     }
-
-    u32x4 ar[PER_ROW];  // wave w's row w, kept for the quantisation
-    norm_stats(ar);
-    __syncthreads();
-    stamp(T_NORM);
-    if (rt < ROUTER_TASKS) router(rt, wr);
-    stamp(T_ROUTER);
-    if ((int)blockIdx.x >= G - S) {
-      if (!route(G - 1 - (int)blockIdx.x)) return false;
-      stamp(T_ROUTE);
+    for (; t < n_rt; t += G) {
+      if (t != (int)blockIdx.x) router_load(t, wr, gr);
+      router_task(t, wr, gr);
     }
-    quant_rows(ar);
+    stamp(T_ROUTER);
+    f32x4 sc[2];
+    if (!gather(n_rt, sc)) return false;
+    stamp(T_GATHER);
+    route_rows(sc, bias);
+    stamp(T_ROUTE);
+    __builtin_amdgcn_s_waitcnt(0);  // the gather's DMA into LDS (and the scale stores) done
     __syncthreads();
-    stamp(T_QUANT);
+    // a shared-expert tile needs no plan: its loads go out before the plan is built
+    if ((int)blockIdx.x < NT) load_task(K_UP, blockIdx.x);
+    plan_from_picks<E, TOPK, FT>(L.plan, S);
+    stamp(T_PLAN);
     return tasks();
   }
 
@@ -213,97 +215,184 @@ class Step {
   i32x8 W[14];  // weights of the next task: an up tile (14) or a down task (8)
   float SC[2 * UP_KBW];  // an up tile's block scales (gate, up a k block), read with each half
 
-  // ---------------------------------------------------------------- norm
-  // Wave w reads row w (lane: 8 consecutive k of each 512) into registers, which it
-  // keeps for the quantisation; row w + 8 is read for its statistics.
-  MONO_DEV void norm_stats(u32x4 (&ar)[PER_ROW]) {
-    const uint16_t* row0 = A.a + (size_t)min(wave, S - 1) * H;
+  // ---------------------------------------------------------------- router
+  // Router task t: experts RT_E (t % RT_EG) .. + RT_E - 1 over rows RT_S (t / RT_EG) ..;
+  // wave w holds k chunks w and w + 8 (lane l: k = 512 j + 8 l .. + 7), the waves past
+  // the last chunk load chunk RCH - 1 again and drop it.
+  MONO_DEV static int chunk_k(int wv, int c, int ln) { return 512 * min(wv + FW * c, RCH - 1) + 8 * ln; }
+
+  MONO_DEV void router_load(int t, u32x4 (&wr)[RT_E][2], u32x4 (&gr)[2]) {
+    const int eg = t % RT_EG;
 #pragma unroll
-    for (int j = 0; j < PER_ROW; ++j) ar[j] = ld_u32x4(row0 + (j * WAVE + lane) * 8);
-    if (wave + FW < S) {
-      u32x4 w[PER_ROW];
-      const uint16_t* row = A.a + (size_t)(wave + FW) * H;
+    for (int c = 0; c < 2; ++c) {
+      const int k = chunk_k(wave, c, lane);
+      gr[c] = ld_u32x4(A.g_post + k);
 #pragma unroll
-      for (int j = 0; j < PER_ROW; ++j) w[j] = ld_u32x4(row + (j * WAVE + lane) * 8);
-      row_rstd(wave + FW, w);
+      for (int e = 0; e < RT_E; ++e) wr[e][c] = ld_nt_u32x4(A.w_router + (size_t)(RT_E * eg + e) * H + k);
     }
-    if (wave < S) row_rstd(wave, ar);
   }
 
-  MONO_DEV void row_rstd(int s, const u32x4 (&w)[PER_ROW]) {
-    float ss = 0.f;
+  MONO_DEV void router_task(int t, const u32x4 (&wr)[RT_E][2], const u32x4 (&gr)[2]) {
+    const int eg = t % RT_EG, s0 = (t / RT_EG) * RT_S;
+    const bool two = wave + FW < RCH;  // wave-uniform: the wave's second chunk is a real one
+    u32x4 av[RT_S][2];
 #pragma unroll
-    for (int j = 0; j < PER_ROW; ++j)
+    for (int si = 0; si < RT_S; ++si)
+#pragma unroll
+      for (int c = 0; c < 2; ++c) av[si][c] = ld_u32x4(A.a + (size_t)min(s0 + si, S - 1) * H + chunk_k(wave, c, lane));
+    // sums of squares: the waves' in LDS, added in wave order
+    float rstd[RT_S];
+#pragma unroll
+    for (int si = 0; si < RT_S; ++si) {
+      float ss = 0.f;
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const bf16x2 v = as_bf16x2(av[si][c][q]);
+          ss = (c == 0 || two) ? __builtin_amdgcn_fdot2_f32_bf16(v, v, ss, false) : ss;
+        }
+      ss = wave_sum(ss);
+      if (lane == 0) L.rt.rss[wave][si] = ss;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int si = 0; si < RT_S; ++si) {
+      float ss = 0.f;
+#pragma unroll
+      for (int w = 0; w < FW; ++w) ss += L.rt.rss[w][si];
+      rstd[si] = hw_rsq(ss * (1.0f / H) + A.eps);
+    }
+    if (t == (int)blockIdx.x) stamp(T_NORM);
+    // the task's FP8 chunk: row s0 + cu / RCH, chunk cu % RCH (eg < RT_S RCH only)
+    const int cu = eg < RT_S * RCH ? eg : -1;
+    float acc[RT_E][RT_S];
+#pragma unroll
+    for (int e = 0; e < RT_E; ++e)
+#pragma unroll
+      for (int si = 0; si < RT_S; ++si) acc[e][si] = 0.f;
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      if (c == 1 && !two) break;
+      float gf[8];
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const float lo = bf16_lo(w[j][q]), hi = bf16_hi(w[j][q]);
-        ss += lo * lo + hi * hi;
+        gf[2 * q] = bf16_lo(gr[c][q]);
+        gf[2 * q + 1] = bf16_hi(gr[c][q]);
       }
-    ss = wave_sum(ss);
-    if (lane == 0) L.rstd[s] = hw_rsq(ss * (1.0f / H) + A.eps);
+#pragma unroll
+      for (int si = 0; si < RT_S; ++si) {
+        // bf16(a * rstd * gamma): the router's operand (stage_x_rmsnorm, kernel.py:1367-1400)
+        float x[8];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          x[2 * q] = bf16_lo(av[si][c][q]) * rstd[si] * gf[2 * q];
+          x[2 * q + 1] = bf16_hi(av[si][c][q]) * rstd[si] * gf[2 * q + 1];
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const bf16x2 xb = as_bf16x2(pack_bf16x2(x[2 * q], x[2 * q + 1]));
+#pragma unroll
+          for (int e = 0; e < RT_E; ++e)
+            acc[e][si] = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(wr[e][c][q]), xb, acc[e][si], false);
+        }
+        if (cu == si * RCH + wave + FW * c && s0 + si < S) quant_chunk(s0 + si, wave + FW * c, x);
+      }
+    }
+    // logits: each 16-lane row's sum by DPP, then the 4 rows of the 8 waves in LDS, added
+    // in a fixed order
+#pragma unroll
+    for (int e = 0; e < RT_E; ++e)
+#pragma unroll
+      for (int si = 0; si < RT_S; ++si) {
+        const float v = row_reduce<16>(acc[e][si], OpAdd());
+        if (r == 0) L.rt.rlg[wave][g][e * RT_S + si] = v;
+      }
+    __syncthreads();
+    if (tid < RT_E * RT_S) {
+      const int e = tid / RT_S, s = s0 + tid % RT_S;
+      float lg = 0.f;
+#pragma unroll
+      for (int w = 0; w < FW; ++w)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) lg += L.rt.rlg[w][q][tid];
+      if (s < S) st_dev(&A.mail.score[s * E + RT_E * eg + e], sigmoid(lg));
+    }
+    // the done word once every word of the task is stored
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    put_done(A.mail.rdone, t, gd.tag);
   }
 
-  // ---------------------------------------------------------------- router
-  MONO_DEV void router_load(int t, u32x4 (&wr)[RSTEP]) {
-    const int et = t % (E / 16), ks = t / (E / 16);
-    const uint16_t* wrow = A.w_router + (size_t)(et * 16 + r) * H + ks * (H / RK) + wave * RKW + g * 8;
+  // Chunk j of row s (the wave's 8 normed values a lane, f32) per 128 to FP8: a lane's
+  // 8 bytes and the 16-lane block's scale, device-coherent (read after the done word).
+  MONO_DEV void quant_chunk(int s, int j, const float (&x)[8]) {
+    float m = 0.f;
 #pragma unroll
-    for (int st = 0; st < RSTEP; ++st) wr[st] = ld_nt_u32x4(wrow + st * 32);
+    for (int q = 0; q < 8; ++q) m = fmaxf(m, fabsf(x[q]));
+    const float amax = group_max<16>(m);
+    const bool nz = amax > 0.f;
+    const float inv = nz ? hw_rcp(amax) * FP8_MAX : 1.0f;
+    uint32_t packed[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      float q4[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) q4[q] = fminf(fmaxf(x[4 * h + q] * inv, -FP8_MAX), FP8_MAX);
+      packed[h] = fp8x4_pack(q4[0], q4[1], q4[2], q4[3]);
+    }
+    const u32x2 v = {packed[0], packed[1]};
+    __builtin_amdgcn_raw_buffer_store_b64(v, coherent_rsrc(A.mail.xq, MAX_ROWS * H), s * H + 512 * j + 8 * lane, 0, SC1);
+    if (r == 0) st_dev(&A.mail.xs[s * KB + 4 * j + g], nz ? amax * (1.0f / FP8_MAX) : 1.0f);
   }
 
-  MONO_DEV void router(int t, const u32x4 (&wr)[RSTEP]) {
-    const int et = t % (E / 16), ks = t / (E / 16);
-    // columns r >= S compute on row S - 1 and are dropped: every load unconditional
-    const int rr = min(r, S - 1);
-    const float rj = L.rstd[rr];
-    const uint16_t* arow = A.a + (size_t)rr * H;
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  // ---------------------------------------------------------------- gather
+  // Once every router task's done word carries the tag: the step's FP8 rows into LDS by
+  // DMA (global_load_lds: no registers), their block scales, and wave w's rows' scores
+  // (row w, and w + 8 when S > 8) into registers, lane l experts 4 l .. 4 l + 3. Plain
+  // cached loads: nothing reads these lines in the launch before the done words, so no
+  // cache holds an older copy, and the XCD's workgroups share its L2 for them. The
+  // caller waits for the DMA (s_waitcnt 0) and meets the workgroup's barrier before
+  // reading the rows in LDS.
+  MONO_DEV bool gather(int n_rt, f32x4 (&sc)[2]) {
+    const uint64_t* rd = done_copy(A.mail.rdone);
+    if (!hint_wait(n_rt, [rd](int i) { return rd + i; }, site0 + W_ROUTER, gd)) return false;
 #pragma unroll
-    for (int st = 0; st < RSTEP; ++st) {
-      const int k = ks * (H / RK) + wave * RKW + st * 32 + g * 8;
-      acc = mfma_bf16(__builtin_bit_cast(bf16x8, wr[st]), normed8(arow + k, A.g_post + k, rj), acc);
-    }
-    L.red[0][wave][lane] = acc;
-    __syncthreads();
-    if (tid < 256) {
-      const int l = tid % WAVE, i = tid / WAVE;
-      float v = 0.f;
+    for (int k = 0; k < 2; ++k)
+      sc[k] = *reinterpret_cast<const f32x4*>(&A.mail.score[min(wave + FW * k, S - 1) * E + 4 * lane]);
+    float xsv[2];
 #pragma unroll
-      for (int w = 0; w < FW; ++w) v += L.red[0][w][l][i];
-      const int s = l % 16, e = et * 16 + 4 * (l / 16) + i;
-      if (s < S) mb_putf(&A.mail.rlog[((size_t)ks * MAX_ROWS + s) * E + e], v, gd.tag);
+    for (int k = 0; k < 2; ++k) xsv[k] = A.mail.xs[min(tid + FT * k, S * KB - 1)];
+    // 16 bytes a lane, a wave's 64 lanes one contiguous KB in both places
+    const int n_xq = S * H / (16 * WAVE);  // wave-sized copies
+    for (int c = wave; c < n_xq; c += FW)
+      __builtin_amdgcn_global_load_lds(A.mail.xq + 16 * (WAVE * c + lane), &L.xq[0][0] + 16 * WAVE * c, 16, 0, 0);
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int i = tid + FT * k, kb = i % KB;
+      if (i < S * KB) L.xs[i / KB][kb / UP_KBW][kb % UP_KBW] = xsv[k];
     }
-    __syncthreads();
+    return true;
   }
 
   // ---------------------------------------------------------------- route
-  MONO_DEV bool route(int s) {
-    bool ok = true;
-    const float bias = A.bias[min(tid, E - 1)];  // before the wait: no round trip after it
-    if (tid < E) {
-      const uint64_t* base = &A.mail.rlog[(size_t)s * E + tid];
-      uint32_t v[RK];
-      const auto at = [base](int ks) { return base + (size_t)ks * MAX_ROWS * E; };
-      ok = poll_words<RK, decltype(at), false, false>(at, v, (1u << RK) - 1u, site0 + W_LOGITS, gd);
-      float lg = 0.f;
+  // Wave w routes row w (and w + 8) from its scores in registers: the top-TOPK of
+  // (score + bias) -> the plan's picks; workgroup 0 also writes the debug outputs.
+  MONO_DEV void route_rows(const f32x4 (&sc)[2], const float (&bias)[4]) {
 #pragma unroll
-      for (int ks = 0; ks < RK; ++ks) lg += __uint_as_float(v[ks]);
-      const float raw = sigmoid(lg);
-      L.rraw[tid] = raw;
-      L.rkey[tid] = radix_key(raw + bias);
-      if (A.scores && ok) A.scores[s * E + tid] = raw;
-    }
-    if (!block_all(ok)) return false;
-    if (wave == 0) {
+    for (int k = 0; k < 2; ++k) {
+      const int s = wave + FW * k;
+      if (s >= S) break;  // wave-uniform
       uint32_t key[4];
       int id[4];
       float raw[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        id[i] = lane + 64 * i;
-        key[i] = L.rkey[id[i]];
-        raw[i] = L.rraw[id[i]];
+        id[i] = 4 * lane + i;
+        raw[i] = sc[k][i];
+        key[i] = radix_key(raw[i] + bias[i]);
       }
+      if (A.scores && blockIdx.x == 0) *reinterpret_cast<f32x4*>(&A.scores[s * E + 4 * lane]) = sc[k];
       float my_raw;  // lane k < TOPK: the raw score and id of pick k
       int my_id;
       wave_topk<TOPK>(key, id, raw, E, my_id, my_raw);
@@ -312,70 +401,15 @@ class Step {
       tot = row_reduce<TOPK>(tot, OpAdd());
       const float w = my_raw * (hw_rcp(tot) * A.route_scale);
       if (lane < TOPK) {
-        mb_put(&A.mail.rsel[s * 2 * MAX_TOPK + lane], (uint32_t)my_id, gd.tag);
-        mb_putf(&A.mail.rsel[s * 2 * MAX_TOPK + MAX_TOPK + lane], w, gd.tag);
-        if (A.topk_ids) A.topk_ids[s * TOPK + lane] = my_id;
-        if (A.topk_w) A.topk_w[s * TOPK + lane] = w;
+        L.plan.pick_id[s][lane] = my_id;
+        L.plan.pick_w[s][lane] = w;
+        if (blockIdx.x == 0) {
+          if (A.topk_ids) A.topk_ids[s * TOPK + lane] = my_id;
+          if (A.topk_w) A.topk_w[s * TOPK + lane] = w;
+        }
       }
     }
-    return true;
   }
-
-  // ---------------------------------------------------------------- xq
-  // Lane quantises 8 consecutive k of a row; 16 lanes make a 128-block. Row w comes
-  // from the registers the norm filled; row w + 8 is read again.
-  MONO_DEV void quant_rows(u32x4 (&ar)[PER_ROW]) {
-    static_assert(MAX_ROWS <= 2 * FW, "two rows a wave at most");
-    u32x4 gr[PER_ROW];
-#pragma unroll
-    for (int j = 0; j < PER_ROW; ++j) gr[j] = ld_u32x4(A.g_post + (j * WAVE + lane) * 8);
-    if (wave < S) quant_row(wave, ar, gr);
-    if (wave + FW < S) {
-      const uint16_t* row = A.a + (size_t)(wave + FW) * H;
-#pragma unroll
-      for (int j = 0; j < PER_ROW; ++j) {
-        ar[j] = ld_u32x4(row + (j * WAVE + lane) * 8);
-        // gamma's bf16 -> f32 unpacking is redone for this row: shared with the first
-        // row it would hold twice gamma's registers
-        asm volatile("" : "+v"(gr[j]));
-      }
-      quant_row(wave + FW, ar, gr);
-    }
-  }
-
-  MONO_DEV void quant_row(int s, const u32x4 (&av)[PER_ROW], const u32x4 (&gv)[PER_ROW]) {
-    const float rj = L.rstd[s];
-#pragma unroll
-    for (int j = 0; j < PER_ROW; ++j) {
-      const int k = (j * WAVE + lane) * 8;
-      float x[8];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        x[2 * q] = bf16_lo(av[j][q]) * rj * bf16_lo(gv[j][q]);
-        x[2 * q + 1] = bf16_hi(av[j][q]) * rj * bf16_hi(gv[j][q]);
-      }
-      float m = 0.f;
-#pragma unroll
-      for (int q = 0; q < 8; ++q) m = fmaxf(m, fabsf(x[q]));
-      const float amax = group_max<16>(m);
-      const bool nz = amax > 0.f;
-      const float inv = nz ? hw_rcp(amax) * FP8_MAX : 1.0f;
-      u32x2 packed;
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        float q4[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) q4[q] = fminf(fmaxf(x[4 * h + q] * inv, -FP8_MAX), FP8_MAX);
-        packed[h] = fp8x4_pack(q4[0], q4[1], q4[2], q4[3]);
-      }
-      *reinterpret_cast<u32x2*>(&L.xq[s][k]) = packed;
-      if ((lane % 16) == 0) L.xs[s][k / 128] = nz ? amax * (1.0f / FP8_MAX) : 1.0f;
-      __builtin_amdgcn_sched_barrier(0);  // one chunk at a time: no interleaved live ranges
-    }
-  }
-
-  // ---------------------------------------------------------------- plan
-  MONO_DEV bool load_plan() { return build_plan<E, TOPK, FT>(L.plan, A.mail.rsel, S, site0 + W_PICKS, gd); }
 
   // ---------------------------------------------------------------- task list
   // kind of task T (the plan is loaded); K_NONE past the list
@@ -405,11 +439,7 @@ class Step {
   // Each turn: consume the task's weights (waiting on its inputs), issue the next
   // task's weight loads, then publish the task's results while those loads fly.
   MONO_DEV bool tasks() {
-    int T = blockIdx.x;
-    // a shared-expert tile needs no plan: its loads go out before the plan is read
-    if (T < NT) load_task(K_UP, T);
-    if (!load_plan()) return false;
-    stamp(T_PLAN);
+    int T = blockIdx.x;  // a shared-expert tile's loads (T < NT) went out before the plan
     int kind = classify(T);
     if (T >= NT) load_task(kind, T);
     // consecutive up tiles, half by half: the next tile's first half goes out once this
@@ -490,11 +520,13 @@ class Step {
   template <int HALF>
   MONO_DEV void up_half(f32x4& ag, f32x4& au) {
     constexpr int J0 = HALF == 0 ? 0 : UP_H0, J1 = HALF == 0 ? UP_H0 : UP_KBW;
+    static_assert(UP_H0 == 4 && UP_KBW <= 8, "a half's activation scales are one 16-byte read");
+    const f32x4 xs4 = *reinterpret_cast<const f32x4*>(&L.xs[r][wave][4 * HALF]);
 #pragma unroll
     for (int j = J0; j < J1; ++j) {
       const int kb = wave * UP_KBW + j;
       const i32x8 b = lds32(&L.xq[r][kb * 128 + g * 32]);
-      const float xsj = L.xs[r][kb];
+      const float xsj = xs4[j - J0];
       const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
       const f32x4 cg = mfma_fp8(W[2 * j], b, zero);
       const f32x4 cu = mfma_fp8(W[2 * j + 1], b, zero);

@@ -22,8 +22,6 @@ struct MoeFp8Args : mono_moe_fp8_args {
 };
 
 bool moe_fp8_supported(const MoeGeom& geo);
-// Router K slices of the FP8 kernel (rows of the rlog mailbox).
-int moe_fp8_router_slices();
 // Workgroups of the persistent launch that fit on one CU (must be >= 1).
 hipError_t moe_fp8_occupancy(int* blocks_per_cu);
 // Enqueue the one persistent launch on `st` with `grid` workgroups (one a CU).

@@ -14,8 +14,11 @@ constexpr int MAX_TOPK = 8;
 // Mailboxes of one MoE runtime (tagged 64-bit words, see sync.h), sized for the
 // runtime's max_rows: at most max_act = min(max_rows * top_k, E) + 1 expert slots.
 struct Mail {
-  uint64_t* rlog;   // [RK][MAX_ROWS][E]     router partial logits, one K slice each
-  uint64_t* rsel;   // [MAX_ROWS][2 * TOPK]  a row's picks: ids, then weights
+  // the FP8 kernel's router tasks' outputs: plain data behind their done words
+  float* score;     // [MAX_ROWS][E]       routing scores
+  uint8_t* xq;      // [MAX_ROWS][H]       the normed rows in FP8
+  float* xs;        // [MAX_ROWS][H / 128] their block scales
+  uint64_t* rdone;  // DONE_BYTES: router task t's done word, replicated
   uint64_t* mid;    // [max_act][MAX_ROWS][I]  silu(gate) * up, f32
   uint64_t* ypart;  // [max_act][MAX_ROWS][H]  an expert's weighted down output, f32
   uint32_t* guard;  // [G_WORDS]
