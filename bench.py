@@ -59,10 +59,13 @@ def cpu_model() -> str:
     return platform.processor() or "unknown"
 
 
-def time_steps(args, dev, step):
-    """``args.warmup`` untimed calls of ``step(i)``, then ``args.steps`` timed ones
-    bracketed by synchronisations, a HIP event on the launch stream after each.
-    Returns (per-step us, mean us, wall s)."""
+def time_steps(args, dev, step, reps: int = 5):
+    """``args.warmup`` untimed calls of ``step(i)``; then the next ``args.steps`` calls
+    captured in one HIP graph (the launches run back to back, with no host work between
+    them) and the graph replayed ``reps`` times, each replay bracketed by HIP events on
+    the launch stream. Falls back to timing the calls eagerly (an event after each) when
+    the capture fails. Returns (per-replay us a step, mean us a step, wall s a replay,
+    how it was timed)."""
     import torch
 
     log(f"warmup {args.warmup} steps")
@@ -70,18 +73,33 @@ def time_steps(args, dev, step):
         step(i)
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream(dev)
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
-    log(f"timing {args.steps} steps")
+    graph = torch.cuda.CUDAGraph()
+    try:
+        with torch.cuda.graph(graph):
+            for i in range(args.steps):
+                step(args.warmup + i)
+        torch.cuda.synchronize()
+        graph.replay()  # untimed
+        torch.cuda.synchronize()
+    except RuntimeError as e:  # pragma: no cover - a path that cannot be captured
+        log(f"graph capture failed ({e}); timing eager launches")
+        graph = None
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
+    log(f"timing {reps} x {args.steps} steps" + (" (graph replays)" if graph is not None else " (eager)"))
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     ev[0].record(stream)
-    for i in range(args.steps):
-        step(args.warmup + i)
-        ev[i + 1].record(stream)
+    for k in range(reps):
+        if graph is not None:
+            graph.replay()
+        else:
+            for i in range(args.steps):
+                step(args.warmup + i)
+        ev[k + 1].record(stream)
     torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    per = [ev[i].elapsed_time(ev[i + 1]) * 1e3 for i in range(args.steps)]
-    return per, ev[0].elapsed_time(ev[-1]) * 1e3 / args.steps, wall
+    wall = (time.perf_counter() - t0) / reps
+    per = [ev[k].elapsed_time(ev[k + 1]) * 1e3 / args.steps for k in range(reps)]
+    return per, statistics.fmean(per), wall, ("graph" if graph is not None else "eager")
 
 
 # ------------------------------------------------------------------ FP8 MoE (config 2)
@@ -122,14 +140,14 @@ def bench_moe_fp8(args, dev):
         wi, ai = pair(i)
         rt.forward_fp8(acts[ai], wsets[wi], out=out)
 
-    per, us, wall = time_steps(args, dev, step)
+    per, us, wall, how = time_steps(args, dev, step)
     rt.check_errors()
 
     exp_b = fp8_expert_bytes(G)
     fixed = E * H * 2 + E * 4 + H * 2 + 2 * S * H * 2  # router, bias, norm weight, a in + out
     step_bytes = [distinct[pair(args.warmup + i)] * exp_b + fixed for i in range(args.steps)]
     mean_bytes = statistics.fmean(step_bytes)
-    achieved = statistics.fmean(b / (t * 1e-6) for b, t in zip(step_bytes, per)) / 1e9  # GB/s
+    achieved = mean_bytes / (us * 1e-6) / 1e9  # GB/s
     d_mean = statistics.fmean(distinct[pair(args.warmup + i)] for i in range(args.steps))
     log(f"{us:.2f} us/step (median {statistics.median(per):.2f}), {achieved:.0f} GB/s, "
         f"{d_mean:.1f} distinct experts, wall {wall:.3f} s")
@@ -146,7 +164,7 @@ def bench_moe_fp8(args, dev):
         config=dict(
             workload="BASELINE config 2: FP8 routed MoE decode, one GPU's TP=4 share",
             rows=S, hidden=H, experts=E, top_k=G.top_k, shared_experts=1, inter=G.inter,
-            weight_sets=len(wsets), activation_batches=len(acts), combos=n_combo,
+            weight_sets=len(wsets), activation_batches=len(acts), combos=n_combo, timed=how,
         ),
         extra=dict(
             us_median=statistics.median(per), us_min=min(per), us_max=max(per),
@@ -252,14 +270,14 @@ def bench_moe_mxfp4(args, dev):
         wi, ai = pair(i)
         rt.forward_mxfp4(acts[ai], lgts[ai], wsets[wi], out=out)
 
-    per, us, wall = time_steps(args, dev, step)
+    per, us, wall, how = time_steps(args, dev, step)
     rt.check_errors()
 
     exp_b = mxfp4_expert_bytes(G)
     fixed = S * E * 4 + 2 * S * H * 2  # logits, x in + out
     step_bytes = [distinct[pair(args.warmup + i)[1]] * exp_b + fixed for i in range(args.steps)]
     mean_bytes = statistics.fmean(step_bytes)
-    achieved = statistics.fmean(b / (t * 1e-6) for b, t in zip(step_bytes, per)) / 1e9
+    achieved = mean_bytes / (us * 1e-6) / 1e9
     d_mean = statistics.fmean(distinct[pair(args.warmup + i)[1]] for i in range(args.steps))
     log(f"{us:.2f} us/step (median {statistics.median(per):.2f}), {achieved:.0f} GB/s, "
         f"{d_mean:.1f} distinct experts, wall {wall:.3f} s")
@@ -276,7 +294,7 @@ def bench_moe_mxfp4(args, dev):
         config=dict(
             workload="BASELINE config 4: MXFP4 A16W4 routed MoE decode, one GPU's TP=4 share",
             rows=S, hidden=H, experts=E, top_k=G.top_k, shared_experts=1, inter=G.inter,
-            weight_sets=len(wsets), activation_batches=len(acts),
+            weight_sets=len(wsets), activation_batches=len(acts), timed=how,
         ),
         extra=dict(
             us_median=statistics.median(per), us_min=min(per), us_max=max(per),
@@ -366,22 +384,14 @@ def bench_attn(args, dev):
     cases = [workloads.attn_case(lens, dev, seed=3000 + i) for i in range(sets)]
     rt = AttnRuntime(S, max(ctx, 1024), device=dev)
     out = torch.empty(S, 32, 512, dtype=torch.bfloat16, device=dev)
-    for i in range(args.warmup):
+
+    def step(i):
         st, ca = cases[i % sets]
         rt.forward(st, ca, out=out)
-    torch.cuda.synchronize()
-    stream = torch.cuda.current_stream(dev)
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
-    ev[0].record(stream)
-    for i in range(args.steps):
-        st, ca = cases[(args.warmup + i) % sets]
-        rt.forward(st, ca, out=out)
-        ev[i + 1].record(stream)
-    torch.cuda.synchronize()
+
+    per, us, wall, how = time_steps(args, dev, step)
     rt.check_errors()
-    per = [ev[i].elapsed_time(ev[i + 1]) * 1e3 for i in range(args.steps)]
-    us = ev[0].elapsed_time(ev[-1]) * 1e3 / args.steps
-    achieved = step_b / (statistics.fmean(per) * 1e-6) / 1e9
+    achieved = step_b / (us * 1e-6) / 1e9
     log(f"{us:.2f} us/step (median {statistics.median(per):.2f}), {achieved:.0f} GB/s")
     cpu = None
     if args.cpu_seconds > 0:
@@ -390,7 +400,7 @@ def bench_attn(args, dev):
     return dict(
         value=us, unit="us", ms_per_step=us / 1e3, dtype="fp4_e2m1 scores, fp8_e4m3 kv (bf16 MFMA, f32 accumulate)",
         config=dict(workload="BASELINE config 3: sparse MLA decode with FP4 indexer top-2048", rows=S,
-                    context=ctx, heads=32, index_heads=64, topk=2048, cache_sets=sets),
+                    context=ctx, heads=32, index_heads=64, topk=2048, cache_sets=sets, timed=how),
         extra=dict(us_median=statistics.median(per), us_min=min(per), us_max=max(per),
                    rows_per_s=S / (us * 1e-6), algorithmic_bytes=step_b),
         roofline=dict(bound="hbm", achieved=achieved, peak=HBM_PEAK_GBS, unit="GB/s", frac=achieved / HBM_PEAK_GBS,
@@ -474,12 +484,25 @@ def bench_layer(args, dev):
     rt = LayerRuntime(S, ctx, dev, mode=args.mode)
     x_in = workloads.rows_bf16(S, 7168, dev, seed=5)
     xb = [torch.empty_like(x_in), torch.empty_like(x_in)]
+    # --routing uniform: every layer takes its own independent random rows instead of the
+    # previous layer's output, and its router bias is zeroed (the synthetic bias, ~N(0,
+    # 0.1), outweighs the spread of the top scores, which sit near 1, and sends every row
+    # to the same experts), so the rows route independently: about 57.4 distinct experts
+    # of 256 at 8 rows x top-8, the traffic of uniform routing
+    own_rows = None
+    if args.routing == "uniform":
+        own_rows = [workloads.rows_bf16(S, 7168, dev, seed=5 + l) for l in range(L)]
+        for w, _, _ in layers:
+            w.moe.bias.zero_()
+
+    def layer_in(l, x):
+        return x if own_rows is None else own_rows[l]
 
     def run_step(marks=None):
         x = x_in
         for l, (w, step, caches) in enumerate(layers):
             hook = None if marks is None else (lambda i, l=l: marks(l, i))
-            x = rt.forward(x, step.seq_lens, step.page_table, caches, w, cos, sin, out=xb[l % 2],
+            x = rt.forward(layer_in(l, x), step.seq_lens, step.page_table, caches, w, cos, sin, out=xb[l % 2],
                            check_weights=False, on_phase=hook)
         return x
 
@@ -488,7 +511,8 @@ def bench_layer(args, dev):
     x = x_in
     for l, (w, step, caches) in enumerate(layers):
         w.proj.check(rt.device)
-        x, it = rt.forward(x, step.seq_lens, step.page_table, caches, w, cos, sin, out=xb[l % 2], keep=True)
+        x, it = rt.forward(layer_in(l, x), step.seq_lens, step.page_table, caches, w, cos, sin, out=xb[l % 2],
+                           keep=True)
         distinct.append(len(set(it["topk_ids"].flatten().tolist())) + 1)
     torch.cuda.synchronize()
     rt.check_errors()
@@ -533,7 +557,7 @@ def bench_layer(args, dev):
         x = x_in
         for l, (w, step, caches) in enumerate(layers):
             pev[k][l][0].record(stream)
-            x = rt.forward(x, step.seq_lens, step.page_table, caches, w, cos, sin, out=xb[l % 2],
+            x = rt.forward(layer_in(l, x), step.seq_lens, step.page_table, caches, w, cos, sin, out=xb[l % 2],
                            check_weights=False, on_phase=lambda i, l=l, k=k: pev[k][l][i + 1].record(stream))
     torch.cuda.synchronize()
     rt.check_errors()
@@ -555,7 +579,7 @@ def bench_layer(args, dev):
             x = x_in
             for l, (w, step, caches) in enumerate(layers):
                 lev[k][l][0].record(stream)
-                x = rt.forward(x, step.seq_lens, step.page_table, caches, w, cos, sin, out=xb[l % 2],
+                x = rt.forward(layer_in(l, x), step.seq_lens, step.page_table, caches, w, cos, sin, out=xb[l % 2],
                                check_weights=False)
                 lev[k][l][1].record(stream)
         torch.cuda.synchronize()
@@ -572,7 +596,7 @@ def bench_layer(args, dev):
         for k in range(n_eager):
             x = x_in
             for l, (w, step, caches) in enumerate(layers):
-                x = rt.forward(x, step.seq_lens, step.page_table, caches, w, cos, sin, out=xb[l % 2],
+                x = rt.forward(layer_in(l, x), step.seq_lens, step.page_table, caches, w, cos, sin, out=xb[l % 2],
                                check_weights=False, ticks=ticks[k, l])
         torch.cuda.synchronize()
         rt.check_errors()
@@ -624,7 +648,9 @@ def bench_layer(args, dev):
         dtype="fp8_e4m3 weights (bf16 / fp8 MFMA, f32 accumulate), fp4 index, fp8 kv",
         config=dict(workload="BASELINE config 5: full fused decoder layer, one GPU's TP=4 share, 61 stacked layers",
                     rows=S, context=ctx, layers=L, hidden=7168, heads=32, experts=256, top_k=8, shared_experts=1,
-                    inter=512, launches_per_layer=rt.launches, graph=True),
+                    inter=512, launches_per_layer=rt.launches, graph=True,
+                    routing=("uniform: each layer's own independent random rows, router bias 0" if own_rows is not None
+                             else "chained: each layer's rows are the previous layer's output")),
         extra=dict(
             us_per_layer_median=statistics.median(per) / L, us_per_layer_min=min(per) / L,
             us_per_layer_max=max(per) / L, rows_per_s=S / (us * 1e-6), step_wall_s=wall / args.steps,
@@ -806,6 +832,8 @@ def main() -> int:
     ap.add_argument("--rows", type=int, default=8)
     ap.add_argument("--workload", choices=sorted(WORKLOADS), default="layer")
     ap.add_argument("--layers", type=int, default=61, help="stacked layers (layer workload)")
+    ap.add_argument("--routing", choices=("chained", "uniform"), default="chained",
+                    help="layer workload: rows chained through the layers, or independent rows a layer")
     ap.add_argument("--mode", choices=("layer", "attn_back", "split"), default="layer",
                     help="layer workload: the launch split (layer: front + one fused launch of attention, back "
                          "and MoE; attn_back: three launches; split: four)")
