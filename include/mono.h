@@ -377,9 +377,9 @@ typedef struct {
    * s_memrealtime tick (100 MHz) at which it [0] began, finished its [1] front tasks,
    * [2] attention tasks, [3] back tasks, [4] had the MoE's expert plan, [5] finished;
    * and the MoE prologue's moments: [6] the attention block's output seen, [7] its
-   * norm statistics, [8] its router task done, [9] its route done (the last `rows`
-   * workgroups only), [10] the rows quantised; the rest 0. The reference's per-CTA
-   * stamps (common/stamps.py:24-33). */
+   * first router task's norm statistics, [8] its router tasks done, [9] the router
+   * outputs gathered, [10] its rows routed; the rest 0. The reference's per-CTA stamps
+   * (common/stamps.py:24-33). */
   int64_t* ticks;
 } mono_layer_args;
 
