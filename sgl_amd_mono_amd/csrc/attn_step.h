@@ -80,7 +80,10 @@ struct TopkLds {
 
 struct SplitLds {
   uint16_t q[NH][Q_STRIDE];
-  uint32_t kvb[SUB * KVW];  // the sub-tile's rows widened to bf16, swizzled (kv_at)
+  union {
+    uint32_t kvb[SUB * KVW];     // the sub-tile's rows widened to bf16, swizzled (kv_at)
+    u32x4 kvb4[SUB * KVW / 4];   // the same as 16-byte groups (kv_at16 / 4): b128 accesses
+  };
   float pf[NH][SUB];
   uint16_t pb[NH][PB_STRIDE];
   int32_t slot[SPLIT];
@@ -151,6 +154,11 @@ MONO_DEV f32x4 mfma_fp4_opb(const u32x4& a, const u32x4& b, int sa, int sb) {
 // their dword index by 8 so a p.v column's 4 lane groups hit different banks; 4-dword
 // groups stay contiguous and aligned for the q.k reads.
 MONO_DEV int kv_at(int t, int w) { return t * KVW + (w ^ (((t >> 3) & 3) << 3)); }
+// the 16-byte group of kv_at(t, w) for w a multiple of 4 (KVW and the XOR term are
+// multiples of 4, so the group is whole), as an index of u32x4 groups: accessed
+// through a u32x4 array the group is one b128 LDS access, where a cast of a uint32_t
+// address is split into 4-byte pairs
+MONO_DEV int kv_at16(int t, int w) { return kv_at(t, w) >> 2; }
 
 // 4 E4M3 bytes -> 4 bf16 as 2 dwords (exact: every E4M3 value is a bf16 value)
 MONO_DEV u32x2 fp8x4_bf16(uint32_t w) {
@@ -751,8 +759,8 @@ class Step {
           }
         }
         // dims 16c .. 16c + 15 are dwords 8c .. 8c + 7: one swizzled 8-dword block
-        *reinterpret_cast<u32x4*>(&P.kvb[kv_at(t, 8 * c)]) = lo;
-        *reinterpret_cast<u32x4*>(&P.kvb[kv_at(t, 8 * c) + 4]) = hi;
+        P.kvb4[kv_at16(t, 8 * c)] = lo;
+        P.kvb4[kv_at16(t, 8 * c) + 1] = hi;
       }
     }
     if (tid < SUB) P.kvs[tid] = P.slot[st * SUB + tid] >= 0 ? gs : 0.f;
@@ -829,13 +837,13 @@ class Step {
         f32x4 d0 = {0.f, 0.f, 0.f, 0.f}, d1 = d0;
         const uint16_t* qrow = &P.q[16 * ht + r][8 * g];
         bf16x8 qa = *reinterpret_cast<const bf16x8*>(qrow);
-        bf16x8 kb = *reinterpret_cast<const bf16x8*>(&P.kvb[kv_at(16 * tt + r, 4 * g)]);
+        bf16x8 kb = __builtin_bit_cast(bf16x8, P.kvb4[kv_at16(16 * tt + r, 4 * g)]);
 #pragma unroll
         for (int ks = 0; ks < DQK / 32; ++ks) {
           bf16x8 qn = qa, kn = kb;
           if (ks + 1 < DQK / 32) {
             qn = *reinterpret_cast<const bf16x8*>(qrow + 32 * (ks + 1));
-            kn = *reinterpret_cast<const bf16x8*>(&P.kvb[kv_at(16 * tt + r, 16 * (ks + 1) + 4 * g)]);
+            kn = __builtin_bit_cast(bf16x8, P.kvb4[kv_at16(16 * tt + r, 16 * (ks + 1) + 4 * g)]);
           }
           if (ks % 2 == 0) d0 = mfma_bf16(qa, kb, d0);
           else d1 = mfma_bf16(qa, kb, d1);
