@@ -21,7 +21,12 @@ pytestmark = pytest.mark.gpu
 G = FP8_MOE
 OUT_MAX_ABS, OUT_REL = 2e-2, 1e-2  # the north star's bf16 output bound
 Y_REL = 1e-2  # the MoE sum itself (f32), relative to its norm
-SCORE_ABS = 1e-4  # sigmoid scores: f32 GEMV order differences only
+# Sigmoid scores. The f32 summation order of the RMSNorm's sum of squares can move rstd
+# by an ulp, which flips the bf16 rounding of a normed element lying on a rounding
+# boundary (about one row in five): that moves every logit of the row by |w_k| ulp(x_k)
+# <= 0.08 * 2^-6 (|x_k| < 4, router weights within 3.4 sigma of 2 / sqrt(H)), a score by
+# at most 0.25 of that, 3.1e-4. Without a flip the scores agree to ~1e-6 (GEMV order).
+SCORE_ABS = 4e-4
 
 
 class CpuExperts:
