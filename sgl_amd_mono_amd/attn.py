@@ -65,7 +65,7 @@ class AttnRuntime(Runtime):
     def n_tasks(self, rows: int) -> int:
         """Tasks of one launch over ``rows`` rows (the timeline's length)."""
         n_score = -(-rows * (self.max_ctx // 1024) // 16) * 16  # padded to whole top-k teams
-        return n_score + rows * 16 + rows * SPLITS + rows * (NH // 2)
+        return n_score + rows * 16 + rows * SPLITS + rows * NH
 
     def forward(self, step: AttnStep, caches: AttnCaches, out: torch.Tensor | None = None,
                 debug: bool = False, timeline: torch.Tensor | None = None):
@@ -88,7 +88,7 @@ class AttnRuntime(Runtime):
 def n_tasks(max_ctx: int, rows: int) -> int:
     """Tasks of one attention launch over ``rows`` rows (the timeline's length)."""
     n_score = -(-rows * (max_ctx // 1024) // 16) * 16  # padded to whole top-k teams
-    return n_score + rows * 16 + rows * SPLITS + rows * (NH // 2)
+    return n_score + rows * 16 + rows * SPLITS + rows * NH
 
 
 def attn_args(dev, max_rows: int, max_ctx: int, step: AttnStep, caches: AttnCaches, out: torch.Tensor | None,

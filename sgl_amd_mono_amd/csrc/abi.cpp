@@ -471,7 +471,7 @@ extern "C" int mono_attn_create(const mono_attn_config* cfg, mono_attn** out) {
   const size_t o_part = cv.take(R * SPLITS * NH * DV * 2);
   const size_t o_ml = cv.take(R * SPLITS * NH * 2 * 4);
   const size_t o_sdone = cv.take(R * SPLITS * 8);
-  const size_t o_mdone = cv.take(R * (NH / 2) * 8);
+  const size_t o_mdone = cv.take(R * NH * 8);
   const size_t o_fob = cv.take((size_t)mono::proj::MAX_ROWS * mono::proj::HEADS * mono::proj::VDIM / 2 * 4);
   const size_t o_fodone = cv.take(mono::DONE_BYTES);
   mono_attn* a = new mono_attn();

@@ -42,7 +42,7 @@ struct Mail {
                     //                                 (untagged; read after sdone)
   float* ml;        // [max_rows][SPLITS][NH][2]      a split's max logit and sum (untagged)
   uint64_t* sdone;  // [max_rows][SPLITS]             a split's part and ml are stored
-  uint64_t* mdone;  // [max_rows][NH / 2]             a merge's output is stored (the fused
+  uint64_t* mdone;  // [max_rows][NH]                 a merge's output is stored (the fused
                     //                                 attention + back launch only)
   uint32_t* guard;  // [G_WORDS]
   int max_ctx;

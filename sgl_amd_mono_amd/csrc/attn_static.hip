@@ -50,7 +50,7 @@ constexpr size_t O_PART = O_CNT + al256((size_t)NA_ROWS * TEAM * 2 * 8);
 constexpr size_t O_ML = O_PART + al256((size_t)NA_ROWS * SPLITS * NH * DV * 2);
 constexpr size_t O_SDONE = O_ML + al256((size_t)NA_ROWS * SPLITS * NH * 2 * 4);
 constexpr size_t O_MDONE = O_SDONE + al256((size_t)NA_ROWS * SPLITS * 8);
-constexpr size_t SCRATCH_BYTES = O_MDONE + al256((size_t)NA_ROWS * (NH / 2) * 8);
+constexpr size_t SCRATCH_BYTES = O_MDONE + al256((size_t)NA_ROWS * NH * 8);
 static_assert(SCRATCH_BYTES <= 10u * 1024 * 1024, "the static scratch stays within 10 MiB");
 
 }  // namespace

@@ -30,7 +30,7 @@
 //          p.v, the per-token scale folded into the logit and the probability, online
 //          softmax -> the split's partials (bf16, 32 KB in one contiguous run) and
 //          (m, l), then its done word (mailbox sdone)
-//   merge  (row, 2 heads): once every split of the row is done,
+//   merge  (row, head): once every split of the row is done,
 //          out = sum_j e^(m_j - M) acc_j / sum_j e^(m_j - M) l_j, bf16
 #pragma once
 
@@ -58,7 +58,7 @@ constexpr int KEYS_WAVE = CHUNK / AW;        // 128 keys a wave of a score task
 constexpr int KTILES = KEYS_WAVE / 16;
 constexpr float NEG_INF = -__builtin_huge_valf();
 static_assert(KPM % AT == 0 && PAGE % KPT == 0 && TEAM <= 16 && KEYS_WAVE % PAGE == 0 && SPLIT % SUB == 0, "tiling");
-static_assert(AT == NH * DV / 32, "a merge task covers 2 heads");
+static_assert(AT == NH * DV / 32, "tiling");
 
 enum { W_SCORE = 0, W_SEL = 1, W_PART = 2, W_TEAM = 3 };
 
@@ -92,8 +92,8 @@ struct SplitLds {
 };
 
 struct MergeLds {
-  float w[2][SPLITS];  // each split's weight e^(m_j - M), 0 for an empty split
-  float den[2];        // sum_j w_j l_j
+  float w[SPLITS];  // each split's weight e^(m_j - M), 0 for an empty split
+  float den;        // sum_j w_j l_j
 };
 
 struct Lds {
@@ -199,7 +199,7 @@ class Step {
   // tasks in the list: score tasks padded to a multiple of TEAM so no top-k team
   // straddles a round, then top-k members, splits, merges
   MONO_DEV int n_score() const { return (A.rows * CH + TEAM - 1) / TEAM * TEAM; }
-  MONO_DEV int n_tasks() const { return n_score() + A.rows * TEAM + A.rows * SPLITS + A.rows * (NH / 2); }
+  MONO_DEV int n_tasks() const { return n_score() + A.rows * TEAM + A.rows * SPLITS + A.rows * NH; }
 
   // This workgroup's tasks (false, workgroup-uniform: a wait failed).
   MONO_DEV bool tasks() {
@@ -226,7 +226,7 @@ class Step {
     for (T = first_at_or_after(n_sc + n_topk + n_split); T < total; T += G) {
       const uint64_t t0 = now_ticks();
       const int j = T - n_sc - n_topk - n_split;
-      const bool ok = merge_task(j / (NH / 2), j % (NH / 2));
+      const bool ok = merge_task(j / NH, j % NH);
       stamp(T, t0, 3);
       if (!ok) return false;
     }
@@ -943,10 +943,12 @@ class Step {
   }
 
   // ---------------------------------------------------------------- merge
-  MONO_DEV bool merge_task(int s, int hp) {
-    static_assert(SPLITS <= WAVE, "a lane a split");
+  // Merge (row s, head h): the first 256 threads each combine one channel pair over the
+  // row's splits (a task takes in the head's 32 KB of partials).
+  MONO_DEV bool merge_task(int s, int h) {
+    static_assert(SPLITS <= WAVE && DV == 2 * 256, "a lane a split; a thread a channel pair");
     MergeLds& Q = L.u.mg;
-    const int hh = tid / 256, h = 2 * hp + hh, d0 = (tid % 256) * 2;
+    const int d0 = (tid % 256) * 2;
     const size_t rb = (size_t)s * SPLITS;
     // every split of the row done: lane j of wave 0 polls split j's word
     bool ok = true;
@@ -956,8 +958,8 @@ class Step {
     }
     if (!block_all(ok)) return false;
     mark_waited();
-    // the split weights: lane j of waves 0 and 4 (heads 2 hp, 2 hp + 1) takes split j
-    if (wave % 4 == 0) {
+    // the split weights: lane j of wave 0 takes split j
+    if (wave == 0) {
       const int jl = min(lane, SPLITS - 1);
       const float m = ld_agent_f32(&A.mail.ml[((rb + jl) * NH + h) * 2]);
       const float l = lane < SPLITS ? ld_agent_f32(&A.mail.ml[((rb + jl) * NH + h) * 2 + 1]) : 0.f;
@@ -965,37 +967,42 @@ class Step {
       const float M = wave_max(live ? m : NEG_INF);
       const float w = live ? hw_exp(m - M) : 0.f;
       const float den = wave_sum(w * l);
-      if (lane < SPLITS) Q.w[hh][lane] = w;
-      if (lane == 0) Q.den[hh] = den;
+      if (lane < SPLITS) Q.w[lane] = w;
+      if (lane == 0) Q.den = den;
     }
     // the channel pair of every split (unconditional loads; an empty split's words are
     // read and ignored)
+    const bool mine = tid < 256;  // wave-uniform
     uint32_t av[SPLITS];
+    if (mine) {
 #pragma unroll
-    for (int j = 0; j < SPLITS; ++j)
-      av[j] = ld_agent_u32(reinterpret_cast<const uint32_t*>(&A.mail.part[((rb + j) * NH + h) * DV + d0]));
+      for (int j = 0; j < SPLITS; ++j)
+        av[j] = ld_agent_u32(reinterpret_cast<const uint32_t*>(&A.mail.part[((rb + j) * NH + h) * DV + d0]));
+    }
     __syncthreads();
-    float o[2] = {0.f, 0.f};
+    if (mine) {
+      float o[2] = {0.f, 0.f};
 #pragma unroll
-    for (int j = 0; j < SPLITS; ++j) {
-      const float w = Q.w[hh][j];
-      if (w > 0.f) {
-        o[0] += w * bf16_lo(av[j]);
-        o[1] += w * bf16_hi(av[j]);
+      for (int j = 0; j < SPLITS; ++j) {
+        const float w = Q.w[j];
+        if (w > 0.f) {
+          o[0] += w * bf16_lo(av[j]);
+          o[1] += w * bf16_hi(av[j]);
+        }
+      }
+      const float den = Q.den;
+      const float inv = den > 0.f ? 1.0f / den : 0.f;
+      uint32_t* po = reinterpret_cast<uint32_t*>(A.out + ((size_t)s * NH + h) * DV + d0);
+      const uint32_t ov = pack_bf16x2(o[0] * inv, o[1] * inv);
+      if (A.publish_out) {  // read in this launch: a device-coherent store, complete before the done word
+        __hip_atomic_store(po, ov, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_s_waitcnt(0);
+      } else {
+        *po = ov;
       }
     }
-    const float den = Q.den[hh];
-    const float inv = den > 0.f ? 1.0f / den : 0.f;
-    uint32_t* po = reinterpret_cast<uint32_t*>(A.out + ((size_t)s * NH + h) * DV + d0);
-    const uint32_t ov = pack_bf16x2(o[0] * inv, o[1] * inv);
-    if (A.publish_out) {  // read in this launch: a device-coherent store, complete before the done word
-      __hip_atomic_store(po, ov, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __builtin_amdgcn_s_waitcnt(0);
-    } else {
-      *po = ov;
-    }
     __syncthreads();  // (and the next task may rewrite the LDS weights)
-    if (A.publish_out && tid == 0) mb_put(&A.mail.mdone[(size_t)s * (NH / 2) + hp], 0u, gd.tag);
+    if (A.publish_out && tid == 0) mb_put(&A.mail.mdone[(size_t)s * NH + h], 0u, gd.tag);
     return true;
   }
 };

@@ -67,7 +67,7 @@ class Back {
   MONO_DEV void poison(bool share) const { poison_bf16(A.a, (size_t)S * HIDDEN, share); }
 
   // Run under another launch's guard (a fused launch: its tag, deadline and fail word),
-  // after that launch's attention merges: their done words [rows][HEADS / 2].
+  // after that launch's attention merges: their done words [rows][HEADS].
   MONO_DEV void adopt(const Guard& g, const uint64_t* merge_done) {
     gd = g;
     merged = merge_done;
@@ -126,8 +126,8 @@ class Back {
       SC[j] = W.s_uv[(rg * 16 / 128) * (KV_LORA / 128) + j];
     }
     if (merged) {  // in the same launch as the attention: every row's merge of this head
-      const uint64_t* md = merged + h / 2;
-      if (!hint_wait(S, [md](int i) { return md + (size_t)i * (HEADS / 2); }, W_OLAT, gd)) return false;
+      const uint64_t* md = merged + h;
+      if (!hint_wait(S, [md](int i) { return md + (size_t)i * HEADS; }, W_OLAT, gd)) return false;
     }
     const __amdgpu_buffer_rsrc_t ro = coherent_rsrc(A.o_lat, S * HEADS * KV_LORA * 2);
     for (int f = tid; f < S * (KV_LORA / 8); f += FT) {
