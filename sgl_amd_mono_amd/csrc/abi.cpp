@@ -347,6 +347,7 @@ extern "C" int mono_moe_create(const mono_moe_config* cfg, mono_moe** out) {
   const size_t o_score = cv.take((size_t)MAX_ROWS * E * 4);
   const size_t o_rdone = cv.take(mono::DONE_BYTES);
   const size_t o_mid = cv.take(max_act * MAX_ROWS * I * 8);
+  const size_t o_mtile = cv.take(max_act * (I / 16) * 8);
   const size_t o_ypart = cv.take(max_act * MAX_ROWS * H * 8);
   mono_moe* m = new mono_moe();
   m->magic = MOE_MAGIC;
@@ -362,6 +363,7 @@ extern "C" int mono_moe_create(const mono_moe_config* cfg, mono_moe** out) {
   m->mail.score = reinterpret_cast<float*>(m->at(o_score));
   m->mail.rdone = reinterpret_cast<uint64_t*>(m->at(o_rdone));
   m->mail.mid = reinterpret_cast<uint64_t*>(m->at(o_mid));
+  m->mail.mtile = reinterpret_cast<uint64_t*>(m->at(o_mtile));
   m->mail.ypart = reinterpret_cast<uint64_t*>(m->at(o_ypart));
   *out = m;
   return ok();

@@ -587,6 +587,9 @@ class Step {
         mb_putf(&A.mail.mid[((size_t)d * MAX_ROWS + s) * I + ch], bf16_round(silu(gs[i]) * us[i]), gd.tag);
       }
     }
+    // the tile's done word, after its mid words: a hint for the down tasks' wait (their
+    // poll of the tagged mid words stays the check)
+    if (lane == 0) mb_put(&A.mail.mtile[T], 0u, gd.tag);
   }
 
   // ---------------------------------------------------------------- down
@@ -600,6 +603,10 @@ class Step {
     const uint64_t* b0 = &A.mail.mid[((size_t)d0 * MAX_ROWS + s) * I + c0];
     const uint64_t* b1 = &A.mail.mid[((size_t)d1 * MAX_ROWS + s) * I + c0];
     constexpr uint32_t ALL = (1u << MPT) - 1u;
+    // first the slots' up tile done words (one a thread, the rest at the barrier): a
+    // waiting workgroup then spins on at most 2 NT words instead of every mid word
+    const uint64_t* tiles = &A.mail.mtile[(size_t)d0 * NT];
+    if (!hint_wait((d1 - d0 + 1) * NT, [tiles](int i) { return tiles + i; }, W_MID, gd)) return false;
     uint32_t v[2 * MPT];
     const bool ok = poll_words<2 * MPT>([b0, b1](int q) { return q < MPT ? b0 + q : b1 + (q - MPT); }, v,
                                         (in0 ? ALL : 0u) | (in1 ? ALL << MPT : 0u), W_MID, gd);

@@ -20,6 +20,7 @@ struct Mail {
   float* xs;        // [MAX_ROWS][H / 128] their block scales
   uint64_t* rdone;  // DONE_BYTES: router task t's done word, replicated
   uint64_t* mid;    // [max_act][MAX_ROWS][I]  silu(gate) * up, f32
+  uint64_t* mtile;  // [max_act][I / 16]     the MXFP4 kernel's up tile done words (hints)
   uint64_t* ypart;  // [max_act][MAX_ROWS][H]  an expert's weighted down output, f32
   uint32_t* guard;  // [G_WORDS]
 };
