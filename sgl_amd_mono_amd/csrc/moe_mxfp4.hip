@@ -374,7 +374,8 @@ class Step {
     bool ok = true;
     // two rotations a pass: the compiler's wait for the first slot consumed after the
     // loop header is conservative (it drains the loads in flight), so a pass of six
-    // turns pays it once per six tasks
+    // turns pays it once per six tasks (a straight-line first pass measured no faster
+    // at 8 rows and slower at 16: the larger code)
     for (;;) {
       if (P[0].kind != K_UP) { b = 0; break; }
       ok &= up_turn<0>();
@@ -406,6 +407,16 @@ class Step {
         if (P[2].kind != K_DOWN) goto finals2;
         down_turn<2>(d0);
       }
+      // one rotation in straight-line code before the loop (a block holds at most three
+      // groups up to 8 rows): at a loop header the waitcnt pass waits for every load in
+      // flight (the copies between the unrolled rotations' registers), which here would
+      // hold the next turn until the refills issued just before it are back
+      if (P[0].kind != K_DOWN) goto finals0;
+      down_turn<0>(d0);
+      if (P[1].kind != K_DOWN) goto finals1;
+      down_turn<1>(d0);
+      if (P[2].kind != K_DOWN) goto finals2;
+      down_turn<2>(d0);
       for (;;) {  // two rotations a pass, as the up loop
         if (P[0].kind != K_DOWN) goto finals0;
         down_turn<0>(d0);
