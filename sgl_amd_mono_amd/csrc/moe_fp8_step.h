@@ -676,7 +676,10 @@ class Step {
       const uint64_t* base = &A.mail.ypart[(size_t)s * H + h];
       const int32_t* slots = L.plan.rowslot[s];
       uint32_t v[NSLOT];
-      ok = poll_words<NSLOT>([base, slots](int k) { return base + (size_t)slots[k] * MAX_ROWS * H; }, v,
+      // every spin sweeps all missing words (no probe): the finals wait at the tail, when
+      // the weight streams are over, and a probe's extra round trip is what costs there
+      const auto at = [base, slots](int k) { return base + (size_t)slots[k] * MAX_ROWS * H; };
+      ok = poll_words<NSLOT, decltype(at), false, false>(at, v,
                              (1u << NSLOT) - 1u, site0 + W_YPART, gd);
       if (ok) {
         float y = 0.f;
