@@ -189,7 +189,8 @@ struct Guard {
 // so callers hold no arrays of pointers. False if the guard expired first.
 //
 // The first pass loads every pending word. While words are missing, a spin loads only
-// the first missing one (the probe) and sweeps the rest once the probe has arrived: a
+// the first missing one (the probe), keeps it once it carries the tag and then sweeps
+// the rest (a single-word wait ends with its probe, one round trip after the word): a
 // waiting workgroup then costs one load a thread a spin, not one a word, so early
 // waiters do not flood the memory system the producers are streaming through.
 //
@@ -238,15 +239,20 @@ MONO_DEV bool poll_words(At at, uint32_t (&v)[N], uint32_t pending, int site, co
       continue;
     }
     uint64_t probe = 0;
-    bool sent = false;
+    uint32_t pbit = 0u;
 #pragma unroll
     for (int j = 0; j < N; ++j)
-      if (!sent && ((pending >> j) & 1u)) {
+      if (!pbit && ((pending >> j) & 1u)) {
         probe = mb_load(at(j));
-        sent = true;
+        pbit = 1u << j;
       }
     if ((uint32_t)(probe >> 32) == g.tag) {
-      sweep();
+      // the probe word is in: keep it (a single-word wait ends here) and sweep the rest
+#pragma unroll
+      for (int j = 0; j < N; ++j)
+        if (pbit == (1u << j)) v[j] = (uint32_t)probe;
+      pending &= ~pbit;
+      if (pending) sweep();
       continue;
     }
     // the deadline after the 1st, 33rd, ... miss; other workgroups' failures after the
