@@ -63,7 +63,9 @@ constexpr int NSLOT = TOPK + 1;
 constexpr int MSTRIDE = I + 8;       // bf16 a mid row in LDS
 constexpr int MPT = MAX_ROWS * I / FT;  // mid words a thread polls when it stages a slot
 constexpr int NW = 6;                // weight registers (u32x4) a task: up 2 x 3 steps, down 2 tiles x 3
-constexpr int D = 3;                 // tasks a workgroup holds in flight
+constexpr int D = 2;                 // tasks a workgroup holds in flight (98 KB: enough for the
+                                     // per-CU ingest with every CU streaming; a third sat in front
+                                     // of the mid poll at the up -> down turn: 35.9 -> 34.2 us)
 constexpr int RING = 4;              // LDS buffers of up partial sums
 static_assert(HS % FW == 0 && I % 128 == 0 && I % MPT == 0 && MPT % 2 == 0, "tiling");
 static_assert(2 * UP_SW == NW && 2 * IS == NW && DN_ROWS == FW * 32, "six 16-byte weight loads a lane a task");
@@ -372,30 +374,30 @@ class Step {
     // consume leaves the other slots' loads in flight
     int b = 0;
     bool ok = true;
-    // two rotations a pass: the compiler's wait for the first slot consumed after the
+    // rotations of two slots: the compiler's wait for the first slot consumed after the
     // loop header is conservative (it drains the loads in flight), so a pass of six
-    // turns pays it once per six tasks (a straight-line first pass measured no faster
-    // at 8 rows and slower at 16: the larger code)
+    // turns (three rotations) pays it once per six tasks (a straight-line first pass
+    // measured no faster at 8 rows and slower at 16: the larger code)
     for (;;) {
       if (P[0].kind != K_UP) { b = 0; break; }
       ok &= up_turn<0>();
       if (P[1].kind != K_UP) { b = 1; break; }
       ok &= up_turn<1>();
-      if (P[2].kind != K_UP) { b = 2; break; }
-      ok &= up_turn<2>();
       if (P[0].kind != K_UP) { b = 0; break; }
       ok &= up_turn<0>();
       if (P[1].kind != K_UP) { b = 1; break; }
       ok &= up_turn<1>();
-      if (P[2].kind != K_UP) { b = 2; break; }
-      ok &= up_turn<2>();
+      if (P[0].kind != K_UP) { b = 0; break; }
+      ok &= up_turn<0>();
+      if (P[1].kind != K_UP) { b = 1; break; }
+      ok &= up_turn<1>();
     }
     if (!ok) gd.fail(W_RING);
     if (!block_all(ok)) return false;
     reduce_ready();  // every arrival is in: the uses still unreduced (claims keep each to one wave)
     // the down groups: the workgroup's block spans at most two slots; both mids are
-    // staged into LDS at once (barriers and one poll), then a loop of down turns alone
-    // (no wait in it)
+    // staged into LDS at once (barriers and one poll), then down turns alone (no wait
+    // in them)
     if (n_dn_b > 0) {
       const int d0 = v0 / DN_GROUPS, d1 = (v0 + n_dn_b - 1) / DN_GROUPS;
       if (!stage_mids(d0, d1)) return false;
@@ -403,11 +405,7 @@ class Step {
         if (P[1].kind != K_DOWN) goto finals1;
         down_turn<1>(d0);
       }
-      if (b >= 1) {
-        if (P[2].kind != K_DOWN) goto finals2;
-        down_turn<2>(d0);
-      }
-      // one rotation in straight-line code before the loop (a block holds at most three
+      // three turns in straight-line code before the loop (a block holds at most three
       // groups up to 8 rows): at a loop header the waitcnt pass waits for every load in
       // flight (the copies between the unrolled rotations' registers), which here would
       // hold the next turn until the refills issued just before it are back
@@ -415,37 +413,29 @@ class Step {
       down_turn<0>(d0);
       if (P[1].kind != K_DOWN) goto finals1;
       down_turn<1>(d0);
-      if (P[2].kind != K_DOWN) goto finals2;
-      down_turn<2>(d0);
+      if (P[0].kind != K_DOWN) goto finals0;
+      down_turn<0>(d0);
       for (;;) {  // two rotations a pass, as the up loop
+        if (P[1].kind != K_DOWN) goto finals1;
+        down_turn<1>(d0);
         if (P[0].kind != K_DOWN) goto finals0;
         down_turn<0>(d0);
         if (P[1].kind != K_DOWN) goto finals1;
         down_turn<1>(d0);
-        if (P[2].kind != K_DOWN) goto finals2;
-        down_turn<2>(d0);
         if (P[0].kind != K_DOWN) goto finals0;
         down_turn<0>(d0);
-        if (P[1].kind != K_DOWN) goto finals1;
-        down_turn<1>(d0);
-        if (P[2].kind != K_DOWN) goto finals2;
-        down_turn<2>(d0);
       }
     }
     if (b == 1) goto finals1;
-    if (b == 2) goto finals2;
     goto finals0;
     // the finals from the slot that holds the first of them
     int st;
   finals1:
     if ((st = turn<1>()) != 0) return st == 1;
-  finals2:
-    if ((st = turn<2>()) != 0) return st == 1;
   finals0:
     for (;;) {
       if ((st = turn<0>()) != 0) return st == 1;
       if ((st = turn<1>()) != 0) return st == 1;
-      if ((st = turn<2>()) != 0) return st == 1;
     }
   }
 
