@@ -7,7 +7,6 @@ per-32 FP4 quantisation of the indexer's query.
 
 from __future__ import annotations
 
-import numpy as np
 import torch
 
 FP8_MAX = 448.0  # glm53/gfx950/config.py:278 (FP8_MAX = 448.0)
@@ -103,15 +102,6 @@ def fp8_block_dequant(codes: torch.Tensor, scales: torch.Tensor, block: int = 12
     return (v * scales[..., None]).reshape(codes.shape)
 
 
-def fp8_weight_dequant(codes: torch.Tensor, scales: torch.Tensor, bn: int = 128, bk: int = 128):
-    """[N, K] E4M3 with f32 [N/bn, K/bk] block scales -> f32 [N, K]
-    (the 128 x 128 block-scaled checkpoint format the reference reads,
-    glm53/gfx950/kernel.py:5-45, 'per-128x128 block scale')."""
-    v = e4m3_decode(codes)
-    s = scales.float().repeat_interleave(bn, -2).repeat_interleave(bk, -1)
-    return v * s
-
-
 def mxfp4_dequant(packed: torch.Tensor, scales: torch.Tensor) -> torch.Tensor:
     """[N, K/2] packed E2M1 + [N, K/32] E8M0 -> f32 [N, K]
     (test/kernels/deepseek_v41/check_ffn.py:107-114, ``deq_fp4``)."""
@@ -143,11 +133,6 @@ def e2m1_decode_codes(codes: torch.Tensor) -> torch.Tensor:
 def bf16_round(x: torch.Tensor) -> torch.Tensor:
     """float32 -> bf16 (round to nearest even) -> float32."""
     return x.float().to(torch.bfloat16).float()
-
-
-def f32_bits(x: torch.Tensor) -> np.ndarray:
-    """float32 tensor -> its IEEE bits as uint32 numpy."""
-    return x.float().contiguous().numpy().view(np.uint32)
 
 
 def aiter_unshuffle(ws: torch.Tensor) -> torch.Tensor:

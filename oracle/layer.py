@@ -20,8 +20,6 @@ widened exactly to bf16 ... the math is exact block-scaled FP8 on bf16 activatio
 
 from __future__ import annotations
 
-import math
-
 import torch
 
 from . import codecs
@@ -126,13 +124,35 @@ def slot_of(page_table: torch.Tensor, pos: torch.Tensor) -> torch.Tensor:
 
 
 def index_fp4(v: torch.Tensor):
-    """An index vector [..., 128] after its projection and norm: RoPE on dims [0, 64)
-    (glm53/gfx950/kernel.py:2128-2131), bf16, Hadamard, bf16, FP4 over 32-dim blocks
-    with power-of-two scales (deepseek_v4/gfx950/kernels/stages/indexer.py:240-246,
-    335-340 ``had_pair`` + ``fp4_block``). ``v`` arrives with RoPE already applied.
-    Returns (codes uint8 [..., 128], e8m0 uint8 [..., 4], dequantised f32)."""
+    """An index vector [..., 128] after its projection, norm and RoPE: bf16, Hadamard,
+    bf16, FP4 over 32-dim blocks with power-of-two scales
+    (deepseek_v4/gfx950/kernels/stages/indexer.py:240-246, 335-340 ``had_pair`` +
+    ``fp4_block``). Returns (codes uint8 [..., 128], e8m0 uint8 [..., 4], dequantised
+    f32, the rotated bf16 vector before FP4)."""
     h = codecs.bf16_round(fwht(codecs.bf16_round(v)))
-    return codecs.fp4_block_quant(h)
+    codes, e8, deq = codecs.fp4_block_quant(h)
+    return codes, e8, deq, h
+
+
+def index_key(ik: torch.Tensor, g_ik, b_ik, c, s):
+    """The indexer's key of rows ``ik`` [S, 128] (the f32 projection) at RoPE angles
+    ``c``/``s`` [S, 32]: LayerNorm, RoPE on dims [0, 64), then ``index_fp4``
+    (glm53/gfx950/kernel.py:2103-2133)."""
+    kn = layernorm(ik, g_ik, b_ik)
+    kn = torch.cat([rope_pairs(kn[:, :PE_DIM], c, s), kn[:, PE_DIM:]], -1)
+    return index_fp4(kn)
+
+
+def index_query(q_an: torch.Tensor, w_iq, s_iq, c, s):
+    """The indexer's query of rows ``q_an`` [S, 1536] (bf16 values) at RoPE angles
+    ``c``/``s`` [S, 32]: W_iq q_an (row h*128 + d is head h's dim d) rounded to bf16,
+    RoPE on each head's dims [0, 64) (the dims the key rotates), then ``index_fp4``
+    (deepseek_v4/gfx950/kernels/stages/indexer.py:271-338; glm53/gfx950/kernel.py:2121-2133).
+    Returns ``index_fp4``'s tuple over [S, 64 heads, 128]."""
+    S = q_an.shape[0]
+    raw = codecs.bf16_round(gemv(q_an, w_iq, s_iq)).reshape(S, INDEX_HEADS, INDEX_DIM)
+    rot = torch.cat([rope_pairs(raw[..., :PE_DIM], c[:, None], s[:, None]), raw[..., PE_DIM:]], -1)
+    return index_fp4(rot)
 
 
 def front(h, pos, page_table, w, cos, sin, kv_scaled: bool = True):
@@ -143,7 +163,8 @@ def front(h, pos, page_table, w, cos, sin, kv_scaled: bool = True):
     q [S, 32, 576] bf16 (q_lat | q_pe), iq [S, 64, 64] uint8 (packed E2M1),
     iqs [S, 64, 4] uint8, iw [S, 64] bf16, and the cache rows this step writes:
     slot [S], kv [S, 576] uint8 E4M3 + kv_scale [S] f32, ikv [S, 4, 16] uint8 + iks
-    [S, 4] uint8; plus intermediates (x, q_a, kv_a, ik, q_an, q_nope, q_pe, q_lat).
+    [S, 4] uint8; plus intermediates (x, q_a, kv_a, ik, q_an, q_nope, q_pe, q_lat, and
+    the index query / key before FP4, iq_h [S, 64, 128] and ik_h [S, 128]).
     ``kv_scaled=False`` writes raw E4M3 MLA rows (scale 1)."""
     S = h.shape[0]
     pos = pos.long()
@@ -170,16 +191,9 @@ def front(h, pos, page_table, w, cos, sin, kv_scaled: bool = True):
     kpe = codecs.bf16_round(rope_pairs(kv_a[:, KV_LORA:], c, s_))
     kv_codes, kv_scale = fp8_row_quant_pow2(torch.cat([kvn, kpe], -1), scaled=kv_scaled)
 
-    # index key: LayerNorm, RoPE on dims [0, 64), Hadamard, FP4 (kernel.py:2103-2131)
-    kn = layernorm(ik, w["g_ik"], w["b_ik"])
-    kn = torch.cat([rope_pairs(kn[:, :PE_DIM], c, s_), kn[:, PE_DIM:]], -1)
-    k_codes, k_e8, _ = index_fp4(kn)
-
-    # index query: W_iq q_an rounded to bf16, RoPE, Hadamard, FP4
-    # (deepseek_v4/gfx950/kernels/stages/indexer.py:271-338)
-    iq_raw = codecs.bf16_round(gemv(q_an, w["w_iq"], w["s_iq"])).reshape(S, INDEX_HEADS, INDEX_DIM)
-    iq_r = torch.cat([rope_pairs(iq_raw[..., :PE_DIM], c[:, None], s_[:, None]), iq_raw[..., PE_DIM:]], -1)
-    q_codes, q_e8, _ = index_fp4(iq_r)
+    # index key and query (LayerNorm / W_iq, RoPE on dims [0, 64), Hadamard, FP4)
+    k_codes, k_e8, _, ik_h = index_key(ik, w["g_ik"], w["b_ik"], c, s_)
+    q_codes, q_e8, _, iq_h = index_query(q_an, w["w_iq"], w["s_iq"], c, s_)
 
     # head weights: bf16(W_iw x) * IHD^-1/2 * IH^-1/2, stored bf16 (indexer.py:340-408)
     iw = (codecs.bf16_round(iw_raw) * INDEX_W_SCALE).to(torch.bfloat16)
@@ -189,6 +203,7 @@ def front(h, pos, page_table, w, cos, sin, kv_scaled: bool = True):
         slot=slot_of(page_table, pos), kv=kv_codes, kv_scale=kv_scale,
         ikv=codecs.e2m1_pack(k_codes).reshape(S, 4, 16), iks=k_e8,
         x=x, q_a=q_a, kv_a=kv_a, ik=ik, q_an=q_an, q_nope=q_nope, q_pe=q_pe, q_lat=q_lat,
+        iq_h=iq_h, ik_h=ik_h,
     )  # fmt: skip
 
 
@@ -215,7 +230,3 @@ def back(o_lat, h, w):
     o = codecs.bf16_round(torch.einsum("hvc,shc->shv", wuv, o_lat.float())).reshape(S, HEADS * V_DIM)
     y = gemv(o, w["w_o"], w["s_o"])
     return dict(o=o, y=y, a=(h.float() + y).to(torch.bfloat16))
-
-
-def softmax_scale() -> float:
-    return 1.0 / math.sqrt(QK_DIM)

@@ -9,7 +9,11 @@ RoPE sign, a wrong Hadamard order, a misplaced scale row, a wrong cache index) f
 * block dequantisation with a partial last row block;
 * the absorbed query against the unabsorbed q_nope . (W_UK^T c) it replaces;
 * the cache writer against the attention phase's reader (oracle.attention.index_keys);
-* the whole front on tiny shapes against an fp64 re-derivation of each output.
+* the whole front on tiny shapes against an fp64 re-derivation of each output;
+* the index query (W_iq rows h*128 + d, RoPE on dims [0, 64), Hadamard, FP4) against
+  an fp64 re-derivation, and the index score's dependence on the position difference
+  alone (query and key rotated on the same dims), each shown to reject a planted slip
+  (the query rotated on [64, 128), the Hadamard dropped, heads and dims transposed).
 """
 
 import numpy as np
@@ -249,3 +253,122 @@ def test_raw_e4m3_mla_row_is_unscaled_and_clamped():
     # the scaled row of the same values is a power of two times codes within range
     codes2, scale2 = ol.fp8_row_quant_pow2(row)
     assert float(scale2) == 8.0 and bool((codecs.e4m3_decode(codes2).abs() <= 448).all())
+
+
+# ---------------------------------------------------------------- index query / key
+def _bf16_64(x: torch.Tensor) -> torch.Tensor:
+    return x.to(torch.bfloat16).double()
+
+
+def _iq_fp64(q_an, w_iq, s_iq, pos):
+    """The index query re-derived in fp64 with the restatement's bf16 rounding points:
+    rows h*128 + d of W_iq (row-major, read by explicit row slices) on q_an, bf16; the
+    complex rotation of each head's dims [0, 64) by the row's position, bf16; the
+    Sylvester Hadamard matrix / sqrt(128), bf16. Returns [S, 64, 128] float64."""
+    W = ol.block_dequant(w_iq, s_iq).double()
+    S = q_an.shape[0]
+    out = torch.zeros(S, ol.INDEX_HEADS, ol.INDEX_DIM, dtype=torch.float64)
+    H = torch.from_numpy(scipy.linalg.hadamard(128).astype(np.float64)) / np.sqrt(128.0)
+    inv = 10000.0 ** (-torch.arange(0, 64, 2, dtype=torch.float64) / 64)
+    for s in range(S):
+        for h in range(ol.INDEX_HEADS):
+            v = _bf16_64(W[h * 128 : (h + 1) * 128] @ q_an[s].double())
+            z = torch.complex(v[0:64:2], v[1:64:2]) * torch.polar(torch.ones(32, dtype=torch.float64), float(pos[s]) * inv)
+            r = v.clone()
+            r[0:64:2], r[1:64:2] = z.real, z.imag
+            out[s, h] = _bf16_64(H @ _bf16_64(r))
+    return out
+
+
+def _check_iq_against_fp64(codes, e8, q_an, w, pos):
+    """FP4 codes / E8M0 scales of an index query against the fp64 re-derivation: each
+    block's scale byte is pow2_ceil(max(amax, 6 * 2^-126) / 6) of the fp64 block (one
+    step off only where amax / 6 sits within 1e-3 of a power of two), and every decoded
+    value lies within one scale unit of the fp64 value (the widest half gap of E2M1,
+    between 4 and 6, plus the bf16 roundings)."""
+    want = _iq_fp64(q_an, w["w_iq"], w["s_iq"], pos)
+    blocks = want.reshape(*want.shape[:-1], 4, 32)
+    amax = blocks.abs().amax(-1).clamp_min(6.0 * 2.0**-126) / 6.0
+    code = torch.ceil(torch.log2(amax)) + 127
+    frac = torch.log2(amax) - torch.round(torch.log2(amax))
+    e8 = e8.reshape(code.shape).double()
+    near = frac.abs() < 1e-3
+    assert bool(((e8 == code) | (near & ((e8 - code).abs() <= 1))).all()), "index-query scale bytes"
+    dec = codecs.e2m1_decode_codes(codes.reshape(want.shape)).double()
+    scale = torch.exp2(e8 - 127).repeat_interleave(32, -1)
+    assert float(((dec * scale - want).abs() / scale).max()) < 1.0 + 12 * 2.0**-9, "index-query values"
+
+
+def _check_relative_position(index_query, index_key, w, seed=21):
+    """RoPE on the same dims of query and key plus one orthogonal Hadamard on both make
+    the index score q . k (before FP4) a function of the position difference alone:
+    shifting the query's and the key's positions by the same delta keeps every
+    head's q . k to within the bf16 roundings, while moving the query alone does not."""
+    g = torch.Generator().manual_seed(seed)
+    q_an = torch.randn(2, ol.Q_LORA, generator=g).to(torch.bfloat16)
+    ik = torch.randn(3, ol.INDEX_DIM, generator=g) * 2
+    cos, sin = ol.rope_tables(4096)
+    m, n = torch.tensor([70, 900]), torch.tensor([5, 2000, 640])
+
+    def dots(dm, dn):
+        qh = index_query(q_an, w["w_iq"], w["s_iq"], cos[m + dm], sin[m + dm])[3].double()
+        kh = index_key(ik, w["g_ik"], w["b_ik"], cos[n + dn], sin[n + dn])[3].double()
+        d = torch.einsum("shd,td->sht", qh, kh)
+        return d / (qh.norm(dim=-1)[..., None] * kh.norm(dim=-1)[None, None])
+
+    # cosines of random 128-dim vectors are ~0.09 rms; the bf16 roundings move them by
+    # ~1.5e-3 at most, a query rotated on other dims than the key by ~0.09 and more
+    base = dots(0, 0)
+    for delta in (1, 37, 1000):
+        assert float((dots(delta, delta) - base).abs().max()) < 0.01, f"shift {delta}"
+    assert float((dots(37, 0) - base).abs().max()) > 0.1  # the check can see a rotation
+
+
+def test_index_query_against_fp64_rederivation(front_case):
+    w, h, pos, pt, cos, sin, _ = front_case
+    f = ol.front(h, pos, pt, w, cos, sin)
+    codes = torch.stack([f["iq"] & 15, f["iq"] >> 4], -1).flatten(-2)
+    _check_iq_against_fp64(codes, f["iqs"], f["q_an"], w, pos)
+
+
+def test_index_score_depends_on_position_difference_only():
+    _check_relative_position(ol.index_query, ol.index_key, _layer_weights())
+
+
+def _mutant_index_query(kind: str):
+    """``layer.index_query`` with one plausible slip planted."""
+
+    def f(q_an, w_iq, s_iq, c, s):
+        S = q_an.shape[0]
+        raw = codecs.bf16_round(ol.gemv(q_an, w_iq, s_iq))
+        if kind == "heads_dims_transposed":
+            raw = raw.reshape(S, ol.INDEX_DIM, ol.INDEX_HEADS).transpose(1, 2)
+        raw = raw.reshape(S, ol.INDEX_HEADS, ol.INDEX_DIM)
+        lo, hi = raw[..., : ol.PE_DIM], raw[..., ol.PE_DIM :]
+        if kind == "rope_high_dims":
+            rot = torch.cat([lo, ol.rope_pairs(hi, c[:, None], s[:, None])], -1)
+        else:
+            rot = torch.cat([ol.rope_pairs(lo, c[:, None], s[:, None]), hi], -1)
+        hv = codecs.bf16_round(rot)
+        if kind != "no_hadamard":
+            hv = codecs.bf16_round(ol.fwht(hv))
+        codes, e8, deq = codecs.fp4_block_quant(hv)
+        return codes, e8, deq, hv
+
+    return f
+
+
+@pytest.mark.parametrize("kind", ["rope_high_dims", "no_hadamard", "heads_dims_transposed"])
+def test_index_query_pins_reject_planted_mistakes(front_case, kind):
+    w, h, pos, pt, cos, sin, _ = front_case
+    mutant = _mutant_index_query(kind)
+    f = ol.front(h, pos, pt, w, cos, sin)
+    codes, e8, _, _ = mutant(f["q_an"], w["w_iq"], w["s_iq"], cos[pos], sin[pos])
+    with pytest.raises(AssertionError):
+        _check_iq_against_fp64(codes, e8, f["q_an"], w, pos)
+    if kind != "heads_dims_transposed":  # a transposed reshape still rotates matching dims
+        with pytest.raises(AssertionError):
+            _check_relative_position(mutant, ol.index_key, w)
+    # the unmutated restatement passes the same checks
+    codes, e8, _, _ = ol.index_query(f["q_an"], w["w_iq"], w["s_iq"], cos[pos], sin[pos])
+    _check_iq_against_fp64(codes, e8, f["q_an"], w, pos)
