@@ -139,7 +139,9 @@ int mono_moe_fp8_forward(mono_moe* moe, const mono_moe_fp8_args* args, void* str
 int mono_moe_set_deadline(mono_moe* moe, double seconds);
 /* Synchronise the device and copy the MONO_GUARD_WORDS guard words to `words`. */
 int mono_moe_read_errors(mono_moe* moe, int32_t* words);
-/* Synchronise, then clear guard words 1.. so the runtime launches again. */
+/* Synchronise, then clear guard words 1-3, zero every mailbox (no word of an earlier
+ * launch survives, both row-histogram copies start at zero) and clear the host word, so
+ * the runtime launches again. The same for every mono_*_clear_errors. */
 int mono_moe_clear_errors(mono_moe* moe);
 /* Tests of the fail-stop path: every wait at site `site` of later launches fails at
  * once, as if its deadline had passed (the host-forced fault of guard.py:79-88); -1
@@ -389,10 +391,10 @@ typedef struct {
  * mono_layer_forward / _front_forward / _tail_forward the caller mixes. */
 int mono_layer_create(const mono_layer_config* cfg, mono_layer** out);
 int mono_layer_destroy(mono_layer* layer);
-/* Glm53LayerOp.launch (runner.py:240-321): the layer's front (as mono_front_forward),
- * then the sparse attention, W_UV, o_proj + residual and the FP8 MoE + residual as ONE
- * persistent launch (glm53/gfx950/kernel.py:2684-5187); results equal the four entry
- * points'. Both launches are stream-ordered on `stream` and never synchronise. */
+/* Glm53LayerOp.launch (runner.py:240-321): the whole decoder layer as ONE persistent
+ * launch (glm53/gfx950/kernel.py:6-45, 1367-5187): the front (as mono_front_forward),
+ * the sparse attention, W_UV, o_proj + residual and the FP8 MoE + residual; results
+ * equal the four entry points'. Stream-ordered on `stream`; never synchronises. */
 int mono_layer_forward(mono_layer* layer, const mono_proj_weights* w, const mono_layer_args* args, void* stream);
 /* The two launches of mono_layer_forward on their own (same checks), for a caller that
  * times or records between them: the front, then the fused rest. No counterpart in the
@@ -414,9 +416,13 @@ int mono_layer_read_errors(mono_layer* layer, int32_t* words);
 /* The layer's pinned host error word, without synchronising: 0, or 1 + the wait site
  * of a launch that failed or was refused since the last clear (-1: not a live layer).
  * No counterpart in the reference, which stops a failed launch by a GPU fault
- * (common/guard.py:91-97); a serving caller checks it once a step. */
+ * (common/guard.py:91-97); a serving caller watches it from a host thread (graph
+ * replays run no host code a step) and ends the process on a hit. A failed launch's
+ * output holds NaN where its failing workgroups wrote it but may keep rows that other
+ * workgroups finished: the host word, not the output, is authoritative. */
 int32_t mono_layer_pending_error(mono_layer* layer);
-/* Synchronise, clear the sticky error and the host word so the layer launches again. */
+/* Synchronise, clear the sticky error, every mailbox and the host word so the layer
+ * launches again. */
 int mono_layer_clear_errors(mono_layer* layer);
 /* Tests of the fail-stop path (the reference's SGLANG_AMD_MONO_FAULT_INJECT
  * rank:site:after, common/guard.py:79-88): every wait at `site` of every launch from
@@ -424,7 +430,9 @@ int mono_layer_clear_errors(mono_layer* layer);
  * the next launch; synchronises when after > 0); site -1 turns it off. */
 int mono_layer_set_fault(mono_layer* layer, int32_t site, int64_t after);
 /* Tests of the tag epochs (synchronises): the next launch takes launch ordinal
- * `ordinal`, i.e. tag ordinal % (2^32 - 2) + 1. No counterpart in the reference. */
+ * `ordinal`, i.e. tag ordinal % (2^32 - 2) + 1. Every mailbox is zeroed as well, so a
+ * jump of any length or direction (odd ones change the row histograms' parity) leaves
+ * no stale word. No counterpart in the reference. */
 int mono_layer_set_launch_ordinal(mono_layer* layer, uint64_t ordinal);
 
 #ifdef __cplusplus

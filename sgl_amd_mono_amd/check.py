@@ -22,9 +22,9 @@ the launch writes its own, so both start from the same caches.
 from __future__ import annotations
 
 import logging
+import math
 
 import torch
-import torch.nn.functional as F
 
 from .attn import PAGE, TOPK
 
@@ -37,14 +37,21 @@ SHARED_EXPERT = 256
 _E2M1 = (0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0, -0.0, -0.5, -1.0, -1.5, -2.0, -3.0, -4.0, -6.0)
 
 
-def _metrics(a: torch.Tensor, b: torch.Tensor) -> dict[str, float]:
-    a, b = a.float().reshape(-1), b.float().reshape(-1)
-    if a.numel() == 0:
+def _distances(got: torch.Tensor, want: torch.Tensor) -> dict[str, float]:
+    """How far ``got`` lies from ``want``, in float64 over the flattened values: the
+    largest elementwise difference, the difference's norm relative to ``want``'s, and
+    the cosine of the angle between them (1 when both are zero)."""
+    g = got.detach().reshape(-1).double()
+    w = want.detach().reshape(-1).double().to(g.device)
+    if g.numel() == 0:
         return {}
+    d = g - w
+    gg, ww, gw = float(g @ g), float(w @ w), float(g @ w)
+    tiny = 1e-60
     return {
-        "max_abs": float((a - b).abs().max()),
-        "rel": float((a - b).norm() / b.norm().clamp_min(1e-30)),
-        "cosine": float(F.cosine_similarity(a, b, dim=0)),
+        "max_abs": float(d.abs().max()),
+        "rel": (float(d @ d) / max(ww, tiny)) ** 0.5,
+        "cosine": 1.0 if gg == ww == 0.0 else gw / max((gg * ww) ** 0.5, tiny),
     }
 
 
@@ -94,32 +101,51 @@ class _Regions:
             c.kv_scale[self.slots] = saved["kv_scale"]
 
 
-def _f32_routing(mlp, top_k: int, route_scale: float):
-    """Hooks that route SGLang's MoE in f32 as the launch does (sigmoid scores, the 8
-    largest of score + bias, weights the scores over their sum times the route scale)
-    where the module's top-k would add the bias in bf16; the fused shared expert's
-    entries keep SGLang's values. Returns the hook handles ([] when the module has no
-    ``gate`` / ``topk`` submodules to hook)."""
-    gate, topk = getattr(mlp, "gate", None), getattr(mlp, "topk", None)
-    if not (hasattr(mlp, "register_forward_pre_hook") and hasattr(topk, "register_forward_hook")):
-        return []
-    seen = {}
+def launch_routing(x: torch.Tensor, gate_w: torch.Tensor, bias: torch.Tensor, top_k: int,
+                   route_scale: float) -> tuple[torch.Tensor, torch.Tensor]:
+    """The launch's routing rule on the host, in f32 (glm53/gfx950/kernel.py:4199-4330):
+    logits of the MoE input against the router rows, sigmoid scores, the ``top_k``
+    experts of the largest score + bias (f32, not bf16), each weighted by its score over
+    the picked scores' sum times ``route_scale``. Returns (ids [S, top_k] int64,
+    weights [S, top_k] f32)."""
+    score = torch.sigmoid(x.float() @ gate_w.float().t())
+    pick = torch.topk(score + bias.float(), top_k, dim=-1).indices
+    chosen = torch.take_along_dim(score, pick, dim=-1)
+    return pick, chosen * (route_scale / chosen.sum(-1, keepdim=True))
 
-    def take_input(mod, args):
-        seen["x"] = args[0]
 
-    def reroute(mod, args, out):
-        x = seen.pop("x")
-        scores = torch.sigmoid(x.float() @ gate.weight.float().t())
-        ids = (scores + gate.e_score_correction_bias.float()).topk(top_k, -1).indices
-        raw = scores.gather(1, ids)
-        routed = out.topk_ids != SHARED_EXPERT
-        new_ids, new_w = out.topk_ids.clone(), out.topk_weights.clone()
-        new_ids[routed] = ids.to(new_ids.dtype).reshape(-1)
-        new_w[routed] = (raw / raw.sum(-1, keepdim=True) * route_scale).to(new_w.dtype).reshape(-1)
-        return out._replace(topk_weights=new_w, topk_ids=new_ids)
+class _RouteAsTheLaunch:
+    """While active, SGLang's MoE module routes as the launch does: a forward hook on
+    its ``topk`` submodule (which receives the MoE input as its first argument) recomputes
+    the routed columns with ``launch_routing`` and keeps the fused shared expert's
+    trailing columns (id ``SHARED_EXPERT``) as SGLang made them. SGLang's own top-k adds
+    the correction bias in bf16, which can pick other experts than the f32 rule. A
+    module without ``gate`` / ``topk`` is left alone."""
 
-    return [mlp.register_forward_pre_hook(take_input), topk.register_forward_hook(reroute)]
+    def __init__(self, mlp, top_k: int, route_scale: float):
+        self.gate, self.topk = getattr(mlp, "gate", None), getattr(mlp, "topk", None)
+        self.k, self.scale = top_k, route_scale
+        self.handle = None
+
+    def __enter__(self):
+        if self.gate is not None and hasattr(self.topk, "register_forward_hook"):
+            self.handle = self.topk.register_forward_hook(self._rewrite, with_kwargs=True)
+        return self
+
+    def __exit__(self, *exc) -> None:
+        if self.handle is not None:
+            self.handle.remove()
+            self.handle = None
+
+    def _rewrite(self, module, args, kwargs, out):
+        x = args[0] if args else kwargs["hidden_states"]
+        ids, weights = launch_routing(x, self.gate.weight, self.gate.e_score_correction_bias, self.k, self.scale)
+        shared_ids, shared_w = out.topk_ids[:, self.k:], out.topk_weights[:, self.k:]
+        if not bool((shared_ids == SHARED_EXPERT).all()):
+            raise ValueError(f"check mode: SGLang's top-k output has {out.topk_ids.shape[1]} columns; the ones "
+                             f"past {self.k} must be the fused shared expert {SHARED_EXPERT}")
+        return out._replace(topk_ids=torch.cat([ids.to(out.topk_ids.dtype), shared_ids], 1),
+                            topk_weights=torch.cat([weights.to(out.topk_weights.dtype), shared_w], 1))
 
 
 def _selection_hook(module, seen: dict):
@@ -142,9 +168,10 @@ def reference(L, positions: torch.Tensor, h: torch.Tensor, forward_batch, S: int
     regions = _Regions(L.caches, forward_batch.out_cache_loc[:S])
     saved = regions.read()
     seen = {}
-    hooks = _f32_routing(getattr(L.module, "mlp", None), top_k, route_scale) + _selection_hook(L.module, seen)
+    hooks = _selection_hook(L.module, seen)
     try:
-        out, residual = L.module(positions[:S], h.clone(), forward_batch, None)
+        with _RouteAsTheLaunch(getattr(L.module, "mlp", None), top_k, route_scale):
+            out, residual = L.module(positions[:S], h.clone(), forward_batch, None)
     finally:
         for hook in hooks:
             hook.remove()
@@ -188,33 +215,38 @@ def _topk_vs_sglang(ref_topk: torch.Tensor, selection: torch.Tensor, own: torch.
     return {"topk": {"rel": rel}, "topk_own": {"max_abs": float(own_missed)}}
 
 
+def _outside(name: str, value: float, bound: float) -> bool:
+    """A cosine is bounded from below, every other metric from above; NaN is outside
+    every bound."""
+    if math.isnan(value):
+        return True
+    return value < bound if name.endswith(".cosine") else value > bound
+
+
 def compare(L, ref: dict, out: torch.Tensor, inter: dict, seq_lens: torch.Tensor, page_table: torch.Tensor,
             positions: torch.Tensor, S: int, numerics) -> tuple[dict, list]:
     """Measure the launch (``out`` and the intermediates ``forward(keep=True)`` returned)
-    against ``ref``; log every value and every violation of ``numerics.bounds``.
-    Returns (values, violations) with violations as (name, value, bound)."""
-    outputs = {"streams": _metrics(out[:S], ref["streams"])}
+    against ``ref``: one INFO record with every value of the layer, one ERROR record per
+    value outside its bound in ``numerics.bounds``. Returns (values, violations), the
+    violations as (name, value, bound)."""
     regions = _Regions(L.caches, ref["slots"])
     got, want = regions.read(), ref["regions"]
+    measured = {"streams": _distances(out[:S], ref["streams"])}
     if regions.slots.numel():
-        outputs["kv"] = _metrics(_kv_values(got["kv"], got.get("kv_scale")),
-                                 _kv_values(want["kv"], want.get("kv_scale")))
-        outputs["index"] = _metrics(_index_values(got["ikv"], got["iks"]), _index_values(want["ikv"], want["iks"]))
+        measured["kv"] = _distances(_kv_values(got["kv"], got.get("kv_scale")),
+                                    _kv_values(want["kv"], want.get("kv_scale")))
+        measured["index"] = _distances(_index_values(got["ikv"], got["iks"]),
+                                       _index_values(want["ikv"], want["iks"]))
     sel = inter["topk_slots"][:S]
-    outputs["topk_exact"] = {"max_abs": float(topk_exact_missed(inter["index_scores"], sel, seq_lens[:S],
-                                                                 page_table))}
+    missed = topk_exact_missed(inter["index_scores"], sel, seq_lens[:S], page_table)
+    measured["topk_exact"] = {"max_abs": float(missed)}
     if ref.get("topk") is not None:
-        outputs.update(_topk_vs_sglang(ref["topk"], sel, regions.slots))
-    values = {f"layer.{o}.{m}": v for o, ms in outputs.items() for m, v in ms.items()}
-    pos = positions[:S]
-    logger.info("monokernel check layer %d (%d rows, positions %d..%d): %s", L.i, S, int(pos.min()), int(pos.max()),
-                " ".join(f"{k}={v:.6g}" for k, v in values.items()))
-    violations = []
-    for name, bound in numerics.bounds.items():
-        v = values.get(name)
-        if v is None:
-            continue
-        if not (v >= bound if name.endswith(".cosine") else v <= bound):
-            violations.append((name, v, bound))
-            logger.error("monokernel check violation: layer %d %s = %.6g, bound %g", L.i, name, v, bound)
+        measured.update(_topk_vs_sglang(ref["topk"], sel, regions.slots))
+    values = {f"layer.{part}.{metric}": v for part, ms in measured.items() for metric, v in ms.items()}
+    lo, hi = int(positions[:S].min()), int(positions[:S].max())
+    logger.info("check mode, layer %d against SGLang's module, %d rows at positions [%d, %d]: %s", L.i, S, lo, hi,
+                ", ".join(f"{k}={v:.6g}" for k, v in values.items()))
+    violations = [(k, values[k], b) for k, b in numerics.bounds.items() if k in values and _outside(k, values[k], b)]
+    for k, v, b in violations:
+        logger.error("check mode, layer %d: %s is %.6g, outside its bound %g", L.i, k, v, b)
     return values, violations

@@ -279,22 +279,41 @@ int guard_read(GuardRef r, int32_t* words) {
   return ok();
 }
 
-// Clear the sticky error (words 1-3, the tickets stay) and the host word.
+// Zero every mailbox region of the guard's scrub table (callers have synchronised).
+// Afterwards no word carries any earlier launch's tag and both copies of the flip
+// accumulators start at zero, whichever launches were refused or skipped before: a
+// refused first launch of a tag epoch never ran its scrub, and a refused launch never
+// cleared its successor's flip copy.
+int guard_scrub_all(GuardRef r) {
+  mono::ScrubRegion table[mono::SCRUB_MAX];
+  HIP_TRY(hipMemcpy(table, r.g->scrub, sizeof(table), hipMemcpyDeviceToHost));
+  for (const mono::ScrubRegion& rg : table) {
+    if (!rg.p) break;
+    HIP_TRY(hipMemset(rg.p, 0, rg.n16 * 16));
+  }
+  return MONO_OK;
+}
+
+// Clear the sticky error (words 1-3, the tickets stay), every mailbox and the host word.
 int guard_clear(GuardRef r) {
   if (int rc = check_device(r.device)) return rc;
   HIP_TRY(hipDeviceSynchronize());
   HIP_TRY(hipMemset(r.g->words + mono::G_ERROR, 0, 3 * sizeof(int32_t)));
+  if (int rc = guard_scrub_all(r)) return rc;
   HIP_TRY(hipDeviceSynchronize());
   r.herr->clear();
   return ok();
 }
 
 // Move the launch ordinal to `ordinal` (synchronises; tests of the tag epochs): the next
-// launch takes tag ordinal % TAG_PERIOD + 1.
+// launch takes tag ordinal % TAG_PERIOD + 1. Every mailbox is zeroed too, so a jump of
+// any length or direction leaves no word that reads as written under a coming tag and
+// no flip copy holding an earlier launch's sums.
 int guard_set_ordinal(GuardRef r, uint64_t ordinal) {
   if (ordinal == UINT64_MAX) return fail(MONO_EINVAL, "ordinal %llu is out of range", (unsigned long long)ordinal);
   if (int rc = check_device(r.device)) return rc;
   HIP_TRY(hipDeviceSynchronize());
+  if (int rc = guard_scrub_all(r)) return rc;
   std::vector<uint64_t> counters((size_t)r.grid, ordinal);
   HIP_TRY(hipMemcpy(r.g->tickets, counters.data(), counters.size() * sizeof(uint64_t), hipMemcpyHostToDevice));
   HIP_TRY(hipMemcpy(r.g->words + mono::G_TICKET, &ordinal, sizeof(ordinal), hipMemcpyHostToDevice));
@@ -628,11 +647,8 @@ extern "C" int mono_attn_read_errors(mono_attn* a, int32_t* words) {
 
 extern "C" int mono_attn_clear_errors(mono_attn* a) {
   if (!live(a, ATTN_MAGIC)) return fail(MONO_ESTATE, "not a live attention runtime");
-  if (int rc = guard_clear(ref(a))) return rc;
-  // a failed launch may have left row histograms uncleared for its successor
-  HIP_TRY(hipMemset(a->mail.rowh, 0, 2 * (size_t)a->cfg.max_rows * mono::attn::ROWH * sizeof(uint32_t)));
-  HIP_TRY(hipDeviceSynchronize());
-  return ok();
+  // the scrub table covers every mailbox, the row histograms' two copies included
+  return guard_clear(ref(a));
 }
 
 // ------------------------------------------------------------------ projection runtime
@@ -962,11 +978,8 @@ extern "C" int32_t mono_layer_pending_error(mono_layer* L) {
 
 extern "C" int mono_layer_clear_errors(mono_layer* L) {
   if (!layer_live(L)) return fail(MONO_ESTATE, "not a live layer runtime");
-  if (int rc = guard_clear(layer_ref(L))) return rc;
-  // a refused launch skipped clearing its successor's row histograms
-  HIP_TRY(hipMemset(L->a->mail.rowh, 0, 2 * (size_t)L->a->cfg.max_rows * mono::attn::ROWH * sizeof(uint32_t)));
-  HIP_TRY(hipDeviceSynchronize());
-  return ok();
+  // the scrub table covers every mailbox, the row histograms' two copies included
+  return guard_clear(layer_ref(L));
 }
 
 extern "C" int mono_layer_set_launch_ordinal(mono_layer* L, uint64_t ordinal) {

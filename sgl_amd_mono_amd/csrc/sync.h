@@ -394,10 +394,11 @@ MONO_DEV bool guard_begin(const GuardArgs& a, Guard& gd, const GuardFetch& f) {
 }
 MONO_DEV bool guard_begin(const GuardArgs& a, Guard& gd) { return guard_begin(a, gd, guard_fetch(a)); }
 
-// A launch that failed or was refused writes NaN over its bf16 output (n elements at p)
-// so a caller that reads it anyway gets no plausible numbers: `share` writes the
-// workgroup's grid-strided share (every workgroup refuses together), otherwise the
-// whole output (the workgroups that saw a failure; others may have finished).
+// A launch that failed or was refused writes NaN over its bf16 output (n elements at p):
+// `share` writes the workgroup's grid-strided share (every workgroup refuses together),
+// otherwise the whole output (the workgroups that saw a failure). Workgroups whose
+// waits succeeded may still store finished rows afterwards, so a failed launch's output
+// can be partly plausible; the host error word is what tells a failure.
 MONO_DEV void poison_bf16(void* p, size_t n, bool share) {
   if (!p) return;
   uint32_t* w = static_cast<uint32_t*>(p);

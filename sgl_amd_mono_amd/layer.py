@@ -13,6 +13,10 @@
 from __future__ import annotations
 
 import ctypes as C
+import logging
+import os
+import sys
+import threading
 from dataclasses import dataclass, fields
 
 import torch
@@ -298,6 +302,58 @@ class LayerHandle(Runtime):
             _lib.check(self._fn("set_launch_ordinal")(self._h, int(ordinal)))
 
 
+FAIL_STOP_EXIT = 70  # the process's exit status when a layer launch stopped (EX_SOFTWARE)
+FAIL_STOP_POLL_S = 5e-4
+
+_log = logging.getLogger(__name__)
+
+
+class FailStopWatch:
+    """A host thread that sees a stopped layer launch within about a millisecond, also
+    when the launch was replayed from a graph (a replayed step runs none of the
+    plugin's host code). The reference ends the process at the failing wait itself, by
+    a store to the null page (common/guard.py:91-97); here the kernel copies the wait
+    site to a pinned host word (``pending()``, a plain memory read, no GPU call) and
+    this thread, polling it every ``interval`` seconds, calls ``on_fail(code)`` once.
+    The default ``on_fail`` logs the site and ends the process with exit status
+    ``FAIL_STOP_EXIT`` (``os._exit``: nothing runs that could wait on the GPU), as
+    the reference's stop does. The window left: a step's tokens can be sampled and
+    handed on between the launch's failure and the thread's next poll (the interval
+    plus the thread's wait for the interpreter lock, a few milliseconds at most)."""
+
+    def __init__(self, pending, on_fail=None, interval: float = FAIL_STOP_POLL_S, name: str = "layer"):
+        self._pending, self.interval = pending, float(interval)
+        self._on_fail = on_fail if on_fail is not None else self._exit
+        self._name = name
+        self._stop = threading.Event()
+        self.code = 0
+        self._thread = threading.Thread(target=self._run, name=f"mono-fail-stop-{name}", daemon=True)
+        self._thread.start()
+
+    def _run(self) -> None:
+        while not self._stop.wait(self.interval):
+            code = int(self._pending())
+            if code > 0:
+                self.code = code
+                self._on_fail(code)
+                return
+
+    def _exit(self, code: int) -> None:
+        site = code - 1
+        msg = (f"sgl_amd_mono_amd: a {self._name} launch stopped at wait "
+               f"'{_lib.LAYER_SITES.get(site, site)}' (deadline passed or refused after an earlier "
+               f"failure); ending the process (exit status {FAIL_STOP_EXIT}) before its output is served")
+        _log.critical(msg)
+        print(msg, file=sys.stderr, flush=True)
+        os._exit(FAIL_STOP_EXIT)
+
+    def stop(self) -> None:
+        """End the thread (idempotent); the runtime calls it before it is destroyed."""
+        self._stop.set()
+        if self._thread.is_alive() and self._thread is not threading.current_thread():
+            self._thread.join()
+
+
 class LayerRuntime:
     """One GPU's TP=4 share of a DeepSeek-V3.2-shaped decoder layer with an FP4 indexer
     its launches on the caller's stream and each phase's outputs
@@ -351,8 +407,25 @@ class LayerRuntime:
         self._a = torch.empty(max_rows, HIDDEN, dtype=torch.bfloat16, device=self.device)
 
     def close(self) -> None:
+        self.unwatch()
         for rt in self.parts:
             rt.close()
+
+    def watch(self, on_fail=None, interval: float = FAIL_STOP_POLL_S) -> FailStopWatch:
+        """Start the fail-stop watcher (one-launch mode): a host thread that polls the
+        pinned error word and calls ``on_fail(code)`` (default: log and end the
+        process) when a launch stops, also for steps replayed from a graph."""
+        if self.mode != "layer":
+            raise ValueError("the fail-stop watcher reads the one-launch layer's pinned host word (mode 'layer')")
+        self.unwatch()
+        self._watch = FailStopWatch(self.handle.pending_error, on_fail, interval)
+        return self._watch
+
+    def unwatch(self) -> None:
+        w = getattr(self, "_watch", None)
+        if w is not None:
+            w.stop()
+            self._watch = None
 
     def set_deadline(self, seconds: float) -> None:
         for rt in self.parts:

@@ -193,7 +193,10 @@ class _Built:
         """``DeepseekV2ForCausalLM.forward`` for a decode or verify step; a step wider
         than the runtime runs the model's own forward."""
         lm = self.lm
-        if self.runtime is not None:  # a launch that stopped earlier: raise, never serve its NaN
+        # a launch that stopped earlier: raise before this step runs (the runtime's
+        # fail-stop watcher ends the process within a millisecond or so of the stop,
+        # also for replayed steps; this check catches an eager step inside that window)
+        if self.runtime is not None:
             self.runtime.raise_pending()
         if plan.key.rows > self.max_rows:
             return type(lm).forward(lm, input_ids, positions, forward_batch, input_embeds, pp_proxy_tensors)
@@ -291,6 +294,8 @@ def _build(model, hf_config, ctx) -> _Built:
     fault = fault_injection(p.tp_rank)
     if fault is not None:
         rt.handle.set_fault(*fault)
+    # a stopped launch ends the process, also in steps replayed from a graph
+    rt.watch()
     return _Built(model, layers, rt, cos, sin, device, context_len)
 
 

@@ -33,10 +33,10 @@ def rt(gpu_device):
     r.close()
 
 
-def _crowding(scores, ctx):
+def _crowding(scores, ctx, bits=16):
     """For each row longer than 2048: how many of its keys share the 2048th largest
-    key's upper 16 bits (the device exchanges them when at most 512, else takes two
-    more radix digits)."""
+    key's upper ``bits`` bits (at 16, the device exchanges them when at most 512, else
+    takes two more radix digits)."""
     out = []
     for s, n in enumerate(ctx):
         if n <= 2048:
@@ -44,17 +44,19 @@ def _crowding(scores, ctx):
         b = scores[s, :n].contiguous().view(torch.int32).long() & 0xFFFFFFFF
         key = torch.where(b >= 2**31, b ^ 0xFFFFFFFF, b | 2**31)
         t = key.sort(descending=True).values[2047]
-        out.append(int(((key >> 16) == (t >> 16)).sum()))
+        out.append(int(((key >> (32 - bits)) == (t >> (32 - bits))).sum()))
     return out
 
 
-def _check(rt, ctx, seed, gpu_device, period=0):
+def _check(rt, ctx, seed, gpu_device, period=0, shape=None):
     print(f"[attn] rows={len(ctx)} seed={seed} period={period} ctx={ctx[:8]}...", flush=True)
     step, caches = workloads.attn_case(ctx, gpu_device, seed=seed)
     if period:  # every page of the index plane a copy of page p % period: repeated scores
         src = torch.arange(caches.ikv.shape[0], device=gpu_device) % period
         caches.ikv.copy_(caches.ikv[src].clone())
         caches.iks.copy_(caches.iks[src].clone())
+    if shape is not None:
+        shape(step, caches)
     out, dbg = rt.forward(step, caches, debug=True)
     torch.cuda.synchronize()
     rt.check_errors()
@@ -70,6 +72,8 @@ def _check(rt, ctx, seed, gpu_device, period=0):
     want_sel = oatt.select_topk(scores, st["seq_lens"], st["page_table"])
     print(f"[attn] keys sharing the threshold's upper 16 bits: {_crowding(scores, ctx)}", flush=True)
     assert torch.equal(sel, want_sel), [s for s in range(len(ctx)) if not torch.equal(sel[s], want_sel[s])]
+    if shape is not None:
+        dbg["crowding"] = [_crowding(scores, ctx, b) for b in (16, 24, 32)]
     ref = oatt.sparse_mla(st["q"], c["kv"], c["kv_scale"], sel)
     got = out.cpu().float()
     err = (got - ref).abs()
@@ -78,7 +82,7 @@ def _check(rt, ctx, seed, gpu_device, period=0):
           f"norm-rel {rel:.3e}", flush=True)
     # the bound as an (atol, rtol) pair, elementwise: |a - b| <= 2e-2 + 1e-2 |b|
     assert bool((err <= OUT_MAX_ABS + OUT_REL * ref.abs()).all()) and rel <= OUT_REL
-    return out, sel
+    return out, sel, dbg
 
 
 def test_attn_8_rows_matches_oracle(rt, gpu_device):
@@ -109,6 +113,57 @@ def test_attn_repeated_scores(rt, gpu_device, period):
     tie in whole groups (512 copies at period 1 and 32768 keys: exactly the largest
     candidate exchange), and the lowest positions of the threshold score are taken."""
     _check(rt, [32768, 20000, 9000, 4100, 2049], 5, gpu_device, period=period)
+
+
+def _crowd_planes(group: int, fine_code: int):
+    """An index plane that crowds the threshold: every page is one base page, whose
+    ``group`` key slots ranked around the 2048th key are made identical (so about
+    ``group`` x 512 keys of a 32768-key row share the threshold's upper 16 bits, more
+    than the 512-word candidate exchange takes). Dims 96-99 of every key (in block 3,
+    scaled down to E8M0 ``fine_code``) then carry codes that vary with the physical
+    page, which moves each score by a small fraction below its upper 16 bits: radix
+    digits 3 and 4 discriminate, and equal perturbations leave exact ties. Every row
+    uses row 0's index query and head weights, so every row is crowded alike."""
+
+    def shape(step, caches):
+        for k in ("iq", "iqs", "iw"):
+            getattr(step, k)[:] = getattr(step, k)[0:1].clone()
+        B, Bs = caches.ikv[0].cpu(), caches.iks[0].cpu()  # [4, 64, 16], [4, 64]
+        sb = oatt.scale_byte(torch.arange(64))
+        Bs[3, sb] = fine_code
+        B[3, :, 0:2] = 0
+        base = oatt.index_scores(step.iq[:1].cpu(), step.iqs[:1].cpu(), step.iw[:1].cpu(), B[None], Bs[None],
+                                 torch.zeros(1, 1, dtype=torch.int32), torch.tensor([64]), 64)[0]
+        order = base.argsort(descending=True)
+        r0 = 3 if group <= 2 else 1  # the group straddles rank 2048 (512 copies a slot)
+        src = int(order[r0])
+        for j in range(r0 + 1, r0 + group):
+            d = int(order[j])
+            B[:, d] = B[:, src]
+            Bs[:, sb[d]] = Bs[:, sb[src]]
+        caches.ikv[:] = B.to(caches.ikv.device)[None]
+        caches.iks[:] = Bs.to(caches.iks.device)[None]
+        p = torch.arange(caches.ikv.shape[0], device=caches.ikv.device)
+        lo = (p % 8) | ((p // 8 % 8) << 4)
+        hi = (p // 64 % 8) | ((p // 512 % 8) << 4)
+        caches.ikv[:, 3, :, 0] = lo[:, None].to(torch.uint8)
+        caches.ikv[:, 3, :, 1] = hi[:, None].to(torch.uint8)
+
+    return shape
+
+
+@pytest.mark.parametrize("rows,group,fine", [(1, 2, 118), (1, 8, 116), (8, 2, 116), (8, 8, 118)])
+def test_attn_crowded_threshold_takes_digits_3_and_4(rt, gpu_device, rows, group, fine):
+    """600-4000 keys share the threshold's upper 16 bits but differ below them: the
+    top-k team's crowded path (digits 3 and 4 over the members' exchanged histograms,
+    then the count exchange) must still give the oracle's exact selection, ties at the
+    threshold going to the lowest positions (indexer.py:693-781 refines the same way)."""
+    _, _, dbg = _check(rt, [32768] * rows, 8, gpu_device, shape=_crowd_planes(group, fine))
+    c16, c24, c32 = dbg["crowding"]
+    print(f"[attn crowd] upper-16 {c16} upper-24 {c24} equal {c32}", flush=True)
+    assert min(c16) > 512  # every row takes the crowded path
+    assert any(a > b for a, b in zip(c16, c24))  # digit 3 discriminates
+    assert any(a > b for a, b in zip(c24, c32))  # digit 4 discriminates
 
 
 def test_attn_ties_take_lowest_positions(rt, gpu_device):

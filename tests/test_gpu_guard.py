@@ -9,6 +9,8 @@ Every comparison is bit for bit: a layer's outputs depend only on its inputs and
 caches, never on the tags its launches carry.
 """
 
+import time
+
 import pytest
 import torch
 
@@ -141,4 +143,64 @@ def test_layer_fault_armed_launches_ahead(gpu_device):
         rt.check_errors()
         _same(again, first, "after clear")
     finally:
+        rt.close()
+
+
+def test_layer_fault_in_a_replayed_graph_reaches_the_watcher(gpu_device):
+    """A step replayed from a HIP graph runs none of the plugin's host code, so the
+    per-step check of the spec never sees it. The fail-stop watcher (a host thread on
+    the pinned error word) must: a fault armed two launches ahead stops the third
+    replay, the watcher reports the site once (its default ends the process; here it
+    records), later replays are refused, and after a clear the graph replays correctly."""
+    cos, sin = workloads.rope_tables(CTX, gpu_device)
+    w = _weights(gpu_device, 95)
+    rt = LayerRuntime(4, CTX, gpu_device)
+    site = 9  # expert outputs
+    seen = []
+    try:
+        step, caches = workloads.attn_case(LENS[:4], gpu_device, seed=97, max_ctx=CTX)
+        x = workloads.rows_bf16(4, HIDDEN, gpu_device, seed=98)
+        out = torch.empty(4, HIDDEN, dtype=torch.bfloat16, device=gpu_device)
+
+        def launch():
+            rt.forward(x, step.seq_lens, step.page_table, caches, w, cos, sin, out=out, check_weights=False)
+
+        launch()
+        torch.cuda.synchronize()
+        rt.check_errors()
+        first = out.clone()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            launch()
+        torch.cuda.synchronize()
+        rt.watch(on_fail=seen.append)
+        rt.handle.set_fault(site, after=2)
+        for k in range(2):
+            print(f"[replay fault] replay {k} (armed)", flush=True)
+            graph.replay()
+            torch.cuda.synchronize()
+            assert rt.handle.pending_error() == 0 and seen == [], k
+            assert torch.equal(out, first), k
+        print("[replay fault] replay 2 (fails at the site)", flush=True)
+        graph.replay()
+        torch.cuda.synchronize()
+        until = time.monotonic() + 5.0
+        while not seen and time.monotonic() < until:
+            time.sleep(1e-3)
+        assert seen == [site + 1]
+        assert bool(out.isnan().any())
+        print("[replay fault] replay 3 (refused)", flush=True)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert rt.handle.pending_error() == site + 1 and seen == [site + 1]
+        rt.unwatch()
+        rt.handle.set_fault(-1)
+        rt.clear_errors()
+        print("[replay fault] replay after clear", flush=True)
+        graph.replay()
+        torch.cuda.synchronize()
+        rt.check_errors()
+        assert torch.equal(out, first)
+    finally:
+        rt.unwatch()
         rt.close()

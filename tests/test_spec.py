@@ -183,8 +183,9 @@ def test_backbone_runs_dense_layers_then_launches():
 
 def test_a_stopped_launch_raises_instead_of_serving():
     """A launch that failed a wait (or was refused after one) sets the runtime's pinned
-    host word; the next forward raises before anything runs, so SGLang never samples
-    tokens from the NaN the stopped launch left in its output."""
+    host word; the next eager forward raises before anything runs. (The step whose
+    launch failed, and steps replayed from a graph, are the fail-stop watcher's: it
+    ends the process, see test_fail_stop_watch_*.)"""
     from sgl_amd_mono_amd import _lib
 
     lm = _Lm(SimpleNamespace(embed_tokens=lambda ids: torch.ones(1, 7168), layers=[], norm=lambda h: h))
@@ -439,3 +440,101 @@ def test_check_mode_is_off_by_default(monkeypatch):
     monkeypatch.delenv(check.CHECK_ENV, raising=False)
     built = mono._Built(_Lm(), {3: None}, None, None, None, "cpu", context_len=4096)
     assert built.check_layers is False
+
+
+def test_fail_stop_watch_reports_once_and_stops():
+    """The watcher polls the pinned word without touching the GPU and calls on_fail
+    once with the first non-zero code; stop() ends it and is idempotent."""
+    import threading
+    import time
+
+    from sgl_amd_mono_amd.layer import FailStopWatch
+
+    words = iter([0, 0, 0, 12, 12, 12])
+    last = [0]
+
+    def pending():
+        last[0] = next(words, last[0])
+        return last[0]
+
+    hit = threading.Event()
+    seen = []
+    w = FailStopWatch(pending, on_fail=lambda c: (seen.append(c), hit.set()), interval=1e-3)
+    assert hit.wait(5.0)
+    time.sleep(0.02)
+    assert seen == [12] and w.code == 12
+    w.stop()
+    w.stop()
+    # a quiet word never calls on_fail, and stop() ends the thread
+    quiet = FailStopWatch(lambda: 0, on_fail=seen.append, interval=1e-3)
+    time.sleep(0.02)
+    quiet.stop()
+    assert seen == [12] and not quiet._thread.is_alive()
+
+
+def test_fail_stop_watch_default_ends_the_process():
+    """The default on_fail logs the wait site and ends the process with exit status
+    FAIL_STOP_EXIT, as the reference's null-page store ends it (common/guard.py:91-97)."""
+    import subprocess
+    import sys
+
+    from sgl_amd_mono_amd.layer import FAIL_STOP_EXIT
+
+    code = (
+        "import time\n"
+        "from sgl_amd_mono_amd.layer import FailStopWatch\n"
+        "FailStopWatch(lambda: 10, interval=1e-3)\n"
+        "time.sleep(30)\n"
+        "print('served')\n"
+    )
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=120,
+                       cwd=str(__import__("pathlib").Path(__file__).resolve().parent.parent))
+    assert r.returncode == FAIL_STOP_EXIT, (r.returncode, r.stderr[-2000:])
+    assert "served" not in r.stdout
+    assert "expert outputs" in r.stderr
+
+
+def test_check_mode_routes_sglangs_moe_as_the_launch():
+    """In check mode SGLang's MoE routes by the launch's f32 rule: the hook on its
+    ``topk`` submodule replaces the routed columns by the 8 largest f32 sigmoid + bias
+    (weights their scores over their sum x 2.5) and keeps the fused shared expert's
+    column. A bias that bf16 cannot tell apart from its neighbour decides the pick."""
+    from collections import namedtuple
+
+    from sgl_amd_mono_amd import check
+
+    TopK = namedtuple("TopK", "topk_weights topk_ids router_logits")
+    g = torch.Generator().manual_seed(4)
+    S, H, E = 3, 64, 32
+    gate = torch.nn.Linear(H, E, bias=False)
+    gate.weight.data = torch.randn(E, H, generator=g) * 0.1
+    gate.weight.data[6] = gate.weight.data[5]  # equal scores: the bias alone orders 5 and 6
+    gate.e_score_correction_bias = torch.zeros(E)
+    gate.e_score_correction_bias[5] = 34.0 + 1 / 64  # bf16(34 + 1/64) == 34
+    gate.e_score_correction_bias[6] = 34.0
+
+    class SglangTopK(torch.nn.Module):  # bf16 bias, fused shared expert appended
+        def forward(self, hidden_states, router_logits):
+            s = router_logits.float().sigmoid()
+            ids = (s.bfloat16() + gate.e_score_correction_bias.bfloat16()).float().topk(8, -1).indices
+            w = torch.full((hidden_states.shape[0], 9), 0.1)
+            ids = torch.cat([ids, torch.full((hidden_states.shape[0], 1), check.SHARED_EXPERT)], 1)
+            return TopK(w, ids.int(), router_logits)
+
+    mlp = torch.nn.Module()
+    mlp.gate, mlp.topk = gate, SglangTopK()
+    x = torch.randn(S, H, generator=g)
+    with check._RouteAsTheLaunch(mlp, 8, 2.5):
+        out = mlp.topk(x, gate(x))
+    plain = mlp.topk(x, gate(x))  # the hook is gone afterwards
+    ids, w = check.launch_routing(x, gate.weight, gate.e_score_correction_bias, 8, 2.5)
+    assert torch.equal(out.topk_ids[:, :8].long(), ids) and bool((out.topk_ids[:, 8] == check.SHARED_EXPERT).all())
+    assert torch.allclose(out.topk_weights[:, :8], w) and torch.allclose(out.topk_weights[:, :8].sum(-1), torch.full((S,), 2.5))
+    assert bool((out.topk_weights[:, 8] == 0.1).all())
+    # the f32 rule ranks expert 5 (bias 34 + 1/64) above 6; rows differ from SGLang's bf16 order
+    assert bool((ids[:, 0] == 5).all()) and bool((ids[:, 1] == 6).all())
+    assert not torch.equal(plain.topk_ids[:, :8].long(), ids)
+    # scores by hand in float64
+    sc = torch.sigmoid(x.double() @ gate.weight.double().t())
+    pick = sc.gather(1, ids)
+    assert torch.allclose(w.double(), pick / pick.sum(-1, keepdim=True) * 2.5, atol=1e-6)
