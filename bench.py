@@ -68,6 +68,13 @@ def time_steps(args, dev, step, reps: int = 5):
     how it was timed)."""
     import torch
 
+    if args.pmc_pass:  # counter runs: eager launches (the profiler sees each) + calibration
+        for i in range(args.warmup + args.steps):
+            step(i)
+        calibration_copy(dev)
+        print(json.dumps({"pmc_pass": True, "workload": args.workload, "launches": args.warmup + args.steps,
+                          "rows": args.rows, "calib_copy_bytes": CALIB_BYTES}), flush=True)
+        raise PmcPassDone()
     log(f"warmup {args.warmup} steps")
     for i in range(args.warmup):
         step(i)
@@ -714,6 +721,22 @@ CALIB_BYTES = 1 << 30  # the calibration copy of a PMC pass: 1 GiB read, 1 GiB w
 TRAFFIC_FILE = ROOT / "profiles" / "traffic_layer_8rows.md"
 
 
+class PmcPassDone(Exception):
+    """A single-phase workload's counter pass ran and printed its own line."""
+
+
+def calibration_copy(dev) -> None:
+    """One device copy of CALIB_BYTES (read once, written once): what FETCH_SIZE and
+    WRITE_SIZE read for it converts each counter to bytes."""
+    import torch
+
+    src = torch.empty(CALIB_BYTES // 4, dtype=torch.float32, device=dev).fill_(1.0)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+
+
 def pmc_pass(args, dev, run_step, distinct):
     """For ``rocprofv3 --pmc FETCH_SIZE`` / ``--pmc WRITE_SIZE`` runs: ``--steps`` eager
     layer steps (every dispatch seen by the profiler; no graph) and then one device copy
@@ -725,11 +748,7 @@ def pmc_pass(args, dev, run_step, distinct):
 
     for _ in range(args.steps):
         run_step()
-    src = torch.empty(CALIB_BYTES // 4, dtype=torch.float32, device=dev).fill_(1.0)
-    dst = torch.empty_like(src)
-    torch.cuda.synchronize()
-    dst.copy_(src)
-    torch.cuda.synchronize()
+    calibration_copy(dev)
     moe_fixed = 256 * 7168 * 2 + 256 * 4 + 7168 * 2 + 2 * args.rows * 7168 * 2
     print(json.dumps({"pmc_pass": True, "steps": args.steps, "layers": args.layers, "rows": args.rows,
                       "calib_copy_bytes": CALIB_BYTES,
@@ -843,7 +862,8 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="wall budget of the CPU baseline sample (0 skips it)")
     ap.add_argument("--pmc-pass", action="store_true",
-                    help="layer workload: eager steps plus a calibration copy, for rocprofv3 --pmc runs")
+                    help="eager launches (warmup + steps; layer: steps) plus a 1 GiB calibration copy, for "
+                         "rocprofv3 --pmc runs")
     args = ap.parse_args()
     if args.steps is None:
         args.steps = DEFAULT_STEPS[args.workload]
@@ -864,7 +884,10 @@ def main() -> int:
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     log(f"device {torch.cuda.get_device_properties(dev).gcnArchName}, workload {args.workload}")
-    r = WORKLOADS[args.workload](args, dev)
+    try:
+        r = WORKLOADS[args.workload](args, dev)
+    except PmcPassDone:
+        return 0
     if r is None:  # a PMC pass printed its own line
         return 0
     line = {

@@ -427,7 +427,9 @@ int mono_layer_clear_errors(mono_layer* layer);
 /* Tests of the fail-stop path (the reference's SGLANG_AMD_MONO_FAULT_INJECT
  * rank:site:after, common/guard.py:79-88): every wait at `site` of every launch from
  * the `after`-th next launch on fails at once, as if its deadline had passed (after 0:
- * the next launch; synchronises when after > 0); site -1 turns it off. */
+ * the next launch; synchronises when after > 0); site -1 turns it off. The fault and
+ * the deadline travel as kernel arguments: a launch captured in a graph keeps the ones
+ * set when it was captured. */
 int mono_layer_set_fault(mono_layer* layer, int32_t site, int64_t after);
 /* Tests of the tag epochs (synchronises): the next launch takes launch ordinal
  * `ordinal`, i.e. tag ordinal % (2^32 - 2) + 1. Every mailbox is zeroed as well, so a

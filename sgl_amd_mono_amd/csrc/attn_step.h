@@ -325,6 +325,19 @@ class Step {
       o.ks[i] = *reinterpret_cast<const uint32_t*>(A.iks + (size_t)(pg[i] * 4 + g) * PAGE + r * 4);
   }
 
+  // key tile kt's logits against the four head tiles of the query
+  MONO_DEV static void score_mfmas(const ScoreOps& o, int kt, f32x4 (&d)[IH / 16]) {
+#pragma unroll
+    for (int ht = 0; ht < IH / 16; ++ht) {
+      switch (kt % 4) {
+        case 0: d[ht] = mfma_fp4_opb<0>(o.qa[ht], o.kb[kt], o.qsc[ht], (int)o.ks[kt / 4]); break;
+        case 1: d[ht] = mfma_fp4_opb<1>(o.qa[ht], o.kb[kt], o.qsc[ht], (int)o.ks[kt / 4]); break;
+        case 2: d[ht] = mfma_fp4_opb<2>(o.qa[ht], o.kb[kt], o.qsc[ht], (int)o.ks[kt / 4]); break;
+        default: d[ht] = mfma_fp4_opb<3>(o.qa[ht], o.kb[kt], o.qsc[ht], (int)o.ks[kt / 4]); break;
+      }
+    }
+  }
+
   // The wave's 128 scores -> mailbox score (lane (g, r) ends with keys k0 + 16 g + r and
   // k0 + 64 + 16 g + r, so each store covers 64 consecutive positions), then the task's
   // histogram of their leading key digits, added into the row's histogram (the top-k's
@@ -342,21 +355,19 @@ class Step {
         wv[ht][2] = bf16_lo(o.w2[ht][1]);
         wv[ht][3] = bf16_hi(o.w2[ht][1]);
       }
+      // a key tile's four head-tile MFMAs are issued together and the next tile's before
+      // this tile's results are consumed, so no MFMA's latency sits in front of its use
+      // (32 MFMAs a wave, each consumed at once, cost ~1 us of exposed latency)
+      f32x4 d[2][IH / 16];
+      score_mfmas(o, 0, d[0]);
 #pragma unroll
       for (int kt = 0; kt < KTILES; ++kt) {
+        if (kt + 1 < KTILES) score_mfmas(o, kt + 1, d[(kt + 1) % 2]);
         float part = 0.f;
 #pragma unroll
-        for (int ht = 0; ht < IH / 16; ++ht) {
-          f32x4 d;
-          switch (kt % 4) {
-            case 0: d = mfma_fp4_opb<0>(o.qa[ht], o.kb[kt], o.qsc[ht], (int)o.ks[kt / 4]); break;
-            case 1: d = mfma_fp4_opb<1>(o.qa[ht], o.kb[kt], o.qsc[ht], (int)o.ks[kt / 4]); break;
-            case 2: d = mfma_fp4_opb<2>(o.qa[ht], o.kb[kt], o.qsc[ht], (int)o.ks[kt / 4]); break;
-            default: d = mfma_fp4_opb<3>(o.qa[ht], o.kb[kt], o.qsc[ht], (int)o.ks[kt / 4]); break;
-          }
+        for (int ht = 0; ht < IH / 16; ++ht)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) part += wv[ht][i] * fmaxf(d[i], 0.f);
-        }
+          for (int i = 0; i < 4; ++i) part += wv[ht][i] * (d[kt % 2][ht][i] > 0.f ? d[kt % 2][ht][i] : 0.f);
         part += __shfl_xor(part, 16, WAVE);  // every lane group now holds key 16 kt + r's sum
         part += __shfl_xor(part, 32, WAVE);
         if (kt % 4 == g) sc[kt / 4] = part;

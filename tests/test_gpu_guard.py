@@ -149,9 +149,11 @@ def test_layer_fault_armed_launches_ahead(gpu_device):
 def test_layer_fault_in_a_replayed_graph_reaches_the_watcher(gpu_device):
     """A step replayed from a HIP graph runs none of the plugin's host code, so the
     per-step check of the spec never sees it. The fail-stop watcher (a host thread on
-    the pinned error word) must: a fault armed two launches ahead stops the third
-    replay, the watcher reports the site once (its default ends the process; here it
-    records), later replays are refused, and after a clear the graph replays correctly."""
+    the pinned error word) must: a fault armed two launches ahead (before the capture,
+    as the served path arms it at build: a launch's fault is one of its kernel
+    arguments, which the graph keeps) stops the third replay, the watcher reports the
+    site once (its default ends the process; here it records), later replays are
+    refused, and after a clear an eager launch gives the first result again."""
     cos, sin = workloads.rope_tables(CTX, gpu_device)
     w = _weights(gpu_device, 95)
     rt = LayerRuntime(4, CTX, gpu_device)
@@ -169,12 +171,13 @@ def test_layer_fault_in_a_replayed_graph_reaches_the_watcher(gpu_device):
         torch.cuda.synchronize()
         rt.check_errors()
         first = out.clone()
+        rt.handle.set_fault(site, after=2)
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
             launch()
         torch.cuda.synchronize()
-        rt.watch(on_fail=seen.append)
-        rt.handle.set_fault(site, after=2)
+        rt.handle.set_fault(-1)  # later eager launches run unarmed; the graph keeps its arguments
+        watch = rt.watch(on_fail=seen.append)
         for k in range(2):
             print(f"[replay fault] replay {k} (armed)", flush=True)
             graph.replay()
@@ -192,12 +195,11 @@ def test_layer_fault_in_a_replayed_graph_reaches_the_watcher(gpu_device):
         print("[replay fault] replay 3 (refused)", flush=True)
         graph.replay()
         torch.cuda.synchronize()
-        assert rt.handle.pending_error() == site + 1 and seen == [site + 1]
+        assert rt.handle.pending_error() == site + 1 and seen == [site + 1] and watch.code == site + 1
         rt.unwatch()
-        rt.handle.set_fault(-1)
         rt.clear_errors()
-        print("[replay fault] replay after clear", flush=True)
-        graph.replay()
+        print("[replay fault] eager launch after clear", flush=True)
+        launch()
         torch.cuda.synchronize()
         rt.check_errors()
         assert torch.equal(out, first)
