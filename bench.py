@@ -524,6 +524,32 @@ def bench_layer(args, dev):
     torch.cuda.synchronize()
     rt.check_errors()
 
+    stacked = args.launch == "stack"
+    stack_parity = None
+    if stacked:
+        # every layer of the step as ONE launch (mono_layer_stack_forward); its output
+        # must equal the chained one-launch-a-layer step's bit for bit
+        chained = x.clone()
+        srt = LayerRuntime(S, ctx, dev, mode="layer", max_layers=L)
+        ws_l = [w for w, _, _ in layers]
+        caches_l = [c for _, _, c in layers]
+        lens_l = [st.seq_lens for _, st, _ in layers]
+        pts_l = [st.page_table for _, st, _ in layers]
+
+        def run_step(marks=None, ticks=None):
+            return srt.forward_layers(x_in, lens_l, pts_l, caches_l, ws_l, cos, sin, check_weights=False,
+                                      ticks=ticks)
+
+        got = run_step()
+        torch.cuda.synchronize()
+        srt.check_errors()
+        stack_parity = bool(torch.equal(got, chained))
+        log(f"stacked step (one launch, {L} layers) equals the chained one-launch-a-layer step: {stack_parity}")
+        if not stack_parity:
+            raise RuntimeError("the stacked step differs from the chained one-launch-a-layer step")
+        rt.close()
+        rt = srt
+
     if args.pmc_pass:
         return pmc_pass(args, dev, run_step, distinct)
     for _ in range(max(args.warmup, 1)):
@@ -556,27 +582,39 @@ def bench_layer(args, dev):
 
     # eager pass with phase events: the breakdown and the MoE launch durations
     n_eager = max(1, min(3, args.steps))
-    phases = rt.phases  # front, then attention + back + MoE (one launch) by default
-    pev = [[[torch.cuda.Event(enable_timing=True) for _ in range(len(phases) + 1)] for _ in range(L)]
-           for _ in range(n_eager)]
-    torch.cuda.synchronize()
-    for k in range(n_eager):
-        x = x_in
-        for l, (w, step, caches) in enumerate(layers):
-            pev[k][l][0].record(stream)
-            x = rt.forward(layer_in(l, x), step.seq_lens, step.page_table, caches, w, cos, sin, out=xb[l % 2],
-                           check_weights=False, on_phase=lambda i, l=l, k=k: pev[k][l][i + 1].record(stream))
-    torch.cuda.synchronize()
-    rt.check_errors()
+    phases = ("layers",) if stacked else rt.phases  # front, then attention + back + MoE (one launch) by default
     ph = {p: [] for p in phases}
-    for k in range(n_eager):
-        for l in range(L):
-            for i, p in enumerate(phases):
-                ph[p].append(pev[k][l][i].elapsed_time(pev[k][l][i + 1]) * 1e3)
+    if stacked:  # one launch a step: an event pair around it, each layer its mean share
+        sev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n_eager)]
+        torch.cuda.synchronize()
+        for k in range(n_eager):
+            sev[k][0].record(stream)
+            run_step()
+            sev[k][1].record(stream)
+        torch.cuda.synchronize()
+        rt.check_errors()
+        step_durs = [a.elapsed_time(b) * 1e3 for a, b in sev]
+        ph["layers"] = [d / L for d in step_durs]
+    else:
+        pev = [[[torch.cuda.Event(enable_timing=True) for _ in range(len(phases) + 1)] for _ in range(L)]
+               for _ in range(n_eager)]
+        torch.cuda.synchronize()
+        for k in range(n_eager):
+            x = x_in
+            for l, (w, step, caches) in enumerate(layers):
+                pev[k][l][0].record(stream)
+                x = rt.forward(layer_in(l, x), step.seq_lens, step.page_table, caches, w, cos, sin, out=xb[l % 2],
+                               check_weights=False, on_phase=lambda i, l=l, k=k: pev[k][l][i + 1].record(stream))
+        torch.cuda.synchronize()
+        rt.check_errors()
+        for k in range(n_eager):
+            for l in range(L):
+                for i, p in enumerate(phases):
+                    ph[p].append(pev[k][l][i].elapsed_time(pev[k][l][i + 1]) * 1e3)
     ph_us = {p: statistics.fmean(v) for p, v in ph.items()}
     eager_layer_us = sum(ph_us.values())
     # one launch a layer: each layer's launch timed alone (an event pair around it, eager)
-    one = rt.launches == 1
+    one = rt.launches == 1 and not stacked
     layer_durs = []
     if one:
         lev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(L)]
@@ -596,11 +634,14 @@ def bench_layer(args, dev):
     # eager pass with in-kernel phase ticks (one launch a layer): the critical path and
     # each phase's span inside the launch
     stamped = None
-    if one:
+    if one or stacked:
         grid = torch.cuda.get_device_properties(dev).multi_processor_count
         ticks = torch.zeros(n_eager, L, grid, 16, dtype=torch.int64, device=dev)
         torch.cuda.synchronize()
         for k in range(n_eager):
+            if stacked:
+                run_step(ticks=ticks[k])
+                continue
             x = x_in
             for l, (w, step, caches) in enumerate(layers):
                 x = rt.forward(layer_in(l, x), step.seq_lens, step.page_table, caches, w, cos, sin, out=xb[l % 2],
@@ -622,15 +663,24 @@ def bench_layer(args, dev):
         phase_bytes["attn_back"] = phase_bytes.pop("attn") + phase_bytes.pop("back")
     if "attn_back_moe" in phases:
         phase_bytes["attn_back_moe"] = phase_bytes.pop("attn") + phase_bytes.pop("back") + phase_bytes.pop("moe")
-    # the dominant launch: the whole layer's (one launch a layer), else the MoE's own
-    dom = "layer" if one else "moe"
-    dom_kernel = {"moe": "k_moe_fp8", "layer": "k_layer"}[dom]
-    dom_fixed = (sum(phase_bytes.values()) if one else phase_bytes["moe"]) - statistics.fmean(moe_b)
+    if stacked:
+        phase_bytes = {"layers": sum(phase_bytes.values())}
+    # the dominant launch: the whole step's (one launch a step), the whole layer's (one
+    # launch a layer), else the MoE's own
+    dom = "stack" if stacked else "layer" if one else "moe"
+    dom_kernel = {"moe": "k_moe_fp8", "layer": "k_layer", "stack": "k_layers"}[dom]
+    dom_fixed = (sum(phase_bytes.values()) if dom != "moe" else phase_bytes["moe"]) - statistics.fmean(moe_b)
     dom_b = [b + dom_fixed for b in moe_b]  # per layer (each layer's own distinct experts)
-    moe_durs = layer_durs if one else ph[dom]
     traffic = read_traffic(dom_kernel)
-    moe_achieved = statistics.fmean(
-        b / (t * 1e-6) for b, t in zip([dom_b[l] for _ in range(n_eager) for l in range(L)], moe_durs)) / 1e9
+    if stacked:  # bytes of every layer over the step launch's duration
+        bytes_launch = sum(dom_b)
+        moe_durs = step_durs
+        moe_achieved = statistics.fmean(bytes_launch / (t * 1e-6) for t in step_durs) / 1e9
+    else:
+        bytes_launch = statistics.fmean(dom_b)
+        moe_durs = layer_durs if one else ph[dom]
+        moe_achieved = statistics.fmean(
+            b / (t * 1e-6) for b, t in zip([dom_b[l] for _ in range(n_eager) for l in range(L)], moe_durs)) / 1e9
     layer_bytes = sum(phase_bytes.values())
     phase_ticks = None
     if stamped is not None:
@@ -655,7 +705,9 @@ def bench_layer(args, dev):
         dtype="fp8_e4m3 weights (bf16 / fp8 MFMA, f32 accumulate), fp4 index, fp8 kv",
         config=dict(workload="BASELINE config 5: full fused decoder layer, one GPU's TP=4 share, 61 stacked layers",
                     rows=S, context=ctx, layers=L, hidden=7168, heads=32, experts=256, top_k=8, shared_experts=1,
-                    inter=512, launches_per_layer=rt.launches, graph=True,
+                    inter=512, launches_per_step=1 if stacked else L * rt.launches, graph=True,
+                    launch=("stack: every layer of the step in ONE persistent launch (k_layers)" if stacked
+                            else "layer: one launch a layer" if one else f"{args.mode}: {rt.launches} a layer"),
                     routing=("uniform: each layer's own independent random rows, router bias 0" if own_rows is not None
                              else "chained: each layer's rows are the previous layer's output")),
         extra=dict(
@@ -664,6 +716,8 @@ def bench_layer(args, dev):
             layer_algorithmic_bytes=layer_bytes, layer_achieved_gbs=layer_bytes / (us * 1e-6) / 1e9,
             phases_us_eager=ph_us, eager_layer_us=eager_layer_us,
             layer_launch_us_eager=statistics.fmean(layer_durs) if one else None,
+            step_launch_us_eager=statistics.fmean(step_durs) if stacked else None,
+            stack_equals_chained_step=stack_parity,
             phases_algorithmic_bytes=phase_bytes,
             phases_achieved_gbs={p: phase_bytes[p] / (ph_us[p] * 1e-6) / 1e9 for p in phases},
             distinct_experts_mean=statistics.fmean(distinct),
@@ -673,8 +727,9 @@ def bench_layer(args, dev):
             bound="hbm", achieved=moe_achieved, peak=HBM_PEAK_GBS, unit="GB/s", frac=moe_achieved / HBM_PEAK_GBS,
             traffic=traffic,
             kernel=(f"{dom_kernel} (the MoE phase: 86% of the layer's bytes)" if dom == "moe" else
+                    f"{dom_kernel} (every decoder layer of the step, one launch)" if dom == "stack" else
                     f"{dom_kernel} (the whole decoder layer, one launch)"),
-            bytes_per_launch=statistics.fmean(dom_b), avg_launch_us=statistics.fmean(moe_durs),
+            bytes_per_launch=bytes_launch, avg_launch_us=statistics.fmean(moe_durs),
         ),
         cpu_baseline=cpu,
     )
@@ -856,6 +911,9 @@ def main() -> int:
     ap.add_argument("--mode", choices=("layer", "attn_back", "split"), default="layer",
                     help="layer workload: the launch split (layer: front + one fused launch of attention, back "
                          "and MoE; attn_back: three launches; split: four)")
+    ap.add_argument("--launch", choices=("stack", "layer"), default=None,
+                    help="layer workload: every layer of a step as ONE persistent launch (stack, the default with "
+                         "--mode layer and chained routing) or one launch (set) a layer")
     ap.add_argument("--sets", type=int, default=2, help="weight sets rotated over the steps")
     ap.add_argument("--batches", type=int, default=16, help="activation batches rotated")
     ap.add_argument("--ctx", type=int, default=32768, help="keys a row (attn workload)")
@@ -867,6 +925,10 @@ def main() -> int:
     args = ap.parse_args()
     if args.steps is None:
         args.steps = DEFAULT_STEPS[args.workload]
+    if args.launch is None:
+        args.launch = "stack" if args.mode == "layer" and args.routing == "chained" else "layer"
+    elif args.launch == "stack" and (args.mode != "layer" or args.routing != "chained"):
+        ap.error("--launch stack runs --mode layer with chained routing")
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:

@@ -44,7 +44,7 @@
 extern "C" {
 #endif
 
-#define MONO_ABI_VERSION 3
+#define MONO_ABI_VERSION 4
 
 enum {
   MONO_OK = 0,
@@ -365,6 +365,7 @@ typedef struct {
   float softmax_scale;  /* (qk_nope + qk_rope)^-1/2 = 192^-1/2 */
   float route_scale;    /* routed_scaling_factor, 2.5 */
   float eps;            /* post-attention RMSNorm epsilon, 1e-6 */
+  int32_t max_layers;   /* most layers of one mono_layer_stack_forward launch (0 or 1: none) */
 } mono_layer_config;
 
 /* One step of one layer: the four parts' arguments as their own entry points take
@@ -411,7 +412,8 @@ int mono_layer_set_deadline(mono_layer* layer, double seconds);
  * output, 5 attention output, 6 router tasks, 7 (not used), 8 expert mid, 9 expert
  * outputs, 10 the attention block's output rows, 11-16 the front's (stage-A partials,
  * q_an, q_nope, raw index query, -, normed input rows), 17 the front's index outputs,
- * 18 the front's q, 31 the tag-epoch scrub. */
+ * 18 the front's q, 19 (a multi-layer launch) the layer before's output rows, 31 the
+ * tag-epoch scrub (and a multi-layer launch's grid meeting before a layer's scrub). */
 int mono_layer_read_errors(mono_layer* layer, int32_t* words);
 /* The layer's pinned host error word, without synchronising: 0, or 1 + the wait site
  * of a launch that failed or was refused since the last clear (-1: not a live layer).
@@ -431,6 +433,26 @@ int mono_layer_clear_errors(mono_layer* layer);
  * the deadline travel as kernel arguments: a launch captured in a graph keeps the ones
  * set when it was captured. */
 int mono_layer_set_fault(mono_layer* layer, int32_t site, int64_t after);
+/* Every decoder layer of one step as ONE persistent launch, in two calls: _stack_set
+ * checks n layers' arguments and keeps them on the device (it synchronises the device;
+ * not during a stream capture), and each _stack_forward launches the layers last set
+ * (stream-ordered, never synchronises; a graph that captured it reads the arguments
+ * last set when it replays). Layer l runs as mono_layer_forward(layer, w[l], args[l])
+ * would, results equal, and reads layer l - 1's output (args[l]->front->h must be
+ * args[l - 1]->moe->out) once that layer's final tasks have announced its rows. No
+ * counterpart in the reference, which launches each layer (glm53/gfx950/runner.py:
+ * 240-321); it removes the launch gap and the launch-counter round trip between layers,
+ * and a layer's front starts its weight loads while the layer before finishes. Every
+ * layer takes its own tag (a launch counts as n launches, rounded up to even, for the
+ * guard) and its own deadline from its start, and fails alone at a wait as its
+ * one-layer launch would; a failed or refused launch writes NaN over the last layer's
+ * output. Layer 0's front->h and every layer's q / iq / iqs / iw, back->a, moe->out and
+ * caches must not overlap (no layer rereads a line a later layer rewrites); ticks,
+ * timelines and debug outputs per layer as mono_layer_forward takes them.
+ * n <= cfg.max_layers. */
+int mono_layer_stack_set(mono_layer* layer, int32_t n_layers, const mono_proj_weights* const* w,
+                         const mono_layer_args* const* args);
+int mono_layer_stack_forward(mono_layer* layer, void* stream);
 /* Tests of the tag epochs (synchronises): the next launch takes launch ordinal
  * `ordinal`, i.e. tag ordinal % (2^32 - 2) + 1. Every mailbox is zeroed as well, so a
  * jump of any length or direction (odd ones change the row histograms' parity) leaves

@@ -11,7 +11,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libmono_gfx950.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 MONO_OK, MONO_EINVAL, MONO_EHIP, MONO_ESTATE, MONO_ENOMEM = 0, 1, 2, 3, 4
 ROUTER_SIGMOID_BIAS, ROUTER_SOFTMAX = 0, 1
@@ -85,7 +85,7 @@ class BackArgs(C.Structure):
 
 class LayerConfig(C.Structure):
     _fields_ = [("device", _I32), ("max_rows", _I32), ("max_ctx", _I32), ("softmax_scale", _F32),
-                ("route_scale", _F32), ("eps", _F32)]
+                ("route_scale", _F32), ("eps", _F32), ("max_layers", _I32)]
 
 
 class LayerArgs(C.Structure):
@@ -132,6 +132,9 @@ SIGNATURES = {
     "mono_layer_forward": (C.c_int, [_VP, C.POINTER(ProjWeights), C.POINTER(LayerArgs), _VP]),
     "mono_layer_front_forward": (C.c_int, [_VP, C.POINTER(ProjWeights), C.POINTER(LayerArgs), _VP]),
     "mono_layer_tail_forward": (C.c_int, [_VP, C.POINTER(ProjWeights), C.POINTER(LayerArgs), _VP]),
+    "mono_layer_stack_set": (C.c_int, [_VP, _I32, C.POINTER(C.POINTER(ProjWeights)),
+                                       C.POINTER(C.POINTER(LayerArgs))]),
+    "mono_layer_stack_forward": (C.c_int, [_VP, _VP]),
     "mono_layer_set_deadline": (C.c_int, [_VP, C.c_double]),
     "mono_layer_read_errors": (C.c_int, [_VP, C.POINTER(C.c_int32)]),
     "mono_layer_pending_error": (C.c_int32, [_VP]),
@@ -153,7 +156,8 @@ PROJ_SITES = {0: "stage-A partial sums", 1: "stage-A q_a tiles", 2: "q_nope", 3:
 LAYER_SITES = {**ATTN_SITES, 4: "W_UV output", 5: "attention output", 6: "router tasks", 7: "(not used)",
                8: "expert mid activations", 9: "expert outputs", 10: "attention block output rows",
                **{11 + k: f"front: {v}" for k, v in {**PROJ_SITES, 5: "normed input rows"}.items()},
-               17: "front index query and keys", 18: "front q", SCRUB_SITE: "tag-epoch scrub"}
+               17: "front index query and keys", 18: "front q",
+               19: "the layer before's output rows (multi-layer launch)", SCRUB_SITE: "tag-epoch scrub"}
 # the front's own sites in a layer runtime's numbering
 LAYER_FRONT_SITE0 = 11
 

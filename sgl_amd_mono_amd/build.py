@@ -42,9 +42,17 @@ COMMON = [
 ]
 
 
+# Per-source flags. The multi-layer kernel runs every phase in a loop over the layers:
+# without machine loop-invariant code motion the compiler keeps each phase's constants
+# where they are used instead of holding them across the loop (they would spill).
+EXTRA = {
+    "layer_stack.hip": ["-mllvm", "-disable-machine-licm"],
+}
+
+
 def _compile(src: Path) -> Path:
     obj = BUILD / (src.stem + src.suffix.replace(".", "_") + ".o")
-    cmd = [hipcc(), *COMMON, "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc(), *COMMON, *EXTRA.get(src.name, []), "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"compiling {src.name} failed:\n{' '.join(cmd)}\n{res.stdout}{res.stderr}")

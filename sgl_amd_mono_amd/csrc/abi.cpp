@@ -814,6 +814,18 @@ struct mono_layer {
   void* extra = nullptr;  // a_done, then the scrub table
   uint64_t* a_done = nullptr;
   mono::GuardArgs guard{};
+  // multi-layer launches (max_layers > 1): each layer's own row histograms and MoE
+  // router outputs (stack_stride bytes a layer), then the final tasks' done words
+  // (scrubbed with every other mailbox); the device table of the layers' kernel
+  // arguments and the host copy of what it holds
+  int max_layers = 0;
+  void* stack_mail = nullptr;
+  size_t stack_stride = 0;
+  size_t stack_o_score = 0, stack_o_xq = 0, stack_o_xs = 0;
+  uint64_t* x_done = nullptr;
+  void* table = nullptr;
+  std::vector<uint8_t> table_host;
+  int stack_n = 0;  // layers of the table's last mono_layer_stack_set (0: none)
 };
 static const uint32_t LAYER_MAGIC = 0x6c617972u;
 static bool layer_live(const mono_layer* L) { return L && L->magic == LAYER_MAGIC; }
@@ -821,6 +833,14 @@ static GuardRef layer_ref(mono_layer* L) { return GuardRef{&L->guard, L->a->devi
 
 static int layer_release(mono_layer* L) {
   int rc = MONO_OK;
+  for (void** pp : {&L->stack_mail, &L->table}) {
+    if (*pp) {
+      hipError_t e = hipFree(*pp);
+      if (e != hipSuccess) rc = fail(MONO_EHIP, "hipFree: %s", hipGetErrorString(e));
+      *pp = nullptr;
+    }
+  }
+  L->x_done = nullptr;
   if (L->extra) {
     hipError_t e = hipFree(L->extra);
     if (e != hipSuccess) rc = fail(MONO_EHIP, "hipFree: %s", hipGetErrorString(e));
@@ -837,12 +857,49 @@ static int layer_release(mono_layer* L) {
   return rc;
 }
 
+constexpr int MAX_STACK_LAYERS = 256;
+
+// A layer runtime's buffers for multi-layer launches: every layer's row histograms and
+// MoE router outputs, the final tasks' done words (one zeroed allocation, the scrub
+// region `rg`) and the device table of the layers' kernel arguments.
+static int stack_alloc(mono_layer* L, int max_layers, mono::ScrubRegion& rg) {
+  using namespace mono;
+  const size_t R = (size_t)L->a->cfg.max_rows;
+  Carve cv;  // a layer's share: rowh at 0, then the router outputs
+  cv.off = 0;
+  cv.take(R * attn::ROWH * 4);
+  L->stack_o_score = cv.take((size_t)moe::MAX_ROWS * 256 * 4);
+  L->stack_o_xq = cv.take((size_t)moe::MAX_ROWS * 7168);
+  L->stack_o_xs = cv.take((size_t)moe::MAX_ROWS * (7168 / 128) * 4);
+  L->stack_stride = align256(cv.off);
+  const size_t bytes = L->stack_stride * (size_t)max_layers + DONE_BYTES;
+  hipError_t e = hipMalloc(&L->stack_mail, bytes);
+  if (e != hipSuccess) {
+    L->stack_mail = nullptr;
+    return fail(MONO_ENOMEM, "hipMalloc(%zu) for the multi-layer mailboxes: %s", bytes, hipGetErrorString(e));
+  }
+  e = hipMemset(L->stack_mail, 0, bytes);
+  if (e != hipSuccess) return fail(MONO_EHIP, "clearing the multi-layer mailboxes: %s", hipGetErrorString(e));
+  L->x_done = reinterpret_cast<uint64_t*>(static_cast<char*>(L->stack_mail) + L->stack_stride * (size_t)max_layers);
+  const size_t tbytes = layer::stack_entry_bytes() * (size_t)max_layers;
+  e = hipMalloc(&L->table, tbytes);
+  if (e != hipSuccess) {
+    L->table = nullptr;
+    return fail(MONO_ENOMEM, "hipMalloc(%zu) for the layers' argument table: %s", tbytes, hipGetErrorString(e));
+  }
+  L->max_layers = max_layers;
+  rg = ScrubRegion{static_cast<uint32_t*>(L->stack_mail), bytes / 16};
+  return MONO_OK;
+}
+
 extern "C" int mono_layer_create(const mono_layer_config* cfg, mono_layer** out) {
   if (!cfg || !out) return fail(MONO_EINVAL, "mono_layer_create: cfg and out must be non-NULL");
   *out = nullptr;
   const mono_layer_config& c = *cfg;
   if (c.max_rows < 1 || c.max_rows > mono::moe::MAX_ROWS)
     return fail(MONO_EINVAL, "max_rows must be in [1, %d], got %d", mono::moe::MAX_ROWS, c.max_rows);
+  if (c.max_layers < 0 || c.max_layers > MAX_STACK_LAYERS)
+    return fail(MONO_EINVAL, "max_layers must be in [0, %d], got %d", MAX_STACK_LAYERS, c.max_layers);
   if (int rc = check_device(c.device)) return rc;
   int per_cu = 0;
   HIP_TRY(mono::layer::tail_occupancy(&per_cu));
@@ -867,11 +924,12 @@ extern "C" int mono_layer_create(const mono_layer_config* cfg, mono_layer** out)
       mono::ScrubRegion table[mono::SCRUB_MAX] = {L->a->mailboxes(), L->p->mailboxes(), L->m->mailboxes(),
                                                   mono::ScrubRegion{reinterpret_cast<uint32_t*>(L->a_done),
                                                                     mono::DONE_BYTES / 16}};
+      if (c.max_layers > 1) rc = stack_alloc(L, c.max_layers, table[4]);
       char* tb = static_cast<char*>(L->extra) + table_off;
-      e = hipMemset(L->extra, 0, table_off + 256);
-      if (e == hipSuccess) e = hipMemcpy(tb, table, sizeof(table), hipMemcpyHostToDevice);
-      if (e == hipSuccess) e = hipDeviceSynchronize();
-      if (e != hipSuccess) rc = fail(MONO_EHIP, "clearing the layer's done words: %s", hipGetErrorString(e));
+      if (!rc) e = hipMemset(L->extra, 0, table_off + 256);
+      if (!rc && e == hipSuccess) e = hipMemcpy(tb, table, sizeof(table), hipMemcpyHostToDevice);
+      if (!rc && e == hipSuccess) e = hipDeviceSynchronize();
+      if (!rc && e != hipSuccess) rc = fail(MONO_EHIP, "clearing the layer's done words: %s", hipGetErrorString(e));
       L->guard = L->a->guard;
       L->guard.scrub = reinterpret_cast<const mono::ScrubRegion*>(tb);
     }
@@ -895,9 +953,8 @@ extern "C" int mono_layer_destroy(mono_layer* L) {
   return rc ? rc : ok();
 }
 
-static int layer_launch(mono_layer* L, const mono_proj_weights* w, const mono_layer_args* args, void* stream,
-                        bool front, bool tail) {
-  if (!layer_live(L)) return fail(MONO_ESTATE, "not a live layer runtime");
+// The checks every layer launch makes of one layer's arguments (the front's too with `front`).
+static int check_layer(mono_layer* L, const mono_proj_weights* w, const mono_layer_args* args, bool front) {
   if (!args || !w || !args->front || !args->attn || !args->back || !args->moe)
     return fail(MONO_EINVAL, "mono_layer_forward: w, args and its four parts must be non-NULL");
   const mono_front_args& f = *args->front;
@@ -914,6 +971,16 @@ static int layer_launch(mono_layer* L, const mono_proj_weights* w, const mono_la
   if (args->moe->a != args->back->a) return fail(MONO_EINVAL, "moe->a must be back->a: the MoE reads the back's output");
   if (int rc = check_attn_back(L->a, args->attn, w, args->back)) return rc;
   if (int rc = check_moe_fp8(L->m, args->moe)) return rc;
+  if (front)
+    if (int rc = check_front(L->p, w, args->front)) return rc;
+  return MONO_OK;
+}
+
+static int layer_launch(mono_layer* L, const mono_proj_weights* w, const mono_layer_args* args, void* stream,
+                        bool front, bool tail) {
+  if (!layer_live(L)) return fail(MONO_ESTATE, "not a live layer runtime");
+  if (int rc = check_layer(L, w, args, front)) return rc;
+  const mono_attn_args& at = *args->attn;
   mono_back_args b = *args->back;
   b.o_lat = at.out;
   const mono::attn::AttnArgs g = attn_args(L->a, at);
@@ -921,7 +988,6 @@ static int layer_launch(mono_layer* L, const mono_proj_weights* w, const mono_la
   const hipStream_t st = static_cast<hipStream_t>(stream);
   hipError_t e;
   if (front) {
-    if (int rc = check_front(L->p, w, args->front)) return rc;
     mono_front_args fa = *args->front;
     int kv_mask = -1;
     if (!fa.kv_scale) {  // raw E4M3 rows: the 1.0 the attention reads too
@@ -954,6 +1020,103 @@ extern "C" int mono_layer_front_forward(mono_layer* L, const mono_proj_weights* 
 extern "C" int mono_layer_tail_forward(mono_layer* L, const mono_proj_weights* w, const mono_layer_args* args,
                                        void* stream) {
   return layer_launch(L, w, args, stream, false, true);
+}
+
+namespace {
+
+// A device range a multi-layer launch writes or rereads: [p, p + bytes), the layer and
+// what it holds (for the error message).
+struct Span {
+  uintptr_t p;
+  size_t bytes;
+  int layer;
+  const char* what;
+};
+
+}  // namespace
+
+extern "C" int mono_layer_stack_set(mono_layer* L, int32_t n, const mono_proj_weights* const* w,
+                                    const mono_layer_args* const* args) {
+  using namespace mono;
+  if (!layer_live(L)) return fail(MONO_ESTATE, "not a live layer runtime");
+  if (L->max_layers < 2) return fail(MONO_ESTATE, "the layer runtime was created without max_layers (> 1)");
+  if (n < 1 || n > L->max_layers)
+    return fail(MONO_EINVAL, "n_layers must be in [1, %d] (the runtime's max_layers), got %d", L->max_layers, n);
+  if (!w || !args) return fail(MONO_EINVAL, "mono_layer_stack_set: w and args must be non-NULL");
+  std::vector<Span> spans;
+  for (int l = 0; l < n; ++l) {
+    if (int rc = check_layer(L, w[l], args[l], true)) {
+      const std::string why = g_error;
+      return fail(rc, "layer %d: %s", l, why.c_str());
+    }
+    const mono_front_args& f = *args[l]->front;
+    const size_t r = (size_t)f.rows, pages = (size_t)f.n_pages;
+    if (l > 0 && f.h != args[l - 1]->moe->out)
+      return fail(MONO_EINVAL, "layer %d: front->h must be layer %d's moe->out", l, l - 1);
+    if (l == 0) spans.push_back({(uintptr_t)f.h, r * 7168 * 2, l, "front->h"});
+    spans.push_back({(uintptr_t)f.q, r * 32 * 576 * 2, l, "q"});
+    spans.push_back({(uintptr_t)f.iq, r * 64 * 32, l, "iq"});
+    spans.push_back({(uintptr_t)f.iqs, r * 64 * 4, l, "iqs"});
+    spans.push_back({(uintptr_t)f.iw, r * 64 * 2, l, "iw"});
+    spans.push_back({(uintptr_t)f.kv, pages * 64 * 576, l, "kv"});
+    spans.push_back({(uintptr_t)f.ikv, pages * 4 * 64 * 16, l, "ikv"});
+    spans.push_back({(uintptr_t)f.iks, pages * 4 * 64, l, "iks"});
+    if (f.kv_scale) spans.push_back({(uintptr_t)f.kv_scale, pages * 64 * 4, l, "kv_scale"});
+    spans.push_back({(uintptr_t)args[l]->back->a, r * 7168 * 2, l, "back->a"});
+    spans.push_back({(uintptr_t)args[l]->moe->out, r * 7168 * 2, l, "moe->out"});
+  }
+  std::sort(spans.begin(), spans.end(), [](const Span& x, const Span& y) { return x.p < y.p; });
+  for (size_t i = 1; i < spans.size(); ++i) {
+    const Span& x = spans[i - 1];
+    const Span& y = spans[i];
+    if (x.p + x.bytes > y.p)
+      return fail(MONO_EINVAL,
+                  "layer %d's %s overlaps layer %d's %s: a multi-layer launch needs each layer's outputs and "
+                  "caches in buffers of their own",
+                  x.layer, x.what, y.layer, y.what);
+  }
+  const size_t eb = layer::stack_entry_bytes();
+  std::vector<uint8_t> table(eb * (size_t)n, 0);
+  for (int l = 0; l < n; ++l) {
+    const mono_layer_args& la = *args[l];
+    const mono_attn_args& at = *la.attn;
+    mono_back_args b = *la.back;
+    b.o_lat = at.out;
+    const attn::AttnArgs g = attn_args(L->a, at);
+    const moe::MoeFp8Args m(*la.moe, L->m->cfg.route_scale, L->m->cfg.eps);
+    mono_front_args fa = *la.front;
+    int kv_mask = -1;
+    if (!fa.kv_scale) {
+      fa.kv_scale = L->a->unit;
+      kv_mask = 0;
+    }
+    char* mail = static_cast<char*>(L->stack_mail) + L->stack_stride * (size_t)l;
+    const layer::StackLayer sl{reinterpret_cast<uint32_t*>(mail), reinterpret_cast<float*>(mail + L->stack_o_score),
+                               reinterpret_cast<uint8_t*>(mail + L->stack_o_xq),
+                               reinterpret_cast<float*>(mail + L->stack_o_xs), l + 1 < n ? L->x_done : nullptr,
+                               l > 0 ? L->x_done : nullptr};
+    hipError_t e = layer::stack_fill(table.data() + eb * (size_t)l, sl, *w[l], fa, L->p->mail, kv_mask, g,
+                                     L->a->mail, L->guard, b, L->a->back_mail, m, L->m->mail, L->a_done, la.ticks);
+    if (e != hipSuccess) return fail(MONO_EINVAL, "layer %d: %s", l, hipGetErrorString(e));
+  }
+  if (int rc = check_device(L->a->device)) return rc;
+  // launches in flight may still read the table
+  HIP_TRY(hipDeviceSynchronize());
+  HIP_TRY(hipMemcpy(L->table, table.data(), table.size(), hipMemcpyHostToDevice));
+  L->table_host.swap(table);
+  L->stack_n = n;
+  return ok();
+}
+
+extern "C" int mono_layer_stack_forward(mono_layer* L, void* stream) {
+  using namespace mono;
+  if (!layer_live(L)) return fail(MONO_ESTATE, "not a live layer runtime");
+  if (L->stack_n < 1) return fail(MONO_ESTATE, "mono_layer_stack_forward: no layers set (mono_layer_stack_set)");
+  if (int rc = check_device(L->a->device)) return rc;
+  const hipError_t e = layer::stack_forward(L->table, L->stack_n, (uint32_t)(L->a->cfg.max_rows * attn::ROWH),
+                                            L->guard, L->a->grid, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(MONO_EHIP, "launching the layers: %s", hipGetErrorString(e));
+  return ok();
 }
 
 extern "C" int mono_layer_set_deadline(mono_layer* L, double seconds) {

@@ -132,6 +132,10 @@ struct Args {
   const uint64_t* fdone;
   int fsite;
   bool publish_out;  // a later stage of the launch reads `out`: each merge puts a done word
+  // the row histograms: 1, two copies by launch parity (each launch clears its
+  // successor's copy, the guard's flip words); 0, one copy that the launch's caller
+  // clears once every reader is done (a layer of a multi-layer launch)
+  int rowh_flip;
   Mail mail;
   GuardArgs guard;
 };
@@ -172,7 +176,7 @@ MONO_DEV u32x2 fp8x4_bf16(uint32_t w) {
 class Step {
  public:
   MONO_DEV Step(const Args& a, Lds& l) : A(a), L(l) {
-    tid = threadIdx.x;
+    tid = thread_index();
     lane = tid % WAVE;
     wave = tid / WAVE;
     g = lane / 16;
@@ -194,6 +198,9 @@ class Step {
   // start clears the copy the next launch adds into.
   MONO_DEV bool begin() { return guard_begin(A.guard, gd); }
 
+  // Run under a guard the caller set up (a layer of a multi-layer launch).
+  MONO_DEV void adopt(const Guard& g) { gd = g; }
+
   MONO_DEV const Guard& guard() const { return gd; }
 
   // tasks in the list: score tasks padded to a multiple of TEAM so no top-k team
@@ -206,7 +213,7 @@ class Step {
     const int n_sc = n_score(), n_topk = A.rows * TEAM;
     const int n_split = A.rows * SPLITS;
     const int total = n_tasks();
-    if (!score_stage(blockIdx.x, A.rows * CH)) return false;
+    if (!score_stage(block_index(), A.rows * CH)) return false;
     // a workgroup's list is ordered by stage: one loop a stage keeps each loop body to
     // one task kind (and its registers)
     int T = first_at_or_after(n_sc);
@@ -245,7 +252,7 @@ class Step {
   // row s's leading-digit histogram of the launch with this tag: launches alternate
   // between two copies, and each launch clears the copy its successor uses
   MONO_DEV uint32_t* row_hist(uint32_t tag, int s) const {
-    return A.mail.rowh + ((size_t)(tag & 1u) * A.mail.max_rows + s) * ROWH;
+    return A.mail.rowh + ((size_t)(A.rowh_flip ? tag & 1u : 0u) * A.mail.max_rows + s) * ROWH;
   }
   MONO_DEV int page_of(int s, int p) const {
     const int pg = A.pt[(size_t)s * A.pt_stride + p / PAGE];
@@ -255,7 +262,7 @@ class Step {
 
   // this workgroup's first task at or after list index `at` (tasks are dealt round-robin)
   MONO_DEV int first_at_or_after(int at) const {
-    const int b = blockIdx.x;
+    const int b = block_index();
     return at <= b ? b : b + ((at - b + G - 1) / G) * G;
   }
 
@@ -267,7 +274,7 @@ class Step {
       tl[0] = (int64_t)t0;
       tl[1] = (int64_t)waited;
       tl[2] = (int64_t)now_ticks();
-      tl[3] = ((int64_t)blockIdx.x << 8) | kind;
+      tl[3] = ((int64_t)block_index() << 8) | kind;
     }
   }
   MONO_DEV void mark_waited() { waited = now_ticks(); }
@@ -1040,6 +1047,7 @@ void fill_args(Args& a, const AttnArgs& g, const Mail& mail, const GuardArgs& gu
   a.timeline = g.timeline;
   a.scale = g.softmax_scale;
   a.publish_out = false;
+  a.rowh_flip = 1;
   a.fdone = nullptr;
   a.fsite = 0;
   a.mail = mail;

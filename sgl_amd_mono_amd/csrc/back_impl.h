@@ -45,7 +45,7 @@ struct Args {
 class Back {
  public:
   MONO_DEV Back(const Args& args, Lds& l) : W(args.w), A(args.a), M(args.mail), L(l) {
-    tid = threadIdx.x;
+    tid = thread_index();
     lane = tid % WAVE;
     wave = tid / WAVE;
     g = lane / 16;
@@ -82,7 +82,7 @@ class Back {
   // This workgroup's tasks when the list's first task sits at index `base` of a longer
   // list dealt round-robin over the grid (false, workgroup-uniform: a wait failed).
   MONO_DEV bool tasks(int base) {
-    const int b = blockIdx.x;
+    const int b = block_index();
     int T = base <= b ? b : b + ((base - b + G - 1) / G) * G;
     for (; T < base + N_TASKS; T += G) {
       const int t = T - base;
@@ -112,7 +112,7 @@ class Back {
       tl[0] = (int64_t)t0;
       tl[1] = (int64_t)waited;
       tl[2] = (int64_t)now_ticks();
-      tl[3] = ((int64_t)blockIdx.x << 8) | kind;
+      tl[3] = ((int64_t)block_index() << 8) | kind;
     }
   }
 

@@ -9,6 +9,32 @@
 
 #define MONO_DEV __device__ __forceinline__
 
+// The thread's and the workgroup's indices. A translation unit that runs the phases in
+// a loop over layers (the multi-layer launch) defines MONO_LAYER_LOOP first: the indices
+// then pass an opaque copy at each use, so the compiler cannot hoist per-thread and
+// per-workgroup arithmetic out of that loop (held across every phase, it spills).
+MONO_DEV int thread_index() {
+#ifdef MONO_LAYER_LOOP
+  int t = (int)threadIdx.x;
+  asm volatile("" : "+v"(t));
+  __builtin_assume(t >= 0 && t < 1024);
+  return t;
+#else
+  return (int)threadIdx.x;
+#endif
+}
+MONO_DEV unsigned block_index() {
+#ifdef MONO_LAYER_LOOP
+  int b = (int)blockIdx.x;
+  asm volatile("" : "+v"(b));
+  b = __builtin_amdgcn_readfirstlane(b);  // uniform: scalar arithmetic and branches
+  __builtin_assume(b >= 0 && b < 65536);
+  return (unsigned)b;
+#else
+  return blockIdx.x;
+#endif
+}
+
 typedef int32_t i32x8 __attribute__((ext_vector_type(8)));
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));

@@ -83,12 +83,19 @@ struct Args {
   GuardArgs guard;
   int kv_mask;  // -1: per-token power-of-two scales into a.kv_scale; 0: raw E4M3 rows
   int site0;    // the launch's first wait site (a layer's guard numbers the front's after its own)
+  // the rows h come from an earlier layer of the launch: its final tasks' replicated done
+  // words (h_done_n of them), awaited at wait site h_site before h is read (NULL: none)
+  const uint64_t* h_done;
+  int h_done_n;
+  int h_site;
 };
 
 class Front {
  public:
-  MONO_DEV Front(const Args& args, Lds& l) : W(args.w), A(args.a), M(args.mail), L(l), kv_mask(args.kv_mask) {
-    tid = threadIdx.x;
+  MONO_DEV Front(const Args& args, Lds& l)
+      : W(args.w), A(args.a), M(args.mail), L(l), kv_mask(args.kv_mask), h_done(args.h_done),
+        h_done_n(args.h_done_n), h_site(args.h_site) {
+    tid = thread_index();
     lane = tid % WAVE;
     wave = tid / WAVE;
     g = lane / 16;
@@ -108,10 +115,12 @@ class Front {
   MONO_DEV void poison(bool share) const { poison_bf16(A.q, (size_t)S * HEADS * (KV_LORA + PE_DIM), share); }
 
   // Run under another phase's guard in the same launch (its tag, deadline and fail
-  // word; wait sites offset by site_base).
-  MONO_DEV void adopt(const Guard& g, int site_base) {
+  // word; wait sites offset by site_base). `h_ready`: the rows h are known to be stored
+  // (a grid barrier met since), so the earlier layer's done words are not awaited.
+  MONO_DEV void adopt(const Guard& g, int site_base, bool h_ready = false) {
     gd = g;
     site0 = site_base;
+    if (h_ready) h_done = nullptr;
   }
 
   // This workgroup's tasks (false, workgroup-uniform: a wait failed).
@@ -119,14 +128,14 @@ class Front {
     for (int p = tid; p < ROW_PIECES; p += FT)
       *reinterpret_cast<u32x4*>(&L.gin[8 * p]) = ld_u32x4(static_cast<const uint16_t*>(W.g_in) + 8 * p);
     __syncthreads();
-    for (int T = blockIdx.x;; T += G) {
+    for (int T = block_index();; T += G) {
       relane();
       int t = T, kind;
       bool ok = true;
       const uint64_t t0 = now_ticks();
       if (t < S) {
         kind = 5;
-        norm_row(t);
+        ok = norm_row(t);
       } else if ((t -= S) < nt_a(S)) {
         kind = 0;
         ok = stage_a(t);
@@ -157,6 +166,8 @@ class Front {
   const Mail& M;
   Lds& L;
   const int kv_mask;
+  const uint64_t* h_done;
+  const int h_done_n, h_site;
   int site0;
   GuardArgs guard_args;
   Guard gd;
@@ -167,7 +178,7 @@ class Front {
   // compiler cannot hoist each stage's per-thread address arithmetic out of the task
   // loop (held across all stages, it spills).
   MONO_DEV void relane() {
-    int t = (int)threadIdx.x;
+    int t = thread_index();
     asm volatile("" : "+v"(t));
     tid = t;
     lane = t % WAVE;
@@ -183,7 +194,7 @@ class Front {
       tl[0] = (int64_t)t0;
       tl[1] = (int64_t)waited;
       tl[2] = (int64_t)now_ticks();
-      tl[3] = ((int64_t)blockIdx.x << 8) | kind;
+      tl[3] = ((int64_t)block_index() << 8) | kind;
     }
   }
   MONO_DEV void mark_waited() { waited = now_ticks(); }
@@ -307,7 +318,14 @@ class Front {
   // row's squares (lane pieces lane + 64 m in order, then the wave sum); every thread
   // writes bf16(x rstd gamma) of its pieces to xn with device-coherent stores; after
   // they complete, the row's done word.
-  MONO_DEV void norm_row(int s) {
+  MONO_DEV bool norm_row(int s) {
+    if (h_done) {  // the rows come from the layer before in this launch: its tag (a tag
+                   // epoch's first layer scrubs after a grid barrier and does not wait here)
+      Guard before = gd;
+      before.tag = gd.tag - 1u;
+      const uint64_t* hd = done_copy(h_done);
+      if (!hint_wait(h_done_n, [hd](int i) { return hd + i; }, h_site, before)) return false;
+    }
     const uint16_t* hrow = static_cast<const uint16_t*>(A.h) + (size_t)s * HIDDEN;
     if (wave == 0) {
       u32x4 x[RPL];
@@ -340,6 +358,7 @@ class Front {
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();  // the row is stored (and L.stat is free again)
     put_done(M.xdone, s, gd.tag);
+    return true;
   }
 
   // The task's K part [k0, k0 + kw) of every normed row into LDS (row stride `stride`),

@@ -88,7 +88,7 @@ MONO_DEV void plan_from_picks(PlanLds<E, TOPK>& P, int S);
 template <int E, int TOPK, int THREADS>
 MONO_DEV void plan_from_picks(PlanLds<E, TOPK>& P, int S) {
   static_assert(THREADS >= E && THREADS / WAVE <= 16, "one thread an expert");
-  const int tid = threadIdx.x, lane = tid % WAVE, wave = tid / WAVE;
+  const int tid = thread_index(), lane = tid % WAVE, wave = tid / WAVE;
   for (int e = tid; e < E; e += THREADS) P.used[e] = 0u;
   __syncthreads();
   if (tid < S * TOPK) {

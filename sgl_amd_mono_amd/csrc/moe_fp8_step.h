@@ -120,6 +120,9 @@ struct Args {
   // the fused layer's phase ticks ([grid][16], NULL: none): workgroup b stamps word
   // 16 b + k at MoE moment k (T_* below)
   int64_t* ticks;
+  // a later layer of the launch reads `out`: each final task puts a replicated done word
+  // once its rows are stored (NULL: none)
+  uint64_t* out_done;
   Mail mail;
   GuardArgs guard;
 };
@@ -135,7 +138,7 @@ enum { T_PLAN = 4, T_A = 6, T_NORM = 7, T_ROUTER = 8, T_GATHER = 9, T_ROUTE = 10
 class Step {
  public:
   MONO_DEV Step(const Args& a, Lds& l) : A(a), L(l) {
-    tid = threadIdx.x;
+    tid = thread_index();
     lane = tid % WAVE;
     wave = __builtin_amdgcn_readfirstlane(tid / WAVE);  // uniform: wave arithmetic stays scalar
     g = lane / 16;
@@ -164,7 +167,7 @@ class Step {
     }
     // the first router task's weights and the route's biases go out before anything waits
     const int n_rt = RT_EG * ((S + RT_S - 1) / RT_S);
-    int t = blockIdx.x;
+    int t = block_index();
     u32x4 wr[RT_E][2], gr[2];
     if (t < n_rt) router_load(t, wr, gr);
     const f32x4 bias4 = *reinterpret_cast<const f32x4*>(A.bias + 4 * lane);
@@ -178,7 +181,7 @@ class Step {
       stamp(T_A);
     }
     for (; t < n_rt; t += G) {
-      if (t != (int)blockIdx.x) router_load(t, wr, gr);
+      if (t != (int)block_index()) router_load(t, wr, gr);
       router_task(t, wr, gr);
     }
     stamp(T_ROUTER);
@@ -190,7 +193,7 @@ class Step {
     __builtin_amdgcn_s_waitcnt(0);  // the gather's DMA into LDS (and the scale stores) done
     __syncthreads();
     // a shared-expert tile needs no plan: its loads go out before the plan is built
-    if ((int)blockIdx.x < NT) load_task(K_UP, blockIdx.x);
+    if ((int)block_index() < NT) load_task(K_UP, block_index());
     plan_from_picks<E, TOPK, FT>(L.plan, S);
     stamp(T_PLAN);
     return tasks();
@@ -201,7 +204,7 @@ class Step {
 
   // this workgroup's tick at MoE moment k (a fused layer with ticks only)
   MONO_DEV void stamp(int k) const {
-    if (A.ticks && tid == 0) A.ticks[blockIdx.x * T_ROW + k] = (int64_t)now_ticks();
+    if (A.ticks && tid == 0) A.ticks[block_index() * T_ROW + k] = (int64_t)now_ticks();
   }
 
  private:
@@ -263,7 +266,7 @@ class Step {
       for (int w = 0; w < FW; ++w) ss += L.rt.rss[w][si];
       rstd[si] = hw_rsq(ss * (1.0f / H) + A.eps);
     }
-    if (t == (int)blockIdx.x) stamp(T_NORM);
+    if (t == (int)block_index()) stamp(T_NORM);
     // the task's FP8 chunk: row s0 + cu / RCH, chunk cu % RCH (eg < RT_S RCH only)
     const int cu = eg < RT_S * RCH ? eg : -1;
     float acc[RT_E][RT_S];
@@ -392,7 +395,7 @@ class Step {
         raw[i] = sc[k][i];
         key[i] = radix_key(raw[i] + bias[i]);
       }
-      if (A.scores && blockIdx.x == 0) *reinterpret_cast<f32x4*>(&A.scores[s * E + 4 * lane]) = sc[k];
+      if (A.scores && block_index() == 0) *reinterpret_cast<f32x4*>(&A.scores[s * E + 4 * lane]) = sc[k];
       float my_raw;  // lane k < TOPK: the raw score and id of pick k
       int my_id;
       wave_topk<TOPK>(key, id, raw, E, my_id, my_raw);
@@ -403,7 +406,7 @@ class Step {
       if (lane < TOPK) {
         L.plan.pick_id[s][lane] = my_id;
         L.plan.pick_w[s][lane] = w;
-        if (blockIdx.x == 0) {
+        if (block_index() == 0) {
           if (A.topk_ids) A.topk_ids[s * TOPK + lane] = my_id;
           if (A.topk_w) A.topk_w[s * TOPK + lane] = w;
         }
@@ -439,7 +442,7 @@ class Step {
   // Each turn: consume the task's weights (waiting on its inputs), issue the next
   // task's weight loads, then publish the task's results while those loads fly.
   MONO_DEV bool tasks() {
-    int T = blockIdx.x;  // a shared-expert tile's loads (T < NT) went out before the plan
+    int T = block_index();  // a shared-expert tile's loads (T < NT) went out before the plan
     int kind = classify(T);
     if (T >= NT) load_task(kind, T);
     // consecutive up tiles, half by half: the next tile's first half goes out once this
@@ -669,7 +672,7 @@ class Step {
     bool ok = true;
     // the thread's row and column re-derived from an opaque copy of its index: hoisted
     // out of the task loop, the row's offset would be held (and spilled) across tasks
-    int t = (int)threadIdx.x;
+    int t = thread_index();
     asm volatile("" : "+v"(t));
     if (t < S * FIN_ROWS) {
       const int s = t / FIN_ROWS, h = f * FIN_ROWS + t % FIN_ROWS;
@@ -686,11 +689,16 @@ class Step {
 #pragma unroll
         for (int k = 0; k < NSLOT; ++k) y += __uint_as_float(v[k]);
         const float res = bf16_bits_to_f32(A.a[(size_t)s * H + h]);
-        A.out[(size_t)s * H + h] = f32_to_bf16_bits(res + y);
+        // write-through: a later layer of a multi-layer launch reads the rows
+        __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16_bits(res + y), coherent_rsrc(A.out, (uint32_t)(S * H * 2)),
+                                              (s * H + h) * 2, 0, SC1);
         if (A.y_out) A.y_out[(size_t)s * H + h] = y;
       }
     }
-    return block_all(ok);
+    if (A.out_done) __builtin_amdgcn_s_waitcnt(0);  // the rows are stored before the done word
+    const bool all = block_all(ok);
+    if (all && A.out_done) put_done(A.out_done, f, gd.tag);
+    return all;
   }
 };
 
@@ -713,6 +721,7 @@ void fill_args(Args& a, const MoeFp8Args& g, const Mail& mail, const GuardArgs& 
   a.route_scale = g.route_scale;
   a.eps = g.eps;
   a.ticks = nullptr;
+  a.out_done = nullptr;
   a.mail = mail;
   a.guard = guard;
 }

@@ -63,7 +63,7 @@ constexpr int POLL_CHECK = 32;
 constexpr uint64_t TAG_PERIOD = 0xFFFFFFFEull;
 // the wait site of the scrub barrier
 constexpr int SCRUB_SITE = 31;
-constexpr int SCRUB_MAX = 4;
+constexpr int SCRUB_MAX = 5;
 
 // A device region of mailboxes the scrub zeroes: n16 16-byte units at p.
 struct ScrubRegion {
@@ -143,9 +143,10 @@ constexpr size_t DONE_STRIDE = 4096 / sizeof(uint64_t);
 constexpr size_t DONE_BYTES = DONE_REPLICAS * 4096;
 // thread k < DONE_REPLICAS of the calling workgroup puts copy k of done word i
 MONO_DEV void put_done(uint64_t* base, int i, uint32_t tag) {
-  if ((int)threadIdx.x < DONE_REPLICAS) mb_put(base + threadIdx.x * DONE_STRIDE + i, 0u, tag);
+  const int t = thread_index();
+  if (t < DONE_REPLICAS) mb_put(base + t * DONE_STRIDE + i, 0u, tag);
 }
-MONO_DEV const uint64_t* done_copy(const uint64_t* base) { return base + (blockIdx.x % DONE_REPLICAS) * DONE_STRIDE; }
+MONO_DEV const uint64_t* done_copy(const uint64_t* base) { return base + (block_index() % DONE_REPLICAS) * DONE_STRIDE; }
 
 // Copy an error code to the host's pinned error word: a plain system-scope store (no
 // atomic read-modify-write over the bus; the device's sticky error word keeps the
@@ -161,26 +162,40 @@ struct Guard {
   uint32_t* host_err;
   uint64_t deadline;  // absolute s_memrealtime tick
   uint32_t tag;
+#ifdef MONO_LAYER_LOOP
+  uint32_t ltag;  // the launch's first tag (its first layer's)
+#endif
   int fault;  // this launch's host-forced fault site (-1: none)
+
+  // What a failure records and the peers' check compares: the launch's first tag, the
+  // same for every layer of a multi-layer launch (a one-layer launch has only `tag`).
+  MONO_DEV uint32_t launch_tag() const {
+#ifdef MONO_LAYER_LOOP
+    return ltag;
+#else
+    return tag;
+#endif
+  }
 
   // Record a failure at `site` (first one wins) and raise the launch's fail tag.
   MONO_DEV void fail(int site) const {
     uint32_t expect = 0;
     if (__hip_atomic_compare_exchange_strong(&words[G_ERROR], &expect, (uint32_t)site + 1u, __ATOMIC_RELAXED,
                                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
-      __hip_atomic_store(&words[G_FAIL_BLOCK], (uint32_t)blockIdx.x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(&words[G_FAIL_BLOCK], (uint32_t)block_index(), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       report_host(host_err, (uint32_t)site + 1u);
     }
-    __hip_atomic_store(&words[G_FAIL_TAG], tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(&words[G_FAIL_TAG], launch_tag(), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   // True (and the failure recorded) once the deadline has passed; with `peers`, also
-  // once another workgroup of this launch has failed (one more memory round trip).
+  // once another workgroup of this launch has failed, in any of its layers (one more
+  // memory round trip).
   MONO_DEV bool expired(int site, bool peers) const {
     if (now_ticks() > deadline) {
       fail(site);
       return true;
     }
-    return peers && ld_agent_u32(&words[G_FAIL_TAG]) == tag;
+    return peers && ld_agent_u32(&words[G_FAIL_TAG]) == launch_tag();
   }
 };
 
@@ -278,7 +293,7 @@ MONO_DEV bool poll_word(const uint64_t* p, uint32_t& v, int site, const Guard& g
 template <class At>
 MONO_DEV bool hint_wait(int n, At at, int site, const Guard& g) {
   bool ok = true;
-  for (int i = threadIdx.x; i < n; i += blockDim.x) {
+  for (int i = thread_index(); i < n; i += blockDim.x) {
     uint32_t v;
     ok = poll_word(at(i), v, site, g) && ok;
   }
@@ -288,13 +303,14 @@ MONO_DEV bool hint_wait(int n, At at, int site, const Guard& g) {
 // Workgroup-uniform AND of a per-thread flag (a full barrier).
 MONO_DEV bool block_all(bool ok) { return __syncthreads_and(ok ? 1 : 0) != 0; }
 
-// Zero the guard's mailboxes (the first launch of a tag epoch), then meet every
-// workgroup of the grid: each adds one to guard word 6 once its zeros are stored and
-// waits until the launch's G arrivals are in (every scrub adds exactly G, so the count
-// is a multiple of G between scrubs). Workgroup-uniform result.
+MONO_DEV bool grid_barrier(const Guard& gd, bool epoch);
+
+// Zero the guard's mailboxes (the first launch or layer of a tag epoch), then meet every
+// workgroup of the grid once its zeros are stored (grid_barrier). Workgroup-uniform
+// result.
 MONO_DEV bool scrub_mailboxes(const GuardArgs& a, const Guard& gd) {
   const uint32_t n_threads = gridDim.x * blockDim.x;
-  const uint32_t me = blockIdx.x * blockDim.x + threadIdx.x;
+  const uint32_t me = block_index() * blockDim.x + (uint32_t)thread_index();
   const u32x4 zero = {0u, 0u, 0u, 0u};
   for (int k = 0; k < SCRUB_MAX; ++k) {
     const ScrubRegion rg = a.scrub[k];
@@ -306,9 +322,17 @@ MONO_DEV bool scrub_mailboxes(const GuardArgs& a, const Guard& gd) {
   }
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
+  return grid_barrier(gd, true);
+}
+
+// Meet every workgroup of the grid: each adds one to guard word 6 and waits until the
+// meeting's G arrivals are in (every meeting adds exactly G, so the count is a multiple
+// of G between meetings). `epoch` (a scrub): workgroup 0 first counts a tag epoch and
+// clears the fail tag. Workgroup-uniform result.
+MONO_DEV bool grid_barrier(const Guard& gd, bool epoch) {
   __shared__ uint32_t target;
-  if (threadIdx.x == 0) {
-    if (blockIdx.x == 0) {
+  if (thread_index() == 0) {
+    if (epoch && block_index() == 0) {
       (void)__hip_atomic_fetch_add(&gd.words[G_EPOCH], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       // a failure's tag of the old epoch must not read as this epoch's (a guard that
       // runs on after a failure reaches the wrap); stored before this workgroup arrives
@@ -321,7 +345,7 @@ MONO_DEV bool scrub_mailboxes(const GuardArgs& a, const Guard& gd) {
   }
   __syncthreads();
   bool ok = true;
-  if (threadIdx.x == 0) {
+  if (thread_index() == 0) {
     const uint32_t want = target;
     for (uint32_t spin = 0;; ++spin) {
       if ((int32_t)(ld_agent_u32(&gd.words[G_BARRIER]) - want) >= 0) break;
@@ -344,30 +368,37 @@ struct GuardFetch {
   uint64_t ord;
   uint32_t err;
 };
-MONO_DEV GuardFetch guard_fetch(const GuardArgs& a) {
+// A launch that runs `count` layers takes `count` ordinals at once (one tag a layer).
+MONO_DEV GuardFetch guard_fetch(const GuardArgs& a, uint64_t count = 1) {
   GuardFetch f{0, 0u};
-  if (threadIdx.x == 0) {
-    f.ord = __hip_atomic_fetch_add(a.tickets + blockIdx.x, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (thread_index() == 0) {
+    f.ord = __hip_atomic_fetch_add(a.tickets + block_index(), count, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     f.err = a.sticky ? ld_agent_u32(&a.words[G_ERROR]) : 0u;
   }
   return f;
 }
 
-// The start of every launch, called by every thread of the workgroup with what
-// guard_fetch returned: set up the guard (tag, deadline, this launch's forced fault),
-// scrub the mailboxes at the start of a tag epoch and clear the successor's copy of the
-// flip accumulators. False (workgroup-uniform) if the guard's sticky error refuses the
-// launch (a refused launch reports the error to the host word) or the scrub failed.
-MONO_DEV bool guard_begin(const GuardArgs& a, Guard& gd, const GuardFetch& f) {
-  __shared__ uint32_t sh[4];
-  if (threadIdx.x == 0) {
-    const uint64_t ord = f.ord;
-    if (blockIdx.x == 0)
-      __hip_atomic_store(reinterpret_cast<uint64_t*>(&a.words[G_TICKET]), ord + 1, __ATOMIC_RELAXED,
+// Layer l of a launch that took `count` ordinals from f (guard_fetch): layer l runs as
+// ordinal f.ord + l, with its own tag, deadline and forced fault, and scrubs the
+// mailboxes if its ordinal starts a tag epoch. The first layer also reports the launches
+// begun to the host and refuses the launch under a standing sticky error. A guard with
+// flip accumulators (a one-layer launch) also clears its successor's copy of them. A
+// scrub at a later layer first meets the whole grid, so no workgroup still works on the
+// layers before when the mailboxes are zeroed; `scrubbed` (if given) reports a scrub.
+MONO_DEV bool guard_layer(const GuardArgs& a, Guard& gd, const GuardFetch& f, int l, uint64_t count,
+                          bool* scrubbed = nullptr) {
+  __shared__ uint32_t sh[5];
+  if (thread_index() == 0) {
+    const uint64_t ord = f.ord + (uint64_t)l;
+#ifdef MONO_LAYER_LOOP
+    sh[4] = (uint32_t)(f.ord % TAG_PERIOD) + 1u;
+#endif
+    if (block_index() == 0 && l == 0)
+      __hip_atomic_store(reinterpret_cast<uint64_t*>(&a.words[G_TICKET]), f.ord + count, __ATOMIC_RELAXED,
                          __HIP_MEMORY_SCOPE_AGENT);
     const uint64_t in_epoch = ord % TAG_PERIOD;
     sh[0] = (uint32_t)in_epoch + 1u;
-    sh[1] = f.err;
+    sh[1] = l == 0 ? f.err : 0u;
     sh[2] = ord >= a.fault_from ? 1u : 0u;
     sh[3] = (in_epoch == 0 && ord != 0) ? 1u : 0u;
   }
@@ -375,23 +406,35 @@ MONO_DEV bool guard_begin(const GuardArgs& a, Guard& gd, const GuardFetch& f) {
   gd.words = a.words;
   gd.host_err = a.host_err;
   gd.tag = sh[0];
+#ifdef MONO_LAYER_LOOP
+  gd.ltag = sh[4];
+#endif
   gd.deadline = now_ticks() + a.deadline_ticks;
   gd.fault = sh[2] ? a.fault_site : -1;
   const uint32_t err = sh[1];
   const bool scrub = sh[3] != 0;
-  __syncthreads();  // sh is read before any later launch's use of it
+  __syncthreads();  // sh is read before any later layer's or launch's use of it
   if (err != 0) {
-    if (threadIdx.x == 0) report_host(a.host_err, err);
+    if (thread_index() == 0) report_host(a.host_err, err);
     return false;
   }
+  if (scrubbed) *scrubbed = scrub;
+  if (scrub && l > 0 && !grid_barrier(gd, false)) return false;
   if (scrub && !scrub_mailboxes(a, gd)) return false;
   if (a.flip) {
     uint32_t* nx = a.flip + (size_t)((gd.tag + 1u) & 1u) * a.flip_words;
-    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < a.flip_words; i += gridDim.x * blockDim.x)
+    for (int i = block_index() * blockDim.x + thread_index(); i < a.flip_words; i += gridDim.x * blockDim.x)
       __hip_atomic_store(&nx[i], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   return true;
 }
+
+// The start of every launch, called by every thread of the workgroup with what
+// guard_fetch returned: set up the guard (tag, deadline, this launch's forced fault),
+// scrub the mailboxes at the start of a tag epoch and clear the successor's copy of the
+// flip accumulators. False (workgroup-uniform) if the guard's sticky error refuses the
+// launch (a refused launch reports the error to the host word) or the scrub failed.
+MONO_DEV bool guard_begin(const GuardArgs& a, Guard& gd, const GuardFetch& f) { return guard_layer(a, gd, f, 0, 1); }
 MONO_DEV bool guard_begin(const GuardArgs& a, Guard& gd) { return guard_begin(a, gd, guard_fetch(a)); }
 
 // A launch that failed or was refused writes NaN over its bf16 output (n elements at p):
@@ -404,7 +447,7 @@ MONO_DEV void poison_bf16(void* p, size_t n, bool share) {
   uint32_t* w = static_cast<uint32_t*>(p);
   const size_t words = n / 2;
   const size_t step = share ? (size_t)gridDim.x * blockDim.x : blockDim.x;
-  for (size_t i = (share ? blockIdx.x * blockDim.x : 0) + threadIdx.x; i < words; i += step) w[i] = 0x7fc07fc0u;
+  for (size_t i = (share ? block_index() * blockDim.x : 0) + (size_t)thread_index(); i < words; i += step) w[i] = 0x7fc07fc0u;
 }
 
 }  // namespace mono

@@ -273,14 +273,14 @@ class LayerHandle(Runtime):
     PREFIX = "mono_layer"
     KIND = "layer"
 
-    def __init__(self, max_rows: int, max_ctx: int, device=None):
+    def __init__(self, max_rows: int, max_ctx: int, device=None, max_layers: int = 0):
         from .attn import SOFTMAX_SCALE
         from .moe import FP8_MOE
 
         super().__init__(device)
         self._create(_lib.LayerConfig(device=self.device.index, max_rows=max_rows, max_ctx=max_ctx,
                                       softmax_scale=SOFTMAX_SCALE, route_scale=FP8_MOE.route_scale,
-                                      eps=FP8_MOE.eps))
+                                      eps=FP8_MOE.eps, max_layers=max_layers))
 
     SITES = _lib.LAYER_SITES
 
@@ -375,7 +375,7 @@ class LayerRuntime:
              "split": ("front", "attn", "back", "moe")}
 
     def __init__(self, max_rows: int = 8, max_ctx: int = 32768, device=None, mode: str = "layer",
-                 fused: bool | None = None):
+                 fused: bool | None = None, max_layers: int = 0):
         from .attn import AttnRuntime
         from .moe import FP8_MOE, MoeRuntime
 
@@ -385,10 +385,14 @@ class LayerRuntime:
             raise ValueError(f"mode must be one of {sorted(self.MODES)}, got {mode!r}")
         if not 1 <= max_rows <= MAX_ROWS:
             raise ValueError(f"max_rows must be in [1, {MAX_ROWS}], got {max_rows}")
+        if max_layers and mode != "layer":
+            raise ValueError("max_layers (the multi-layer launch) needs mode 'layer'")
         self.mode = mode
         self.max_rows, self.max_ctx = max_rows, max_ctx
+        self.max_layers = max_layers
+        self._stack_key = None
         if mode == "layer":
-            self.handle = LayerHandle(max_rows, max_ctx, device)
+            self.handle = LayerHandle(max_rows, max_ctx, device, max_layers)
             self.device = self.handle.device
             self.parts = (self.handle,)
         else:
@@ -405,6 +409,10 @@ class LayerRuntime:
         self._front = FrontOut.empty(max_rows, self.device)
         self._o_lat = torch.empty(max_rows, HEADS, KV_LORA, dtype=torch.bfloat16, device=self.device)
         self._a = torch.empty(max_rows, HIDDEN, dtype=torch.bfloat16, device=self.device)
+        if max_layers:  # the multi-layer launch's buffers: each layer's own
+            self._fronts = [FrontOut.empty(max_rows, self.device) for _ in range(max_layers)]
+            self._as = torch.empty(max_layers, max_rows, HIDDEN, dtype=torch.bfloat16, device=self.device)
+            self._xs = torch.empty(max_layers, max_rows, HIDDEN, dtype=torch.bfloat16, device=self.device)
 
     def close(self) -> None:
         self.unwatch()
@@ -513,6 +521,81 @@ class LayerRuntime:
         inter = dict(q=fo.q.clone(), iq=fo.iq.clone(), iqs=fo.iqs.clone(), iw=fo.iw.clone(), o_lat=o_lat.clone(),
                      a=a.clone(), index_scores=adbg["scores"], topk_slots=adbg["topk"], **mdbg)
         return x, inter
+
+    def forward_layers(self, h: torch.Tensor, seq_lens, page_table, caches, ws, rope_cos: torch.Tensor,
+                       rope_sin: torch.Tensor, out: torch.Tensor | None = None, check_weights: bool = True,
+                       ticks: torch.Tensor | None = None) -> torch.Tensor:
+        """x_out [rows, 7168] bf16 of ``len(ws)`` decoder layers applied in turn to rows
+        ``h`` as ONE persistent launch (mono_layer_stack_forward): layer l runs as
+        ``forward`` would with ``ws[l]`` and ``caches[l]`` (each layer's own caches) and
+        takes layer l - 1's output rows, results equal layer by layer. ``seq_lens`` and
+        ``page_table`` are one tensor for every layer or a sequence of one a layer.
+        ``ticks`` (int64 [layers, grid, 16]) receives each layer's phase ticks.
+
+        The layers' arguments are packed and uploaded (mono_layer_stack_set, which
+        synchronises the device) only when the buffers change: the key is the objects
+        passed (held here while they are the last set) and the data pointers of h, out
+        and ticks, so a caller that swaps a tensor inside a weights or caches object it
+        passed again calls ``reset_layers()`` first. No other call synchronises, so a
+        step can be captured in a HIP graph once its arguments are set (a replay reads
+        the arguments last set)."""
+        from .attn import AttnStep, attn_args
+        from .moe import fp8_args
+
+        n = len(ws)
+        if not 1 <= n <= self.max_layers:
+            raise ValueError(f"{n} layers: the runtime takes 1 to max_layers = {self.max_layers} a launch")
+        if len(caches) != n:
+            raise ValueError(f"caches: expected {n} (one a layer), got {len(caches)}")
+        lens = list(seq_lens) if isinstance(seq_lens, (list, tuple)) else [seq_lens] * n
+        tables = list(page_table) if isinstance(page_table, (list, tuple)) else [page_table] * n
+        if len(lens) != n or len(tables) != n:
+            raise ValueError(f"seq_lens / page_table: one tensor or {n} (one a layer)")
+        S = _rows(h, "h", self.max_rows)
+        x_last = self._xs[n - 1, :S] if out is None else out
+        P = _lib.ptr
+        key = (n, S, P(h), P(x_last), P(ticks), P(rope_cos), P(rope_sin), tuple(map(id, ws)),
+               tuple(map(id, caches)), tuple(map(id, lens)), tuple(map(id, tables)))
+        if key != self._stack_key:
+            dev = self.device
+            if ticks is not None:
+                grid = torch.cuda.get_device_properties(dev).multi_processor_count
+                need(ticks, "ticks", (n, grid, _lib.LAYER_TICK_WORDS), torch.int64, dev)
+            keep, wps, lps = [], [], []
+            x = h
+            for l in range(n):
+                fr = self._fronts[l]
+                fo = FrontOut(q=fr.q[:S], iq=fr.iq[:S], iqs=fr.iqs[:S], iw=fr.iw[:S])
+                fargs, _, wst = front_args(dev, self.max_rows, x, lens[l], tables[l], caches[l], ws[l].proj,
+                                           rope_cos, rope_sin, fo, check_weights, None)
+                step = AttnStep(iq=fo.iq, iqs=fo.iqs, iw=fo.iw, q=fo.q, page_table=tables[l], seq_lens=lens[l])
+                aargs, o_lat, _ = attn_args(dev, self.max_rows, self.max_ctx, step, caches[l], self._o_lat[:S],
+                                            False, None)
+                a = self._as[l, :S]
+                bargs = _lib.BackArgs(o_lat=P(o_lat), h=P(x), a=P(a), o=None, rows=S, timeline=None)
+                xo = x_last if l == n - 1 else self._xs[l, :S]
+                margs, _, _ = fp8_args(dev, self.max_rows, self.geo, a, ws[l].moe, xo, False)
+                largs = _lib.LayerArgs(C.pointer(fargs), C.pointer(aargs), C.pointer(bargs), C.pointer(margs),
+                                       None if ticks is None else P(ticks[l]))
+                keep.append((fargs, aargs, bargs, margs, largs, wst))
+                wps.append(C.pointer(wst))
+                lps.append(C.pointer(largs))
+                x = xo
+            warr = (C.POINTER(_lib.ProjWeights) * n)(*wps)
+            larr = (C.POINTER(_lib.LayerArgs) * n)(*lps)
+            self._stack_key = None
+            with torch.cuda.device(self.device):
+                _lib.check(_lib.lib().mono_layer_stack_set(self.handle._h, n, warr, larr))
+            # the objects whose ids make the key stay alive while it is the last set
+            self._stack_key, self._stack_refs = key, (ws, caches, lens, tables, keep)
+        _lib.check(_lib.lib().mono_layer_stack_forward(self.handle._h, self.handle._stream()))
+        return x_last
+
+    def reset_layers(self) -> None:
+        """Forget the multi-layer launch's packed arguments: the next forward_layers
+        packs and uploads them again."""
+        self._stack_key = None
+        self._stack_refs = None
 
     def check_errors(self) -> None:
         for rt in self.parts:
