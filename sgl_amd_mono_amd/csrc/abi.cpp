@@ -21,6 +21,7 @@
 #include "mono.h"
 #include "moe_ops.h"
 #include "proj_ops.h"
+#include "row_ssq.h"
 
 namespace {
 
@@ -815,14 +816,14 @@ struct mono_layer {
   uint64_t* a_done = nullptr;
   mono::GuardArgs guard{};
   // multi-layer launches (max_layers > 1): each layer's own row histograms and MoE
-  // router outputs (stack_stride bytes a layer), then the final tasks' done words
-  // (scrubbed with every other mailbox); the device table of the layers' kernel
-  // arguments and the host copy of what it holds
+  // router outputs (stack_stride bytes a layer), then the final tasks' tagged tile sums
+  // of squares (scrubbed with every other mailbox); the device table of the layers'
+  // kernel arguments and the host copy of what it holds
   int max_layers = 0;
   void* stack_mail = nullptr;
   size_t stack_stride = 0;
   size_t stack_o_score = 0, stack_o_xq = 0, stack_o_xs = 0;
-  uint64_t* x_done = nullptr;
+  uint64_t* x_ssq = nullptr;
   void* table = nullptr;
   std::vector<uint8_t> table_host;
   int stack_n = 0;  // layers of the table's last mono_layer_stack_set (0: none)
@@ -840,7 +841,7 @@ static int layer_release(mono_layer* L) {
       *pp = nullptr;
     }
   }
-  L->x_done = nullptr;
+  L->x_ssq = nullptr;
   if (L->extra) {
     hipError_t e = hipFree(L->extra);
     if (e != hipSuccess) rc = fail(MONO_EHIP, "hipFree: %s", hipGetErrorString(e));
@@ -872,7 +873,8 @@ static int stack_alloc(mono_layer* L, int max_layers, mono::ScrubRegion& rg) {
   L->stack_o_xq = cv.take((size_t)moe::MAX_ROWS * 7168);
   L->stack_o_xs = cv.take((size_t)moe::MAX_ROWS * (7168 / 128) * 4);
   L->stack_stride = align256(cv.off);
-  const size_t bytes = L->stack_stride * (size_t)max_layers + DONE_BYTES;
+  const size_t ssq_bytes = (size_t)moe::MAX_ROWS * SSQ_TILES * sizeof(uint64_t);
+  const size_t bytes = L->stack_stride * (size_t)max_layers + ssq_bytes;
   hipError_t e = hipMalloc(&L->stack_mail, bytes);
   if (e != hipSuccess) {
     L->stack_mail = nullptr;
@@ -880,7 +882,7 @@ static int stack_alloc(mono_layer* L, int max_layers, mono::ScrubRegion& rg) {
   }
   e = hipMemset(L->stack_mail, 0, bytes);
   if (e != hipSuccess) return fail(MONO_EHIP, "clearing the multi-layer mailboxes: %s", hipGetErrorString(e));
-  L->x_done = reinterpret_cast<uint64_t*>(static_cast<char*>(L->stack_mail) + L->stack_stride * (size_t)max_layers);
+  L->x_ssq = reinterpret_cast<uint64_t*>(static_cast<char*>(L->stack_mail) + L->stack_stride * (size_t)max_layers);
   const size_t tbytes = layer::stack_entry_bytes() * (size_t)max_layers;
   e = hipMalloc(&L->table, tbytes);
   if (e != hipSuccess) {
@@ -1093,8 +1095,8 @@ extern "C" int mono_layer_stack_set(mono_layer* L, int32_t n, const mono_proj_we
     char* mail = static_cast<char*>(L->stack_mail) + L->stack_stride * (size_t)l;
     const layer::StackLayer sl{reinterpret_cast<uint32_t*>(mail), reinterpret_cast<float*>(mail + L->stack_o_score),
                                reinterpret_cast<uint8_t*>(mail + L->stack_o_xq),
-                               reinterpret_cast<float*>(mail + L->stack_o_xs), l + 1 < n ? L->x_done : nullptr,
-                               l > 0 ? L->x_done : nullptr};
+                               reinterpret_cast<float*>(mail + L->stack_o_xs), l + 1 < n ? L->x_ssq : nullptr,
+                               l > 0 ? L->x_ssq : nullptr};
     hipError_t e = layer::stack_fill(table.data() + eb * (size_t)l, sl, *w[l], fa, L->p->mail, kv_mask, g,
                                      L->a->mail, L->guard, b, L->a->back_mail, m, L->m->mail, L->a_done, la.ticks);
     if (e != hipSuccess) return fail(MONO_EINVAL, "layer %d: %s", l, hipGetErrorString(e));

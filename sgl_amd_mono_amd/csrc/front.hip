@@ -31,8 +31,7 @@ hipError_t front_forward(const mono_proj_weights& w, const mono_front_args& a, i
   args.guard = guard;
   args.kv_mask = kv_mask;
   args.site0 = site0;
-  args.h_done = nullptr;
-  args.h_done_n = 0;
+  args.h_ssq = nullptr;
   args.h_site = 0;
   k_front<<<grid, FT, 0, st>>>(args);
   return hipGetLastError();

@@ -29,6 +29,7 @@
 #include "common.h"
 #include "proj_common.h"
 #include "proj_ops.h"
+#include "row_ssq.h"
 #include "sync.h"
 
 namespace mono {
@@ -55,6 +56,10 @@ constexpr int MAX_STEPS_W = 7;               // 128-k steps a wave of a stage-A 
 constexpr float EPS = 1e-6f;
 constexpr float LN_EPS = 1e-6f;
 constexpr float INDEX_W_SCALE = 0.011048543456039804f;  // 128^-1/2 * 64^-1/2
+static_assert(SSQ_COLS == HIDDEN, "the shared sum-of-squares order covers the input rows");
+
+// a row's input-RMSNorm factor from its sum of squares
+MONO_DEV float row_rstd(float ssq) { return 1.0f / sqrtf(ssq / (float)HIDDEN + EPS); }
 static_assert(ROW_PIECES % WAVE == 0 && KPW <= MAX_PARTS, "stage A split");
 
 // FP8 tiles of stage A are split in K in kp_fp8(S) parts: whole (8 rows of K fit the
@@ -73,6 +78,7 @@ struct Lds {
   } u;
   f32x4 red[FW][WAVE];
   float stat[FW][2];
+  float tsum[SSQ_PIECES / 4];  // a norm task's tile sums of squares (zeros past the row)
   uint16_t gin[HIDDEN];  // the input RMSNorm weight, loaded once a launch
 };
 
@@ -83,18 +89,19 @@ struct Args {
   GuardArgs guard;
   int kv_mask;  // -1: per-token power-of-two scales into a.kv_scale; 0: raw E4M3 rows
   int site0;    // the launch's first wait site (a layer's guard numbers the front's after its own)
-  // the rows h come from an earlier layer of the launch: its final tasks' replicated done
-  // words (h_done_n of them), awaited at wait site h_site before h is read (NULL: none)
-  const uint64_t* h_done;
-  int h_done_n;
+  // the rows h come from the layer before in this launch: its final tasks' tile sums of
+  // squares (tagged words [MAX_ROWS][SSQ_TILES], that layer's tag), awaited at wait site
+  // h_site by the norm tasks, which take each row's rstd from them (NULL: the norm tasks
+  // form it from the row)
+  const uint64_t* h_ssq;
   int h_site;
 };
 
 class Front {
  public:
   MONO_DEV Front(const Args& args, Lds& l)
-      : W(args.w), A(args.a), M(args.mail), L(l), kv_mask(args.kv_mask), h_done(args.h_done),
-        h_done_n(args.h_done_n), h_site(args.h_site) {
+      : W(args.w), A(args.a), M(args.mail), L(l), kv_mask(args.kv_mask), h_ssq(args.h_ssq),
+        h_site(args.h_site) {
     tid = thread_index();
     lane = tid % WAVE;
     wave = tid / WAVE;
@@ -116,11 +123,12 @@ class Front {
 
   // Run under another phase's guard in the same launch (its tag, deadline and fail
   // word; wait sites offset by site_base). `h_ready`: the rows h are known to be stored
-  // (a grid barrier met since), so the earlier layer's done words are not awaited.
+  // (a grid barrier met since, whose scrub zeroed the tile sums), so the norm tasks
+  // normalise them as in a one-layer launch.
   MONO_DEV void adopt(const Guard& g, int site_base, bool h_ready = false) {
     gd = g;
     site0 = site_base;
-    if (h_ready) h_done = nullptr;
+    if (h_ready) h_ssq = nullptr;
   }
 
   // This workgroup's tasks (false, workgroup-uniform: a wait failed).
@@ -166,8 +174,8 @@ class Front {
   const Mail& M;
   Lds& L;
   const int kv_mask;
-  const uint64_t* h_done;
-  const int h_done_n, h_site;
+  const uint64_t* h_ssq;
+  const int h_site;
   int site0;
   GuardArgs guard_args;
   Guard gd;
@@ -314,49 +322,101 @@ class Front {
   }
 
   // Stage N, row s: the input RMSNorm (glm53/gfx950/kernel.py:1367-1398) once for every
-  // stage-A task. Wave 0 sums the
-  // row's squares (lane pieces lane + 64 m in order, then the wave sum); every thread
-  // writes bf16(x rstd gamma) of its pieces to xn with device-coherent stores; after
-  // they complete, the row's done word.
+  // stage-A task (a stacked layer's from the layer before's tile sums, norm_from_tiles).
+  // The row's sum of squares in the order every path shares
+  // (row_ssq.h: a 16-byte piece a thread, four threads a tile, wave 0 the tiles); every
+  // thread writes bf16(x rstd gamma) of its pieces to xn with device-coherent stores;
+  // after they complete, the row's done word.
   MONO_DEV bool norm_row(int s) {
-    if (h_done) {  // the rows come from the layer before in this launch: its tag (a tag
-                   // epoch's first layer scrubs after a grid barrier and does not wait here)
-      Guard before = gd;
-      before.tag = gd.tag - 1u;
-      const uint64_t* hd = done_copy(h_done);
-      if (!hint_wait(h_done_n, [hd](int i) { return hd + i; }, h_site, before)) return false;
-    }
+    if (h_ssq) return norm_from_tiles(s);
     const uint16_t* hrow = static_cast<const uint16_t*>(A.h) + (size_t)s * HIDDEN;
+    static_assert(SSQ_PIECES == 2 * FT, "two 16-byte pieces a thread");
+    u32x4 x[2];
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      const int p = tid + FT * m;
+      x[m] = ld_u32x4(hrow + 8 * min(p, ROW_PIECES - 1));
+    }
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      const int p = tid + FT * m;
+      const float t = tile_sum_of_pieces(p < ROW_PIECES ? piece_sum_of_squares(x[m]) : 0.f);
+      if (lane % 4 == 0) L.tsum[p / 4] = t;
+    }
+    __syncthreads();
     if (wave == 0) {
-      u32x4 x[RPL];
-#pragma unroll
-      for (int m = 0; m < RPL; ++m) x[m] = ld_u32x4(hrow + 8 * (lane + WAVE * m));
-      float ss = 0.f;
-#pragma unroll
-      for (int m = 0; m < RPL; ++m)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) ss += bf16_lo(x[m][e]) * bf16_lo(x[m][e]) + bf16_hi(x[m][e]) * bf16_hi(x[m][e]);
-      ss = wave_sum(ss);
-      if (lane == 0) L.stat[0][0] = 1.0f / sqrtf(ss / (float)HIDDEN + EPS);
+      const float r = row_rstd(tiles_sum(L.tsum[4 * lane], L.tsum[4 * lane + 1], L.tsum[4 * lane + 2],
+                                         L.tsum[4 * lane + 3]));
+      if (lane == 0) L.stat[0][0] = r;
     }
     __syncthreads();
     mark_waited();
     const float rstd = L.stat[0][0];
     const __amdgpu_buffer_rsrc_t rs = coherent_rsrc(M.xn + (size_t)s * (HIDDEN / 2), HIDDEN * 2);
-    for (int p = tid; p < ROW_PIECES; p += FT) {
-      const u32x4 x = ld_u32x4(hrow + 8 * p);
-      const u32x4 gw = *reinterpret_cast<const u32x4*>(&L.gin[8 * p]);
-      u32x4 o;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float y0 = mul_rn(mul_rn(bf16_lo(x[e]), rstd), bf16_lo(gw[e]));
-        const float y1 = mul_rn(mul_rn(bf16_hi(x[e]), rstd), bf16_hi(gw[e]));
-        o[e] = pack_bf16x2(y0, y1);
+    for (int m = 0; m < 2; ++m) {
+      const int p = tid + FT * m;
+      if (p < ROW_PIECES) {
+        const u32x4 gw = *reinterpret_cast<const u32x4*>(&L.gin[8 * p]);
+        __builtin_amdgcn_raw_buffer_store_b128(normed8(x[m], gw, rstd), rs, p * 16, 0, SC1);
       }
-      __builtin_amdgcn_raw_buffer_store_b128(o, rs, p * 16, 0, SC1);
     }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();  // the row is stored (and L.stat is free again)
+    put_done(M.xdone, s, gd.tag);
+    return true;
+  }
+
+  // bf16(x rstd gamma) of 8 columns (the RMSNorm's rounding points, kernel.py:1367-1415)
+  MONO_DEV static u32x4 normed8(const u32x4& x, const u32x4& gw, float rstd) {
+    u32x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float y0 = mul_rn(mul_rn(bf16_lo(x[e]), rstd), bf16_lo(gw[e]));
+      const float y1 = mul_rn(mul_rn(bf16_hi(x[e]), rstd), bf16_hi(gw[e]));
+      o[e] = pack_bf16x2(y0, y1);
+    }
+    return o;
+  }
+
+  // Norm task of row s in a stacked layer: thread f < 224 polls the layer before's tile
+  // sum f of the row (a tagged word of that layer's tag, wait site h_site; it certifies
+  // the tile's 32 columns stored) and then loads those columns, so the row comes in
+  // while the last tiles land; the row's rstd follows from the tile sums in the shared
+  // order, and the normed tile goes to xn as norm_row writes it.
+  MONO_DEV bool norm_from_tiles(int s) {
+    Guard before = gd;
+    before.tag = gd.tag - 1u;
+    const uint16_t* hrow = static_cast<const uint16_t*>(A.h) + (size_t)s * HIDDEN;
+    bool ok = true;
+    u32x4 x[4];
+    if (tid < SSQ_PIECES / 4) {
+      uint32_t v = 0;
+      if (tid < SSQ_TILES) ok = poll_word(&h_ssq[(size_t)s * SSQ_TILES + tid], v, h_site, before);
+      L.tsum[tid] = __uint_as_float(v);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) x[q] = ld_u32x4(hrow + 8 * (4 * min(tid, SSQ_TILES - 1) + q));
+    }
+    if (!block_all(ok)) return false;
+    mark_waited();
+    if (wave == 0) {
+      const float r = row_rstd(tiles_sum(L.tsum[4 * lane], L.tsum[4 * lane + 1], L.tsum[4 * lane + 2],
+                                         L.tsum[4 * lane + 3]));
+      if (lane == 0) L.stat[0][0] = r;
+    }
+    __syncthreads();
+    const float rstd = L.stat[0][0];
+    if (tid < SSQ_TILES) {
+      const __amdgpu_buffer_rsrc_t rs = coherent_rsrc(M.xn + (size_t)s * (HIDDEN / 2), HIDDEN * 2);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int p = 4 * tid + q;
+        const u32x4 gw = *reinterpret_cast<const u32x4*>(&L.gin[8 * p]);
+        __builtin_amdgcn_raw_buffer_store_b128(normed8(x[q], gw, rstd), rs, p * 16, 0, SC1);
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();  // the row is stored (and L.stat, L.tsum are free again)
     put_done(M.xdone, s, gd.tag);
     return true;
   }

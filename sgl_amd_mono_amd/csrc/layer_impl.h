@@ -106,8 +106,7 @@ hipError_t fill_layer(LayerArgs& a, const mono_proj_weights& w, const mono_front
   a.fr.guard = guard;
   a.fr.kv_mask = kv_mask;
   a.fr.site0 = FRONT_SITE0;
-  a.fr.h_done = nullptr;
-  a.fr.h_done_n = 0;
+  a.fr.h_ssq = nullptr;
   a.fr.h_site = 0;
   attn::fill_args(a.tail.at, g, amail, guard);
   a.tail.at.publish_out = true;

@@ -22,15 +22,15 @@ constexpr int STACK_H_SITE = 19;
 
 // A layer's own buffers in a multi-layer launch (its table entry points at them): its
 // row histograms, its MoE router outputs (read with plain loads, so no two layers of a
-// launch share them), the done words its final tasks put (NULL: the last layer) and
-// those its front awaits (NULL: the first layer).
+// launch share them), the tile sums of squares its final tasks put (NULL: the last
+// layer) and those its stage A awaits (NULL: the first layer).
 struct StackLayer {
   uint32_t* rowh;
   float* score;
   uint8_t* xq;
   float* xs;
-  uint64_t* out_done;
-  const uint64_t* h_done;
+  uint64_t* out_ssq;
+  const uint64_t* h_ssq;
 };
 
 // workgroups a CU holds of the least of the layer's launches (the multi-layer one too)
@@ -50,8 +50,6 @@ hipError_t layer_forward(const mono_proj_weights& w, const mono_front_args& f, c
                          const moe::Mail& mmail, uint64_t* a_done, int64_t* ticks, int grid, hipStream_t st);
 // bytes of one layer's entry in a multi-layer launch's table
 size_t stack_entry_bytes();
-// the final tasks a layer has (the done words its output rows are announced by)
-int moe_fin_tasks();
 // Fill a table entry (host memory of stack_entry_bytes()) with one layer's arguments,
 // as layer_forward takes them, on the layer's own buffers `sl`.
 hipError_t stack_fill(void* entry, const StackLayer& sl, const mono_proj_weights& w, const mono_front_args& f,

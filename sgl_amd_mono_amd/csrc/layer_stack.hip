@@ -66,8 +66,6 @@ hipError_t stack_occupancy(int* blocks_per_cu) {
   return hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, k_layers, 512, 0);
 }
 
-int moe_fin_tasks() { return moe::FIN_TASKS; }
-
 size_t stack_entry_bytes() { return sizeof(LayerArgs); }
 
 hipError_t stack_fill(void* entry, const StackLayer& sl, const mono_proj_weights& w, const mono_front_args& f,
@@ -84,9 +82,8 @@ hipError_t stack_fill(void* entry, const StackLayer& sl, const mono_proj_weights
   a.tail.mo.mail.score = sl.score;
   a.tail.mo.mail.xq = sl.xq;
   a.tail.mo.mail.xs = sl.xs;
-  a.tail.mo.out_done = sl.out_done;
-  a.fr.h_done = sl.h_done;
-  a.fr.h_done_n = sl.h_done ? moe_fin_tasks() : 0;
+  a.tail.mo.out_ssq = sl.out_ssq;
+  a.fr.h_ssq = sl.h_ssq;
   a.fr.h_site = STACK_H_SITE;
   return hipSuccess;
 }

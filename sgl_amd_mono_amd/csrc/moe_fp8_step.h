@@ -46,6 +46,7 @@
 #include "moe_common.h"
 #include "moe_ops.h"
 #include "moe_plan.h"
+#include "row_ssq.h"
 #include "sync.h"
 
 namespace mono {
@@ -120,9 +121,10 @@ struct Args {
   // the fused layer's phase ticks ([grid][16], NULL: none): workgroup b stamps word
   // 16 b + k at MoE moment k (T_* below)
   int64_t* ticks;
-  // a later layer of the launch reads `out`: each final task puts a replicated done word
-  // once its rows are stored (NULL: none)
-  uint64_t* out_done;
+  // a later layer of the launch reads `out`: once its rows are stored, each final task
+  // puts its 32 columns' sum of squares of every row as a tagged word
+  // [MAX_ROWS][SSQ_TILES] (row_ssq.h; NULL: none)
+  uint64_t* out_ssq;
   Mail mail;
   GuardArgs guard;
 };
@@ -674,6 +676,7 @@ class Step {
     // out of the task loop, the row's offset would be held (and spilled) across tasks
     int t = thread_index();
     asm volatile("" : "+v"(t));
+    float tile = 0.f;  // the row's sum of squares over this task's columns (out_ssq)
     if (t < S * FIN_ROWS) {
       const int s = t / FIN_ROWS, h = f * FIN_ROWS + t % FIN_ROWS;
       const uint64_t* base = &A.mail.ypart[(size_t)s * H + h];
@@ -689,15 +692,19 @@ class Step {
 #pragma unroll
         for (int k = 0; k < NSLOT; ++k) y += __uint_as_float(v[k]);
         const float res = bf16_bits_to_f32(A.a[(size_t)s * H + h]);
+        const uint16_t o = f32_to_bf16_bits(res + y);
         // write-through: a later layer of a multi-layer launch reads the rows
-        __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16_bits(res + y), coherent_rsrc(A.out, (uint32_t)(S * H * 2)),
-                                              (s * H + h) * 2, 0, SC1);
+        __builtin_amdgcn_raw_buffer_store_b16(o, coherent_rsrc(A.out, (uint32_t)(S * H * 2)), (s * H + h) * 2, 0, SC1);
         if (A.y_out) A.y_out[(size_t)s * H + h] = y;
+        if (A.out_ssq) tile = bf16_bits_to_f32(o);
       }
+      static_assert(FIN_ROWS == SSQ_TILE && FIN_TASKS == SSQ_TILES, "a final task is a tile of the rows");
+      if (A.out_ssq) tile = tile_sum_of_columns(tile);  // a row's 32 columns are a half wave
     }
-    if (A.out_done) __builtin_amdgcn_s_waitcnt(0);  // the rows are stored before the done word
+    if (A.out_ssq) __builtin_amdgcn_s_waitcnt(0);  // the rows are stored before their tile sums
     const bool all = block_all(ok);
-    if (all && A.out_done) put_done(A.out_done, f, gd.tag);
+    if (all && A.out_ssq && t < S * FIN_ROWS && t % FIN_ROWS == 0)
+      mb_put(&A.out_ssq[(size_t)(t / FIN_ROWS) * SSQ_TILES + f], __float_as_uint(tile), gd.tag);
     return all;
   }
 };
@@ -721,7 +728,7 @@ void fill_args(Args& a, const MoeFp8Args& g, const Mail& mail, const GuardArgs& 
   a.route_scale = g.route_scale;
   a.eps = g.eps;
   a.ticks = nullptr;
-  a.out_done = nullptr;
+  a.out_ssq = nullptr;
   a.mail = mail;
   a.guard = guard;
 }
