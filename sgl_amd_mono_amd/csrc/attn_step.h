@@ -207,9 +207,17 @@ class Step {
   // straddles a round, then top-k members, splits, merges
   MONO_DEV int n_score() const { return (A.rows * CH + TEAM - 1) / TEAM * TEAM; }
   MONO_DEV int n_tasks() const { return n_score() + A.rows * TEAM + A.rows * SPLITS + A.rows * NH; }
+  MONO_DEV int n_topk() const { return A.rows * TEAM; }
 
   // This workgroup's tasks (false, workgroup-uniform: a wait failed).
   MONO_DEV bool tasks() {
+    return tasks([] { return true; });
+  }
+
+  // The same with `between()` (workgroup-uniform; false: a wait failed) run after this
+  // workgroup's top-k tasks and before its splits: the fused layer's deferred work.
+  template <class Between>
+  MONO_DEV bool tasks(Between&& between) {
     const int n_sc = n_score(), n_topk = A.rows * TEAM;
     const int n_split = A.rows * SPLITS;
     const int total = n_tasks();
@@ -223,6 +231,7 @@ class Step {
       stamp(T, t0, 1);
       if (!ok) return false;  // workgroup-uniform
     }
+    if (!between()) return false;
     for (T = first_at_or_after(n_sc + n_topk); T < n_sc + n_topk + n_split; T += G) {
       const uint64_t t0 = now_ticks();
       const int j = T - n_sc - n_topk;

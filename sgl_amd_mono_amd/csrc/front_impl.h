@@ -131,6 +131,20 @@ class Front {
     if (h_ready) h_ssq = nullptr;
   }
 
+  // Leave stage D (the absorbed query, whose output only the attention's splits read)
+  // out of tasks(): the layer runs it later with deferred_d, on workgroups that would
+  // otherwise wait for the top-k, so no score task waits behind it.
+  MONO_DEV void set_defer_d(bool v) { defer_d = v; }
+
+  // Stage-D task of head h outside tasks() (its timeline row as tasks() would stamp it).
+  MONO_DEV bool deferred_d(int h) {
+    relane();
+    const uint64_t t0 = now_ticks();
+    if (!stage_d(h)) return false;
+    stamp(S + nt_a(S) + S + NT_C + h, t0, 3);
+    return true;
+  }
+
   // This workgroup's tasks (false, workgroup-uniform: a wait failed).
   MONO_DEV bool tasks() {
     for (int p = tid; p < ROW_PIECES; p += FT)
@@ -155,6 +169,7 @@ class Front {
         ok = stage_c(t);
       } else if ((t -= NT_C) < HEADS) {
         kind = 3;
+        if (defer_d) continue;  // run later, by deferred_d
         ok = stage_d(t);
       } else if ((t -= HEADS) < S * (IH / FW)) {
         kind = 4;
@@ -176,6 +191,7 @@ class Front {
   const int kv_mask;
   const uint64_t* h_ssq;
   const int h_site;
+  bool defer_d = false;
   int site0;
   GuardArgs guard_args;
   Guard gd;

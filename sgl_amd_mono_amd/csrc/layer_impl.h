@@ -79,14 +79,33 @@ MONO_DEV bool run_layer(const LayerArgs& args, LayerLds& lds, const Guard& g, bo
   stamp(args.tail.ticks, T_BEGIN);
   attn::Step st(args.tail.at, lds.tail.at);
   st.adopt(g);
+  // Stage D (the absorbed query, read only by the splits) leaves the front when the
+  // workgroups after the top-k teams can take it: head d runs on workgroup
+  // (scores + top-k tasks + d) mod G between its score and split tasks, which holds no
+  // top-k task, so no score task waits behind a D task.
+  const int d0 = st.n_score() + st.n_topk();
+  const bool defer_d = st.n_topk() + proj::HEADS <= (int)gridDim.x;
   {
     proj::fr::Front f(args.fr, lds.fr);
     f.adopt(g, FRONT_SITE0, h_ready);
+    f.set_defer_d(defer_d);
     if (!f.tasks()) return false;
   }
   stamp(args.tail.ticks, T_FRONT);
   __syncthreads();  // the LDS passes from the front's layout to the attention's
-  if (!st.tasks()) return false;
+  const auto deferred = [&]() -> bool {
+    if (!defer_d) return true;
+    const int G = (int)gridDim.x, b = (int)block_index();
+    for (int d = ((b - d0) % G + G) % G; d < proj::HEADS; d += G) {
+      __syncthreads();  // the LDS passes to the front's layout
+      proj::fr::Front f(args.fr, lds.fr);
+      f.adopt(g, FRONT_SITE0);
+      if (!f.deferred_d(d)) return false;
+      __syncthreads();  // and back to the attention's
+    }
+    return true;
+  };
+  if (!st.tasks(deferred)) return false;
   stamp(args.tail.ticks, T_ATTN);
   return back_moe(args.tail, lds.tail, st, g);
 }
