@@ -364,7 +364,7 @@ extern "C" int mono_moe_create(const mono_moe_config* cfg, mono_moe** out) {
   Carve cv;
   const size_t o_xq = cv.take((size_t)MAX_ROWS * H);
   const size_t o_xs = cv.take((size_t)MAX_ROWS * (H / 128) * 4);
-  const size_t o_score = cv.take((size_t)MAX_ROWS * E * 4);
+  const size_t o_score = cv.take((size_t)MAX_ROWS * E * 8);
   const size_t o_rdone = cv.take(mono::DONE_BYTES);
   const size_t o_mid = cv.take(max_act * MAX_ROWS * I * 8);
   const size_t o_mtile = cv.take(max_act * (I / 16) * 8);
@@ -380,7 +380,7 @@ extern "C" int mono_moe_create(const mono_moe_config* cfg, mono_moe** out) {
   m->mail.guard = m->guard.words;
   m->mail.xq = reinterpret_cast<uint8_t*>(m->at(o_xq));
   m->mail.xs = reinterpret_cast<float*>(m->at(o_xs));
-  m->mail.score = reinterpret_cast<float*>(m->at(o_score));
+  m->mail.score = reinterpret_cast<uint64_t*>(m->at(o_score));
   m->mail.rdone = reinterpret_cast<uint64_t*>(m->at(o_rdone));
   m->mail.mid = reinterpret_cast<uint64_t*>(m->at(o_mid));
   m->mail.mtile = reinterpret_cast<uint64_t*>(m->at(o_mtile));
@@ -815,14 +815,14 @@ struct mono_layer {
   void* extra = nullptr;  // a_done, then the scrub table
   uint64_t* a_done = nullptr;
   mono::GuardArgs guard{};
-  // multi-layer launches (max_layers > 1): each layer's own row histograms and MoE
-  // router outputs (stack_stride bytes a layer), then the final tasks' tagged tile sums
+  // multi-layer launches (max_layers > 1): each layer's own row histograms and MoE FP8
+  // rows with their scales (stack_stride bytes a layer), then the final tasks' tagged tile sums
   // of squares (scrubbed with every other mailbox); the device table of the layers'
   // kernel arguments and the host copy of what it holds
   int max_layers = 0;
   void* stack_mail = nullptr;
   size_t stack_stride = 0;
-  size_t stack_o_score = 0, stack_o_xq = 0, stack_o_xs = 0;
+  size_t stack_o_xq = 0, stack_o_xs = 0;
   uint64_t* x_ssq = nullptr;
   void* table = nullptr;
   std::vector<uint8_t> table_host;
@@ -861,15 +861,15 @@ static int layer_release(mono_layer* L) {
 constexpr int MAX_STACK_LAYERS = 256;
 
 // A layer runtime's buffers for multi-layer launches: every layer's row histograms and
-// MoE router outputs, the final tasks' done words (one zeroed allocation, the scrub
-// region `rg`) and the device table of the layers' kernel arguments.
+// MoE FP8 rows with their scales, the final tasks' tagged tile sums of squares (one
+// zeroed allocation, the scrub region `rg`) and the device table of the layers' kernel
+// arguments.
 static int stack_alloc(mono_layer* L, int max_layers, mono::ScrubRegion& rg) {
   using namespace mono;
   const size_t R = (size_t)L->a->cfg.max_rows;
-  Carve cv;  // a layer's share: rowh at 0, then the router outputs
+  Carve cv;  // a layer's share: rowh at 0, then the MoE's FP8 rows and scales
   cv.off = 0;
   cv.take(R * attn::ROWH * 4);
-  L->stack_o_score = cv.take((size_t)moe::MAX_ROWS * 256 * 4);
   L->stack_o_xq = cv.take((size_t)moe::MAX_ROWS * 7168);
   L->stack_o_xs = cv.take((size_t)moe::MAX_ROWS * (7168 / 128) * 4);
   L->stack_stride = align256(cv.off);
@@ -1093,8 +1093,7 @@ extern "C" int mono_layer_stack_set(mono_layer* L, int32_t n, const mono_proj_we
       kv_mask = 0;
     }
     char* mail = static_cast<char*>(L->stack_mail) + L->stack_stride * (size_t)l;
-    const layer::StackLayer sl{reinterpret_cast<uint32_t*>(mail), reinterpret_cast<float*>(mail + L->stack_o_score),
-                               reinterpret_cast<uint8_t*>(mail + L->stack_o_xq),
+    const layer::StackLayer sl{reinterpret_cast<uint32_t*>(mail), reinterpret_cast<uint8_t*>(mail + L->stack_o_xq),
                                reinterpret_cast<float*>(mail + L->stack_o_xs), l + 1 < n ? L->x_ssq : nullptr,
                                l > 0 ? L->x_ssq : nullptr};
     hipError_t e = layer::stack_fill(table.data() + eb * (size_t)l, sl, *w[l], fa, L->p->mail, kv_mask, g,

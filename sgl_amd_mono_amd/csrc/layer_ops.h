@@ -21,12 +21,11 @@ constexpr int ATTN_FRONT_SITE = 17;
 constexpr int STACK_H_SITE = 19;
 
 // A layer's own buffers in a multi-layer launch (its table entry points at them): its
-// row histograms, its MoE router outputs (read with plain loads, so no two layers of a
-// launch share them), the tile sums of squares its final tasks put (NULL: the last
-// layer) and those its stage A awaits (NULL: the first layer).
+// row histograms, its MoE FP8 rows and their scales (read with plain loads, so no two
+// layers of a launch share them), the tile sums of squares its final tasks put (NULL:
+// the last layer) and those its norm tasks await (NULL: the first layer).
 struct StackLayer {
   uint32_t* rowh;
-  float* score;
   uint8_t* xq;
   float* xs;
   uint64_t* out_ssq;

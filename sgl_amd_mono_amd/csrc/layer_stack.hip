@@ -78,8 +78,7 @@ hipError_t stack_fill(void* entry, const StackLayer& sl, const mono_proj_weights
   // the layer's own row histograms (one copy, cleared by the launch once read)
   a.tail.at.rowh_flip = 0;
   a.tail.at.mail.rowh = sl.rowh;
-  // the MoE's router outputs, read with plain loads: the layer's own copies
-  a.tail.mo.mail.score = sl.score;
+  // the MoE's FP8 rows and scales, read with plain loads: the layer's own copies
   a.tail.mo.mail.xq = sl.xq;
   a.tail.mo.mail.xs = sl.xs;
   a.tail.mo.out_ssq = sl.out_ssq;

@@ -321,9 +321,9 @@ class Step {
       for (int w = 0; w < FW; ++w)
 #pragma unroll
         for (int q = 0; q < 4; ++q) lg += L.rt.rlg[w][q][tid];
-      if (s < S) st_dev(&A.mail.score[s * E + RT_E * eg + e], sigmoid(lg));
+      if (s < S) mb_putf(&A.mail.score[s * E + RT_E * eg + e], sigmoid(lg), gd.tag);
     }
-    // the done word once every word of the task is stored
+    // the done word (for the FP8 rows) once every word of the task is stored
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     put_done(A.mail.rdone, t, gd.tag);
@@ -352,19 +352,30 @@ class Step {
   }
 
   // ---------------------------------------------------------------- gather
-  // Once every router task's done word carries the tag: the step's FP8 rows into LDS by
-  // DMA (global_load_lds: no registers), their block scales, and wave w's rows' scores
-  // (row w, and w + 8 when S > 8) into registers, lane l experts 4 l .. 4 l + 3. Plain
-  // cached loads: nothing reads these lines in the launch before the done words, so no
-  // cache holds an older copy, and the XCD's workgroups share its L2 for them. The
-  // caller waits for the DMA (s_waitcnt 0) and meets the workgroup's barrier before
-  // reading the rows in LDS.
+  // Wave w's rows' scores (row w, and w + 8 when S > 8; lane l experts 4 l .. 4 l + 3)
+  // polled as tagged words, and in the same pass (thread t < n_rt) every router task's
+  // done word; then the step's FP8 rows into LDS by DMA (global_load_lds: no registers)
+  // and their block scales. Plain cached loads for the rows: nothing reads these lines
+  // in the launch before the done words, so no cache holds an older copy, and the
+  // XCD's workgroups share its L2 for them. The caller waits for the DMA (s_waitcnt 0)
+  // and meets the workgroup's barrier before reading the rows in LDS.
   MONO_DEV bool gather(int n_rt, f32x4 (&sc)[2]) {
-    const uint64_t* rd = done_copy(A.mail.rdone);
-    if (!hint_wait(n_rt, [rd](int i) { return rd + i; }, site0 + W_ROUTER, gd)) return false;
+    bool ok = true;
 #pragma unroll
-    for (int k = 0; k < 2; ++k)
-      sc[k] = *reinterpret_cast<const f32x4*>(&A.mail.score[min(wave + FW * k, S - 1) * E + 4 * lane]);
+    for (int k = 0; k < 2; ++k) {
+      const int s = wave + FW * k;
+      uint32_t v[4] = {0u, 0u, 0u, 0u};
+      if (s < S) {  // wave-uniform
+        const uint64_t* row = A.mail.score + (size_t)s * E + 4 * lane;
+        ok = poll_words<4>([row](int j) { return row + j; }, v, 0xfu, site0 + W_ROUTER, gd) && ok;
+      }
+      sc[k] = f32x4{__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]), __uint_as_float(v[3])};
+    }
+    if (tid < n_rt) {
+      uint32_t v;
+      ok = poll_word(done_copy(A.mail.rdone) + tid, v, site0 + W_ROUTER, gd) && ok;
+    }
+    if (!block_all(ok)) return false;
     float xsv[2];
 #pragma unroll
     for (int k = 0; k < 2; ++k) xsv[k] = A.mail.xs[min(tid + FT * k, S * KB - 1)];

@@ -14,8 +14,9 @@ constexpr int MAX_TOPK = 8;
 // Mailboxes of one MoE runtime (tagged 64-bit words, see sync.h), sized for the
 // runtime's max_rows: at most max_act = min(max_rows * top_k, E) + 1 expert slots.
 struct Mail {
-  // the FP8 kernel's router tasks' outputs: plain data behind their done words
-  float* score;     // [MAX_ROWS][E]       routing scores
+  // the FP8 kernel's router tasks' outputs: tagged scores, and plain rows behind the
+  // tasks' done words
+  uint64_t* score;  // [MAX_ROWS][E]       routing scores, f32 (tagged)
   uint8_t* xq;      // [MAX_ROWS][H]       the normed rows in FP8
   float* xs;        // [MAX_ROWS][H / 128] their block scales
   uint64_t* rdone;  // DONE_BYTES: router task t's done word, replicated
