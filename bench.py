@@ -5,9 +5,11 @@ JSON line. A step is one pass of the hot path over one batch of synthetic decode
 whose inputs and weights are already resident in HBM:
 
 * ``layer`` (default): 61 stacked, independently seeded decoder
-  layers at 8 rows over 32768-key contexts, each layer ONE persistent launch (front,
-  sparse attention, back and FP8 MoE in ``k_layer``); one step runs every layer once and
-  is replayed from a HIP graph. ``value`` is microseconds per layer.
+  layers at 8 rows over 32768-key contexts. Each layer is one persistent pass (front,
+  sparse attention, back and FP8 MoE); by default the 61 layers of a step run as ONE
+  launch (``k_layers``, ``--launch stack``), or one launch a layer (``k_layer``,
+  ``--launch layer``). The step is replayed from a HIP graph. ``value`` is
+  microseconds per layer.
 * ``moe_fp8`` (BASELINE config 2 at 8 rows): the FP8 routed + shared MoE half of the
   layer (RMSNorm, router, top-8, W8A8 experts, residual) through ``mono_moe_fp8_forward``.
 * ``moe_mxfp4``: the MXFP4 A16W4 routed + shared MoE behind a
@@ -463,11 +465,13 @@ BACK_W = ("w_uv", "s_uv", "w_o", "s_o")
 def bench_layer(args, dev):
     """``--layers`` (61) stacked, independently seeded decoder layers
     at ``--rows`` (8) rows, every row a ``--ctx``-key (32768) request whose new token is
-    its last. One step runs all layers once; it is captured in a HIP graph (61
-    persistent launches, one a layer) and replayed, so host dispatch is off the timed
-    path. The value is microseconds per layer. A second region runs the same step
-    eagerly with a HIP event pair around every layer's launch (the launch duration for
-    ``roofline``); in-kernel ticks give the phase breakdown."""
+    its last. One step runs all layers once, as ONE persistent launch (``--launch
+    stack``, the default) or one launch a layer (``--launch layer``); it is captured in a
+    HIP graph and replayed, so host dispatch is off the timed path. The value is
+    microseconds per layer. The stacked step's output is first checked bit for bit
+    against the chained one-launch-a-layer step. A second region runs the step eagerly
+    with HIP event pairs around the launches (the launch duration for ``roofline``);
+    in-kernel ticks give the phase breakdown."""
     import torch
 
     from sgl_amd_mono_amd import workloads
