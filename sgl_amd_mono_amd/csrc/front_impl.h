@@ -166,7 +166,9 @@ class Front {
         ok = stage_b(t);
       } else if ((t -= S) < NT_C) {
         kind = 2;
-        ok = stage_c(t);
+        // the index-query tiles first: stage E, whose output the score tasks await,
+        // waits on them; the q_b tiles feed only stage D (the splits' q)
+        ok = stage_c(t < NT_C - QB_TILES ? QB_TILES + t : t - (NT_C - QB_TILES));
       } else if ((t -= NT_C) < HEADS) {
         kind = 3;
         if (defer_d) continue;  // run later, by deferred_d
