@@ -21,7 +21,12 @@ from . import _lib
 from .runtime import Runtime, need
 
 IH, ID, NH, DQK, DV, PAGE, TOPK = 64, 128, 32, 576, 512, 64, 2048
-SPLITS = 32  # split tasks a row (64 selected tokens each)
+
+
+def splits_of(rows: int) -> int:
+    """Attention splits a row (and merges: 32 / splits heads each): 32 up to 16 rows, then
+    fewer and longer ones, so a step's splits fill one round of a 256-CU grid."""
+    return 32 if rows <= 16 else 8 if rows <= 32 else 4
 SOFTMAX_SCALE = (128 + 64) ** -0.5  # (qk_nope + qk_rope)^-1/2, glm53/gfx950/config.py:171-173
 
 
@@ -64,8 +69,7 @@ class AttnRuntime(Runtime):
 
     def n_tasks(self, rows: int) -> int:
         """Tasks of one launch over ``rows`` rows (the timeline's length)."""
-        n_score = -(-rows * (self.max_ctx // 1024) // 16) * 16  # padded to whole top-k teams
-        return n_score + rows * 16 + rows * SPLITS + rows * NH
+        return n_tasks(self.max_ctx, rows)
 
     def forward(self, step: AttnStep, caches: AttnCaches, out: torch.Tensor | None = None,
                 debug: bool = False, timeline: torch.Tensor | None = None):
@@ -88,7 +92,7 @@ class AttnRuntime(Runtime):
 def n_tasks(max_ctx: int, rows: int) -> int:
     """Tasks of one attention launch over ``rows`` rows (the timeline's length)."""
     n_score = -(-rows * (max_ctx // 1024) // 16) * 16  # padded to whole top-k teams
-    return n_score + rows * 16 + rows * SPLITS + rows * NH
+    return n_score + rows * 16 + 2 * rows * splits_of(rows)
 
 
 def attn_args(dev, max_rows: int, max_ctx: int, step: AttnStep, caches: AttnCaches, out: torch.Tensor | None,

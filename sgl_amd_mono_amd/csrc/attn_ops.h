@@ -19,8 +19,13 @@ constexpr int TOPK = 2048;      // tokens a row attends
 constexpr int MAX_ROWS = 64;
 constexpr int MAX_CTX = 32768;  // keys a row at most (2048 a top-k team member)
 constexpr int CHUNK = 1024;     // keys a score task
-constexpr int SPLITS = 32;      // attention splits a row (64 selected tokens each)
-constexpr int SPLIT = TOPK / SPLITS;
+constexpr int SPLITS = 32;      // attention splits a row at most (64 selected tokens each)
+constexpr int SPLIT_MAX = TOPK / 4;  // selected tokens a split at most
+// Attention splits a row: 32 up to 16 rows (the layer's widest step), then fewer and
+// longer ones, so a step's splits (rows x splits <= 256) fill one round of a 256-CU
+// grid; a row's merges are as many, of 32 / splits heads each.
+__host__ __device__ constexpr int splits_of(int rows) { return rows <= 16 ? 32 : rows <= 32 ? 8 : 4; }
+constexpr int LONG_ROWS = 16;  // steps above this take long splits (only k_attn holds them)
 constexpr int TEAM = 16;        // workgroups selecting one row's top-k together
 constexpr int PASSES = 4;       // 8-bit radix digits of a 32-bit key
 constexpr int CMAX = 512;       // threshold candidates a row exchanged as (key, position)
@@ -59,6 +64,9 @@ struct AttnArgs : mono_attn_args {
 
 hipError_t attn_occupancy(int* blocks_per_cu);
 hipError_t attn_forward(const AttnArgs& a, int grid, const Mail& mail, const GuardArgs& guard, hipStream_t st);
+// the launch of a step above LONG_ROWS rows (attn_forward dispatches to it)
+hipError_t attn_long_occupancy(int* blocks_per_cu);
+hipError_t attn_long_forward(const AttnArgs& a, int grid, const Mail& mail, const GuardArgs& guard, hipStream_t st);
 
 }  // namespace attn
 }  // namespace mono

@@ -57,10 +57,16 @@ constexpr int PB_STRIDE = SUB + 8;           // bf16 a probability row in LDS
 constexpr int KEYS_WAVE = CHUNK / AW;        // 128 keys a wave of a score task
 constexpr int KTILES = KEYS_WAVE / 16;
 constexpr float NEG_INF = -__builtin_huge_valf();
-static_assert(KPM % AT == 0 && PAGE % KPT == 0 && TEAM <= 16 && KEYS_WAVE % PAGE == 0 && SPLIT % SUB == 0, "tiling");
+static_assert(KPM % AT == 0 && PAGE % KPT == 0 && TEAM <= 16 && KEYS_WAVE % PAGE == 0 && SPLIT_MAX <= AT, "tiling");
 static_assert(AT == NH * DV / 32, "tiling");
 
 enum { W_SCORE = 0, W_SEL = 1, W_PART = 2, W_TEAM = 3 };
+
+#ifdef MONO_ATTN_LONG
+constexpr bool kLongSplits = true;
+#else
+constexpr bool kLongSplits = false;
+#endif
 
 struct ScoreLds {
   uint32_t hist[256];  // the task's leading-digit histogram
@@ -86,14 +92,14 @@ struct SplitLds {
   };
   float pf[NH][SUB];
   uint16_t pb[NH][PB_STRIDE];
-  int32_t slot[SPLIT];
+  int32_t slot[SPLIT_MAX];
   float kvs[SUB];
   float alpha[NH];
 };
 
 struct MergeLds {
-  float w[SPLITS];  // each split's weight e^(m_j - M), 0 for an empty split
-  float den;        // sum_j w_j l_j
+  float w[8][SPLITS];  // each split's weight e^(m_j - M) a head of the task, 0 for an empty split
+  float den[8];        // sum_j w_j l_j a head
 };
 
 struct Lds {
@@ -206,7 +212,8 @@ class Step {
   // tasks in the list: score tasks padded to a multiple of TEAM so no top-k team
   // straddles a round, then top-k members, splits, merges
   MONO_DEV int n_score() const { return (A.rows * CH + TEAM - 1) / TEAM * TEAM; }
-  MONO_DEV int n_tasks() const { return n_score() + A.rows * TEAM + A.rows * SPLITS + A.rows * NH; }
+  // (a row's splits_of(rows) merges of 32 / splits_of(rows) heads each cover its NH heads)
+  MONO_DEV int n_tasks() const { return n_score() + A.rows * TEAM + 2 * A.rows * splits_of(A.rows); }
   MONO_DEV int n_topk() const { return A.rows * TEAM; }
 
   // This workgroup's tasks (false, workgroup-uniform: a wait failed).
@@ -219,8 +226,8 @@ class Step {
   template <class Between>
   MONO_DEV bool tasks(Between&& between) {
     const int n_sc = n_score(), n_topk = A.rows * TEAM;
-    const int n_split = A.rows * SPLITS;
-    const int total = n_tasks();
+    const int nsp = splits_of(A.rows);
+    const int n_split = A.rows * nsp;
     if (!score_stage(block_index(), A.rows * CH)) return false;
     // a workgroup's list is ordered by stage: one loop a stage keeps each loop body to
     // one task kind (and its registers)
@@ -232,21 +239,28 @@ class Step {
       if (!ok) return false;  // workgroup-uniform
     }
     if (!between()) return false;
-    for (T = first_at_or_after(n_sc + n_topk); T < n_sc + n_topk + n_split; T += G) {
-      const uint64_t t0 = now_ticks();
-      const int j = T - n_sc - n_topk;
-      const bool ok = split_task(j / SPLITS, j % SPLITS);
-      stamp(T, t0, 2);
-      if (!ok) return false;
+    // one sub-tile a split up to LONG_ROWS rows (its loop over sub-tiles compiles away),
+    // long splits above, in k_attn_long alone (MONO_ATTN_LONG): every other launch takes
+    // at most LONG_ROWS rows.
+    if (!kLongSplits || nsp == SPLITS) {
+      for (T = first_at_or_after(n_sc + n_topk); T < n_sc + n_topk + n_split; T += G) {
+        const uint64_t t0 = now_ticks();
+        const int j = T - n_sc - n_topk;
+        const bool ok = split_task<false>(j / SPLITS, j % SPLITS, SPLITS);
+        stamp(T, t0, 2);
+        if (!ok) return false;
+      }
+    } else {
+      for (T = first_at_or_after(n_sc + n_topk); T < n_sc + n_topk + n_split; T += G) {
+        const uint64_t t0 = now_ticks();
+        const int j = T - n_sc - n_topk;
+        const bool ok = split_task<true>(j / nsp, j % nsp, nsp);
+        stamp(T, t0, 2);
+        if (!ok) return false;
+      }
     }
-    for (T = first_at_or_after(n_sc + n_topk + n_split); T < total; T += G) {
-      const uint64_t t0 = now_ticks();
-      const int j = T - n_sc - n_topk - n_split;
-      const bool ok = merge_task(j / NH, j % NH);
-      stamp(T, t0, 3);
-      if (!ok) return false;
-    }
-    return true;
+    if (!kLongSplits || nsp == SPLITS) return merges<SPLITS>(n_sc + n_topk + n_split);
+    return nsp == 8 ? merges<8>(n_sc + n_topk + n_split) : merges<4>(n_sc + n_topk + n_split);
   }
 
  private:
@@ -793,11 +807,15 @@ class Step {
     if (tid < SUB) P.kvs[tid] = P.slot[st * SUB + tid] >= 0 ? gs : 0.f;
   }
 
-  MONO_DEV bool split_task(int s, int j) {
+  // Split j of row s's nsp: its TOPK / nsp selected tokens in sub-tiles of SUB. LONG: a
+  // split may hold several sub-tiles (fewer than SPLITS splits a row).
+  template <bool LONG>
+  MONO_DEV bool split_task(int s, int j, int nsp) {
     SplitLds& P = L.u.sp;
     const int nsel = min(row_len(s), TOPK);
-    const int lo = j * SPLIT;
-    const int cnt = min(max(nsel - lo, 0), SPLIT);
+    const int len = LONG ? TOPK / nsp : TOPK / SPLITS;
+    const int lo = j * len;
+    const int cnt = min(max(nsel - lo, 0), len);
     const size_t mlb = ((size_t)s * SPLITS + j) * NH;
     if (cnt == 0) {  // an empty split contributes nothing to the merge
       if (tid < NH) {
@@ -827,7 +845,7 @@ class Step {
       }
     }
     bool ok = true;
-    if (tid < SPLIT) {
+    if (tid < len) {
       int slot = -1;
       if (tid < cnt) {
         uint32_t v = 0;
@@ -840,7 +858,10 @@ class Step {
     if (!block_all(ok)) return false;
     mark_waited();
 
-    const int ht = wave / 4, tt = wave % 4;  // logit tile of this wave
+    // logit tile of this wave: heads 16 ht .. 16 ht + 15, tokens 16 tt .. 16 tt + 15 of
+    // the sub-tile (lane (g, r): heads 16 ht + 4 g + i, token 16 tt + r); its running
+    // maximum and its own tokens' running sum a head, i
+    const int ht = wave / 4, tt = wave % 4;
     f32x4 acc[2][4];
 #pragma unroll
     for (int a = 0; a < 2; ++a)
@@ -854,6 +875,10 @@ class Step {
 
 #pragma unroll 1
     for (int st = 0; st < nsub; ++st) {
+      // a long split: the lane's indices afresh each sub-tile (opaque copies), so the q.k,
+      // softmax and p.v LDS addresses are derived inside the loop, not hoisted out of it
+      // and held across it
+      const int lane = LONG ? opaque_v(tid) % WAVE : this->lane, g = lane / 16, r = lane % 16;
       gather_store(P, st, gv, gs);
       __syncthreads();
       if (st + 1 < nsub) gather_load(P, st + 1, gv, gs);  // in flight while this sub-tile computes
@@ -970,66 +995,96 @@ class Step {
   }
 
   // ---------------------------------------------------------------- merge
-  // Merge (row s, head h): the first 256 threads each combine one channel pair over the
-  // row's splits (a task takes in the head's 32 KB of partials).
-  MONO_DEV bool merge_task(int s, int h) {
-    static_assert(SPLITS <= WAVE && DV == 2 * 256, "a lane a split; a thread a channel pair");
+  // This workgroup's merges: list index `at` + k is merge k (row k / NSP, heads
+  // (k % NSP) HM ..), HM = 32 / NSP heads a task.
+  template <int NSP>
+  MONO_DEV bool merges(int at) {
+    const int n = A.rows * NSP;
+    for (int T = first_at_or_after(at); T < at + n; T += G) {
+      const uint64_t t0 = now_ticks();
+      const int k = T - at;
+      const bool ok = merge_task<NSP>(k / NSP, k % NSP);
+      stamp(T, t0, 3);
+      if (!ok) return false;
+    }
+    return true;
+  }
+
+  // Merge (row s, heads hg HM .. hg HM + HM - 1) over the row's NSP splits, HM = 32 /
+  // NSP: each thread combines IPT channel pairs (a task takes in NSP x HM KB = 32 KB of
+  // partials).
+  template <int NSP>
+  MONO_DEV bool merge_task(int s, int hg) {
+    constexpr int HM = SPLITS / NSP;
+    constexpr int ITEMS = HM * DV / 2;                // channel pairs of the task
+    constexpr int IPT = ITEMS > AT ? ITEMS / AT : 1;  // pairs a thread
+    static_assert(NSP <= WAVE && HM <= AW && HM <= 8 && (ITEMS % AT == 0 || ITEMS < AT) && NH % HM == 0,
+                  "a lane a split; a wave a head's weights");
     MergeLds& Q = L.u.mg;
-    const int d0 = (tid % 256) * 2;
+    const int h0 = hg * HM;
     const size_t rb = (size_t)s * SPLITS;
     // every split of the row done: lane j of wave 0 polls split j's word
     bool ok = true;
-    if (wave == 0 && lane < SPLITS) {
+    if (wave == 0 && lane < NSP) {
       uint32_t v;
       ok = poll_word(&A.mail.sdone[rb + lane], v, W_PART, gd);
     }
     if (!block_all(ok)) return false;
     mark_waited();
-    // the split weights: lane j of wave 0 takes split j
-    if (wave == 0) {
-      const int jl = min(lane, SPLITS - 1);
+    // the split weights: wave w takes head h0 + w, lane j split j
+    if (wave < HM) {
+      const int h = h0 + wave;
+      const int jl = min(lane, NSP - 1);
       const float m = ld_agent_f32(&A.mail.ml[((rb + jl) * NH + h) * 2]);
-      const float l = lane < SPLITS ? ld_agent_f32(&A.mail.ml[((rb + jl) * NH + h) * 2 + 1]) : 0.f;
+      const float l = lane < NSP ? ld_agent_f32(&A.mail.ml[((rb + jl) * NH + h) * 2 + 1]) : 0.f;
       const bool live = l > 0.f;
       const float M = wave_max(live ? m : NEG_INF);
       const float w = live ? hw_exp(m - M) : 0.f;
       const float den = wave_sum(w * l);
-      if (lane < SPLITS) Q.w[lane] = w;
-      if (lane == 0) Q.den = den;
+      if (lane < NSP) Q.w[wave][lane] = w;
+      if (lane == 0) Q.den[wave] = den;
     }
-    // the channel pair of every split (unconditional loads; an empty split's words are
+    // the channel pairs of every split (unconditional loads; an empty split's words are
     // read and ignored)
-    const bool mine = tid < 256;  // wave-uniform
-    uint32_t av[SPLITS];
+    const bool mine = tid < ITEMS;  // wave-uniform
+    uint32_t av[IPT][NSP];
     if (mine) {
 #pragma unroll
-      for (int j = 0; j < SPLITS; ++j)
-        av[j] = ld_agent_u32(reinterpret_cast<const uint32_t*>(&A.mail.part[((rb + j) * NH + h) * DV + d0]));
+      for (int k = 0; k < IPT; ++k) {
+        const int it = tid + AT * k, h = h0 + it / (DV / 2), d0 = (it % (DV / 2)) * 2;
+#pragma unroll
+        for (int j = 0; j < NSP; ++j)
+          av[k][j] = ld_agent_u32(reinterpret_cast<const uint32_t*>(&A.mail.part[((rb + j) * NH + h) * DV + d0]));
+      }
     }
     __syncthreads();
     if (mine) {
-      float o[2] = {0.f, 0.f};
 #pragma unroll
-      for (int j = 0; j < SPLITS; ++j) {
-        const float w = Q.w[j];
-        if (w > 0.f) {
-          o[0] += w * bf16_lo(av[j]);
-          o[1] += w * bf16_hi(av[j]);
+      for (int k = 0; k < IPT; ++k) {
+        const int it = tid + AT * k, hh = it / (DV / 2), h = h0 + hh, d0 = (it % (DV / 2)) * 2;
+        float o[2] = {0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < NSP; ++j) {
+          const float w = Q.w[hh][j];
+          if (w > 0.f) {
+            o[0] += w * bf16_lo(av[k][j]);
+            o[1] += w * bf16_hi(av[k][j]);
+          }
+        }
+        const float den = Q.den[hh];
+        const float inv = den > 0.f ? 1.0f / den : 0.f;
+        uint32_t* po = reinterpret_cast<uint32_t*>(A.out + ((size_t)s * NH + h) * DV + d0);
+        const uint32_t ov = pack_bf16x2(o[0] * inv, o[1] * inv);
+        if (A.publish_out) {  // read in this launch: a device-coherent store, complete before the done word
+          __hip_atomic_store(po, ov, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+          *po = ov;
         }
       }
-      const float den = Q.den;
-      const float inv = den > 0.f ? 1.0f / den : 0.f;
-      uint32_t* po = reinterpret_cast<uint32_t*>(A.out + ((size_t)s * NH + h) * DV + d0);
-      const uint32_t ov = pack_bf16x2(o[0] * inv, o[1] * inv);
-      if (A.publish_out) {  // read in this launch: a device-coherent store, complete before the done word
-        __hip_atomic_store(po, ov, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __builtin_amdgcn_s_waitcnt(0);
-      } else {
-        *po = ov;
-      }
+      if (A.publish_out) __builtin_amdgcn_s_waitcnt(0);
     }
     __syncthreads();  // (and the next task may rewrite the LDS weights)
-    if (A.publish_out && tid == 0) mb_put(&A.mail.mdone[(size_t)s * NH + h], 0u, gd.tag);
+    if (A.publish_out && tid < HM) mb_put(&A.mail.mdone[(size_t)s * NH + h0 + tid], 0u, gd.tag);
     return true;
   }
 };

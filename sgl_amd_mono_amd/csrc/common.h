@@ -35,6 +35,13 @@ MONO_DEV unsigned block_index() {
 #endif
 }
 
+// An opaque copy of a per-lane value: arithmetic derived from it inside a loop cannot be
+// hoisted out of the loop and held in registers across it.
+MONO_DEV int opaque_v(int v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
 typedef int32_t i32x8 __attribute__((ext_vector_type(8)));
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));

@@ -14,6 +14,10 @@ namespace layer {
 
 namespace {
 
+// the launches that hold the attention with other phases take at most proj::MAX_ROWS
+// rows: their attention has one sub-tile a split (no long splits compiled in)
+static_assert(proj::MAX_ROWS <= attn::LONG_ROWS, "fused launches: short splits only");
+
 struct Args {
   attn::Args at;
   proj::Args bk;

@@ -100,6 +100,15 @@ def test_attn_48_rows_mixed_contexts(rt, gpu_device):
     _check(rt, ctx, 2, gpu_device)
 
 
+def test_attn_24_rows_long_splits(rt, gpu_device):
+    """24 rows take 8 splits a row of 256 selected tokens (four sub-tiles each) and merges
+    of 4 heads: the same selection and, within the bound, the same output."""
+    g = torch.Generator().manual_seed(4)
+    ctx = torch.randint(1, 32768, (24,), generator=g).tolist()
+    ctx[0], ctx[1], ctx[2], ctx[3] = 32768, 2048, 2049, 300
+    _check(rt, ctx, 9, gpu_device)
+
+
 def test_attn_48_rows_full_contexts(rt, gpu_device):
     """BASELINE config 3 at its largest size: 48 rows of (nearly) 32768 keys each."""
     ctx = [32768] * 44 + [32767, 32704, 30001, 16385]
