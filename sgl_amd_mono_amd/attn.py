@@ -91,8 +91,9 @@ class AttnRuntime(Runtime):
 
 def n_tasks(max_ctx: int, rows: int) -> int:
     """Tasks of one attention launch over ``rows`` rows (the timeline's length)."""
-    n_score = -(-rows * (max_ctx // 1024) // 16) * 16  # padded to whole top-k teams
-    return n_score + rows * 16 + 2 * rows * splits_of(rows)
+    team = 16 if rows <= 16 else 4  # top-k team members a row
+    n_score = -(-rows * (max_ctx // 1024) // team) * team  # padded to whole top-k teams
+    return n_score + rows * team + 2 * rows * splits_of(rows)
 
 
 def attn_args(dev, max_rows: int, max_ctx: int, step: AttnStep, caches: AttnCaches, out: torch.Tensor | None,

@@ -27,6 +27,7 @@ constexpr int SPLIT_MAX = TOPK / 4;  // selected tokens a split at most
 __host__ __device__ constexpr int splits_of(int rows) { return rows <= 16 ? 32 : rows <= 32 ? 8 : 4; }
 constexpr int LONG_ROWS = 16;  // steps above this take long splits (only k_attn holds them)
 constexpr int TEAM = 16;        // workgroups selecting one row's top-k together
+constexpr int TEAM_LONG = 4;    // the same above LONG_ROWS rows (k_attn_long): one round of teams
 constexpr int PASSES = 4;       // 8-bit radix digits of a 32-bit key
 constexpr int CMAX = 512;       // threshold candidates a row exchanged as (key, position)
 constexpr int HW = 136;         // words a member's histogram: 128 of two 16-bit bins, 1 count

@@ -44,9 +44,17 @@ namespace attn {
 
 namespace {
 
+#ifdef MONO_ATTN_LONG
+constexpr bool kLongSplits = true;
+constexpr int TMK = TEAM_LONG;  // members of a row's top-k team in this launch
+#else
+constexpr bool kLongSplits = false;
+constexpr int TMK = TEAM;
+#endif
+
 constexpr int AT = 512;
 constexpr int AW = AT / WAVE;
-constexpr int KPM = MAX_CTX / TEAM;          // keys a top-k team member owns
+constexpr int KPM = MAX_CTX / TMK;           // keys a top-k team member owns
 constexpr int KPT = KPM / AT;                // keys a thread of a member holds
 constexpr int SUB = 64;                      // tokens a split sub-tile
 constexpr int Q_STRIDE = DQK + 8;            // bf16 a q row in LDS
@@ -57,16 +65,12 @@ constexpr int PB_STRIDE = SUB + 8;           // bf16 a probability row in LDS
 constexpr int KEYS_WAVE = CHUNK / AW;        // 128 keys a wave of a score task
 constexpr int KTILES = KEYS_WAVE / 16;
 constexpr float NEG_INF = -__builtin_huge_valf();
-static_assert(KPM % AT == 0 && PAGE % KPT == 0 && TEAM <= 16 && KEYS_WAVE % PAGE == 0 && SPLIT_MAX <= AT, "tiling");
+static_assert(KPM % AT == 0 && PAGE % KPT == 0 && TMK <= 16 && KPT % 4 == 0 && KEYS_WAVE % PAGE == 0 && SPLIT_MAX <= AT, "tiling");
 static_assert(AT == NH * DV / 32, "tiling");
 
 enum { W_SCORE = 0, W_SEL = 1, W_PART = 2, W_TEAM = 3 };
 
-#ifdef MONO_ATTN_LONG
-constexpr bool kLongSplits = true;
-#else
-constexpr bool kLongSplits = false;
-#endif
+
 
 struct ScoreLds {
   uint32_t hist[256];  // the task's leading-digit histogram
@@ -78,8 +82,8 @@ struct TopkLds {
   uint32_t tot[256];        // the team's
   uint32_t pre[256];        // the members' before this one
   uint32_t cu[CMAX];        // the team's threshold candidates, 0 past the last
-  int32_t xw[TEAM];         // the members' keys above the first digit
-  int32_t cnt[TEAM][2];     // the team's keys above / at the threshold
+  int32_t xw[TMK];          // the members' keys above the first digit
+  int32_t cnt[TMK][2];      // the team's keys above / at the threshold
   uint32_t digit, uT;
   int32_t above, pre_above;
 };
@@ -209,12 +213,12 @@ class Step {
 
   MONO_DEV const Guard& guard() const { return gd; }
 
-  // tasks in the list: score tasks padded to a multiple of TEAM so no top-k team
+  // tasks in the list: score tasks padded to a multiple of TMK so no top-k team
   // straddles a round, then top-k members, splits, merges
-  MONO_DEV int n_score() const { return (A.rows * CH + TEAM - 1) / TEAM * TEAM; }
+  MONO_DEV int n_score() const { return (A.rows * CH + TMK - 1) / TMK * TMK; }
   // (a row's splits_of(rows) merges of 32 / splits_of(rows) heads each cover its NH heads)
-  MONO_DEV int n_tasks() const { return n_score() + A.rows * TEAM + 2 * A.rows * splits_of(A.rows); }
-  MONO_DEV int n_topk() const { return A.rows * TEAM; }
+  MONO_DEV int n_tasks() const { return n_score() + A.rows * TMK + 2 * A.rows * splits_of(A.rows); }
+  MONO_DEV int n_topk() const { return A.rows * TMK; }
 
   // This workgroup's tasks (false, workgroup-uniform: a wait failed).
   MONO_DEV bool tasks() {
@@ -225,7 +229,7 @@ class Step {
   // workgroup's top-k tasks and before its splits: the fused layer's deferred work.
   template <class Between>
   MONO_DEV bool tasks(Between&& between) {
-    const int n_sc = n_score(), n_topk = A.rows * TEAM;
+    const int n_sc = n_score(), n_topk = A.rows * TMK;
     const int nsp = splits_of(A.rows);
     const int n_split = A.rows * nsp;
     if (!score_stage(block_index(), A.rows * CH)) return false;
@@ -234,7 +238,7 @@ class Step {
     int T = first_at_or_after(n_sc);
     for (; T < n_sc + n_topk; T += G) {
       const uint64_t t0 = now_ticks();
-      const bool ok = topk_member((T - n_sc) / TEAM, (T - n_sc) % TEAM);
+      const bool ok = topk_member((T - n_sc) / TMK, (T - n_sc) % TMK);
       stamp(T, t0, 1);
       if (!ok) return false;  // workgroup-uniform
     }
@@ -553,17 +557,17 @@ class Step {
 #pragma unroll
     for (int q = 0; q < KPT; ++q) hist_add(K.hist, q < cnt && (key[q] & mask) == prefix, (key[q] >> shift) & 0xffu);
     __syncthreads();
-    uint64_t* hb = &A.mail.hist[((size_t)s * PASSES + pass) * TEAM * HW];
+    uint64_t* hb = &A.mail.hist[((size_t)s * PASSES + pass) * TMK * HW];
     bool ok = true;
     if (tid < 128) {
       mb_put(&hb[m * HW + tid], K.hist[2 * tid] | (K.hist[2 * tid + 1] << 16), gd.tag);
-      uint32_t v[TEAM];
+      uint32_t v[TMK];
       const uint64_t* col = hb + tid;
       const auto at = [col](int j) { return col + j * HW; };
-      ok = poll_words<TEAM, decltype(at), false, false>(at, v, (1u << TEAM) - 1u, W_TEAM, gd);
-      uint32_t t = 0, p = 0;  // two 16-bit sums side by side (at most TEAM KPM keys)
+      ok = poll_words<TMK, decltype(at), false, false>(at, v, (1u << TMK) - 1u, W_TEAM, gd);
+      uint32_t t = 0, p = 0;  // two 16-bit sums side by side (at most TMK KPM keys)
 #pragma unroll
-      for (int j = 0; j < TEAM; ++j) {
+      for (int j = 0; j < TMK; ++j) {
         t += v[j];
         p += j < m ? v[j] : 0u;
       }
@@ -571,7 +575,7 @@ class Step {
       K.tot[2 * tid + 1] = t >> 16;
       K.pre[2 * tid] = p & 0xffffu;
       K.pre[2 * tid + 1] = p >> 16;
-    } else if (count >= 0 && tid < 128 + TEAM) {
+    } else if (count >= 0 && tid < 128 + TMK) {
       const int j = tid - 128;
       if (j == m) mb_put(&hb[m * HW + 128], (uint32_t)count, gd.tag);
       uint32_t v = 0;
@@ -617,16 +621,18 @@ class Step {
       ok = poll_word(&A.mail.cdone[(size_t)s * CH + tid], v, W_SCORE, gd);
     }
     if (!block_all(ok)) return false;
-    // then a thread's KPT consecutive scores: one 16-byte device-coherent load (the
-    // buffer reads zeros past the row), and the row histogram
+    // then a thread's KPT consecutive scores: 16-byte device-coherent loads (the buffer
+    // reads zeros past the row), and the row histogram
     uint32_t key[KPT];
     {
-      static_assert(KPT == 4, "a thread's keys are one 16-byte load");
       const __amdgpu_buffer_rsrc_t rs =
           __builtin_amdgcn_make_buffer_rsrc(A.mail.score + (size_t)s * A.mail.max_ctx, 0, n * 4, BUF_DWORD3);
-      const u32x4 k4 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, p0 * 4, 0, SC1));
+      u32x4 k4[KPT / 4];
 #pragma unroll
-      for (int q = 0; q < KPT; ++q) key[q] = radix_key(__uint_as_float(k4[q]));
+      for (int i = 0; i < KPT / 4; ++i)
+        k4[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, (p0 + 4 * i) * 4, 0, SC1));
+#pragma unroll
+      for (int q = 0; q < KPT; ++q) key[q] = radix_key(__uint_as_float(k4[q / 4][q % 4]));
     }
     if (tid < 256) K.tot[tid] = ld_agent_u32(&row_hist(gd.tag, s)[tid]);
     __syncthreads();
@@ -705,13 +711,13 @@ class Step {
       }
       const int gt_in = block_excl_scan(c_gt), eq_in = block_excl_scan(c_eq);
       if (tid == AT - 1) {  // the last thread's inclusive sums are the member's totals
-        mb_put(&A.mail.cnt[((size_t)s * TEAM + m) * 2], (uint32_t)(gt_in + c_gt), gd.tag);
-        mb_put(&A.mail.cnt[((size_t)s * TEAM + m) * 2 + 1], (uint32_t)(eq_in + c_eq), gd.tag);
+        mb_put(&A.mail.cnt[((size_t)s * TMK + m) * 2], (uint32_t)(gt_in + c_gt), gd.tag);
+        mb_put(&A.mail.cnt[((size_t)s * TMK + m) * 2 + 1], (uint32_t)(eq_in + c_eq), gd.tag);
       }
       ok = true;
-      if (tid < 2 * TEAM) {
+      if (tid < 2 * TMK) {
         uint32_t v = 0;
-        ok = poll_word(&A.mail.cnt[(size_t)s * TEAM * 2 + tid], v, W_TEAM, gd);
+        ok = poll_word(&A.mail.cnt[(size_t)s * TMK * 2 + tid], v, W_TEAM, gd);
         K.cnt[tid / 2][tid % 2] = (int)v;
       }
       if (!block_all(ok)) return false;
