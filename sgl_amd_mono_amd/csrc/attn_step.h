@@ -26,10 +26,12 @@
 //          above the threshold and the lowest positions equal to it, ascending -> cache
 //          slots (page_table[p / 64] * 64 + p % 64) -> mailbox sel (glm53/check.py:100-117)
 //   split  (row, 64 selected tokens): sub-tiles of 64 tokens gathered from the FP8
-//          cache and widened exactly to bf16 in LDS, bf16 MFMA 16x16x32 for q.k and
-//          p.v, the per-token scale folded into the logit and the probability, online
-//          softmax -> the split's partials (bf16, 32 KB in one contiguous run) and
-//          (m, l), then its done word (mailbox sdone)
+//          cache into LDS as they lie (q.k operands, widened exactly to bf16 in
+//          registers) and, their value dims, widened and transposed (p.v operands); q
+//          in registers; bf16 MFMA 16x16x32 for q.k (two waves a token tile, each half
+//          of the 576 dims) and p.v, the per-token scale folded into the logit and the
+//          probability, online softmax -> the split's partials (bf16, 32 KB in one
+//          contiguous run) and (m, l), then its done word (mailbox sdone)
 //   merge  (row, head): once every split of the row is done,
 //          out = sum_j e^(m_j - M) acc_j / sum_j e^(m_j - M) l_j, bf16
 #pragma once
@@ -57,11 +59,19 @@ constexpr int AW = AT / WAVE;
 constexpr int KPM = MAX_CTX / TMK;           // keys a top-k team member owns
 constexpr int KPT = KPM / AT;                // keys a thread of a member holds
 constexpr int SUB = 64;                      // tokens a split sub-tile
-constexpr int Q_STRIDE = DQK + 8;            // bf16 a q row in LDS
-// dwords a cached row in LDS, as bf16 pairs: 16-byte aligned rows; the swizzle below
-// spreads a p.v column (8 rows, 8 apart for the 4 lane groups) over the banks
-constexpr int KVW = DQK / 2 + 4;
+constexpr int QK_HALF = DQK / 2;             // dims of q.k a wave sums (two waves a token tile)
+constexpr int QK_STEPS = QK_HALF / 32;       // its bf16 MFMA k steps
+// dwords a cached FP8 row in LDS: 16-byte aligned, and 20 banks (mod 64) from the next
+// row, so the 16 rows of a q.k operand read fall on distinct banks
+constexpr int KF_W = DQK / 4 + 4;
+constexpr int VT_STRIDE = SUB + 8;           // bf16 a transposed value row (one dim) in LDS
+constexpr int PF_STRIDE = SUB + 4;           // f32 a logit row in LDS
 constexpr int PB_STRIDE = SUB + 8;           // bf16 a probability row in LDS
+constexpr int ROPE_CH = (DQK - DV) / 16;     // 16-byte chunks of a row past the value dims
+// 16-byte units a staged q row (one head): padded by one, so the 16 heads of a q
+// operand read fall on distinct banks
+constexpr int Q_UNITS = DQK / 8 + 1;
+static_assert(DV / 16 * (SUB / 4) == AT && ROPE_CH * SUB <= AT && QK_HALF % 32 == 0, "gather tiling");
 constexpr int KEYS_WAVE = CHUNK / AW;        // 128 keys a wave of a score task
 constexpr int KTILES = KEYS_WAVE / 16;
 constexpr float NEG_INF = -__builtin_huge_valf();
@@ -88,18 +98,32 @@ struct TopkLds {
   int32_t above, pre_above;
 };
 
+// Typed views of 16- and 8-byte units: an access through a pointer cast from a narrower
+// element type is split by the compiler into 4-byte pairs (the cast's alignment is
+// not known to it); through an array of the unit type it is one b128 / b64 access.
 struct SplitLds {
-  uint16_t q[NH][Q_STRIDE];
-  union {
-    uint32_t kvb[SUB * KVW];     // the sub-tile's rows widened to bf16, swizzled (kv_at)
-    u32x4 kvb4[SUB * KVW / 4];   // the same as 16-byte groups (kv_at16 / 4): b128 accesses
+  union {  // the sub-tile's cached rows as they lie (E4M3): q.k operands (8 dims a unit)
+    u32x4 kf16[SUB][KF_W / 4];
+    u32x2 kf8[SUB][KF_W / 2];
   };
-  float pf[NH][SUB];
-  uint16_t pb[NH][PB_STRIDE];
+  union {  // their first DV dims widened to bf16, a row a dim (vt_unit): p.v operands
+    u32x4 vt16[DV][VT_STRIDE / 8];  // 8 tokens a unit
+    u32x2 vt8[DV][VT_STRIDE / 4];   // 4 tokens a unit
+    u32x4 q16[NH][Q_UNITS];         // before the first sub-tile: the row's q (bf16)
+  };
+  union {  // logits [dim half][head][token]: sums over dims [0, 288) and [288, 576)
+    f32x4 pf4[2][NH][PF_STRIDE / 4];
+    float pf[2][NH][PF_STRIDE];
+  };
+  union {  // probabilities times the tokens' scales, bf16 [head][token]
+    u32x4 pb16[NH][PB_STRIDE / 8];
+    uint16_t pb[NH][PB_STRIDE];
+  };
   int32_t slot[SPLIT_MAX];
   float kvs[SUB];
   float alpha[NH];
 };
+static_assert(KF_W % 4 == 0 && VT_STRIDE % 8 == 0 && PF_STRIDE % 4 == 0 && PB_STRIDE % 8 == 0, "16-byte units");
 
 struct MergeLds {
   float w[8][SPLITS];  // each split's weight e^(m_j - M) a head of the task, 0 for an empty split
@@ -164,23 +188,17 @@ MONO_DEV f32x4 mfma_fp4_opb(const u32x4& a, const u32x4& b, int sa, int sb) {
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A, B, z, 4, 4, 0, sa, OPB, sb);
 }
 
-// Dword of (token t, dims 2 w, 2 w + 1) in a sub-tile's bf16 rows: rows 8 apart XOR
-// their dword index by 8 so a p.v column's 4 lane groups hit different banks; 4-dword
-// groups stay contiguous and aligned for the q.k reads.
-MONO_DEV int kv_at(int t, int w) { return t * KVW + (w ^ (((t >> 3) & 3) << 3)); }
-// the 16-byte group of kv_at(t, w) for w a multiple of 4 (KVW and the XOR term are
-// multiples of 4, so the group is whole), as an index of u32x4 groups: accessed
-// through a u32x4 array the group is one b128 LDS access, where a cast of a uint32_t
-// address is split into 4-byte pairs
-MONO_DEV int kv_at16(int t, int w) { return kv_at(t, w) >> 2; }
+// E4M3 bytes 2 HW, 2 HW + 1 of a dword -> two bf16 as a dword, the first in the low half
+// (exact: every E4M3 value is a bf16 value)
+template <bool HW>
+MONO_DEV uint32_t fp8x2_bf16(uint32_t w) {
+  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, HW));
+}
 
-// 4 E4M3 bytes -> 4 bf16 as 2 dwords (exact: every E4M3 value is a bf16 value)
-MONO_DEV u32x2 fp8x4_bf16(uint32_t w) {
-  const f32x2 lo = fp8x2_unpack<false>(w), hi = fp8x2_unpack<true>(w);
-  u32x2 o;
-  o[0] = (__float_as_uint(lo[0]) >> 16) | (__float_as_uint(lo[1]) & 0xffff0000u);
-  o[1] = (__float_as_uint(hi[0]) >> 16) | (__float_as_uint(hi[1]) & 0xffff0000u);
-  return o;
+// 8 E4M3 bytes (two dwords) -> 8 bf16: an MFMA operand of 8 consecutive k
+MONO_DEV bf16x8 fp8x8_bf16x8(const u32x2& w) {
+  const u32x4 o = {fp8x2_bf16<false>(w[0]), fp8x2_bf16<true>(w[0]), fp8x2_bf16<false>(w[1]), fp8x2_bf16<true>(w[1])};
+  return __builtin_bit_cast(bf16x8, o);
 }
 
 class Step {
@@ -755,62 +773,63 @@ class Step {
   }
 
   // ---------------------------------------------------------------- split
-  static constexpr int GATHER = (SUB * (DQK / 16) + AT - 1) / AT;  // 16-byte loads a thread a sub-tile
+  // A thread's share of a sub-tile's rows: value chunk c = tid % 32 (dims 16 c .. 16 c +
+  // 15) of the 4 tokens 4 m .. 4 m + 3, m = tid / 32 (a wave's load covers 512
+  // contiguous bytes of each of 2 rows), and (the first SUB x ROPE_CH threads) one
+  // 16-byte chunk past the value dims; the scale of token tid % SUB.
+  struct Gather {
+    u32x4 v[4];
+    u32x4 rope;
+    float sc;
+  };
 
-  // Issue sub-tile st's cache-row loads: consecutive lanes read consecutive 16-byte
-  // chunks of a row. Every load is unconditional (an empty slot or a surplus chunk
-  // reads row 0 and is masked later): a load under a condition is waited for at the
-  // join, which would serialize the gather's round trips.
-  MONO_DEV void gather_load(const SplitLds& P, int st, u32x4 (&gv)[GATHER], float& gs) {
+  // Issue sub-tile st's cache-row loads. Every load is unconditional (an empty slot reads
+  // row 0, zeroed at the store): a load under a condition is waited for at the join,
+  // which would serialize the gather's round trips.
+  MONO_DEV void gather_load(const SplitLds& P, int st, Gather& gt) {
+    const int c = tid % (DV / 16), m = tid / (DV / 16);
+    const int32_t* sl = P.slot + st * SUB;
 #pragma unroll
-    for (int i = 0; i < GATHER; ++i) {
-      const int f = min(tid + i * AT, SUB * (DQK / 16) - 1);
-      const int t = f / (DQK / 16), c = f % (DQK / 16);
-      const int slot = max(P.slot[st * SUB + t], 0);
-      gv[i] = ld_nt_u32x4(A.kv + (size_t)slot * DQK + c * 16);
-    }
-    gs = A.kv_scale[max(P.slot[st * SUB + tid % SUB], 0) & A.kv_mask];
+    for (int k = 0; k < 4; ++k) gt.v[k] = ld_nt_u32x4(A.kv + (size_t)max(sl[4 * m + k], 0) * DQK + 16 * c);
+    const int f = min(tid, ROPE_CH * SUB - 1);
+    gt.rope = ld_nt_u32x4(A.kv + (size_t)max(sl[f / ROPE_CH], 0) * DQK + DV + 16 * (f % ROPE_CH));
+    gt.sc = A.kv_scale[max(sl[tid % SUB], 0) & A.kv_mask];
   }
 
-  // bf16 column d of 8 consecutive rows from t0: a p.v operand (8 tokens of one dim).
-  MONO_DEV static bf16x8 column8(const SplitLds& P, int t0, int d) {
-    const uint16_t* b = reinterpret_cast<const uint16_t*>(P.kvb);
-    u32x4 w;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const uint32_t lo = b[2 * kv_at(t0 + 2 * j, d >> 1) + (d & 1)];
-      const uint32_t hi = b[2 * kv_at(t0 + 2 * j + 1, d >> 1) + (d & 1)];
-      w[j] = lo | (hi << 16);
-    }
-    return __builtin_bit_cast(bf16x8, w);
-  }
+  // The 16-byte unit of vt row d holding tokens 8 u .. 8 u + 7: a row's units XOR the
+  // row's 16-dim group, so the 32 dim groups a wave's transposed store spans fall on 8
+  // different bank groups instead of one (a p.v read stays one aligned unit).
+  MONO_DEV static int vt_unit(int d, int u) { return u ^ ((d >> 4) & 7); }
 
-  // Store the gathered rows of sub-tile st widened to bf16, row-major (swizzled); the
-  // rows of empty slots as zeros (their loads read row 0).
-  MONO_DEV void gather_store(SplitLds& P, int st, const u32x4 (&gv)[GATHER], float gs) {
+  // Store sub-tile st's rows: as they lie into kf8, and the value dims widened to bf16
+  // and transposed into vt (a thread writes one dim of its 4 tokens as 8 bytes); the
+  // rows of empty slots as zeros.
+  MONO_DEV void gather_store(SplitLds& P, int st, const Gather& gt) {
+    const int c = tid % (DV / 16), m = tid / (DV / 16);
+    const int32_t* sl = P.slot + st * SUB;
+    u32x4 w[4];
 #pragma unroll
-    for (int i = 0; i < GATHER; ++i) {
-      const int f = tid + i * AT;
-      if (f < SUB * (DQK / 16)) {
-        const int t = f / (DQK / 16), c = f % (DQK / 16);
-        const bool live = P.slot[st * SUB + t] >= 0;
-        u32x4 lo = {0u, 0u, 0u, 0u}, hi = {0u, 0u, 0u, 0u};
-#pragma unroll
-        for (int q = 0; q < 2; ++q) {
-          const u32x2 a = fp8x4_bf16(gv[i][q]), b = fp8x4_bf16(gv[i][q + 2]);
-          if (live) {
-            lo[2 * q] = a[0];
-            lo[2 * q + 1] = a[1];
-            hi[2 * q] = b[0];
-            hi[2 * q + 1] = b[1];
-          }
-        }
-        // dims 16c .. 16c + 15 are dwords 8c .. 8c + 7: one swizzled 8-dword block
-        P.kvb4[kv_at16(t, 8 * c)] = lo;
-        P.kvb4[kv_at16(t, 8 * c) + 1] = hi;
-      }
+    for (int k = 0; k < 4; ++k) {
+      const bool live = sl[4 * m + k] >= 0;
+      w[k] = live ? gt.v[k] : u32x4{0u, 0u, 0u, 0u};
+      P.kf16[4 * m + k][c] = w[k];
     }
-    if (tid < SUB) P.kvs[tid] = P.slot[st * SUB + tid] >= 0 ? gs : 0.f;
+#pragma unroll
+    for (int p = 0; p < 8; ++p) {  // dims 16 c + 2 p, 16 c + 2 p + 1
+      uint32_t b[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) b[k] = p % 2 ? fp8x2_bf16<true>(w[k][p / 2]) : fp8x2_bf16<false>(w[k][p / 2]);
+      const u32x2 lo = {__builtin_amdgcn_perm(b[1], b[0], 0x05040100u), __builtin_amdgcn_perm(b[3], b[2], 0x05040100u)};
+      const u32x2 hi = {__builtin_amdgcn_perm(b[1], b[0], 0x07060302u), __builtin_amdgcn_perm(b[3], b[2], 0x07060302u)};
+      const int h8 = 2 * vt_unit(16 * c, m / 2) + m % 2;
+      P.vt8[16 * c + 2 * p][h8] = lo;
+      P.vt8[16 * c + 2 * p + 1][h8] = hi;
+    }
+    if (tid < ROPE_CH * SUB) {
+      const int t = tid / ROPE_CH;
+      P.kf16[t][DV / 16 + tid % ROPE_CH] = sl[t] >= 0 ? gt.rope : u32x4{0u, 0u, 0u, 0u};
+    }
+    if (tid < SUB) P.kvs[tid] = sl[tid] >= 0 ? gt.sc : 0.f;
   }
 
   // Split j of row s's nsp: its TOPK / nsp selected tokens in sub-tiles of SUB. LONG: a
@@ -836,18 +855,17 @@ class Step {
       if (!hint_wait(NH, [fd](int i) { return fd + i; }, A.fsite + 1, gd)) return false;
       q_ready = true;
     }
+    // the row's q into LDS while the selection is awaited (each byte read once; the
+    // waves take their operands from there while the cache rows are in flight)
     {
-      constexpr int QL = (NH * DQK / 8 + AT - 1) / AT;
+      constexpr int QN = NH * DQK / 8, QL = (QN + AT - 1) / AT;
       u32x4 qv[QL];
 #pragma unroll
-      for (int i = 0; i < QL; ++i) {
-        const int f = min(tid + i * AT, NH * DQK / 8 - 1);  // unconditional (see gather_load)
-        qv[i] = ld_u32x4(A.q + (size_t)s * NH * DQK + (size_t)f * 8);
-      }
+      for (int i = 0; i < QL; ++i) qv[i] = ld_u32x4(A.q + (size_t)s * NH * DQK + (size_t)min(tid + i * AT, QN - 1) * 8);
 #pragma unroll
       for (int i = 0; i < QL; ++i) {
-        const int f = tid + i * AT;
-        if (f < NH * DQK / 8) *reinterpret_cast<u32x4*>(&P.q[f / (DQK / 8)][(f % (DQK / 8)) * 8]) = qv[i];
+        const int f = tid + i * AT;  // unconditional loads (see gather_load), guarded stores
+        if (f < QN) P.q16[f / (DQK / 8)][f % (DQK / 8)] = qv[i];
       }
     }
     bool ok = true;
@@ -864,20 +882,27 @@ class Step {
     if (!block_all(ok)) return false;
     mark_waited();
 
-    // logit tile of this wave: heads 16 ht .. 16 ht + 15, tokens 16 tt .. 16 tt + 15 of
-    // the sub-tile (lane (g, r): heads 16 ht + 4 g + i, token 16 tt + r); its running
-    // maximum and its own tokens' running sum a head, i
-    const int ht = wave / 4, tt = wave % 4;
-    f32x4 acc[2][4];
+    // p.v of wave w: dims 64 w + 16 b + [0, 16) (b = 0..3) x heads 16 a + [0, 16) (a = 0, 1);
+    // lane (g, r) holds dims 64 w + 16 b + 4 g + i of head 16 a + r. Softmax of heads
+    // 4 w .. 4 w + 3 (lane = token): their running maxima and sums.
+    f32x4 acc[4][2];
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+      for (int a = 0; a < 2; ++a) acc[b][a] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m_run[4] = {NEG_INF, NEG_INF, NEG_INF, NEG_INF}, l_run[4] = {0.f, 0.f, 0.f, 0.f};
+    const int nsub = (cnt + SUB - 1) / SUB;
+    Gather gt;
+    gather_load(P, 0, gt);
+    // q.k of wave (kh, tt): dims QK_HALF kh .. of tokens 16 tt .. 16 tt + 15 against every
+    // head; its q operands (heads 16 a + r, 8 dims a k step) held in registers
+    bf16x8 qa[2][QK_STEPS];
 #pragma unroll
     for (int a = 0; a < 2; ++a)
 #pragma unroll
-      for (int b = 0; b < 4; ++b) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
-    float m_run[4] = {NEG_INF, NEG_INF, NEG_INF, NEG_INF}, l_run[4] = {0.f, 0.f, 0.f, 0.f};
-    const int nsub = (cnt + SUB - 1) / SUB;
-    u32x4 gv[GATHER];
-    float gs;
-    gather_load(P, 0, gv, gs);
+      for (int ks = 0; ks < QK_STEPS; ++ks)
+        qa[a][ks] = __builtin_bit_cast(bf16x8, P.q16[16 * a + r][QK_HALF / 8 * (wave / 4) + 4 * ks + g]);
+    __syncthreads();  // every wave holds its q before the first sub-tile's rows overwrite it
 
 #pragma unroll 1
     for (int st = 0; st < nsub; ++st) {
@@ -885,101 +910,112 @@ class Step {
       // softmax and p.v LDS addresses are derived inside the loop, not hoisted out of it
       // and held across it
       const int lane = LONG ? opaque_v(tid) % WAVE : this->lane, g = lane / 16, r = lane % 16;
-      gather_store(P, st, gv, gs);
+      const int wv = LONG ? opaque_v(tid) / WAVE : wave;
+      gather_store(P, st, gt);
       __syncthreads();
-      if (st + 1 < nsub) gather_load(P, st + 1, gv, gs);  // in flight while this sub-tile computes
-      // logits of 16 heads x 16 tokens a wave: K = 576 in 18 bf16 steps
+      if (st + 1 < nsub) gather_load(P, st + 1, gt);  // in flight while this sub-tile computes
+      // logits, transposed: A = 16 cached rows (FP8, widened in registers), B = 16 heads
+      // of q; lane (g, r) ends with tokens 16 tt + 4 g + i of head 16 a + r
       {
-        // two accumulators and operands read a step ahead: the LDS reads of step ks + 1
-        // overlap the MFMA of step ks
-        f32x4 d0 = {0.f, 0.f, 0.f, 0.f}, d1 = d0;
-        const uint16_t* qrow = &P.q[16 * ht + r][8 * g];
-        bf16x8 qa = *reinterpret_cast<const bf16x8*>(qrow);
-        bf16x8 kb = __builtin_bit_cast(bf16x8, P.kvb4[kv_at16(16 * tt + r, 4 * g)]);
+        const u32x2* krow = &P.kf8[16 * (wv % 4) + r][QK_HALF / 8 * (wv / 4) + g];
+        u32x2 kw[QK_STEPS];
 #pragma unroll
-        for (int ks = 0; ks < DQK / 32; ++ks) {
-          bf16x8 qn = qa, kn = kb;
-          if (ks + 1 < DQK / 32) {
-            qn = *reinterpret_cast<const bf16x8*>(qrow + 32 * (ks + 1));
-            kn = __builtin_bit_cast(bf16x8, P.kvb4[kv_at16(16 * tt + r, 16 * (ks + 1) + 4 * g)]);
-          }
-          if (ks % 2 == 0) d0 = mfma_bf16(qa, kb, d0);
-          else d1 = mfma_bf16(qa, kb, d1);
-          qa = qn;
-          kb = kn;
+        for (int ks = 0; ks < QK_STEPS; ++ks) kw[ks] = krow[4 * ks];
+        f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = s0;
+#pragma unroll
+        for (int ks = 0; ks < QK_STEPS; ++ks) {
+          const bf16x8 ka = fp8x8_bf16x8(kw[ks]);
+          s0 = mfma_bf16(ka, qa[0][ks], s0);
+          s1 = mfma_bf16(ka, qa[1][ks], s1);
         }
-        const f32x4 d = d0 + d1;
-        const int t = 16 * tt + r;
-        const bool valid = st * SUB + t < cnt && P.slot[st * SUB + t] >= 0;
-        const float sc = P.kvs[t] * A.scale;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) P.pf[16 * ht + 4 * g + i][t] = valid ? d[i] * sc : NEG_INF;
+        P.pf4[wv / 4][r][4 * (wv % 4) + g] = s0;
+        P.pf4[wv / 4][16 + r][4 * (wv % 4) + g] = s1;
       }
       __syncthreads();
-      // online softmax of heads 4 wave .. 4 wave + 3; lane = token
+      // online softmax of heads 4 w .. 4 w + 3; lane = token (the four heads' reductions
+      // side by side)
+      {
+        const int t = lane;
+        const bool valid = P.slot[st * SUB + t] >= 0;
+        const float ksc = P.kvs[t], sc = ksc * A.scale;
+        float x[4], mx[4], pr[4], al[4];
 #pragma unroll
-      for (int hh = 0; hh < 4; ++hh) {
-        const int h = 4 * wave + hh;
-        const float x = P.pf[h][lane];
-        const float m_new = fmaxf(m_run[hh], wave_max(x));
-        const float p = (m_new == NEG_INF || x == NEG_INF) ? 0.f : hw_exp(x - m_new);
-        const float alpha = m_run[hh] == NEG_INF ? (m_new == NEG_INF ? 1.f : 0.f) : hw_exp(m_run[hh] - m_new);
-        l_run[hh] = l_run[hh] * alpha + wave_sum(p);
-        m_run[hh] = m_new;
-        P.pb[h][lane] = f32_to_bf16_bits(p * P.kvs[lane]);
-        if (lane == 0) P.alpha[h] = alpha;
+        for (int hh = 0; hh < 4; ++hh) {
+          const int h = 4 * wv + hh;
+          x[hh] = valid ? (P.pf[0][h][t] + P.pf[1][h][t]) * sc : NEG_INF;
+        }
+#pragma unroll
+        for (int hh = 0; hh < 4; ++hh) mx[hh] = fmaxf(m_run[hh], wave_max(x[hh]));
+#pragma unroll
+        for (int hh = 0; hh < 4; ++hh) {
+          pr[hh] = (mx[hh] == NEG_INF || x[hh] == NEG_INF) ? 0.f : hw_exp(x[hh] - mx[hh]);
+          al[hh] = m_run[hh] == NEG_INF ? (mx[hh] == NEG_INF ? 1.f : 0.f) : hw_exp(m_run[hh] - mx[hh]);
+        }
+#pragma unroll
+        for (int hh = 0; hh < 4; ++hh) {
+          l_run[hh] = l_run[hh] * al[hh] + wave_sum(pr[hh]);
+          m_run[hh] = mx[hh];
+          P.pb[4 * wv + hh][t] = f32_to_bf16_bits(pr[hh] * ksc);
+        }
+        if (lane < 4) P.alpha[4 * wv + lane] = lane == 0 ? al[0] : lane == 1 ? al[1] : lane == 2 ? al[2] : al[3];
       }
       __syncthreads();
-      // o[32 heads x 64 dims of this wave] = alpha o + p . v
+      // o^T[dims x heads] = alpha o^T + v^T p^T: A = 16 dims of the transposed values,
+      // B = 16 heads' probabilities, k = 32 tokens a step
+      {
+        float alh[2];
 #pragma unroll
-      for (int a = 0; a < 2; ++a) {
-        float al[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) al[i] = P.alpha[16 * a + 4 * g + i];
+        for (int a = 0; a < 2; ++a) alh[a] = P.alpha[16 * a + r];
 #pragma unroll
         for (int b = 0; b < 4; ++b)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) acc[a][b][i] *= al[i];
-      }
+          for (int a = 0; a < 2; ++a)
 #pragma unroll
-      for (int kt = 0; kt < SUB / 32; ++kt) {
-        bf16x8 pa[2], vb[4];  // every operand of the k step read before its MFMAs
+            for (int i = 0; i < 4; ++i) acc[b][a][i] *= alh[a];
 #pragma unroll
-        for (int a = 0; a < 2; ++a) pa[a] = *reinterpret_cast<const bf16x8*>(&P.pb[16 * a + r][32 * kt + 8 * g]);
+        for (int kt = 0; kt < SUB / 32; ++kt) {
+          bf16x8 pv[2], va[4];  // every operand of the k step read before its MFMAs
 #pragma unroll
-        for (int b = 0; b < 4; ++b) vb[b] = column8(P, 32 * kt + 8 * g, 16 * (4 * wave + b) + r);
+          for (int a = 0; a < 2; ++a) pv[a] = __builtin_bit_cast(bf16x8, P.pb16[16 * a + r][4 * kt + g]);
 #pragma unroll
-        for (int b = 0; b < 4; ++b)
+          for (int b = 0; b < 4; ++b) {
+            const int d = 64 * wv + 16 * b + r;
+            va[b] = __builtin_bit_cast(bf16x8, P.vt16[d][vt_unit(d, 4 * kt + g)]);
+          }
 #pragma unroll
-          for (int a = 0; a < 2; ++a) acc[a][b] = mfma_bf16(pa[a], vb[b], acc[a][b]);
+          for (int b = 0; b < 4; ++b)
+#pragma unroll
+            for (int a = 0; a < 2; ++a) acc[b][a] = mfma_bf16(va[b], pv[a], acc[b][a]);
+        }
       }
       __syncthreads();
     }
     // the partials (bf16, the reference's split partials, kernel.py:4040-4066) staged as
-    // [head][dim] in LDS (lane r holds dim 16 n + r, its neighbour r ^ 1 the other half
-    // of a pair), then stored as the split's contiguous 32 KB by 16-byte
-    // device-coherent stores; then (m, l); then the split's done word
-    uint32_t* ot = P.kvb;  // free after the last P.V step's barrier
-    static_assert(sizeof(P.kvb) >= NH * DV * 2, "partial staging");
+    // [head][dim] in LDS (a lane's 4 consecutive dims of a head as 8 bytes), then stored
+    // as the split's contiguous 32 KB by 16-byte device-coherent stores (whole lines);
+    // then (m, l); then the split's done word
+    // (a head's row padded by 16 bytes: the 16 heads of a lane group's store fall on
+    // distinct banks)
+    constexpr int OT_ROW = DV / 8 + 1;  // 16-byte units a staged head row
+    u32x2* ot = &P.vt8[0][0];           // free after the last p.v step's barrier
+    static_assert(sizeof(P.vt8) >= NH * OT_ROW * 16, "partial staging");
 #pragma unroll
-    for (int a = 0; a < 2; ++a)
+    for (int b = 0; b < 4; ++b)
 #pragma unroll
-      for (int b = 0; b < 4; ++b)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float mine = acc[a][b][i], other = dpp_f<DPP_XOR1>(mine);
-          const int h = 16 * a + 4 * g + i, dim = 16 * (4 * wave + b) + r;
-          if ((r & 1) == 0) ot[(h * DV + dim) / 2] = pack_bf16x2(mine, other);
-        }
+      for (int a = 0; a < 2; ++a) {
+        const u32x2 o = {pack_bf16x2(acc[b][a][0], acc[b][a][1]), pack_bf16x2(acc[b][a][2], acc[b][a][3])};
+        ot[(16 * a + r) * 2 * OT_ROW + (64 * wave + 16 * b + 4 * g) / 4] = o;
+      }
     __syncthreads();
     {
       const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
           A.mail.part + ((size_t)s * SPLITS + j) * NH * DV, 0, NH * DV * 2, BUF_DWORD3);
+      const u32x4* ot16 = &P.vt16[0][0];
       constexpr int CH16 = NH * DV * 2 / 16;  // 16-byte chunks of the split's partials
 #pragma unroll
       for (int q = 0; q < CH16 / AT; ++q) {
         const int c = tid + AT * q;
-        __builtin_amdgcn_raw_buffer_store_b128(*reinterpret_cast<const u32x4*>(&ot[4 * c]), rs, 16 * c, 0, SC1);
+        __builtin_amdgcn_raw_buffer_store_b128(ot16[(c / (DV / 8)) * OT_ROW + c % (DV / 8)], rs, 16 * c, 0, SC1);
       }
     }
     if (lane < 4) {
@@ -989,7 +1025,7 @@ class Step {
       st_agent_f32(&A.mail.ml[(mlb + h) * 2], m);
       st_agent_f32(&A.mail.ml[(mlb + h) * 2 + 1], l);
     }
-    split_done(s, j);  // its barrier also frees the staging LDS for the next task
+    split_done(s, j);  // its barrier also frees the LDS for the next task
     return true;
   }
 
