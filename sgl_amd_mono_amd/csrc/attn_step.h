@@ -117,13 +117,20 @@ struct SplitLds {
   };
   union {  // probabilities times the tokens' scales, bf16 [head][token]
     u32x4 pb16[NH][PB_STRIDE / 8];
-    uint16_t pb[NH][PB_STRIDE];
+    u32x2 pb8[NH][PB_STRIDE / 4];
   };
-  int32_t slot[SPLIT_MAX];
-  float kvs[SUB];
+  union {
+    int32_t slot[SPLIT_MAX];
+    i32x4 slot4[SPLIT_MAX / 4];
+  };
+  union {
+    float kvs[SUB];
+    f32x4 kvs4[SUB / 4];
+  };
   float alpha[NH];
 };
 static_assert(KF_W % 4 == 0 && VT_STRIDE % 8 == 0 && PF_STRIDE % 4 == 0 && PB_STRIDE % 8 == 0, "16-byte units");
+static_assert(NH * 16 == AT && SUB == 16 * 4, "softmax: a 16-lane row a head, 4 tokens a lane");
 
 struct MergeLds {
   float w[8][SPLITS];  // each split's weight e^(m_j - M) a head of the task, 0 for an empty split
@@ -855,8 +862,6 @@ class Step {
       if (!hint_wait(NH, [fd](int i) { return fd + i; }, A.fsite + 1, gd)) return false;
       q_ready = true;
     }
-    // the row's q into LDS while the selection is awaited (each byte read once; the
-    // waves take their operands from there while the cache rows are in flight)
     {
       constexpr int QN = NH * DQK / 8, QL = (QN + AT - 1) / AT;
       u32x4 qv[QL];
@@ -883,14 +888,15 @@ class Step {
     mark_waited();
 
     // p.v of wave w: dims 64 w + 16 b + [0, 16) (b = 0..3) x heads 16 a + [0, 16) (a = 0, 1);
-    // lane (g, r) holds dims 64 w + 16 b + 4 g + i of head 16 a + r. Softmax of heads
-    // 4 w .. 4 w + 3 (lane = token): their running maxima and sums.
+    // lane (g, r) holds dims 64 w + 16 b + 4 g + i of head 16 a + r. Softmax: each
+    // 16-lane row of the workgroup one head (tid / 16), a lane 4 tokens; the head's
+    // running maximum and sum (every lane of the row holds them).
     f32x4 acc[4][2];
 #pragma unroll
     for (int b = 0; b < 4; ++b)
 #pragma unroll
       for (int a = 0; a < 2; ++a) acc[b][a] = f32x4{0.f, 0.f, 0.f, 0.f};
-    float m_run[4] = {NEG_INF, NEG_INF, NEG_INF, NEG_INF}, l_run[4] = {0.f, 0.f, 0.f, 0.f};
+    float m_run = NEG_INF, l_run = 0.f;
     const int nsub = (cnt + SUB - 1) / SUB;
     Gather gt;
     gather_load(P, 0, gt);
@@ -932,32 +938,27 @@ class Step {
         P.pf4[wv / 4][16 + r][4 * (wv % 4) + g] = s1;
       }
       __syncthreads();
-      // online softmax of heads 4 w .. 4 w + 3; lane = token (the four heads' reductions
-      // side by side)
+      // online softmax: head tid / 16, tokens 4 (tid % 16) .. + 3; the head's reductions
+      // inside the lane's 16-lane row (DPP)
       {
-        const int t = lane;
-        const bool valid = P.slot[st * SUB + t] >= 0;
-        const float ksc = P.kvs[t], sc = ksc * A.scale;
-        float x[4], mx[4], pr[4], al[4];
+        const int ti = LONG ? opaque_v(tid) : tid, h = ti / 16, tq = ti % 16;
+        const f32x4 x0 = P.pf4[0][h][tq], x1 = P.pf4[1][h][tq], ks = P.kvs4[tq];
+        const i32x4 sl = P.slot4[st * (SUB / 4) + tq];
+        float x[4];
 #pragma unroll
-        for (int hh = 0; hh < 4; ++hh) {
-          const int h = 4 * wv + hh;
-          x[hh] = valid ? (P.pf[0][h][t] + P.pf[1][h][t]) * sc : NEG_INF;
+        for (int i = 0; i < 4; ++i) x[i] = sl[i] >= 0 ? (x0[i] + x1[i]) * (ks[i] * A.scale) : NEG_INF;
+        const float mx = fmaxf(m_run, row_reduce<16>(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])), OpMax()));
+        float pr[4], ps = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          pr[i] = (mx == NEG_INF || x[i] == NEG_INF) ? 0.f : hw_exp(x[i] - mx);
+          ps += pr[i];
         }
-#pragma unroll
-        for (int hh = 0; hh < 4; ++hh) mx[hh] = fmaxf(m_run[hh], wave_max(x[hh]));
-#pragma unroll
-        for (int hh = 0; hh < 4; ++hh) {
-          pr[hh] = (mx[hh] == NEG_INF || x[hh] == NEG_INF) ? 0.f : hw_exp(x[hh] - mx[hh]);
-          al[hh] = m_run[hh] == NEG_INF ? (mx[hh] == NEG_INF ? 1.f : 0.f) : hw_exp(m_run[hh] - mx[hh]);
-        }
-#pragma unroll
-        for (int hh = 0; hh < 4; ++hh) {
-          l_run[hh] = l_run[hh] * al[hh] + wave_sum(pr[hh]);
-          m_run[hh] = mx[hh];
-          P.pb[4 * wv + hh][t] = f32_to_bf16_bits(pr[hh] * ksc);
-        }
-        if (lane < 4) P.alpha[4 * wv + lane] = lane == 0 ? al[0] : lane == 1 ? al[1] : lane == 2 ? al[2] : al[3];
+        const float al = m_run == NEG_INF ? (mx == NEG_INF ? 1.f : 0.f) : hw_exp(m_run - mx);
+        l_run = l_run * al + row_reduce<16>(ps, OpAdd());
+        m_run = mx;
+        P.pb8[h][tq] = u32x2{pack_bf16x2(pr[0] * ks[0], pr[1] * ks[1]), pack_bf16x2(pr[2] * ks[2], pr[3] * ks[3])};
+        if (tq == 0) P.alpha[h] = al;
       }
       __syncthreads();
       // o^T[dims x heads] = alpha o^T + v^T p^T: A = 16 dims of the transposed values,
@@ -1018,12 +1019,9 @@ class Step {
         __builtin_amdgcn_raw_buffer_store_b128(ot16[(c / (DV / 8)) * OT_ROW + c % (DV / 8)], rs, 16 * c, 0, SC1);
       }
     }
-    if (lane < 4) {
-      const float m = lane == 0 ? m_run[0] : lane == 1 ? m_run[1] : lane == 2 ? m_run[2] : m_run[3];
-      const float l = lane == 0 ? l_run[0] : lane == 1 ? l_run[1] : lane == 2 ? l_run[2] : l_run[3];
-      const int h = 4 * wave + lane;
-      st_agent_f32(&A.mail.ml[(mlb + h) * 2], m);
-      st_agent_f32(&A.mail.ml[(mlb + h) * 2 + 1], l);
+    if (tid % 16 == 0) {
+      st_agent_f32(&A.mail.ml[(mlb + tid / 16) * 2], m_run);
+      st_agent_f32(&A.mail.ml[(mlb + tid / 16) * 2 + 1], l_run);
     }
     split_done(s, j);  // its barrier also frees the LDS for the next task
     return true;
