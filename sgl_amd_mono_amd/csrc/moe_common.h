@@ -101,8 +101,9 @@ MONO_DEV void plan_from_picks(PlanLds<E, TOPK>& P, int S) {
   const int before = __popcll(bal & ((1ull << lane) - 1ull));
   if (lane == 0) P.wcount[wave] = __popcll(bal);
   __syncthreads();
-  int off = 1;
-  for (int w = 0; w < wave; ++w) off += P.wcount[w];
+  int off = 1;  // fixed trip count: the LDS reads issue together, not one wait a wave
+#pragma unroll
+  for (int w = 0; w < THREADS / WAVE; ++w) off += w < wave ? P.wcount[w] : 0;
   if (f) {
     const int d = off + before;
     P.expert[d] = tid;
