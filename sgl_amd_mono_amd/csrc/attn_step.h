@@ -708,10 +708,18 @@ class Step {
       K.cu[tid] = u;
       if (!block_all(ok)) return false;
       if (wave * WAVE < n_cand) {  // wave-uniform
-        int rank = 0;              // candidates ranked before this thread's
-        for (int j = 0; j < n_cand; j += 4) {
-          const u32x4 x = *reinterpret_cast<const u32x4*>(&K.cu[j]);
-          rank += (x[0] > u ? 1 : 0) + (x[1] > u ? 1 : 0) + (x[2] > u ? 1 : 0) + (x[3] > u ? 1 : 0);
+        // candidates ranked before this thread's, 32 a step with the step's LDS reads issued
+        // together (K.cu holds zeros past the last candidate, and a step starting below
+        // n_cand <= CMAX ends inside K.cu)
+        static_assert(CMAX % 32 == 0, "whole steps");
+        int rank = 0;
+        for (int j = 0; j < n_cand; j += 32) {
+          u32x4 x[8];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) x[i] = *reinterpret_cast<const u32x4*>(&K.cu[j + 4 * i]);
+#pragma unroll
+          for (int i = 0; i < 8; ++i)
+            rank += (x[i][0] > u ? 1 : 0) + (x[i][1] > u ? 1 : 0) + (x[i][2] > u ? 1 : 0) + (x[i][3] > u ? 1 : 0);
         }
         if (tid < n_cand && rank == need - 1) K.uT = u;
       }
