@@ -521,6 +521,10 @@ class Step {
   MONO_DEV void hist_add(uint32_t* hist, bool live, uint32_t d) {
     const uint64_t act = __ballot(live);
     if (act == 0) return;  // wave-uniform
+    if (__popcll(act) <= 16) {  // few live lanes (wave-uniform): plain atomics, no scalar chain
+      if (live) atomicAdd(&hist[d], 1u);
+      return;
+    }
     const int first = __builtin_ctzll(act);
     const uint32_t d0 = (uint32_t)__builtin_amdgcn_readlane((int)d, first);
     const uint64_t same = __ballot(live && d == d0);
