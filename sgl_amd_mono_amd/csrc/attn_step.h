@@ -342,6 +342,7 @@ class Step {
     uint32_t w2[IH / 16][2];
     u32x4 kb[KTILES];
     uint32_t ks[KEYS_WAVE / PAGE];
+    int pg[KEYS_WAVE / PAGE];
   };
 
   MONO_DEV void score_load(int T, ScoreOps& o) {
@@ -384,6 +385,25 @@ class Step {
       o.ks[i] = *reinterpret_cast<const uint32_t*>(A.iks + (size_t)(pg[i] * 4 + g) * PAGE + r * 4);
   }
 
+  // The next task's query and page numbers; its key tiles and scales are issued from
+  // inside the current task's compute (score_compute), so no wave sits in one 70 KB
+  // issue burst (the CU's memory queue fills and stalls it) while it could compute.
+  MONO_DEV void score_load_head(int T, ScoreOps& o) const {
+    score_where(T, o);
+    if (o.k0 >= o.n) return;
+    score_query(o);
+#pragma unroll
+    for (int i = 0; i < KEYS_WAVE / PAGE; ++i) o.pg[i] = page_of(o.s, o.k0 + i * PAGE);
+  }
+  MONO_DEV void score_key_tile(ScoreOps& o, int kt) const {
+    o.kb[kt] = ld_nt_u32x4(A.ikv + ((size_t)(o.pg[kt / 4] * 4 + g) * PAGE + (kt % 4) * 16 + r) * 16);
+  }
+  MONO_DEV void score_key_scales(ScoreOps& o) const {
+#pragma unroll
+    for (int i = 0; i < KEYS_WAVE / PAGE; ++i)
+      o.ks[i] = *reinterpret_cast<const uint32_t*>(A.iks + (size_t)(o.pg[i] * 4 + g) * PAGE + r * 4);
+  }
+
   // key tile kt's logits against the four head tiles of the query
   MONO_DEV static void score_mfmas(const ScoreOps& o, int kt, f32x4 (&d)[IH / 16]) {
 #pragma unroll
@@ -402,8 +422,11 @@ class Step {
   // histogram of their leading key digits, added into the row's histogram (the top-k's
   // first radix pass) before the chunk is marked done (mailbox cdone). Every wave
   // reaches the barriers; a wave past the row computes nothing.
-  MONO_DEV void score_compute(const ScoreOps& o) {
+  MONO_DEV void score_compute(const ScoreOps& o, ScoreOps& nx, bool more) {
     const bool live = o.k0 < o.n;  // wave-uniform
+    // the next task's key tiles: two an iteration over the second half of this task's
+    // tiles (its page numbers have landed by then)
+    const bool nx_live = more && nx.k0 < nx.n;  // wave-uniform
     float sc[2] = {0.f, 0.f};
     if (live) {
       float wv[IH / 16][4];
@@ -422,6 +445,11 @@ class Step {
 #pragma unroll
       for (int kt = 0; kt < KTILES; ++kt) {
         if (kt + 1 < KTILES) score_mfmas(o, kt + 1, d[(kt + 1) % 2]);
+        static_assert(KTILES % 2 == 0, "two tiles an iteration");
+        if (nx_live && kt >= KTILES / 2) {
+          score_key_tile(nx, 2 * kt - KTILES);
+          score_key_tile(nx, 2 * kt - KTILES + 1);
+        }
         float part = 0.f;
 #pragma unroll
         for (int ht = 0; ht < IH / 16; ++ht)
@@ -431,7 +459,11 @@ class Step {
         part += __shfl_xor(part, 32, WAVE);
         if (kt % 4 == g) sc[kt / 4] = part;
       }
+    } else if (nx_live) {
+#pragma unroll
+      for (int kt = 0; kt < KTILES; ++kt) score_key_tile(nx, kt);
     }
+    if (nx_live) score_key_scales(nx);
     bool kl[2];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
@@ -487,8 +519,8 @@ class Step {
     for (int T = T0; T < n_score; T += G) {
       const uint64_t t0 = now_ticks();
       const bool more = T + G < n_score;
-      if (more) score_load(T + G, nxt);
-      score_compute(cur);
+      if (more) score_load_head(T + G, nxt);
+      score_compute(cur, nxt, more);
       stamp(T, t0, 0);
       if (more) cur = nxt;
     }
