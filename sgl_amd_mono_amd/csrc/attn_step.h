@@ -841,13 +841,24 @@ class Step {
   // row 0, zeroed at the store): a load under a condition is waited for at the join,
   // which would serialize the gather's round trips.
   MONO_DEV void gather_load(const SplitLds& P, int st, Gather& gt) {
+#pragma unroll
+    for (int part = 0; part < 3; ++part) gather_load_part(P, st, gt, part);
+  }
+  // part 0: value chunks of tokens 4 m, 4 m + 1; part 1: of 4 m + 2, 4 m + 3; part 2: the
+  // chunk past the value dims and the scale (a long split issues the next sub-tile's
+  // parts between its phases, so no wave stalls in one burst)
+  MONO_DEV void gather_load_part(const SplitLds& P, int st, Gather& gt, int part) {
     const int c = tid % (DV / 16), m = tid / (DV / 16);
     const int32_t* sl = P.slot + st * SUB;
+    if (part < 2) {
 #pragma unroll
-    for (int k = 0; k < 4; ++k) gt.v[k] = ld_nt_u32x4(A.kv + (size_t)max(sl[4 * m + k], 0) * DQK + 16 * c);
-    const int f = min(tid, ROPE_CH * SUB - 1);
-    gt.rope = ld_nt_u32x4(A.kv + (size_t)max(sl[f / ROPE_CH], 0) * DQK + DV + 16 * (f % ROPE_CH));
-    gt.sc = A.kv_scale[max(sl[tid % SUB], 0) & A.kv_mask];
+      for (int k = 2 * part; k < 2 * part + 2; ++k)
+        gt.v[k] = ld_nt_u32x4(A.kv + (size_t)max(sl[4 * m + k], 0) * DQK + 16 * c);
+    } else {
+      const int f = min(tid, ROPE_CH * SUB - 1);
+      gt.rope = ld_nt_u32x4(A.kv + (size_t)max(sl[f / ROPE_CH], 0) * DQK + DV + 16 * (f % ROPE_CH));
+      gt.sc = A.kv_scale[max(sl[tid % SUB], 0) & A.kv_mask];
+    }
   }
 
   // The 16-byte unit of vt row d holding tokens 8 u .. 8 u + 7: a row's units XOR the
@@ -966,7 +977,10 @@ class Step {
       const int wv = LONG ? opaque_v(tid) / WAVE : wave;
       gather_store(P, st, gt);
       __syncthreads();
-      if (st + 1 < nsub) gather_load(P, st + 1, gt);  // in flight while this sub-tile computes
+      // the next sub-tile's rows, in flight while this one computes (in three parts, one
+      // before each phase)
+      const bool next = st + 1 < nsub;
+      if (next) gather_load_part(P, st + 1, gt, 0);
       // logits, transposed: A = 16 cached rows (FP8, widened in registers), B = 16 heads
       // of q; lane (g, r) ends with tokens 16 tt + 4 g + i of head 16 a + r
       {
@@ -984,6 +998,7 @@ class Step {
         P.pf4[wv / 4][r][4 * (wv % 4) + g] = s0;
         P.pf4[wv / 4][16 + r][4 * (wv % 4) + g] = s1;
       }
+      if (next) gather_load_part(P, st + 1, gt, 1);
       __syncthreads();
       // online softmax: head tid / 16, tokens 4 (tid % 16) .. + 3; the head's reductions
       // inside the lane's 16-lane row (DPP)
@@ -1007,6 +1022,7 @@ class Step {
         P.pb8[h][tq] = u32x2{pack_bf16x2(pr[0] * ks[0], pr[1] * ks[1]), pack_bf16x2(pr[2] * ks[2], pr[3] * ks[3])};
         if (tq == 0) P.alpha[h] = al;
       }
+      if (next) gather_load_part(P, st + 1, gt, 2);
       __syncthreads();
       // o^T[dims x heads] = alpha o^T + v^T p^T: A = 16 dims of the transposed values,
       // B = 16 heads' probabilities, k = 32 tokens a step
