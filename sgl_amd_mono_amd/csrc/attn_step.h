@@ -869,16 +869,30 @@ class Step {
   // Store sub-tile st's rows: as they lie into kf8, and the value dims widened to bf16
   // and transposed into vt (a thread writes one dim of its 4 tokens as 8 bytes); the
   // rows of empty slots as zeros.
-  MONO_DEV void gather_store(SplitLds& P, int st, const Gather& gt) {
+  // (the rows as they lie, for q.k; the thread's value chunks stay in w. `vt_now`: the
+  // transposed values now, else gather_store_vt later: a long split runs it under its q.k
+  // MFMAs, 0.4-0.9 us faster at 24 and 48 rows; one-sub-tile splits measured 0.3-0.6 us
+  // slower that way and transpose here)
+  MONO_DEV void gather_store(SplitLds& P, int st, const Gather& gt, u32x4 (&w)[4], bool vt_now) {
     const int c = tid % (DV / 16), m = tid / (DV / 16);
     const int32_t* sl = P.slot + st * SUB;
-    u32x4 w[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       const bool live = sl[4 * m + k] >= 0;
       w[k] = live ? gt.v[k] : u32x4{0u, 0u, 0u, 0u};
       P.kf16[4 * m + k][c] = w[k];
     }
+    if (vt_now) gather_store_vt(P, w);
+    if (tid < ROPE_CH * SUB) {
+      const int t = tid / ROPE_CH;
+      P.kf16[t][DV / 16 + tid % ROPE_CH] = sl[t] >= 0 ? gt.rope : u32x4{0u, 0u, 0u, 0u};
+    }
+    if (tid < SUB) P.kvs[tid] = sl[tid] >= 0 ? gt.sc : 0.f;
+  }
+
+  // The thread's value chunks widened to bf16 and transposed into vt.
+  MONO_DEV void gather_store_vt(SplitLds& P, const u32x4 (&w)[4]) {
+    const int c = tid % (DV / 16), m = tid / (DV / 16);
 #pragma unroll
     for (int p = 0; p < 8; ++p) {  // dims 16 c + 2 p, 16 c + 2 p + 1
       uint32_t b[4];
@@ -890,11 +904,6 @@ class Step {
       P.vt8[16 * c + 2 * p][h8] = lo;
       P.vt8[16 * c + 2 * p + 1][h8] = hi;
     }
-    if (tid < ROPE_CH * SUB) {
-      const int t = tid / ROPE_CH;
-      P.kf16[t][DV / 16 + tid % ROPE_CH] = sl[t] >= 0 ? gt.rope : u32x4{0u, 0u, 0u, 0u};
-    }
-    if (tid < SUB) P.kvs[tid] = sl[tid] >= 0 ? gt.sc : 0.f;
   }
 
   // Split j of row s's nsp: its TOPK / nsp selected tokens in sub-tiles of SUB. LONG: a
@@ -975,7 +984,8 @@ class Step {
       // and held across it
       const int lane = LONG ? opaque_v(tid) % WAVE : this->lane, g = lane / 16, r = lane % 16;
       const int wv = LONG ? opaque_v(tid) / WAVE : wave;
-      gather_store(P, st, gt);
+      u32x4 w[4];
+      gather_store(P, st, gt, w, !LONG);
       __syncthreads();
       // the next sub-tile's rows, in flight while this one computes (in three parts, one
       // before each phase)
@@ -998,6 +1008,7 @@ class Step {
         P.pf4[wv / 4][r][4 * (wv % 4) + g] = s0;
         P.pf4[wv / 4][16 + r][4 * (wv % 4) + g] = s1;
       }
+      if (LONG) gather_store_vt(P, w);  // under the q.k MFMAs (read by p.v, after the softmax's barrier)
       if (next) gather_load_part(P, st + 1, gt, 1);
       __syncthreads();
       // online softmax: head tid / 16, tokens 4 (tid % 16) .. + 3; the head's reductions
