@@ -24,9 +24,14 @@ IH, ID, NH, DQK, DV, PAGE, TOPK = 64, 128, 32, 576, 512, 64, 2048
 
 
 def splits_of(rows: int) -> int:
-    """Attention splits a row (and merges: 32 / splits heads each): 32 up to 16 rows, then
-    fewer and longer ones, so a step's splits fill one round of a 256-CU grid."""
-    return 32 if rows <= 16 else 8 if rows <= 32 else 4
+    """Attention splits a row: 32 up to 16 rows, then fewer and longer ones, so a step's
+    splits fill one round of a 256-CU grid."""
+    return 32 if rows <= 16 else 8 if rows <= 32 else 5 if rows <= 48 else 4
+
+
+def merges_of(rows: int) -> int:
+    """Merge tasks a row (32 / merges heads each): as many as splits, except 4 with 5."""
+    return 4 if splits_of(rows) == 5 else splits_of(rows)
 SOFTMAX_SCALE = (128 + 64) ** -0.5  # (qk_nope + qk_rope)^-1/2, glm53/gfx950/config.py:171-173
 
 
@@ -93,7 +98,7 @@ def n_tasks(max_ctx: int, rows: int) -> int:
     """Tasks of one attention launch over ``rows`` rows (the timeline's length)."""
     team = 16 if rows <= 16 else 4  # top-k team members a row
     n_score = -(-rows * (max_ctx // 1024) // team) * team  # padded to whole top-k teams
-    return n_score + rows * team + 2 * rows * splits_of(rows)
+    return n_score + rows * team + rows * (splits_of(rows) + merges_of(rows))
 
 
 def attn_args(dev, max_rows: int, max_ctx: int, step: AttnStep, caches: AttnCaches, out: torch.Tensor | None,

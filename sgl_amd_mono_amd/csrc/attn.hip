@@ -18,8 +18,10 @@ __global__ __launch_bounds__(AT, 1) void k_attn(Args args) {
 hipError_t attn_occupancy(int* blocks_per_cu) {
   int a = 0, b = 0;
   hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&a, k_attn, AT, 0);
+  int c = 0;
   if (e == hipSuccess) e = attn_long_occupancy(&b);
-  *blocks_per_cu = a < b ? a : b;
+  if (e == hipSuccess) e = attn_wide_occupancy(&c);
+  *blocks_per_cu = a < b ? (a < c ? a : c) : (b < c ? b : c);
   return e;
 }
 
@@ -27,6 +29,7 @@ hipError_t attn_occupancy(int* blocks_per_cu) {
 hipError_t attn_forward(const AttnArgs& g, int grid, const Mail& mail, const GuardArgs& guard, hipStream_t st) {
   if (g.rows < 1 || g.rows > MAX_ROWS || grid < 1 || mail.max_ctx % CHUNK || mail.max_ctx > MAX_CTX)
     return hipErrorInvalidConfiguration;
+  if (g.rows > WIDE_ROWS) return attn_wide_forward(g, grid, mail, guard, st);
   if (g.rows > LONG_ROWS) return attn_long_forward(g, grid, mail, guard, st);
   Args a;
   fill_args(a, g, mail, guard);

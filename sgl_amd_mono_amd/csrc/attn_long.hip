@@ -24,7 +24,7 @@ hipError_t attn_long_occupancy(int* blocks_per_cu) {
 }
 
 hipError_t attn_long_forward(const AttnArgs& g, int grid, const Mail& mail, const GuardArgs& guard, hipStream_t st) {
-  if (g.rows <= LONG_ROWS || g.rows > MAX_ROWS || grid < 1 || mail.max_ctx % CHUNK || mail.max_ctx > MAX_CTX)
+  if (g.rows <= LONG_ROWS || g.rows > WIDE_ROWS || grid < 1 || mail.max_ctx % CHUNK || mail.max_ctx > MAX_CTX)
     return hipErrorInvalidConfiguration;
   Args a;
   fill_args(a, g, mail, guard);

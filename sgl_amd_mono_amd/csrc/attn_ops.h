@@ -23,9 +23,12 @@ constexpr int SPLITS = 32;      // attention splits a row at most (64 selected t
 constexpr int SPLIT_MAX = TOPK / 4;  // selected tokens a split at most
 // Attention splits a row: 32 up to 16 rows (the layer's widest step), then fewer and
 // longer ones, so a step's splits (rows x splits <= 256) fill one round of a 256-CU
-// grid; a row's merges are as many, of 32 / splits heads each.
-__host__ __device__ constexpr int splits_of(int rows) { return rows <= 16 ? 32 : rows <= 32 ? 8 : 4; }
+// grid (split j of n takes the 64-token sub-tiles [32 j / n, 32 (j + 1) / n)); a row's
+// merges are as many, of 32 / splits heads each, except with 5 splits: 4 merges of 8.
+__host__ __device__ constexpr int splits_of(int rows) { return rows <= 16 ? 32 : rows <= 32 ? 8 : rows <= 48 ? 5 : 4; }
+__host__ __device__ constexpr int merges_of(int rows) { return splits_of(rows) == 5 ? 4 : splits_of(rows); }
 constexpr int LONG_ROWS = 16;  // steps above this take long splits (only k_attn holds them)
+constexpr int WIDE_ROWS = 48;  // steps above this take 4 even splits a row (k_attn_wide)
 constexpr int TEAM = 16;        // workgroups selecting one row's top-k together
 constexpr int TEAM_LONG = 4;    // the same above LONG_ROWS rows (k_attn_long): one round of teams
 constexpr int PASSES = 4;       // 8-bit radix digits of a 32-bit key
@@ -68,6 +71,10 @@ hipError_t attn_forward(const AttnArgs& a, int grid, const Mail& mail, const Gua
 // the launch of a step above LONG_ROWS rows (attn_forward dispatches to it)
 hipError_t attn_long_occupancy(int* blocks_per_cu);
 hipError_t attn_long_forward(const AttnArgs& a, int grid, const Mail& mail, const GuardArgs& guard, hipStream_t st);
+// the launch of a step above WIDE_ROWS rows (the same phase built with 4 even splits a
+// row only: the 5-split merges cost these steps 1.3-1.9 us in one kernel)
+hipError_t attn_wide_occupancy(int* blocks_per_cu);
+hipError_t attn_wide_forward(const AttnArgs& a, int grid, const Mail& mail, const GuardArgs& guard, hipStream_t st);
 
 }  // namespace attn
 }  // namespace mono

@@ -241,8 +241,8 @@ class Step {
   // tasks in the list: score tasks padded to a multiple of TMK so no top-k team
   // straddles a round, then top-k members, splits, merges
   MONO_DEV int n_score() const { return (A.rows * CH + TMK - 1) / TMK * TMK; }
-  // (a row's splits_of(rows) merges of 32 / splits_of(rows) heads each cover its NH heads)
-  MONO_DEV int n_tasks() const { return n_score() + A.rows * TMK + 2 * A.rows * splits_of(A.rows); }
+  // (a row's merges_of(rows) merges of 32 / merges_of(rows) heads each cover its NH heads)
+  MONO_DEV int n_tasks() const { return n_score() + A.rows * TMK + A.rows * (splits_of(A.rows) + merges_of(A.rows)); }
   MONO_DEV int n_topk() const { return A.rows * TMK; }
 
   // This workgroup's tasks (false, workgroup-uniform: a wait failed).
@@ -288,8 +288,13 @@ class Step {
         if (!ok) return false;
       }
     }
-    if (!kLongSplits || nsp == SPLITS) return merges<SPLITS>(n_sc + n_topk + n_split);
-    return nsp == 8 ? merges<8>(n_sc + n_topk + n_split) : merges<4>(n_sc + n_topk + n_split);
+    if (!kLongSplits || nsp == SPLITS) return merges<SPLITS, 1>(n_sc + n_topk + n_split);
+#ifdef MONO_ATTN_WIDE
+    return nsp == 8 ? merges<8, 4>(n_sc + n_topk + n_split) : merges<4, 8>(n_sc + n_topk + n_split);
+#else
+    if (nsp == 8) return merges<8, 4>(n_sc + n_topk + n_split);
+    return nsp == 5 ? merges<5, 8>(n_sc + n_topk + n_split) : merges<4, 8>(n_sc + n_topk + n_split);
+#endif
   }
 
  private:
@@ -906,14 +911,21 @@ class Step {
     }
   }
 
-  // Split j of row s's nsp: its TOPK / nsp selected tokens in sub-tiles of SUB. LONG: a
-  // split may hold several sub-tiles (fewer than SPLITS splits a row).
+  // Split j of row s's nsp: its selected tokens in sub-tiles of SUB, [32 j / nsp, 32 (j +
+  // 1) / nsp) of the row's 32. LONG: a split may hold several sub-tiles (fewer than
+  // SPLITS splits a row).
   template <bool LONG>
   MONO_DEV bool split_task(int s, int j, int nsp) {
     SplitLds& P = L.u.sp;
     const int nsel = min(row_len(s), TOPK);
-    const int len = LONG ? TOPK / nsp : TOPK / SPLITS;
+#ifdef MONO_ATTN_WIDE
+    const int len = LONG ? TOPK / nsp : TOPK / SPLITS;  // 4 even splits a row
     const int lo = j * len;
+#else
+    constexpr int NST = TOPK / SUB;  // sub-tiles a row
+    const int lo = LONG ? (j * NST / nsp) * SUB : j * (TOPK / SPLITS);
+    const int len = LONG ? ((j + 1) * NST / nsp) * SUB - lo : TOPK / SPLITS;
+#endif
     const int cnt = min(max(nsel - lo, 0), len);
     const size_t mlb = ((size_t)s * SPLITS + j) * NH;
     if (cnt == 0) {  // an empty split contributes nothing to the merge
@@ -1109,27 +1121,26 @@ class Step {
   }
 
   // ---------------------------------------------------------------- merge
-  // This workgroup's merges: list index `at` + k is merge k (row k / NSP, heads
-  // (k % NSP) HM ..), HM = 32 / NSP heads a task.
-  template <int NSP>
+  // This workgroup's merges over a row's NSP splits: list index `at` + k is merge k (row
+  // k / (32 / HM), heads (k % (32 / HM)) HM ..), HM heads a task.
+  template <int NSP, int HM>
   MONO_DEV bool merges(int at) {
-    const int n = A.rows * NSP;
+    constexpr int MPR = SPLITS / HM;  // merges a row
+    const int n = A.rows * MPR;
     for (int T = first_at_or_after(at); T < at + n; T += G) {
       const uint64_t t0 = now_ticks();
       const int k = T - at;
-      const bool ok = merge_task<NSP>(k / NSP, k % NSP);
+      const bool ok = merge_task<NSP, HM>(k / MPR, k % MPR);
       stamp(T, t0, 3);
       if (!ok) return false;
     }
     return true;
   }
 
-  // Merge (row s, heads hg HM .. hg HM + HM - 1) over the row's NSP splits, HM = 32 /
-  // NSP: each thread combines IPT channel pairs (a task takes in NSP x HM KB = 32 KB of
-  // partials).
-  template <int NSP>
+  // Merge (row s, heads hg HM .. hg HM + HM - 1) over the row's NSP splits: each thread
+  // combines IPT channel pairs (a task takes in NSP x HM KB of partials, 32 or 40 KB).
+  template <int NSP, int HM>
   MONO_DEV bool merge_task(int s, int hg) {
-    constexpr int HM = SPLITS / NSP;
     constexpr int ITEMS = HM * DV / 2;                // channel pairs of the task
     constexpr int IPT = ITEMS > AT ? ITEMS / AT : 1;  // pairs a thread
     static_assert(NSP <= WAVE && HM <= AW && HM <= 8 && (ITEMS % AT == 0 || ITEMS < AT) && NH % HM == 0,

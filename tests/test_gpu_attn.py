@@ -110,9 +110,19 @@ def test_attn_24_rows_long_splits(rt, gpu_device):
 
 
 def test_attn_48_rows_full_contexts(rt, gpu_device):
-    """BASELINE config 3 at its largest size: 48 rows of (nearly) 32768 keys each."""
+    """BASELINE config 3 at its largest size: 48 rows of (nearly) 32768 keys each (5 splits
+    a row of 6 or 7 sub-tiles, merges of 8 heads)."""
     ctx = [32768] * 44 + [32767, 32704, 30001, 16385]
     _check(rt, ctx, 7, gpu_device)
+
+
+def test_attn_56_rows_wide_launch(rt, gpu_device):
+    """Above 48 rows the launch takes 4 even splits a row (its own kernel build): the same
+    selection and, within the bound, the same output."""
+    g = torch.Generator().manual_seed(11)
+    ctx = torch.randint(1, 32768, (56,), generator=g).tolist()
+    ctx[0], ctx[1], ctx[2], ctx[3] = 32768, 2048, 2049, 300
+    _check(rt, ctx, 13, gpu_device)
 
 
 @pytest.mark.parametrize("period", [1, 6])
