@@ -396,9 +396,9 @@ class Step {
   MONO_DEV void score_load_head(int T, ScoreOps& o) const {
     score_where(T, o);
     if (o.k0 >= o.n) return;
-    score_query(o);
 #pragma unroll
     for (int i = 0; i < KEYS_WAVE / PAGE; ++i) o.pg[i] = page_of(o.s, o.k0 + i * PAGE);
+    score_query(o);  // after the page numbers: their wait does not wait for the query
   }
   MONO_DEV void score_key_tile(ScoreOps& o, int kt) const {
     o.kb[kt] = ld_nt_u32x4(A.ikv + ((size_t)(o.pg[kt / 4] * 4 + g) * PAGE + (kt % 4) * 16 + r) * 16);
@@ -429,8 +429,9 @@ class Step {
   // reaches the barriers; a wave past the row computes nothing.
   MONO_DEV void score_compute(const ScoreOps& o, ScoreOps& nx, bool more) {
     const bool live = o.k0 < o.n;  // wave-uniform
-    // the next task's key tiles: two an iteration over the second half of this task's
-    // tiles (its page numbers have landed by then)
+    // the next task's key tiles: two an iteration over this task's tiles 2-5 (its page
+    // numbers, loaded first, have landed by then; tiles 4-7 measured 2.6 us slower at 48
+    // rows, their loads still in flight at the task's acknowledgement wait)
     const bool nx_live = more && nx.k0 < nx.n;  // wave-uniform
     float sc[2] = {0.f, 0.f};
     if (live) {
@@ -451,9 +452,9 @@ class Step {
       for (int kt = 0; kt < KTILES; ++kt) {
         if (kt + 1 < KTILES) score_mfmas(o, kt + 1, d[(kt + 1) % 2]);
         static_assert(KTILES % 2 == 0, "two tiles an iteration");
-        if (nx_live && kt >= KTILES / 2) {
-          score_key_tile(nx, 2 * kt - KTILES);
-          score_key_tile(nx, 2 * kt - KTILES + 1);
+        if (nx_live && kt >= 2 && kt < 2 + KTILES / 2) {
+          score_key_tile(nx, 2 * kt - 4);
+          score_key_tile(nx, 2 * kt - 3);
         }
         float part = 0.f;
 #pragma unroll
